@@ -1,0 +1,118 @@
+/*
+ * urb_oracle.h -- CPU restatement of the reference's routed-expert MoE path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker and the timed CPU baseline.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the product
+ * (urbilateria_amd/, include/urb_moe.h) never links, loads or calls it.
+ *
+ * Every function restates one function of inspirewind/Urbilateria 0.2.4 (Rust), cited as
+ * file:line.  The reference cannot be compiled here (no Rust toolchain, crates not vendored),
+ * so these are restatements, pinned by the reference's own known-answer tests and by closed
+ * forms in tests/test_oracle_*.py.
+ *
+ * Host assumptions the reference makes at run time and this restatement fixes:
+ *   - x86_64 with AVX2 + FMA: the reference then selects the 8-lane FP32-FMA BF16 GEMV
+ *     (src/model/bf16.rs:249-251) and the compact 1x32 MXFP8 kernel (src/math/mxfp.rs:720-729).
+ *   - Rust f32::exp is the platform libm expf (glibc on x86_64-linux-gnu).
+ */
+#ifndef URB_ORACLE_H
+#define URB_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: the reference's error enums collapsed to one integer space. */
+enum {
+    URBO_OK = 0,
+    URBO_SHAPE = 1,            /* MxError::Shape, MatrixError::{InvalidShape,InputLength} */
+    URBO_INVALID_SCALE = 2,    /* MxError::InvalidScale (E8M0 0xFF) */
+    URBO_NONFINITE = 3,        /* MxError::NonFinite, MatrixError::NonFinite, RouteError::NonFinite */
+    URBO_INVALID_GEOMETRY = 4, /* RouteError::InvalidGeometry, Qwen38MoeError::InvalidGeometry */
+};
+
+enum { URBO_FMT_BF16 = 0, URBO_FMT_MXFP4 = 1, URBO_FMT_MXFP8 = 2 };
+enum { URBO_ROUTER_SOFTMAX_TOPK = 0, URBO_ROUTER_SIGMOID_NOAUX_TC = 1 };
+/* QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243).
+ * GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176). */
+enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1 };
+
+/* ---- element decoders (src/math/mxfp.rs, src/model/bf16.rs, src/models/qwen3_8/math.rs) ---- */
+int urbo_decode_e8m0(uint8_t code, float *out);
+float urbo_decode_e2m1(uint8_t code);
+float urbo_decode_e4m3fn(uint8_t code);
+uint8_t urbo_encode_e4m3fn_finite(float value);
+float urbo_power_of_two_ceiling(float value);
+int urbo_simulate_e4m3_activation(float *values, size_t n, size_t block);
+int urbo_round_to_bf16(float value, float *out);
+int urbo_round_to_bf16_in_place(float *values, size_t n);
+
+/* ---- matrices: row-major [rows, cols] in the reference's packed layouts ---- */
+int urbo_validate(int format, const uint8_t *data, const uint8_t *scales, size_t rows, size_t cols);
+int urbo_row(int format, const uint8_t *data, const uint8_t *scales, size_t rows, size_t cols,
+             size_t row, float *out);
+/* WeightMatrix::matvec_rows for the format (BF16 and MXFP4: ordered f64; MXFP8 1x32: compact FMA). */
+int urbo_matvec_rows(int format, const uint8_t *data, const uint8_t *scales, size_t rows,
+                     size_t cols, size_t start, size_t count, const float *x, float *out);
+/* Bf16Matrix::matvec_rows_fp32 (8-lane FMA tree). */
+int urbo_bf16_matvec_rows_fp32(const uint16_t *data, size_t rows, size_t cols, size_t start,
+                               size_t count, const float *x, float *out);
+/* MxFp4Matrix::matvec_rows_fp32 (sequential fp32, no FMA). */
+int urbo_mxfp4_matvec_rows_fp32(const uint8_t *packed, const uint8_t *scales, size_t rows,
+                                size_t cols, size_t start, size_t count, const float *x,
+                                float *out);
+/* MxFp8Matrix::matvec_rows with the ordered-f64 kernel (non-AVX2 hosts / block layouts). */
+int urbo_mxfp8_matvec_rows_f64(const uint8_t *codes, const uint8_t *scales, size_t rows,
+                               size_t cols, size_t start, size_t count, const float *x,
+                               float *out);
+
+/* ---- routers ---- */
+int urbo_route_softmax_top_k(const float *logits, size_t n, size_t top_k, int32_t *ids,
+                             float *weights);
+int urbo_route_noaux_tc(const float *logits, const float *bias, size_t n, size_t top_k,
+                        size_t n_group, size_t topk_group, int normalize, float scale,
+                        int32_t *ids, float *weights, float *selection);
+float urbo_silu(float value);
+
+/* ---- one MoE layer ---- */
+typedef struct {
+    const uint8_t *data;   /* BF16 LE bytes, packed E2M1 nibbles, or E4M3 bytes */
+    const uint8_t *scales; /* E8M0 [rows, cols/32]; NULL for BF16 */
+} urbo_matrix;
+
+typedef struct {
+    uint32_t hidden, n_experts, top_k, intermediate, shared_intermediate;
+    int32_t expert_format, shared_format, router, composition;
+    uint32_t n_group, topk_group;
+    int32_t normalize;
+    float routed_scaling_factor;
+    const uint16_t *router_weight; /* [E, H] BF16 */
+    const float *correction_bias;  /* [E] or NULL (zeros) */
+    const urbo_matrix *experts;    /* [E][3] = gate [I,H], up [I,H], down [H,I] */
+    const urbo_matrix *shared;     /* [3] or NULL */
+} urbo_layer;
+
+/* GatedMlp::forward (src/model/mlp.rs:90-99) over n tokens [n, H] -> [n, H]. */
+int urbo_gated_mlp(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
+                   uint32_t intermediate, const float *x, uint32_t n, float *y, int threads);
+/* Qwen38Expert::forward_projections_batch with BF16 weights (src/models/qwen3_8/expert.rs:209-312). */
+int urbo_qwen_expert(const urbo_matrix *gate_up_down, uint32_t hidden, uint32_t intermediate,
+                     const float *x, uint32_t n, float *y, int threads);
+
+/* Forward T tokens [T, H] -> y [T, H]; routes per token in ranking order (ids, weights [T, k]);
+ * router logits [T, E] (may be NULL).  threads >= 1 selects the row-parallel pool width; every
+ * row keeps its scalar reduction order so results are identical for any thread count.
+ * Returns the first error in token order. */
+int urbo_moe_forward(const urbo_layer *layer, const float *x, uint32_t tokens, float *y,
+                     int32_t *ids, float *weights, float *logits, int threads);
+
+/* Bytes of one expert matrix for a format. */
+size_t urbo_matrix_bytes(int format, size_t rows, size_t cols, size_t *scale_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,388 @@
+"""Pins the oracle's matvec kernels, routers and layer composition: reference KATs,
+exact-rational sums (fractions) on small inputs, and the reference's own tolerance contracts."""
+
+import json
+import math
+import os
+import struct
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from urbilateria_amd import configs as C
+from urbilateria_amd import synth
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+EPS32 = float(np.finfo(np.float32).eps)
+
+
+def bf16_bits(values):
+    return synth.bf16_rne_bits(np.asarray(values, np.float32))
+
+
+def test_bf16_matrix_contract_kat():
+    k = KATS["bf16_matrix_contract"]
+    w = bf16_bits(k["weights"])
+    x = np.array(k["input"], np.float32)
+    assert list(O.matvec_rows(O.FMT_BF16, w, None, 2, 2, x)) == k["matvec"]
+    assert list(O.row(O.FMT_BF16, w, None, 2, 2, 0)) == k["row0"]
+    assert list(O.bf16_matvec_rows_fp32(w, 2, 2, x)) == k["matvec"]
+
+
+def test_bf16_linear_rounds_to_bf16_kat():
+    # qwen3_8/math.rs:139-148: FP32 GEMV of [1,1]·[1.001,1.001] then BF16 -> 2.0
+    k = KATS["bf16_linear_materializes_bf16"]
+    w = bf16_bits(k["weight"])
+    y = O.bf16_matvec_rows_fp32(w, 1, 2, np.array(k["input"], np.float32))
+    assert O.round_to_bf16(float(y[0])) == k["bf16_output"]
+
+
+def test_bf16_f64_matvec_signed_zero():
+    # bf16.rs:1000-1022: a row of -0.0 times +1 sums to -0.0 (sum starts at -0.0).
+    for cols in (1, 7, 8, 9, 32, 33):
+        w = bf16_bits([-0.0] * cols)
+        y = O.matvec_rows(O.FMT_BF16, w, None, 1, cols, np.ones(cols, np.float32))
+        assert struct.pack("<f", y[0]) == struct.pack("<f", -0.0)
+
+
+def _rng_bf16(rng, n, scale=1.0):
+    return bf16_bits(rng.standard_normal(n).astype(np.float32) * scale)
+
+
+@pytest.mark.parametrize("cols", [1, 7, 8, 9, 31, 65, 512, 2048])
+def test_bf16_f64_matvec_is_the_correctly_rounded_exact_sum_on_exact_partials(cols):
+    # With small-integer weights and inputs every partial f64 sum is exact, so the ordered sum
+    # equals the exact rational sum: a dropped term, wrong index or sign shows up here.
+    rng = np.random.default_rng(cols)
+    rows = 5
+    w = rng.integers(-8, 9, rows * cols).astype(np.float32)
+    x = rng.integers(-8, 9, cols).astype(np.float32)
+    y = O.matvec_rows(O.FMT_BF16, bf16_bits(w), None, rows, cols, x)
+    exact = w.reshape(rows, cols).astype(np.int64) @ x.astype(np.int64)
+    assert np.array_equal(y, exact.astype(np.float32))
+    y32 = O.bf16_matvec_rows_fp32(bf16_bits(w), rows, cols, x)
+    assert np.array_equal(y32, exact.astype(np.float32))
+
+
+def test_bf16_fp32_tree_stays_within_reference_contract():
+    # bf16.rs:1025-1052 (same index-formula inputs): |fp32 - f64| <= 64 eps sum|p|.
+    rows, cols = 17, 97
+    values = np.array([((i * 29) % 257 - 128.0) / 64.0 for i in range(rows * cols)], np.float32)
+    x = np.array([((i * 17) % 127 - 63.0) / 32.0 for i in range(cols)], np.float32)
+    w = bf16_bits(values)
+    ref = O.matvec_rows(O.FMT_BF16, w, None, rows, cols, x)
+    got = O.bf16_matvec_rows_fp32(w, rows, cols, x)
+    vals = synth.bf16_to_f32(w).reshape(rows, cols)
+    for r in range(rows):
+        abs_sum = float(np.sum(np.abs(vals[r].astype(np.float64) * x.astype(np.float64))))
+        assert abs(float(got[r]) - float(ref[r])) <= 64 * EPS32 * max(abs_sum, 1.0)
+
+
+def test_bf16_fp32_tree_lane_order_kat():
+    # Hand-derived: lane 0 receives columns 0, 8, 16 (products 2^24, 1, 1) so it absorbs both 1s
+    # (2^24 + 1 rounds to 2^24 twice); lane 1 gets -2^24.  Tree: (2^24) + (-2^24) + 0... = 0.
+    # A column-sequential f32 sum would give 2^24 - 2^24 + 1 + 1 = 2 instead.
+    cols = 24
+    w = np.zeros(cols, np.float32)
+    w[0], w[1], w[8], w[16] = 2.0 ** 24, -(2.0 ** 24), 1.0, 1.0
+    x = np.ones(cols, np.float32)
+    y = O.bf16_matvec_rows_fp32(bf16_bits(w), 1, cols, x)
+    assert y[0] == 0.0
+    # f64 ordered reference keeps the two ones.
+    assert O.matvec_rows(O.FMT_BF16, bf16_bits(w), None, 1, cols, x)[0] == 2.0
+    # Tail columns (cols % 8) are added after the lane sum with a separate multiply and add.
+    w2 = np.zeros(9, np.float32)
+    w2[0], w2[8] = 2.0 ** 24, 1.0
+    assert O.bf16_matvec_rows_fp32(bf16_bits(w2), 1, 9, np.ones(9, np.float32))[0] == 2.0 ** 24
+
+
+def _exact_mxfp4_dot(packed, scales, cols, x):
+    acc = Fraction(0)
+    for c in range(cols):
+        b = int(packed[c // 2])
+        code = b & 15 if c % 2 == 0 else b >> 4
+        w = Fraction(float(O.decode_e2m1(code))) * Fraction(math.ldexp(1.0, int(scales[c // 32]) - 127))
+        acc += w * Fraction(float(x[c]))
+    return acc
+
+
+@pytest.mark.parametrize("cols", [2, 32, 64, 130, 2048])
+def test_mxfp4_f64_matvec_vs_exact_rational(cols):
+    rng = np.random.default_rng(cols)
+    rows = 3
+    packed = rng.integers(0, 256, (rows, (cols + 1) // 2)).astype(np.uint8)
+    scales = rng.integers(119, 126, (rows, (cols + 31) // 32)).astype(np.uint8)
+    x = synth.bf16_values(rng.standard_normal(cols).astype(np.float32))
+    y = O.matvec_rows(O.FMT_MXFP4, packed, scales, rows, cols, x)
+    for r in range(rows):
+        ex = _exact_mxfp4_dot(packed[r], scales[r], cols, x)
+        # bf16 x times E2M1*2^k: partial sums are exact in f64, so the f32 result is the
+        # correctly rounded exact value.
+        assert y[r] == np.float32(float(ex)), (r, y[r], float(ex))
+
+
+def test_mxfp4_fp32_sequential_kat_and_errors():
+    # mxfp.rs:2719-2760 style: the fp32 form is the explicit sequential loop
+    # sum += (e2m1 * scale) * x.  Checked here on a case where order matters.
+    cols = 34
+    packed = np.zeros(17, np.uint8)
+    packed[0] = 0x07          # col0 = 6.0, col1 = 0
+    packed[1] = 0x0F          # col2 = -6.0
+    packed[16] = 0x02         # col32 = 1.0 (second group)
+    scales = np.array([127 + 22, 127], np.uint8)  # group0 scale 2^22, group1 scale 1
+    x = np.ones(cols, np.float32)
+    # sequential: 6*2^22 - 6*2^22 + 1 = 1 exactly
+    assert O.mxfp4_matvec_rows_fp32(packed, scales, 1, cols, x)[0] == 1.0
+    # non-finite output is an error in the fp32 form (mxfp.rs:1719-1721)
+    big = np.array([254], np.uint8)
+    with pytest.raises(O.OracleError):
+        O.mxfp4_matvec_rows_fp32(np.full(16, 0x77, np.uint8), big, 1, 32, np.ones(32, np.float32))
+    # infinite input is rejected
+    with pytest.raises(O.OracleError):
+        x2 = np.ones(32, np.float32)
+        x2[7] = np.inf
+        O.matvec_rows(O.FMT_MXFP4, np.full(16, 0x22, np.uint8), np.array([127], np.uint8), 1, 32, x2)
+
+
+def test_mxfp8_compact_within_reference_contract():
+    # mxfp.rs:2302-2343 inputs: rows 17, cols 97, codes cycling a finite list.
+    rows, cols = 17, 97
+    finite = [0x00, 0x07, 0x18, 0x38, 0x48, 0x70, 0x7E, 0xB8, 0xFE]
+    codes = np.array([finite[(i * 17) % len(finite)] for i in range(rows * cols)], np.uint8)
+    sc = (cols + 31) // 32
+    scales = np.array([119 + (i * 13) % 17 for i in range(rows * sc)], np.uint8)
+    x = np.array([((i * 29) % 127 - 63.0) / 128.0 for i in range(cols)], np.float32)
+    got = O.matvec_rows(O.FMT_MXFP8, codes, scales, rows, cols, x)
+    ref64 = O.mxfp8_matvec_rows_f64(codes, scales, rows, cols, x)
+    for r in range(rows):
+        exact = 0.0
+        abs_sum = 0.0
+        for c in range(cols):
+            p = float(O.decode_e4m3fn(int(codes[r * cols + c]))) * math.ldexp(1.0, int(scales[r * sc + c // 32]) - 127) * float(x[c])
+            exact += p
+            abs_sum += abs(p)
+        tol = 64 * EPS32 * max(abs_sum, 1.0)
+        assert abs(float(got[r]) - exact) <= tol
+        assert abs(float(ref64[r]) - exact) <= tol
+
+
+def test_mxfp8_compact_lane_order_kat():
+    # lane 0 gets columns 0, 8 (1x32 block: groups of 8 columns feed lanes 0..7).
+    cols = 32
+    codes = np.zeros(cols, np.uint8)
+    e = lambda v: O.encode_e4m3fn_finite(v)
+    codes[0], codes[1], codes[8] = e(256.0), e(-256.0), e(2.0 ** -8)
+    scales = np.array([127 + 16], np.uint8)   # x 2^16 -> 2^24, -2^24, 2^8
+    x = np.ones(cols, np.float32)
+    # lanes: l0 = fma(2^24,1,0)=2^24 then fma(2^8,1,2^24)=2^24+2^8 (exact), l1 = -2^24.
+    assert O.matvec_rows(O.FMT_MXFP8, codes, scales, 1, cols, x)[0] == 2.0 ** 8
+
+
+def test_mxfp8_validation_order():
+    codes = np.full(32, 0x38, np.uint8)
+    scales = np.array([127], np.uint8)
+    assert O.validate(O.FMT_MXFP8, codes, scales, 1, 32) == O.OK
+    for inv in (0x7F, 0xFF):
+        c = codes.copy()
+        c[5] = inv
+        assert O.validate(O.FMT_MXFP8, c, scales, 1, 32) == O.NONFINITE
+        # E4M3 NaN is reported before an invalid scale (mxfp.rs:448-453)
+        assert O.validate(O.FMT_MXFP8, c, np.array([255], np.uint8), 1, 32) == O.NONFINITE
+    assert O.validate(O.FMT_MXFP8, codes, np.array([255], np.uint8), 1, 32) == O.INVALID_SCALE
+    w = bf16_bits(np.ones(4, np.float32))
+    assert O.validate(O.FMT_BF16, w, None, 1, 4) == O.OK
+    w[2] = 0x7F80
+    assert O.validate(O.FMT_BF16, w, None, 1, 4) == O.NONFINITE
+
+
+# ---------------------------------------------------------------------- routers
+def test_softmax_topk_kats():
+    k = KATS["softmax_topk_ties"]
+    ids, w = O.route_softmax_top_k(np.array(k["logits"], np.float32), k["top_k"])
+    assert list(ids) == k["experts"]
+    assert np.all(np.abs(w - np.array(k["weights"])) < k["tolerance"])
+    k = KATS["softmax_topk_renormalised"]
+    ids, w = O.route_softmax_top_k(np.log(np.array(k["logits_ln"], np.float32)), k["top_k"])
+    assert list(ids) == k["experts"]
+    assert np.all(np.abs(w - np.array(k["weights"])) < k["tolerance"])
+    assert abs(float(w.sum()) - 1.0) < 1e-6
+    for case in KATS["qwen3_8_tiny_fixture_routes"]["cases"]:
+        ids, w = O.route_softmax_top_k(np.array(case["router_logits"], np.float32), 1)
+        assert list(ids) == case["experts"] and list(w) == case["weights"]
+
+
+def test_softmax_topk_errors():
+    with pytest.raises(O.OracleError) as e:
+        O.route_softmax_top_k(np.array([1.0, np.inf], np.float32), 1)
+    assert e.value.status == O.NONFINITE
+    with pytest.raises(O.OracleError) as e:
+        O.route_softmax_top_k(np.array([1.0, 2.0], np.float32), 3)
+    assert e.value.status == O.INVALID_GEOMETRY
+
+
+def test_softmax_topk_matches_sorting_definition():
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        logits = rng.standard_normal(160).astype(np.float32)
+        ids, w = O.route_softmax_top_k(logits, 8)
+        p = np.exp(logits.astype(np.float64) - logits.max())
+        p /= p.sum()
+        order = sorted(range(160), key=lambda i: (-p[i], i))[:8]
+        assert list(ids) == order
+        assert np.allclose(w, p[order] / p[order].sum(), rtol=1e-5)
+
+
+def test_noaux_tc_kats():
+    k = KATS["noaux_bias_selects_not_weights"]
+    ids, w, _ = O.route_noaux_tc(np.array(k["logits"], np.float32), None, k["top_k"],
+                                 k["n_group"], k["topk_group"], k["normalize"], k["scale"])
+    assert list(ids) == k["unbiased_experts"]
+    ids, w, _ = O.route_noaux_tc(np.array(k["logits"], np.float32), np.array(k["bias"], np.float32),
+                                 k["top_k"], k["n_group"], k["topk_group"], k["normalize"], k["scale"])
+    assert list(ids) == k["biased_experts"]
+    assert abs(w[0] - k["biased_weight0"]) < k["tolerance"]
+
+    k = KATS["noaux_normalised_sum"]
+    ids, w, _ = O.route_noaux_tc(np.array(k["logits"], np.float32), None, k["top_k"], k["n_group"],
+                                 k["topk_group"], k["normalize"], k["scale"])
+    assert abs(float(w.sum()) - k["weight_sum"]) < k["tolerance"]
+
+    k = KATS["noaux_group_masking"]
+    ids, w, _ = O.route_noaux_tc(np.array(k["logits"], np.float32), None, k["top_k"], k["n_group"],
+                                 k["topk_group"], k["normalize"], k["scale"])
+    assert all(i < k["all_experts_below"] for i in ids)
+
+    k = KATS["noaux_underflow_epsilon"]
+    ids, w, _ = O.route_noaux_tc(np.array(k["logits"], np.float32), None, k["top_k"], k["n_group"],
+                                 k["topk_group"], k["normalize"], k["scale"])
+    assert list(w) == k["weights"] and np.all(np.isfinite(w))
+
+    k = KATS["noaux_grouped_bias"]
+    ids, w, sel = O.route_noaux_tc(np.array(k["logits"], np.float32), np.array(k["bias"], np.float32),
+                                   k["top_k"], k["n_group"], k["topk_group"], k["normalize"], k["scale"])
+    assert list(ids) == k["experts"]
+    s4 = np.float32(0.5)
+    s5 = np.float32(1.0) / (np.float32(1.0) + np.float32(math.exp(1.0)))
+    d = np.float32(s4 + s5) + np.float32(1e-20)
+    assert abs(w[0] - s4 / d * 2) < 1e-6 and abs(w[1] - s5 / d * 2) < 1e-6
+
+
+def test_noaux_tc_matches_sorting_definition():
+    rng = np.random.default_rng(5)
+    n, k, g, tg = 256, 8, 8, 4
+    for _ in range(30):
+        logits = rng.standard_normal(n).astype(np.float32) * 1.7
+        ids, w, _ = O.route_noaux_tc(logits, None, k, g, tg, True, 1.0)
+        gate = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+        per = n // g
+        gs = [np.sort(gate[i * per:(i + 1) * per])[::-1][:2].sum() for i in range(g)]
+        keep = sorted(range(g), key=lambda i: (-gs[i], i))[:tg]
+        cand = [e for e in range(n) if e // per in keep]
+        order = sorted(cand, key=lambda e: (-gate[e], e))[:k]
+        assert list(ids) == order
+        assert np.allclose(w, gate[order] / gate[order].sum(), rtol=1e-5)
+
+
+def test_gated_mlp_formula_kat():
+    k = KATS["gated_mlp_formula"]
+    tr = [(bf16_bits(k[n]), None) for n in ("gate", "up", "down")]
+    y = O.gated_mlp(O.FMT_BF16, tr, 2, 2, np.array(k["input"], np.float32))[0]
+    first = 1.0 / (1 + math.exp(-1.0)) * 2.0
+    second = -2.0 / (1 + math.exp(2.0)) * -6.0
+    assert abs(y[0] - (first + second)) < k["tolerance"]
+    assert abs(y[1] - (first - second)) < k["tolerance"]
+
+
+# ---------------------------------------------------------------------- layer composition
+def _tokenwise(layer: C.HostLayer, x: np.ndarray):
+    """Second formulation: route and execute every token on its own, in the loop-nest order
+    of execute_streamed_moe / RuntimeMoeLayer::forward, from the oracle's element functions."""
+    s = layer.spec
+    T = x.shape[0]
+    out = np.zeros((T, s.hidden), np.float32)
+    for t in range(T):
+        xt = x[t]
+        if s.composition == C.COMPOSE_QWEN36:
+            lg = O.bf16_matvec_rows_fp32(layer.router_weight, s.n_experts, s.hidden, xt)
+            lg = np.array([O.round_to_bf16(v) for v in lg], np.float32)
+            ids, w = O.route_softmax_top_k(lg, s.top_k)
+            w = np.array([O.round_to_bf16(v) for v in w], np.float32)
+            acc = np.zeros(s.hidden, np.float32)
+            for j in sorted(range(s.top_k), key=lambda j: ids[j]):
+                y = O.qwen_expert(layer.experts[ids[j]], s.hidden, s.intermediate, xt)[0]
+                for h in range(s.hidden):
+                    c = O.round_to_bf16(np.float32(w[j] * y[h]))
+                    acc[h] = O.round_to_bf16(np.float32(acc[h] + c))
+            out[t] = acc
+        else:
+            lg = O.matvec_rows(O.FMT_BF16, layer.router_weight, None, s.n_experts, s.hidden, xt)
+            if s.router == C.ROUTER_SOFTMAX_TOPK:
+                ids, w = O.route_softmax_top_k(lg, s.top_k)
+            else:
+                ids, w, _ = O.route_noaux_tc(lg, layer.correction_bias, s.top_k, s.n_group,
+                                             s.topk_group, s.normalize, s.routed_scaling_factor)
+            acc = np.zeros(s.hidden, np.float64)
+            if layer.shared is not None:
+                acc += O.gated_mlp(s.shared_format, layer.shared, s.hidden,
+                                   s.shared_intermediate, xt)[0]
+            for j in range(s.top_k):
+                y = O.gated_mlp(s.expert_format, layer.experts[ids[j]], s.hidden,
+                                s.intermediate, xt)[0]
+                acc += np.float64(w[j]) * y.astype(np.float64)
+            out[t] = acc.astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("name", list(C.WORKLOADS))
+def test_grouped_layer_equals_tokenwise_layer_bit_for_bit(name):
+    # The reference's own grouped-vs-tokenwise equality (qwen3_6/runtime.rs:1799-1864),
+    # restated at tiny shapes for every workload's composition and formats.
+    w = C.WORKLOADS[name]
+    spec = C.small_spec(w.spec, hidden=64, n_experts=8, intermediate=32, top_k=4)
+    bias = None
+    if w.zipf_s:
+        bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.05)
+    layer = C.make_host_layer(spec, bias=bias)
+    x = synth.activations("x", 5, spec.hidden)
+    res = O.moe_forward(spec, layer.experts, layer.router_weight, x, layer.correction_bias,
+                        layer.shared, threads=3)
+    tok = _tokenwise(layer, x)
+    assert np.array_equal(res.output.view(np.uint32), tok.view(np.uint32))
+    # Thread count never changes a bit.
+    res1 = O.moe_forward(spec, layer.experts, layer.router_weight, x, layer.correction_bias,
+                         layer.shared, threads=1)
+    assert np.array_equal(res.output.view(np.uint32), res1.output.view(np.uint32))
+
+
+def test_glm_layer_vs_float64_mathematics():
+    # Independent float64 numpy evaluation of the GLM equation; the oracle's f64 paths must
+    # agree to f32 rounding.
+    w = C.WORKLOADS["c3_mxfp4_decode"]
+    spec = C.small_spec(w.spec, hidden=64, n_experts=8, intermediate=32, top_k=4)
+    layer = C.make_host_layer(spec)
+    x = synth.activations("x", 3, spec.hidden)
+    res = O.moe_forward(spec, layer.experts, layer.router_weight, x, None, layer.shared)
+
+    def deq(fmt, d, s, rows, cols):
+        return np.stack([O.row(fmt, d, s, rows, cols, r) for r in range(rows)]).astype(np.float64)
+
+    H, I = spec.hidden, spec.intermediate
+    R = synth.bf16_to_f32(layer.router_weight).astype(np.float64)
+    for t in range(3):
+        xt = x[t].astype(np.float64)
+        logits = (R @ xt).astype(np.float32)
+        assert np.array_equal(logits, res.logits[t])
+        ids = res.ids[t]
+        acc = np.zeros(H)
+        def mlp(fmt, tr, Ii):
+            g = deq(fmt, *tr[0], Ii, H) @ xt
+            u = deq(fmt, *tr[1], Ii, H) @ xt
+            a = (g / (1 + np.exp(-g))) * u
+            return deq(fmt, *tr[2], H, Ii) @ a
+        acc += mlp(spec.shared_format, layer.shared, spec.shared_intermediate)
+        for j in range(spec.top_k):
+            acc += float(res.weights[t, j]) * mlp(spec.expert_format, layer.experts[ids[j]], I)
+        rel = np.linalg.norm(res.output[t] - acc) / np.linalg.norm(acc)
+        assert rel < 1e-5

@@ -1,0 +1,223 @@
+"""Layer geometry and the five benchmark workloads.
+
+``LayerSpec`` mirrors the fields the reference's MoE layers carry: ``MoeGeometry``
+(src/models/glm/moe_geometry.rs:3-9: top_k, n_group, topk_group, normalize,
+routed_scaling_factor) plus the projection formats of ``WeightMatrix``
+(src/model/weight.rs:54-61) and the composition of the calling adapter:
+
+* ``COMPOSE_QWEN36`` -- execute_streamed_moe / execute_batched_moe
+  (src/models/qwen3_6/runtime.rs:1067-1243): FP32 router GEMV + BF16 logits, softmax top-k,
+  BF16 route weights, Qwen SwiGLU experts with BF16 boundaries, BF16 combine in ascending
+  expert id.
+* ``COMPOSE_GLM`` -- RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176): ordered
+  f64 router GEMV, softmax top-k or sigmoid noaux_tc, GatedMlp experts, f64 combine in ranking
+  order on top of the shared expert.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field, replace
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+
+from . import synth
+
+FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
+ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC = 0, 1
+COMPOSE_QWEN36, COMPOSE_GLM = 0, 1
+FORMAT_NAMES = {FMT_BF16: "bf16", FMT_MXFP4: "mxfp4", FMT_MXFP8: "mxfp8"}
+
+
+@dataclass(frozen=True)
+class LayerSpec:
+    hidden: int
+    n_experts: int
+    top_k: int
+    intermediate: int
+    shared_intermediate: int = 0
+    expert_format: int = FMT_BF16
+    shared_format: int = FMT_BF16
+    router: int = ROUTER_SOFTMAX_TOPK
+    composition: int = COMPOSE_GLM
+    n_group: int = 1
+    topk_group: int = 1
+    normalize: bool = True
+    routed_scaling_factor: float = 1.0
+
+
+def matrix_bytes(fmt: int, rows: int, cols: int) -> Tuple[int, int]:
+    """(payload bytes, scale bytes) of one [rows, cols] matrix."""
+    if fmt == FMT_BF16:
+        return rows * cols * 2, 0
+    groups = rows * ((cols + 31) // 32)
+    if fmt == FMT_MXFP4:
+        return rows * ((cols + 1) // 2), groups
+    return rows * cols, groups
+
+
+def expert_bytes(spec: LayerSpec) -> int:
+    H, I = spec.hidden, spec.intermediate
+    t = 0
+    for r, c in ((I, H), (I, H), (H, I)):
+        a, b = matrix_bytes(spec.expert_format, r, c)
+        t += a + b
+    return t
+
+
+def shared_bytes(spec: LayerSpec) -> int:
+    if not spec.shared_intermediate:
+        return 0
+    H, I = spec.hidden, spec.shared_intermediate
+    t = 0
+    for r, c in ((I, H), (I, H), (H, I)):
+        a, b = matrix_bytes(spec.shared_format, r, c)
+        t += a + b
+    return t
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    spec: LayerSpec
+    tokens: Tuple[int, ...]
+    zipf_s: Optional[float] = None
+    description: str = ""
+
+
+# The five benchmark configurations (shapes, routers, formats and value distributions).
+WORKLOADS: Dict[str, Workload] = {
+    "c1_bf16_decode": Workload(
+        "c1_bf16_decode",
+        LayerSpec(hidden=2048, n_experts=128, top_k=8, intermediate=768,
+                  expert_format=FMT_BF16, router=ROUTER_SOFTMAX_TOPK,
+                  composition=COMPOSE_QWEN36),
+        (1,), description="BF16 layer H2048 E128 top-8 softmax I768, decode 1 token"),
+    "c2_bf16_prefill": Workload(
+        "c2_bf16_prefill",
+        LayerSpec(hidden=2048, n_experts=128, top_k=8, intermediate=768,
+                  expert_format=FMT_BF16, router=ROUTER_SOFTMAX_TOPK,
+                  composition=COMPOSE_QWEN36),
+        (128,), description="BF16 layer H2048 E128 top-8 softmax I768, prefill 128 tokens"),
+    "c3_mxfp4_decode": Workload(
+        "c3_mxfp4_decode",
+        LayerSpec(hidden=7168, n_experts=256, top_k=8, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_BF16,
+                  router=ROUTER_SIGMOID_NOAUX_TC, composition=COMPOSE_GLM, n_group=8,
+                  topk_group=4, normalize=True, routed_scaling_factor=1.0),
+        (1, 32), description="MXFP4 H7168 E256 sigmoid group-limited top-8 (8 groups, top-4) "
+                             "I2048 + BF16 shared, decode 1 and 32 tokens"),
+    "c4_mxfp8": Workload(
+        "c4_mxfp8",
+        LayerSpec(hidden=6144, n_experts=160, top_k=8, intermediate=2048,
+                  expert_format=FMT_MXFP8, router=ROUTER_SOFTMAX_TOPK,
+                  composition=COMPOSE_GLM),
+        (1, 512), description="MXFP8 H6144 E160 softmax top-8 I2048, decode 1, prefill 512"),
+    "c5_mxfp4_zipf_prefill": Workload(
+        "c5_mxfp4_zipf_prefill",
+        LayerSpec(hidden=7168, n_experts=384, top_k=8, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_BF16,
+                  router=ROUTER_SIGMOID_NOAUX_TC, composition=COMPOSE_GLM, n_group=1,
+                  topk_group=1, normalize=True, routed_scaling_factor=1.0),
+        (1024,), zipf_s=1.1,
+        description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias I2048 + BF16 shared, "
+                    "prefill 1024"),
+}
+
+
+@dataclass
+class HostLayer:
+    """Packed host weights of one layer, in the reference's on-disk layouts."""
+    spec: LayerSpec
+    router_weight: np.ndarray                       # [E, H] uint16 BF16 bits
+    experts: List[List[Tuple[np.ndarray, Optional[np.ndarray]]]]  # [E][gate, up, down]
+    shared: Optional[List[Tuple[np.ndarray, Optional[np.ndarray]]]] = None
+    correction_bias: Optional[np.ndarray] = None     # [E] f32
+
+
+def _matrix(fmt: int, name: str, rows: int, cols: int, base_seed: int):
+    if fmt == FMT_BF16:
+        return synth.bf16_matrix(name, rows, cols, 0.02, base_seed), None
+    if fmt == FMT_MXFP4:
+        return synth.mxfp4_matrix(name, rows, cols, base_seed)
+    return synth.mxfp8_matrix(name, rows, cols, base_seed)
+
+
+def make_host_layer(spec: LayerSpec, base_seed: int = synth.BASE_SEED,
+                    bias: Optional[np.ndarray] = None) -> HostLayer:
+    """Generates a layer on the host (numpy).  Practical for small shapes only; full-size
+    layers are generated on the device by ``urbilateria_amd.device.make_device_layer``."""
+    H, I, E = spec.hidden, spec.intermediate, spec.n_experts
+    router = synth.bf16_matrix("router", E, H, 0.02, base_seed)
+    experts = []
+    for e in range(E):
+        experts.append([
+            _matrix(spec.expert_format, f"expert.{e}.gate", I, H, base_seed),
+            _matrix(spec.expert_format, f"expert.{e}.up", I, H, base_seed),
+            _matrix(spec.expert_format, f"expert.{e}.down", H, I, base_seed),
+        ])
+    shared = None
+    if spec.shared_intermediate:
+        Is = spec.shared_intermediate
+        shared = [
+            _matrix(spec.shared_format, "shared.gate", Is, H, base_seed),
+            _matrix(spec.shared_format, "shared.up", Is, H, base_seed),
+            _matrix(spec.shared_format, "shared.down", H, Is, base_seed),
+        ]
+    return HostLayer(spec, router, experts, shared, bias)
+
+
+def zipf_bias(n_experts: int, s: float, beta: float, base_seed: int = synth.BASE_SEED) -> np.ndarray:
+    """Correction bias b_e = beta * ln(p_e) with p_e proportional to rank_e^-s; ranks come
+    from a seeded permutation of the expert ids."""
+    keys = synth.splitmix64(synth.stream_seed("zipf.rank", base_seed), 0, n_experts)
+    rank = np.empty(n_experts, np.int64)
+    rank[np.argsort(keys, kind="stable")] = np.arange(1, n_experts + 1)
+    p = rank.astype(np.float64) ** (-s)
+    p /= p.sum()
+    return (beta * np.log(p)).astype(np.float32)
+
+
+def calibrate_zipf_beta(n_experts: int, top_k: int, s: float, logit_std: np.ndarray,
+                        tokens: int = 4096, base_seed: int = synth.BASE_SEED) -> float:
+    """Bisection on beta so the log-log slope of expert selection frequency against popularity
+    rank is -s.  Router logits are drawn as independent N(0, logit_std[e]^2), the distribution
+    a BF16 N(0, 0.02) router produces on N(0, 1) activations (logit_std[e] = ||w_e||)."""
+    z = synth.normals(synth.stream_seed("zipf.calibration", base_seed), tokens * n_experts)
+    logits = z.reshape(tokens, n_experts).astype(np.float64) * logit_std[None, :]
+    gates = 1.0 / (1.0 + np.exp(-logits))
+    keys = synth.splitmix64(synth.stream_seed("zipf.rank", base_seed), 0, n_experts)
+    rank = np.empty(n_experts, np.int64)
+    rank[np.argsort(keys, kind="stable")] = np.arange(1, n_experts + 1)
+
+    def slope(beta: float) -> float:
+        bias = zipf_bias(n_experts, s, beta, base_seed).astype(np.float64)
+        sel = gates + bias[None, :]
+        top = np.argpartition(-sel, top_k - 1, axis=1)[:, :top_k]
+        freq = np.bincount(top.ravel(), minlength=n_experts).astype(np.float64)
+        ok = freq > 0
+        return float(np.polyfit(np.log(rank[ok]), np.log(freq[ok]), 1)[0])
+
+    lo, hi = 0.0, 4.0
+    for _ in range(40):
+        mid = 0.5 * (lo + hi)
+        if slope(mid) > -s:
+            lo = mid
+        else:
+            hi = mid
+    return 0.5 * (lo + hi)
+
+
+def with_tokens(w: Workload, tokens: int) -> Tuple[LayerSpec, int]:
+    return w.spec, tokens
+
+
+def small_spec(spec: LayerSpec, hidden: int = 64, n_experts: int = 8, intermediate: int = 32,
+               top_k: Optional[int] = None) -> LayerSpec:
+    """A reduced copy of a spec for fast parity tests (keeps formats and routing rules)."""
+    k = min(spec.top_k, n_experts) if top_k is None else top_k
+    groups = spec.n_group if spec.n_group > 1 and n_experts % spec.n_group == 0 and \
+        n_experts // spec.n_group >= 2 else 1
+    return replace(spec, hidden=hidden, n_experts=n_experts, intermediate=intermediate,
+                   top_k=k, n_group=groups, topk_group=min(spec.topk_group, groups),
+                   shared_intermediate=(intermediate if spec.shared_intermediate else 0))
