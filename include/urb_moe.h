@@ -1,0 +1,158 @@
+/*
+ * urb_moe.h -- C ABI of the MI355X (gfx950) routed-expert MoE layer.
+ *
+ * Plain pointers and sizes only.  Every pointer named "device" is HBM memory on the current
+ * HIP device; `stream` is a hipStream_t passed as void* (NULL = the default stream).  All calls
+ * on one context are stream-ordered and must not overlap on different streams.
+ *
+ * Each entry point replaces a reference (inspirewind/Urbilateria 0.2.4, Rust) interface, cited
+ * below as file:line.  Status codes 1..4 mirror the reference's error enums.
+ */
+#ifndef URB_MOE_H
+#define URB_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  URB_OK = 0,
+  URB_ERR_SHAPE = 1,            /* MxError::Shape, MatrixError::{InvalidShape, InputLength} */
+  URB_ERR_INVALID_SCALE = 2,    /* MxError::InvalidScale (E8M0 0xFF)                         */
+  URB_ERR_NONFINITE = 3,        /* MxError/MatrixError/RouteError::NonFinite                 */
+  URB_ERR_INVALID_GEOMETRY = 4, /* RouteError::InvalidGeometry, Qwen38MoeError::InvalidGeometry */
+  URB_ERR_DEVICE = 5,           /* HIP runtime failure                                        */
+  URB_ERR_OUT_OF_MEMORY = 6,
+  URB_ERR_ARGUMENT = 7          /* null pointer, unsupported option                           */
+} urb_status;
+
+/* Expert weight formats: WeightMatrix::{Bf16, MxFp4, MxFp8} (src/model/weight.rs:54-61).
+ * MX formats use E8M0 scales per 32 consecutive columns of a row (MXFP8: ModelOpt 1x32). */
+typedef enum { URB_FMT_BF16 = 0, URB_FMT_MXFP4 = 1, URB_FMT_MXFP8 = 2 } urb_format;
+
+/* route_softmax_top_k (src/models/qwen3_8/moe.rs:91-159) or route_noaux_tc
+ * (src/math/routing.rs:38-155). */
+typedef enum { URB_ROUTER_SOFTMAX_TOPK = 0, URB_ROUTER_SIGMOID_NOAUX_TC = 1 } urb_router;
+
+/* Which adapter's layer call the context reproduces:
+ *  QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243):
+ *          BF16 router GEMV (FP32, 8-lane tree) + BF16 logits, BF16 route weights, BF16
+ *          boundaries inside experts and in the ascending-expert-id combine.
+ *  GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176): f64 router GEMV,
+ *          GatedMlp experts, f64 combine in ranking order on top of the shared expert. */
+typedef enum { URB_COMPOSE_QWEN36 = 0, URB_COMPOSE_GLM = 1 } urb_composition;
+
+/* Where urb_moe_create reads the weights from. */
+typedef enum {
+  URB_SOURCE_HOST = 0,          /* host memory: copied verbatim into HBM                    */
+  URB_SOURCE_DEVICE_COPY = 1,   /* device memory: copied into the context's own HBM arena  */
+  URB_SOURCE_DEVICE_BORROW = 2  /* device memory: used in place; must outlive the context   */
+} urb_weight_source;
+
+/* One matrix in its on-disk layout (row-major [rows, cols]):
+ *   BF16:  little-endian u16 [rows, cols]                     (Bf16Matrix, src/model/bf16.rs:10-15)
+ *   MXFP4: E2M1 nibbles [rows, cols/2], low nibble first      (MxFp4Matrix, src/math/mxfp.rs:1362-1369)
+ *   MXFP8: E4M3FN bytes [rows, cols]                          (MxFp8Matrix, src/math/mxfp.rs:321-329)
+ *   scales: E8M0 [rows, cols/32] for MX formats, NULL for BF16. */
+typedef struct {
+  const void *data;
+  const uint8_t *scales;
+} urb_matrix;
+
+/* Layer geometry: MoeGeometry (src/models/glm/moe_geometry.rs:3-9) plus projection formats. */
+typedef struct {
+  uint32_t hidden;               /* H */
+  uint32_t n_experts;            /* E */
+  uint32_t top_k;                /* k */
+  uint32_t intermediate;         /* I of each routed expert */
+  uint32_t shared_intermediate;  /* I of the always-on shared expert, 0 = none (GLM only) */
+  urb_format expert_format;
+  urb_format shared_format;      /* BF16 */
+  urb_router router;
+  urb_composition composition;
+  uint32_t n_group, topk_group;  /* noaux_tc group limiting; 1, 1 = none */
+  int32_t normalize;             /* noaux_tc: divide by the selected gate sum */
+  float routed_scaling_factor;   /* noaux_tc */
+  uint32_t max_tokens;           /* largest token count one forward call may pass */
+} urb_moe_desc;
+
+typedef struct {
+  const uint16_t *router_weight;   /* [E, H] BF16 */
+  const float *correction_bias;    /* [E] f32 selection bias (noaux_tc), NULL = zeros */
+  const urb_matrix *experts;       /* [E * 3]: gate [I, H], up [I, H], down [H, I] */
+  const urb_matrix *shared;        /* [3] or NULL */
+} urb_moe_weights;
+
+typedef struct urb_moe_ctx urb_moe_ctx;
+
+/* Builds a layer: shape/geometry checks, verbatim upload, one validation pass over every payload
+ * (E8M0 0xFF -> URB_ERR_INVALID_SCALE; E4M3 0x7F/0xFF or non-finite BF16 -> URB_ERR_NONFINITE).
+ * Replaces RuntimeMoeLayer::new (src/models/glm/runtime/moe.rs:78-125) together with the
+ * payload checks of MxFp4Matrix::from_packed (src/math/mxfp.rs:1371-1443), MxFp8Matrix::
+ * from_packed (src/math/mxfp.rs:338-457) and Bf16Matrix::from_le_bytes (src/model/bf16.rs:18-70). */
+urb_status urb_moe_create(const urb_moe_desc *desc, const urb_moe_weights *weights,
+                          urb_weight_source source, urb_moe_ctx **out);
+void urb_moe_destroy(urb_moe_ctx *ctx);
+
+/* One layer call over `tokens` rows x [tokens, H] (device, f32) -> y [tokens, H] (device, f32);
+ * routes per token in ranking order: ids [tokens, k] (device, i32) and weights [tokens, k]
+ * (device, f32), either may be NULL.  Replaces execute_streamed_moe / execute_batched_moe
+ * (src/models/qwen3_6/runtime.rs:1067-1243) for QWEN36 and RuntimeMoeLayer::forward
+ * (src/models/glm/runtime/moe.rs:138-176) for GLM.  Enqueues only: numerical failures the
+ * reference reports (non-finite input, activations or outputs) are latched on the device and
+ * returned by urb_moe_sync. */
+urb_status urb_moe_forward(urb_moe_ctx *ctx, const float *x, uint32_t tokens, float *y,
+                           int32_t *ids, float *weights, void *stream);
+
+/* Router only: logits [tokens, E] (device, may be NULL), ids/weights as above.  Replaces
+ * `linear(router)` + route_softmax_top_k (src/models/qwen3_8/math.rs:10-26,
+ * src/models/qwen3_8/moe.rs:91-159) and router.matvec + route_noaux_tc
+ * (src/models/glm/runtime/moe.rs:152-161). */
+urb_status urb_moe_route(urb_moe_ctx *ctx, const float *x, uint32_t tokens, float *logits,
+                         int32_t *ids, float *weights, void *stream);
+
+/* Waits for `stream` and returns the first numerical failure latched since the previous
+ * urb_moe_sync (URB_OK if none), then clears it.  The Result of the reference's layer calls. */
+urb_status urb_moe_sync(urb_moe_ctx *ctx, void *stream);
+
+/* Dequantised rows [count, cols] f32 (device) of one matrix (device): Bf16Matrix::write_row
+ * (src/model/bf16.rs:92-113), MxFp4Matrix::row (src/math/mxfp.rs:1828-1846), MxFp8Matrix::row
+ * (src/math/mxfp.rs:855-877).  Bit-exact: value = decode(code) * scale in f32. */
+urb_status urb_dequant_rows(urb_format format, const void *data, const uint8_t *scales,
+                            uint32_t rows, uint32_t cols, uint32_t row0, uint32_t count,
+                            float *out, void *stream);
+
+/* Device-time spans per stage of a layer call: the counterpart of the reference's profiling
+ * spans (ProfileStage, src/profiling.rs:75-136; span_with_work, src/profiling.rs:581-600).
+ * While enabled, every forward call brackets each stage with HIP events on the stream the
+ * stage's kernels run on and waits for them, so enable it for measurement runs only. */
+typedef enum {
+  URB_STAGE_ROUTER = 0,          /* router GEMV/GEMM -> logits           */
+  URB_STAGE_ROUTE = 1,           /* top-k routing                        */
+  URB_STAGE_PERMUTE = 2,         /* token -> expert permutation          */
+  URB_STAGE_GATE_UP = 3,         /* routed gate+up projections + SwiGLU  */
+  URB_STAGE_DOWN = 4,            /* routed down projections              */
+  URB_STAGE_SHARED_GATE_UP = 5,  /* shared expert gate+up + SwiGLU       */
+  URB_STAGE_SHARED_DOWN = 6,     /* shared expert down                   */
+  URB_STAGE_COMBINE = 7,         /* weighted combine                     */
+  URB_STAGE_COUNT = 8
+} urb_stage;
+
+/* Starts (enable != 0) or stops collecting; starting clears the totals. */
+urb_status urb_moe_profile(urb_moe_ctx *ctx, int enable);
+/* Total milliseconds and number of launches per stage since profiling was enabled
+ * (arrays of URB_STAGE_COUNT). */
+urb_status urb_moe_profile_read(const urb_moe_ctx *ctx, double *ms, uint64_t *launches);
+
+/* HBM bytes the context holds for weights (own arena; 0 when borrowed) and workspace. */
+urb_status urb_moe_memory(const urb_moe_ctx *ctx, size_t *weight_bytes, size_t *workspace_bytes);
+
+const char *urb_status_string(urb_status status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* URB_MOE_H */

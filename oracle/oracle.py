@@ -237,6 +237,8 @@ def moe_forward(spec, experts: Sequence, router_weight: np.ndarray, x: np.ndarra
     keep = []
     mats = (_Matrix * (E * 3))()
     for e in range(E):
+        if experts[e] is None:  # not supplied: the oracle reports SHAPE if routing needs it
+            continue
         for m in range(3):
             d, s = experts[e][m]
             keep += [d, s]

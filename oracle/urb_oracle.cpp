@@ -753,6 +753,7 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
         for (size_t i = 0; i < n; ++i)
             std::memcpy(&xin[i * H], x + g.tokens[i] * H, H * 4);
         const urbo_matrix *m = L->experts + g.expert * 3;
+        if (!m[0].data || !m[1].data || !m[2].data) return URBO_SHAPE;  // expert not supplied
         st = qwen ? qwen_expert(p, m, H, I, xin.data(), n, yo.data())
                   : gated_mlp(p, L->expert_format, m, H, I, xin.data(), n, yo.data());
         if (st) return st;

@@ -1,0 +1,244 @@
+"""GPU parity tests: the HIP path through the C ABI against the CPU oracle on the same seeded
+inputs.  Bars: dequantised weights bit-exact; top-k ids identical except near-ties (< 1e-6);
+layer outputs within 1e-3 relative L2."""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from urbilateria_amd import configs as C
+from urbilateria_amd import native as N
+from urbilateria_amd import synth
+
+from .gpu_helpers import REL_L2_BAR, ids_match, noaux_scores, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu(require_gpu):
+    from urbilateria_amd import moe  # noqa: F401  (fails loudly without liburb_moe.so)
+    torch.cuda.set_device(0)
+    yield
+
+
+def moe_mod():
+    from urbilateria_amd import moe
+    return moe
+
+
+def _oracle(host: C.HostLayer, x: np.ndarray, threads: int = 4):
+    return O.moe_forward(host.spec, host.experts, host.router_weight, x, host.correction_bias,
+                         host.shared, threads=threads)
+
+
+def _scores(spec, res, bias):
+    if spec.router == C.ROUTER_SOFTMAX_TOPK:
+        return res.logits
+    return noaux_scores(res.logits, bias)
+
+
+# ------------------------------------------------------------------------------- dequant
+def test_mxfp4_dequant_bit_exact_every_code_and_scale():
+    rows, cols = 255, 32
+    nib = np.tile(np.arange(16, dtype=np.uint8), 2)
+    packed = np.tile((nib[0::2] | (nib[1::2] << 4)).astype(np.uint8), (rows, 1))
+    scales = np.arange(255, dtype=np.uint8).reshape(rows, 1)
+    got = moe_mod().dequant_rows(C.FMT_MXFP4, torch.from_numpy(packed).cuda(),
+                                 torch.from_numpy(scales).cuda(), rows, cols).cpu().numpy()
+    ref = np.stack([O.row(O.FMT_MXFP4, packed, scales, rows, cols, r) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_mxfp8_dequant_bit_exact_every_code_and_scale():
+    codes = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)  # 254 finite codes
+    cols = 256
+    row = np.zeros(cols, np.uint8)
+    row[:len(codes)] = codes
+    rows = 255
+    data = np.tile(row, (rows, 1))
+    scales = np.repeat(np.arange(255, dtype=np.uint8).reshape(rows, 1), cols // 32, axis=1)
+    got = moe_mod().dequant_rows(C.FMT_MXFP8, torch.from_numpy(data).cuda(),
+                                 torch.from_numpy(np.ascontiguousarray(scales)).cuda(), rows,
+                                 cols).cpu().numpy()
+    ref = np.stack([O.row(O.FMT_MXFP8, data, scales, rows, cols, r) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_bf16_dequant_bit_exact_every_finite_encoding():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = (bits & 0x7F80) != 0x7F80
+    data = bits[finite]
+    data = data[: len(data) // 64 * 64].reshape(-1, 64)
+    got = moe_mod().dequant_rows(C.FMT_BF16, torch.from_numpy(data.view(np.int16)).cuda(), None,
+                                 data.shape[0], 64).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), data.astype(np.uint32) << 16)
+
+
+def test_device_generator_matches_host_generator():
+    spec = C.small_spec(C.WORKLOADS["c4_mxfp8"].spec, hidden=128, n_experts=4, intermediate=64)
+    dev = moe_mod().DeviceLayer.synthesize(spec).to_host()
+    host = C.make_host_layer(spec)
+    assert np.array_equal(dev.router_weight, host.router_weight)
+    for e in range(spec.n_experts):
+        for m in range(3):
+            assert np.array_equal(dev.experts[e][m][0].ravel(), host.experts[e][m][0].ravel())
+            assert np.array_equal(dev.experts[e][m][1].ravel(), host.experts[e][m][1].ravel())
+    spec4 = C.small_spec(C.WORKLOADS["c3_mxfp4_decode"].spec, hidden=128, n_experts=4,
+                         intermediate=64)
+    dev4 = moe_mod().DeviceLayer.synthesize(spec4).to_host()
+    host4 = C.make_host_layer(spec4)
+    for e in range(spec4.n_experts):
+        for m in range(3):
+            assert np.array_equal(dev4.experts[e][m][0].ravel(), host4.experts[e][m][0].ravel())
+    for m in range(3):
+        assert np.array_equal(dev4.shared[m][0].ravel(), host4.shared[m][0].view(np.uint8).ravel())
+    x = moe_mod().synth_activations(3, 128).cpu().numpy()
+    assert np.array_equal(x, synth.activations("x", 3, 128))
+
+
+# ------------------------------------------------------------------------------- layers
+SMALL = [(name, T) for name in C.WORKLOADS for T in (1, 3, 40)]
+
+
+def _small_layer(name, hidden=256, n_experts=16, intermediate=64):
+    w = C.WORKLOADS[name]
+    spec = C.small_spec(w.spec, hidden=hidden, n_experts=n_experts, intermediate=intermediate)
+    bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.05) if w.zipf_s else None
+    return C.make_host_layer(spec, bias=bias)
+
+
+@pytest.mark.parametrize("name,T", SMALL)
+def test_small_layer_matches_oracle(name, T):
+    host = _small_layer(name)
+    spec = host.spec
+    x = synth.activations(f"x.{T}", T, spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y, ids, w = layer.forward(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+    err = rel_l2(y.cpu().numpy(), ref.output)
+    assert err < REL_L2_BAR, err
+    assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    layer.close()
+
+
+@pytest.mark.parametrize("name", list(C.WORKLOADS))
+def test_router_logits_match_oracle(name):
+    host = _small_layer(name, hidden=512, n_experts=64)
+    spec = host.spec
+    x = synth.activations("x.router", 17, spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=17)
+    logits, ids, w = layer.route(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    logits = logits.cpu().numpy()
+    if spec.composition == C.COMPOSE_QWEN36:
+        # the 8-lane FP32 tree is reproduced exactly, BF16 logits are bit-identical
+        assert np.array_equal(logits.view(np.uint32), ref.logits.view(np.uint32))
+    else:
+        ulp = np.abs(logits.view(np.int32).astype(np.int64) - ref.logits.view(np.int32))
+        assert ulp.max() <= 1
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+    layer.close()
+
+
+def test_forward_is_deterministic_and_chunked_calls_equal_tokenwise():
+    host = _small_layer("c5_mxfp4_zipf_prefill", hidden=128, n_experts=16, intermediate=64)
+    T = 1100  # > one 1024-token internal chunk
+    x = torch.from_numpy(synth.activations("x.chunk", T, 128)).cuda()
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y1, i1, _ = layer.forward(x)
+    y2, i2, _ = layer.forward(x)
+    assert torch.equal(y1, y2) and torch.equal(i1, i2)
+    single = moe_mod().MoeLayer(host, max_tokens=1)
+    for t in (0, 1023, 1024, 1099):
+        ys, _, _ = single.forward(x[t:t + 1].contiguous())
+        assert rel_l2(ys.cpu().numpy(), y1[t:t + 1].cpu().numpy()) < 1e-6
+    layer.close()
+    single.close()
+
+
+# ------------------------------------------------------------------------------- errors
+def test_nonfinite_input_is_reported():
+    for name in ("c1_bf16_decode", "c3_mxfp4_decode"):
+        host = _small_layer(name)
+        layer = moe_mod().MoeLayer(host, max_tokens=2)
+        x = torch.from_numpy(synth.activations("x", 2, host.spec.hidden)).cuda()
+        x[1, 7] = float("inf")
+        with pytest.raises(N.UrbError) as e:
+            layer.forward(x)
+        assert e.value.status == N.ERR_NONFINITE
+        x[1, 7] = 0.5
+        layer.forward(x)  # the latched error was cleared; a good call succeeds
+        layer.close()
+
+
+def test_invalid_payloads_rejected_at_create():
+    host = _small_layer("c3_mxfp4_decode")
+    host.experts[3][1][1][2, 1] = 0xFF
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(host, max_tokens=1)
+    assert e.value.status == N.ERR_INVALID_SCALE
+    host = _small_layer("c4_mxfp8")
+    host.experts[2][2][0][5, 9] = 0x7F
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(host, max_tokens=1)
+    assert e.value.status == N.ERR_NONFINITE
+    host = _small_layer("c1_bf16_decode")
+    host.experts[0][0][0][0, 0] = 0x7F80
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(host, max_tokens=1)
+    assert e.value.status == N.ERR_NONFINITE
+    host = _small_layer("c5_mxfp4_zipf_prefill")
+    host.correction_bias[4] = np.nan
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(host, max_tokens=1)
+    assert e.value.status == N.ERR_INVALID_GEOMETRY
+
+
+def test_shape_and_geometry_errors():
+    import dataclasses
+    host = _small_layer("c3_mxfp4_decode")
+    bad = dataclasses.replace(host.spec, n_group=3)
+    h2 = C.HostLayer(bad, host.router_weight, host.experts, host.shared)
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(h2, max_tokens=1)
+    assert e.value.status == N.ERR_INVALID_GEOMETRY
+    layer = moe_mod().MoeLayer(host, max_tokens=2)
+    x = torch.zeros((3, host.spec.hidden), device="cuda")
+    with pytest.raises(N.UrbError) as e:
+        layer.forward(x)  # more tokens than max_tokens
+    assert e.value.status == N.ERR_SHAPE
+    layer.close()
+
+
+# ------------------------------------------------------------------------------- full size
+FULL = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
+        ("c3_mxfp4_decode", 32), ("c4_mxfp8", 1), ("c4_mxfp8", 512),
+        ("c5_mxfp4_zipf_prefill", 1024)]
+
+
+@pytest.mark.parametrize("name,T", FULL)
+def test_full_size_workload_matches_oracle_on_sampled_tokens(name, T):
+    w = C.WORKLOADS[name]
+    spec = w.spec
+    bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.1) if w.zipf_s else None
+    dev = moe_mod().DeviceLayer.synthesize(spec, correction_bias=bias)
+    x = moe_mod().synth_activations(T, spec.hidden)
+    layer = moe_mod().MoeLayer(dev, max_tokens=T)
+    y, ids, wts = layer.forward(x)
+    sample = sorted(set([0, T - 1] + list(range(0, T, max(1, T // 6)))))[:8]
+    ids_np = ids.cpu().numpy()
+    used = sorted(set(ids_np[sample].ravel().tolist()))
+    host = dev.to_host(experts=used)
+    xs = x.cpu().numpy()[sample]
+    ref = _oracle(host, xs, threads=8)
+    assert ids_match(ids_np[sample], ref.ids, _scores(spec, ref, bias))
+    err = rel_l2(y.cpu().numpy()[sample], ref.output)
+    print(f"{name} T={T}: rel L2 {err:.3e} over tokens {sample}")
+    assert err < REL_L2_BAR
+    layer.close()

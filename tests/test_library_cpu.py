@@ -1,0 +1,98 @@
+"""CPU-side checks of the product: the C-ABI libraries load and export every declared symbol,
+the host workload generator matches published SplitMix64/FNV values and the oracle's encoders,
+and the byte accounting matches the benchmark definition.  No GPU calls."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from urbilateria_amd import configs as C
+from urbilateria_amd import native as N
+from urbilateria_amd import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    return sorted(set(re.findall(r"\b(urb_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_moe_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(N.MOE_LIB)
+    declared = _declared("urb_moe.h")
+    assert declared, "no declarations found"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(N.EXPORTS) == set(declared)
+
+
+def test_synth_library_exports():
+    lib = ctypes.CDLL(N.SYNTH_LIB)
+    for name in N.SYNTH_EXPORTS:
+        assert hasattr(lib, name), name
+
+
+def test_status_strings():
+    lib = N.moe_lib()
+    for s in range(8):
+        assert lib.urb_status_string(s)
+
+
+def test_splitmix64_published_vectors():
+    # SplitMix64 (Steele, Lea, Flood 2014) seeded with 0; the reference's generator
+    # (src/generation.rs:419-440) uses the same constants.
+    got = [int(v) for v in synth.splitmix64(0, 0, 3)]
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    # counter form: draw n of seed s equals draw 0 of seed s + n * gamma
+    a = synth.splitmix64(12345, 7, 1)[0]
+    b = synth.splitmix64((12345 + 7 * 0x9E3779B97F4A7C15) & (2**64 - 1), 0, 1)[0]
+    assert a == b
+
+
+def test_fnv1a64_published_vectors():
+    assert synth.fnv1a64("") == 0xCBF29CE484222325
+    assert synth.fnv1a64("a") == 0xAF63DC4C8601EC8C
+    assert synth.fnv1a64("foobar") == 0x85944171F73967E8
+
+
+def test_host_encoders_agree_with_oracle():
+    from oracle import oracle as O
+    rng = np.random.default_rng(11)
+    vals = np.concatenate([rng.standard_normal(3000).astype(np.float32) * 60,
+                           rng.standard_normal(500).astype(np.float32) * 1e-3,
+                           np.array([0.0, -0.0, 448.0, -448.0, 1000.0, -1e9], np.float32)])
+    codes = synth.encode_e4m3fn(vals)
+    for v, c in zip(vals, codes):
+        assert int(c) == O.encode_e4m3fn_finite(float(v)), v
+    bits = synth.bf16_rne_bits(vals[:3000])
+    for v, b in zip(vals[:3000], bits):
+        assert (np.uint32(b) << np.uint32(16)).view(np.float32) == O.round_to_bf16(float(v))
+
+
+def test_generator_distributions():
+    z = synth.normals(synth.stream_seed("x"), 200000)
+    assert abs(float(z.mean())) < 0.01 and abs(float(z.std()) - 1.0) < 0.01
+    p, s = synth.mxfp4_matrix("m", 64, 256)
+    nib = np.concatenate([p & 15, p >> 4]).ravel()
+    assert set(np.unique(nib)) == set(range(16))
+    assert s.min() >= 119 and s.max() <= 125 and s.shape == (64, 8)
+    c, s8 = synth.mxfp8_matrix("m8", 16, 64)
+    assert not np.any((c & 0x7F) == 0x7F)
+
+
+def test_benchmark_byte_accounting():
+    W = C.WORKLOADS
+    assert C.expert_bytes(W["c1_bf16_decode"].spec) == 9_437_184
+    assert C.expert_bytes(W["c3_mxfp4_decode"].spec) == 23_396_352
+    assert C.expert_bytes(W["c4_mxfp8"].spec) == 38_928_384
+    assert C.shared_bytes(W["c3_mxfp4_decode"].spec) == 88_080_384
+
+
+def test_zipf_bias_is_monotone_in_rank():
+    b = C.zipf_bias(384, 1.1, 0.1)
+    assert b.shape == (384,) and np.all(np.isfinite(b))
+    assert len(np.unique(b)) == 384

@@ -1,0 +1,72 @@
+// urb_kernels.hpp -- host-side launch interface of the MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace urb {
+
+// Error bits written to the per-context status word (the host maps them to urb_status).
+constexpr int kStatusNonFinite = 1;
+
+// One expert's three projections in HBM (gate [I,H], up [I,H], down [H,I]).
+struct ExpertMats {
+  const uint8_t* data[3];
+  const uint8_t* scales[3];
+};
+
+// Token -> expert permutation for one forward chunk.  Stable (expert, token) order, the
+// execute_batched_moe grouping (src/models/qwen3_6/runtime.rs:1123-1132).
+struct Perm {
+  const int32_t* meta;        // meta[0] = number of active experts
+  const int32_t* active;      // active expert ids, ascending
+  const int32_t* offsets;     // [E + 1] first permuted position of each expert
+  const int32_t* counts;      // [E] tokens routed to each expert
+  const int32_t* perm_token;  // [T * k] token of each permuted position
+  int dense_tokens;           // > 0: one dense expert (table entry 0) over tokens 0..n-1
+};
+
+struct RouteParams {
+  int router;        // 0 softmax top-k, 1 sigmoid noaux_tc
+  int qwen;          // round route weights to BF16
+  int n_group, topk_group, normalize;
+  float scale;
+  const float* bias; // [E] or nullptr
+};
+
+// Router logits.
+void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
+                         int* status, hipStream_t s);
+void launch_router_f64(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
+                       int* status, hipStream_t s);
+void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s);
+// Top-k routing, one wavefront per token.
+void launch_route(const float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
+                  float* weights, int32_t* asc, int* status, hipStream_t s);
+// Permutation for T <= kMaxChunkTokens tokens.
+constexpr int kMaxChunkTokens = 1024;
+void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
+                    int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
+                    hipStream_t s);
+// Decode projections (GEMV family): gate+up with the SwiGLU epilogue, then down.
+// `qwen` selects the BF16 boundaries of Qwen38Expert; otherwise GatedMlp's f32 path.
+void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
+                         int H, int I, const float* x, float* act, int qwen, int* status,
+                         hipStream_t s);
+void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active, int H,
+                      int I, const float* act, float* y, int qwen, int* status, hipStream_t s);
+// Combines: Qwen BF16 ascending-id, GLM f64 ranking order.
+void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
+                         const int32_t* asc, int T, int K, int H, float* out, int* status,
+                         hipStream_t s);
+void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
+                        const float* shared, int T, int K, int H, float* out, hipStream_t s);
+// Payload validation: bit 1 = non-finite BF16 / E4M3 NaN code, bit 2 = E8M0 0xFF.
+void launch_validate(int fmt, const uint8_t* data, size_t data_bytes, const uint8_t* scales,
+                     size_t scale_bytes, int* flags, hipStream_t s);
+void launch_dequant(int fmt, const uint8_t* data, const uint8_t* scales, int rows, int cols,
+                    int row0, int count, float* out, hipStream_t s);
+void launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t s);
+void launch_check_finite(const float* x, size_t n, int* status, hipStream_t s);
+
+}  // namespace urb

@@ -1,0 +1,548 @@
+// urb_moe_host.cpp -- the C ABI (include/urb_moe.h): layer construction, validation, HBM
+// arena, workspace and the per-call launch sequence.
+#include "../../include/urb_moe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "urb_kernels.hpp"
+
+namespace {
+
+using urb::ExpertMats;
+using urb::Perm;
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+size_t matrix_bytes(urb_format f, size_t rows, size_t cols, size_t* scales) {
+  *scales = f == URB_FMT_BF16 ? 0 : rows * (cols / 32);
+  switch (f) {
+    case URB_FMT_BF16: return rows * cols * 2;
+    case URB_FMT_MXFP4: return rows * cols / 2;
+    default: return rows * cols;
+  }
+}
+
+struct Workspace {
+  float* logits = nullptr;
+  int32_t* ids = nullptr;
+  float* weights = nullptr;
+  int32_t* asc = nullptr;
+  int32_t* meta = nullptr;
+  int32_t* active = nullptr;
+  int32_t* offsets = nullptr;
+  int32_t* counts = nullptr;
+  int32_t* perm_token = nullptr;
+  int32_t* pos_of_slot = nullptr;
+  float* act = nullptr;
+  float* y_perm = nullptr;
+  float* shared_act = nullptr;
+  float* shared_out = nullptr;
+  int* status = nullptr;  // [0] latched numerical failures, [1] validation flags
+};
+
+// Sequential bump allocator over one device allocation.
+struct Bump {
+  char* base;
+  size_t off = 0;
+  template <class T>
+  T* take(size_t count) {
+    T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+    off += align_up(count * sizeof(T));
+    return p;
+  }
+};
+
+}  // namespace
+
+struct urb_moe_ctx {
+  urb_moe_desc desc{};
+  int device = 0;
+  uint32_t chunk = 0;                  // tokens per internal launch sequence
+  void* arena = nullptr;               // router, bias and (unless borrowed) the expert weights
+  size_t arena_bytes = 0, weight_bytes = 0;
+  void* work = nullptr;
+  size_t work_bytes = 0;
+  const uint16_t* router = nullptr;    // [E, H] BF16
+  uint16_t* router_lane8 = nullptr;    // per-lane chain layout (QWEN36)
+  const float* bias = nullptr;         // [E] or nullptr
+  ExpertMats* table = nullptr;         // device [E]
+  ExpertMats* shared_table = nullptr;  // device [1]
+  Workspace ws;
+  hipStream_t side = nullptr;          // shared expert runs here, concurrently with routing
+  hipEvent_t fork = nullptr, join = nullptr;
+  // stage spans (urb_moe_profile)
+  bool profiling = false;
+  hipEvent_t ev[URB_STAGE_COUNT][2] = {};
+  bool pending[URB_STAGE_COUNT] = {};
+  double stage_ms[URB_STAGE_COUNT] = {};
+  uint64_t stage_calls[URB_STAGE_COUNT] = {};
+};
+
+namespace {
+
+// Brackets one stage's launches with events on the stream they run on (profiling only).
+struct Span {
+  urb_moe_ctx* c;
+  int stage;
+  hipStream_t s;
+  Span(urb_moe_ctx* c_, int stage_, hipStream_t s_) : c(c_), stage(stage_), s(s_) {
+    if (c->profiling) (void)hipEventRecord(c->ev[stage][0], s);
+  }
+  ~Span() {
+    if (c->profiling) {
+      (void)hipEventRecord(c->ev[stage][1], s);
+      c->pending[stage] = true;
+    }
+  }
+};
+
+urb_status collect_spans(urb_moe_ctx* c) {
+  for (int st = 0; st < URB_STAGE_COUNT; ++st) {
+    if (!c->pending[st]) continue;
+    c->pending[st] = false;
+    if (hipEventSynchronize(c->ev[st][1]) != hipSuccess) return URB_ERR_DEVICE;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, c->ev[st][0], c->ev[st][1]) != hipSuccess) return URB_ERR_DEVICE;
+    c->stage_ms[st] += ms;
+    c->stage_calls[st] += 1;
+  }
+  return URB_OK;
+}
+
+}  // namespace
+
+#define URB_HIP(call)                            \
+  do {                                           \
+    hipError_t e_ = (call);                      \
+    if (e_ == hipErrorOutOfMemory) return URB_ERR_OUT_OF_MEMORY; \
+    if (e_ != hipSuccess) return URB_ERR_DEVICE; \
+  } while (0)
+
+extern "C" {
+
+const char* urb_status_string(urb_status s) {
+  switch (s) {
+    case URB_OK: return "ok";
+    case URB_ERR_SHAPE: return "invalid shape";
+    case URB_ERR_INVALID_SCALE: return "E8M0 scale byte 0xff is NaN";
+    case URB_ERR_NONFINITE: return "NaN or infinity";
+    case URB_ERR_INVALID_GEOMETRY: return "invalid router geometry";
+    case URB_ERR_DEVICE: return "HIP runtime error";
+    case URB_ERR_OUT_OF_MEMORY: return "out of device memory";
+    case URB_ERR_ARGUMENT: return "invalid argument";
+  }
+  return "unknown status";
+}
+
+}  // extern "C"
+
+static bool finite_host(float v) { return v == v && v <= 3.4028235e38f && v >= -3.4028235e38f; }
+
+static urb_status check_desc(const urb_moe_desc* d) {
+  if (d->hidden == 0 || d->n_experts == 0 || d->intermediate == 0 || d->max_tokens == 0)
+    return URB_ERR_SHAPE;
+  if (d->top_k == 0 || d->top_k > d->n_experts) return URB_ERR_INVALID_GEOMETRY;
+  if (d->top_k > 32 || d->n_experts > 512) return URB_ERR_ARGUMENT;
+  for (urb_format f : {d->expert_format, d->shared_format})
+    if (f != URB_FMT_BF16 && f != URB_FMT_MXFP4 && f != URB_FMT_MXFP8) return URB_ERR_ARGUMENT;
+  // 128-bit row chunks: H a multiple of 32 (the MX block), I of 32 (MX) or 8 (BF16).
+  if (d->hidden % 32) return URB_ERR_SHAPE;
+  if (d->intermediate % (d->expert_format == URB_FMT_BF16 ? 8 : 32)) return URB_ERR_SHAPE;
+  if (d->shared_intermediate % (d->shared_format == URB_FMT_BF16 ? 8 : 32)) return URB_ERR_SHAPE;
+  if (d->composition == URB_COMPOSE_QWEN36) {
+    // The Qwen3.6 composition reproduced here: BF16 experts, softmax router, no shared expert.
+    if (d->expert_format != URB_FMT_BF16 || d->shared_intermediate != 0 ||
+        d->router != URB_ROUTER_SOFTMAX_TOPK)
+      return URB_ERR_ARGUMENT;
+  } else if (d->composition != URB_COMPOSE_GLM) {
+    return URB_ERR_ARGUMENT;
+  }
+  if (d->router == URB_ROUTER_SIGMOID_NOAUX_TC) {
+    // route_noaux_tc geometry (src/math/routing.rs:66-112), checked once at construction as
+    // RuntimeMoeLayer::new does (src/models/glm/runtime/moe.rs:108-116).
+    if (!finite_host(d->routed_scaling_factor)) return URB_ERR_NONFINITE;
+    if (d->routed_scaling_factor <= 0.0f) return URB_ERR_INVALID_GEOMETRY;
+    if (d->n_group == 0 || d->n_experts % d->n_group) return URB_ERR_INVALID_GEOMETRY;
+    if (d->topk_group == 0 || d->topk_group > d->n_group) return URB_ERR_INVALID_GEOMETRY;
+    uint32_t per = d->n_experts / d->n_group;
+    if (per < 2) return URB_ERR_INVALID_GEOMETRY;
+    if (per * d->topk_group < d->top_k) return URB_ERR_INVALID_GEOMETRY;
+    if (d->n_group > 64) return URB_ERR_ARGUMENT;
+  } else if (d->router != URB_ROUTER_SOFTMAX_TOPK) {
+    return URB_ERR_ARGUMENT;
+  }
+  return URB_OK;
+}
+
+static void destroy_ctx(urb_moe_ctx* c) {
+  if (!c) return;
+  for (auto& pair : c->ev)
+    for (hipEvent_t e : pair)
+      if (e) (void)hipEventDestroy(e);
+  if (c->side) (void)hipStreamDestroy(c->side);
+  if (c->fork) (void)hipEventDestroy(c->fork);
+  if (c->join) (void)hipEventDestroy(c->join);
+  if (c->arena) (void)hipFree(c->arena);
+  if (c->work) (void)hipFree(c->work);
+  delete c;
+}
+
+static void carve_workspace(urb_moe_ctx* c, Bump& b) {
+  const urb_moe_desc& d = c->desc;
+  const size_t C = c->chunk, E = d.n_experts, K = d.top_k, H = d.hidden, I = d.intermediate;
+  Workspace& w = c->ws;
+  w.status = b.take<int>(4);
+  w.logits = b.take<float>(C * E);
+  w.ids = b.take<int32_t>(C * K);
+  w.weights = b.take<float>(C * K);
+  w.asc = b.take<int32_t>(C * K);
+  w.meta = b.take<int32_t>(4);
+  w.active = b.take<int32_t>(E);
+  w.offsets = b.take<int32_t>(E + 1);
+  w.counts = b.take<int32_t>(E);
+  w.perm_token = b.take<int32_t>(C * K);
+  w.pos_of_slot = b.take<int32_t>(C * K);
+  w.act = b.take<float>(C * K * I);
+  w.y_perm = b.take<float>(C * K * H);
+  w.shared_act = b.take<float>(C * std::max<size_t>(d.shared_intermediate, 1));
+  w.shared_out = b.take<float>(C * H);
+}
+
+static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
+                              urb_weight_source src, urb_moe_ctx* c) {
+  const size_t H = d->hidden, E = d->n_experts, I = d->intermediate, Is = d->shared_intermediate;
+  const bool has_shared = Is != 0;
+  const bool qwen = d->composition == URB_COMPOSE_QWEN36;
+  if (!w->router_weight || !w->experts || (has_shared && !w->shared)) return URB_ERR_ARGUMENT;
+  if (src != URB_SOURCE_HOST && src != URB_SOURCE_DEVICE_COPY && src != URB_SOURCE_DEVICE_BORROW)
+    return URB_ERR_ARGUMENT;
+  const bool mx = d->expert_format != URB_FMT_BF16;
+  for (size_t i = 0; i < E * 3; ++i)
+    if (!w->experts[i].data || (mx && !w->experts[i].scales)) return URB_ERR_ARGUMENT;
+  if (has_shared)
+    for (int i = 0; i < 3; ++i)
+      if (!w->shared[i].data || (d->shared_format != URB_FMT_BF16 && !w->shared[i].scales))
+        return URB_ERR_ARGUMENT;
+  URB_HIP(hipGetDevice(&c->device));
+  c->desc = *d;
+  // The permutation keeps an [E][chunk/32] token bitmap in LDS: cap it at 60 KiB.
+  const uint32_t bitmap_chunk = (uint32_t)(60 * 1024 / (4 * E)) * 32;
+  c->chunk = std::min<uint32_t>({d->max_tokens, (uint32_t)urb::kMaxChunkTokens, bitmap_chunk});
+
+  const bool borrow = src == URB_SOURCE_DEVICE_BORROW;
+  const hipMemcpyKind kind = src == URB_SOURCE_HOST ? hipMemcpyHostToDevice
+                                                    : hipMemcpyDeviceToDevice;
+  // Matrix geometry: gate [I, H], up [I, H], down [H, I].
+  const size_t dims[3][2] = {{I, H}, {I, H}, {H, I}};
+  const size_t sdims[3][2] = {{Is, H}, {Is, H}, {H, Is}};
+
+  // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
+  size_t arena = align_up(E * H * 2) + (qwen ? align_up(E * H * 2) : 0) + align_up(E * 4);
+  size_t wbytes = 0;
+  if (!borrow) {
+    for (int m = 0; m < 3; ++m) {
+      size_t sb, db = matrix_bytes(d->expert_format, dims[m][0], dims[m][1], &sb);
+      wbytes += E * (align_up(db) + align_up(sb));
+      if (has_shared) {
+        size_t ssb, sdb = matrix_bytes(d->shared_format, sdims[m][0], sdims[m][1], &ssb);
+        wbytes += align_up(sdb) + align_up(ssb);
+      }
+    }
+  }
+  arena += wbytes + align_up(sizeof(ExpertMats) * (E + 1));
+  URB_HIP(hipMalloc(&c->arena, arena));
+  c->arena_bytes = arena;
+  c->weight_bytes = wbytes;
+  Bump ab{static_cast<char*>(c->arena)};
+  uint16_t* router = ab.take<uint16_t>(E * H);
+  c->router_lane8 = qwen ? ab.take<uint16_t>(E * H) : nullptr;
+  float* bias = ab.take<float>(E);
+  c->table = ab.take<ExpertMats>(E);
+  c->shared_table = ab.take<ExpertMats>(1);
+  URB_HIP(hipMemcpy(router, w->router_weight, E * H * 2, kind));
+  c->router = router;
+  if (w->correction_bias) {
+    URB_HIP(hipMemcpy(bias, w->correction_bias, E * 4, kind));
+    c->bias = bias;
+  }
+
+  std::vector<ExpertMats> table(E);
+  auto place = [&](urb_format f, size_t rows, size_t cols, const urb_matrix& mat,
+                   const uint8_t** data, const uint8_t** scales) -> urb_status {
+    size_t sb, db = matrix_bytes(f, rows, cols, &sb);
+    if (borrow) {
+      *data = static_cast<const uint8_t*>(mat.data);
+      *scales = sb ? mat.scales : nullptr;
+      return URB_OK;
+    }
+    uint8_t* dd = ab.take<uint8_t>(db);
+    uint8_t* ss = sb ? ab.take<uint8_t>(sb) : nullptr;
+    URB_HIP(hipMemcpy(dd, mat.data, db, kind));
+    if (sb) URB_HIP(hipMemcpy(ss, mat.scales, sb, kind));
+    *data = dd;
+    *scales = ss;
+    return URB_OK;
+  };
+  for (size_t e = 0; e < E; ++e)
+    for (int m = 0; m < 3; ++m) {
+      urb_status st = place(d->expert_format, dims[m][0], dims[m][1], w->experts[e * 3 + m],
+                            &table[e].data[m], &table[e].scales[m]);
+      if (st) return st;
+    }
+  ExpertMats shared{};
+  if (has_shared)
+    for (int m = 0; m < 3; ++m) {
+      urb_status st = place(d->shared_format, sdims[m][0], sdims[m][1], w->shared[m],
+                            &shared.data[m], &shared.scales[m]);
+      if (st) return st;
+    }
+  URB_HIP(hipMemcpy(c->table, table.data(), sizeof(ExpertMats) * E, hipMemcpyHostToDevice));
+  URB_HIP(hipMemcpy(c->shared_table, &shared, sizeof(ExpertMats), hipMemcpyHostToDevice));
+
+  // ---- workspace
+  Bump sizing{nullptr};
+  carve_workspace(c, sizing);
+  URB_HIP(hipMalloc(&c->work, sizing.off));
+  c->work_bytes = sizing.off;
+  Bump wb{static_cast<char*>(c->work)};
+  carve_workspace(c, wb);
+  urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
+
+  // ---- one validation pass over every payload
+  int* flags = c->ws.status + 1;
+  urb::launch_validate(URB_FMT_BF16, reinterpret_cast<const uint8_t*>(router), E * H * 2, nullptr,
+                       0, flags, nullptr);
+  for (size_t e = 0; e < E; ++e)
+    for (int m = 0; m < 3; ++m) {
+      size_t sb, db = matrix_bytes(d->expert_format, dims[m][0], dims[m][1], &sb);
+      urb::launch_validate(d->expert_format, table[e].data[m], db, table[e].scales[m], sb, flags,
+                           nullptr);
+    }
+  if (has_shared)
+    for (int m = 0; m < 3; ++m) {
+      size_t sb, db = matrix_bytes(d->shared_format, sdims[m][0], sdims[m][1], &sb);
+      urb::launch_validate(d->shared_format, shared.data[m], db, shared.scales[m], sb, flags,
+                           nullptr);
+    }
+  if (c->bias) urb::launch_check_finite(c->bias, E, c->ws.status + 2, nullptr);
+  URB_HIP(hipGetLastError());
+  int host_flags[4] = {0, 0, 0, 0};
+  URB_HIP(hipDeviceSynchronize());
+  URB_HIP(hipMemcpy(host_flags, c->ws.status, sizeof(host_flags), hipMemcpyDeviceToHost));
+  if (host_flags[2]) return URB_ERR_INVALID_GEOMETRY;  // moe.rs:92-96: non-finite bias
+  if (host_flags[1] & 1) return URB_ERR_NONFINITE;
+  if (host_flags[1] & 2) return URB_ERR_INVALID_SCALE;
+  urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
+
+  if (qwen) urb::launch_relayout_lane8(router, (int)E, (int)H, c->router_lane8, nullptr);
+  URB_HIP(hipGetLastError());
+  URB_HIP(hipDeviceSynchronize());
+
+  URB_HIP(hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking));
+  URB_HIP(hipEventCreateWithFlags(&c->fork, hipEventDisableTiming));
+  URB_HIP(hipEventCreateWithFlags(&c->join, hipEventDisableTiming));
+  for (auto& pair : c->ev)
+    for (hipEvent_t& e : pair) URB_HIP(hipEventCreate(&e));
+  return URB_OK;
+}
+
+extern "C" {
+
+urb_status urb_moe_create(const urb_moe_desc* desc, const urb_moe_weights* weights,
+                          urb_weight_source source, urb_moe_ctx** out) {
+  if (!desc || !weights || !out) return URB_ERR_ARGUMENT;
+  *out = nullptr;
+  urb_status st = check_desc(desc);
+  if (st) return st;
+  urb_moe_ctx* c = new urb_moe_ctx();
+  st = create_impl(desc, weights, source, c);
+  if (st) {
+    (void)hipDeviceSynchronize();
+    destroy_ctx(c);
+    return st;
+  }
+  *out = c;
+  return URB_OK;
+}
+
+void urb_moe_destroy(urb_moe_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipDeviceSynchronize();
+  destroy_ctx(ctx);
+}
+
+static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logits,
+                              int32_t* ids, float* weights, hipStream_t s) {
+  const urb_moe_desc& d = c->desc;
+  const bool qwen = d.composition == URB_COMPOSE_QWEN36;
+  const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
+  {
+    Span span(c, URB_STAGE_ROUTER, s);
+    if (qwen) urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, c->ws.status, s);
+    else urb::launch_router_f64(c->router, E, H, x, n, logits, c->ws.status, s);
+  }
+  urb::RouteParams rp{(int)d.router, qwen ? 1 : 0, (int)d.n_group, (int)d.topk_group,
+                      d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias};
+  {
+    Span span(c, URB_STAGE_ROUTE, s);
+    urb::launch_route(logits, n, E, K, rp, ids, weights, qwen ? c->ws.asc : nullptr,
+                      c->ws.status, s);
+  }
+  return URB_OK;
+}
+
+urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, float* y,
+                           int32_t* ids, float* weights, void* stream) {
+  if (!c || !x || !y) return URB_ERR_ARGUMENT;
+  if (tokens == 0 || tokens > c->desc.max_tokens) return URB_ERR_SHAPE;
+  const urb_moe_desc& d = c->desc;
+  const bool qwen = d.composition == URB_COMPOSE_QWEN36;
+  const bool has_shared = d.shared_intermediate != 0;
+  const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
+  const int Is = (int)d.shared_intermediate;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Workspace& ws = c->ws;
+  for (uint32_t c0 = 0; c0 < tokens; c0 += c->chunk) {
+    const int n = (int)std::min<uint32_t>(c->chunk, tokens - c0);
+    const float* xc = x + (size_t)c0 * H;
+    float* yc = y + (size_t)c0 * H;
+    int32_t* idc = ids ? ids + (size_t)c0 * K : ws.ids;
+    float* wc = weights ? weights + (size_t)c0 * K : ws.weights;
+    if (has_shared) {
+      // GatedMlp shared expert (src/models/glm/runtime/moe.rs:162) does not depend on the
+      // routes: it runs on the side stream while the router, top-k and permutation run here.
+      URB_HIP(hipEventRecord(c->fork, s));
+      URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
+      Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n};
+      {
+        Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
+        urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, xc,
+                                 ws.shared_act, 0, ws.status, c->side);
+      }
+      {
+        Span span(c, URB_STAGE_SHARED_DOWN, c->side);
+        urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_act,
+                              ws.shared_out, 0, ws.status, c->side);
+      }
+      URB_HIP(hipEventRecord(c->join, c->side));
+    }
+    route_chunk(c, xc, n, ws.logits, idc, wc, s);
+    {
+      Span span(c, URB_STAGE_PERMUTE, s);
+      urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts,
+                          ws.perm_token, ws.pos_of_slot, s);
+    }
+    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0};
+    const int max_active = std::min(E, n * K);
+    {
+      Span span(c, URB_STAGE_GATE_UP, s);
+      urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, xc, ws.act,
+                               qwen ? 1 : 0, ws.status, s);
+    }
+    {
+      Span span(c, URB_STAGE_DOWN, s);
+      urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act,
+                            ws.y_perm, qwen ? 1 : 0, ws.status, s);
+    }
+    if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+    {
+      Span span(c, URB_STAGE_COMBINE, s);
+      if (qwen)
+        urb::launch_combine_qwen(ws.y_perm, ws.pos_of_slot, wc, ws.asc, n, K, H, yc, ws.status,
+                                 s);
+      else
+        urb::launch_combine_glm(ws.y_perm, ws.pos_of_slot, wc,
+                                has_shared ? ws.shared_out : nullptr, n, K, H, yc, s);
+    }
+    if (c->profiling) {
+      urb_status st = collect_spans(c);
+      if (st) return st;
+    }
+  }
+  URB_HIP(hipGetLastError());
+  return URB_OK;
+}
+
+urb_status urb_moe_profile(urb_moe_ctx* c, int enable) {
+  if (!c) return URB_ERR_ARGUMENT;
+  URB_HIP(hipDeviceSynchronize());
+  if (enable) {
+    for (int st = 0; st < URB_STAGE_COUNT; ++st) {
+      c->stage_ms[st] = 0.0;
+      c->stage_calls[st] = 0;
+      c->pending[st] = false;
+    }
+  }
+  c->profiling = enable != 0;
+  return URB_OK;
+}
+
+urb_status urb_moe_profile_read(const urb_moe_ctx* c, double* ms, uint64_t* launches) {
+  if (!c) return URB_ERR_ARGUMENT;
+  for (int st = 0; st < URB_STAGE_COUNT; ++st) {
+    if (ms) ms[st] = c->stage_ms[st];
+    if (launches) launches[st] = c->stage_calls[st];
+  }
+  return URB_OK;
+}
+
+urb_status urb_moe_route(urb_moe_ctx* c, const float* x, uint32_t tokens, float* logits,
+                         int32_t* ids, float* weights, void* stream) {
+  if (!c || !x) return URB_ERR_ARGUMENT;
+  if (tokens == 0 || tokens > c->desc.max_tokens) return URB_ERR_SHAPE;
+  const urb_moe_desc& d = c->desc;
+  const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (uint32_t c0 = 0; c0 < tokens; c0 += c->chunk) {
+    const int n = (int)std::min<uint32_t>(c->chunk, tokens - c0);
+    float* lc = logits ? logits + (size_t)c0 * E : c->ws.logits;
+    int32_t* idc = ids ? ids + (size_t)c0 * K : c->ws.ids;
+    float* wc = weights ? weights + (size_t)c0 * K : c->ws.weights;
+    route_chunk(c, x + (size_t)c0 * H, n, lc, idc, wc, s);
+  }
+  URB_HIP(hipGetLastError());
+  return URB_OK;
+}
+
+urb_status urb_moe_sync(urb_moe_ctx* c, void* stream) {
+  if (!c) return URB_ERR_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int st = 0;
+  URB_HIP(hipStreamSynchronize(s));
+  URB_HIP(hipStreamSynchronize(c->side));
+  URB_HIP(hipMemcpy(&st, c->ws.status, sizeof(int), hipMemcpyDeviceToHost));
+  urb::launch_fill_i32(c->ws.status, 0, 1, s);
+  URB_HIP(hipGetLastError());
+  URB_HIP(hipStreamSynchronize(s));
+  if (st & urb::kStatusNonFinite) return URB_ERR_NONFINITE;
+  return URB_OK;
+}
+
+urb_status urb_dequant_rows(urb_format format, const void* data, const uint8_t* scales,
+                            uint32_t rows, uint32_t cols, uint32_t row0, uint32_t count,
+                            float* out, void* stream) {
+  if (!data || !out || (format != URB_FMT_BF16 && !scales)) return URB_ERR_ARGUMENT;
+  if (format != URB_FMT_BF16 && format != URB_FMT_MXFP4 && format != URB_FMT_MXFP8)
+    return URB_ERR_ARGUMENT;
+  if (rows == 0 || cols == 0 || (format != URB_FMT_BF16 && cols % 32)) return URB_ERR_SHAPE;
+  if ((uint64_t)row0 + count > rows) return URB_ERR_SHAPE;
+  if (count == 0) return URB_OK;
+  urb::launch_dequant(format, static_cast<const uint8_t*>(data), scales, (int)rows, (int)cols,
+                      (int)row0, (int)count, out, static_cast<hipStream_t>(stream));
+  URB_HIP(hipGetLastError());
+  return URB_OK;
+}
+
+urb_status urb_moe_memory(const urb_moe_ctx* c, size_t* weight_bytes, size_t* workspace_bytes) {
+  if (!c) return URB_ERR_ARGUMENT;
+  if (weight_bytes) *weight_bytes = c->weight_bytes;
+  if (workspace_bytes) *workspace_bytes = c->work_bytes;
+  return URB_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// urb_synth.hip -- device-side generator for the seeded synthetic workloads.
+//
+// Bit-for-bit the same definition as urbilateria_amd/synth.py: SplitMix64 (the reference's
+// src/generation.rs:419-440) indexed by draw number, Box-Muller normals on draws 2i and 2i+1,
+// RNE BF16, E2M1 nibbles from the low 4 bits of each draw, E8M0 = 119 + draw % 7, E4M3 = the
+// nearest-even finite encoding of clamp(N(0,1), +-448).  Used to build full-size layers
+// directly in HBM; these entry points are workload tooling, not part of the MoE ABI.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+__device__ __forceinline__ uint64_t splitmix(uint64_t seed, uint64_t n) {
+  uint64_t z = seed + (n + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ double unit(uint64_t u) {
+  return (double)(u >> 11) * (1.0 / 9007199254740992.0);
+}
+__device__ __forceinline__ float normal(uint64_t seed, uint64_t i, double mean, double std) {
+  double u0 = unit(splitmix(seed, 2 * i)), u1 = unit(splitmix(seed, 2 * i + 1));
+  double z = sqrt(-2.0 * log(1.0 - u0)) * cos(6.283185307179586 * u1);
+  return (float)(mean + std * z);
+}
+__device__ __forceinline__ uint16_t bf16_bits(float v) {
+  uint32_t b = __float_as_uint(v);
+  return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ uint8_t e4m3_encode(float value) {
+  value = fminf(fmaxf(value, -448.0f), 448.0f);
+  float mag = fabsf(value);
+  if (mag == 0.0f) return 0;
+  uint32_t code;
+  if (mag < 0.015625f) {
+    code = (uint32_t)rintf(mag * 512.0f);
+  } else {
+    uint32_t bits = __float_as_uint(mag);
+    uint32_t rounded = (bits + ((1u << 19) - 1) + ((bits >> 20) & 1u)) & 0xfff00000u;
+    uint32_t e = (rounded >> 23) & 0xffu;
+    e = e > 120 ? e - 120 : 0;
+    code = min((e << 3) | ((rounded >> 20) & 7u), 0x7eu);
+  }
+  if (signbit(value) && code != 0) code |= 0x80u;
+  return (uint8_t)code;
+}
+
+__global__ void bf16_kernel(uint64_t seed, size_t n, double mean, double std, uint16_t* out) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = bf16_bits(normal(seed, i, mean, std));
+}
+__global__ void act_kernel(uint64_t seed, size_t n, float* out) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = __uint_as_float((uint32_t)bf16_bits(normal(seed, i, 0.0, 1.0)) << 16);
+}
+__global__ void fp4_kernel(uint64_t seed, size_t nbytes, uint8_t* out) {
+  for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nbytes;
+       b += (size_t)gridDim.x * blockDim.x) {
+    uint32_t lo = (uint32_t)(splitmix(seed, 2 * b) & 0xf);
+    uint32_t hi = (uint32_t)(splitmix(seed, 2 * b + 1) & 0xf);
+    out[b] = (uint8_t)(lo | (hi << 4));
+  }
+}
+__global__ void fp8_kernel(uint64_t seed, size_t n, uint8_t* out) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = e4m3_encode(normal(seed, i, 0.0, 1.0));
+}
+__global__ void e8m0_kernel(uint64_t seed, size_t n, uint8_t* out) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = (uint8_t)(119 + splitmix(seed, i) % 7);
+}
+
+int grid_for(size_t n) {
+  size_t b = (n + 255) / 256;
+  return (int)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+}  // namespace
+
+extern "C" {
+
+// BF16 N(mean, std) matrix, `n` elements of u16 bits.
+int urb_synth_bf16(uint64_t seed, size_t n, double mean, double std, void* out, void* stream) {
+  bf16_kernel<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(seed, n, mean, std, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+// N(0, 1) activations rounded to BF16, as f32.
+int urb_synth_activations(uint64_t seed, size_t n, float* out, void* stream) {
+  act_kernel<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(seed, n, out);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+// E2M1 nibbles, `nbytes` packed bytes (two codes per byte, low nibble first).
+int urb_synth_fp4(uint64_t seed, size_t nbytes, void* out, void* stream) {
+  fp4_kernel<<<grid_for(nbytes), 256, 0, (hipStream_t)stream>>>(seed, nbytes, (uint8_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+// E4M3FN codes of clamp(N(0,1), +-448).
+int urb_synth_fp8(uint64_t seed, size_t n, void* out, void* stream) {
+  fp8_kernel<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(seed, n, (uint8_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+// E8M0 scales 119 + draw % 7.
+int urb_synth_e8m0(uint64_t seed, size_t n, void* out, void* stream) {
+  e8m0_kernel<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(seed, n, (uint8_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+}  // extern "C"

@@ -1,0 +1,127 @@
+"""ctypes binding of the C ABI in ``include/urb_moe.h`` (``liburb_moe.so``) and of the device
+workload generator (``liburb_synth.so``).
+
+The shared libraries are built in-tree by ``__graft_entry__.build()``.  Loading fails loudly
+when they are missing: there is no CPU fallback for any entry point.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+MOE_LIB = os.path.join(_HERE, "liburb_moe.so")
+SYNTH_LIB = os.path.join(_HERE, "liburb_synth.so")
+
+OK, ERR_SHAPE, ERR_INVALID_SCALE, ERR_NONFINITE, ERR_INVALID_GEOMETRY = 0, 1, 2, 3, 4
+ERR_DEVICE, ERR_OUT_OF_MEMORY, ERR_ARGUMENT = 5, 6, 7
+SOURCE_HOST, SOURCE_DEVICE_COPY, SOURCE_DEVICE_BORROW = 0, 1, 2
+
+# Every symbol include/urb_moe.h declares.
+EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_route",
+           "urb_moe_sync", "urb_dequant_rows", "urb_moe_memory", "urb_status_string",
+           "urb_moe_profile", "urb_moe_profile_read")
+STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
+          "combine")
+SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
+                 "urb_synth_e8m0")
+
+
+class UrbError(RuntimeError):
+    """A non-OK urb_status, carrying the code (1..4 mirror the reference's error enums)."""
+
+    def __init__(self, status: int, where: str = ""):
+        msg = _status_string(status)
+        super().__init__(f"{where}: urb_status {status} ({msg})" if where else msg)
+        self.status = status
+
+
+class Matrix(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("scales", ctypes.c_void_p)]
+
+
+class Desc(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_uint32), ("n_experts", ctypes.c_uint32),
+        ("top_k", ctypes.c_uint32), ("intermediate", ctypes.c_uint32),
+        ("shared_intermediate", ctypes.c_uint32),
+        ("expert_format", ctypes.c_int), ("shared_format", ctypes.c_int),
+        ("router", ctypes.c_int), ("composition", ctypes.c_int),
+        ("n_group", ctypes.c_uint32), ("topk_group", ctypes.c_uint32),
+        ("normalize", ctypes.c_int32), ("routed_scaling_factor", ctypes.c_float),
+        ("max_tokens", ctypes.c_uint32),
+    ]
+
+
+class Weights(ctypes.Structure):
+    _fields_ = [("router_weight", ctypes.c_void_p), ("correction_bias", ctypes.c_void_p),
+                ("experts", ctypes.c_void_p), ("shared", ctypes.c_void_p)]
+
+
+_moe = None
+_synth = None
+
+
+def _status_string(status: int) -> str:
+    try:
+        return moe_lib().urb_status_string(status).decode()
+    except Exception:
+        return "unknown"
+
+
+def moe_lib() -> ctypes.CDLL:
+    global _moe
+    if _moe is None:
+        if not os.path.exists(MOE_LIB):
+            raise RuntimeError(f"{MOE_LIB} is not built: run __graft_entry__.build() "
+                               "(the MoE path has no CPU fallback)")
+        lib = ctypes.CDLL(MOE_LIB)
+        P, u32 = ctypes.c_void_p, ctypes.c_uint32
+        lib.urb_moe_create.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Weights), ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_void_p)]
+        lib.urb_moe_create.restype = ctypes.c_int
+        lib.urb_moe_destroy.argtypes = [P]
+        lib.urb_moe_destroy.restype = None
+        lib.urb_moe_forward.argtypes = [P, P, u32, P, P, P, P]
+        lib.urb_moe_forward.restype = ctypes.c_int
+        lib.urb_moe_route.argtypes = [P, P, u32, P, P, P, P]
+        lib.urb_moe_route.restype = ctypes.c_int
+        lib.urb_moe_sync.argtypes = [P, P]
+        lib.urb_moe_sync.restype = ctypes.c_int
+        lib.urb_dequant_rows.argtypes = [ctypes.c_int, P, P, u32, u32, u32, u32, P, P]
+        lib.urb_dequant_rows.restype = ctypes.c_int
+        lib.urb_moe_memory.argtypes = [P, ctypes.POINTER(ctypes.c_size_t),
+                                       ctypes.POINTER(ctypes.c_size_t)]
+        lib.urb_moe_memory.restype = ctypes.c_int
+        lib.urb_moe_profile.argtypes = [P, ctypes.c_int]
+        lib.urb_moe_profile.restype = ctypes.c_int
+        lib.urb_moe_profile_read.argtypes = [P, P, P]
+        lib.urb_moe_profile_read.restype = ctypes.c_int
+        lib.urb_status_string.argtypes = [ctypes.c_int]
+        lib.urb_status_string.restype = ctypes.c_char_p
+        _moe = lib
+    return _moe
+
+
+def synth_lib() -> ctypes.CDLL:
+    global _synth
+    if _synth is None:
+        if not os.path.exists(SYNTH_LIB):
+            raise RuntimeError(f"{SYNTH_LIB} is not built: run __graft_entry__.build()")
+        lib = ctypes.CDLL(SYNTH_LIB)
+        P, sz, u64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64
+        lib.urb_synth_bf16.argtypes = [u64, sz, ctypes.c_double, ctypes.c_double, P, P]
+        lib.urb_synth_activations.argtypes = [u64, sz, P, P]
+        lib.urb_synth_fp4.argtypes = [u64, sz, P, P]
+        lib.urb_synth_fp8.argtypes = [u64, sz, P, P]
+        lib.urb_synth_e8m0.argtypes = [u64, sz, P, P]
+        for f in SYNTH_EXPORTS:
+            getattr(lib, f).restype = ctypes.c_int
+        _synth = lib
+    return _synth
+
+
+def check(status: int, where: str = "") -> None:
+    if status != OK:
+        raise UrbError(status, where)
