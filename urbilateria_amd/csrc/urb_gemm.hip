@@ -1,0 +1,303 @@
+// urb_gemm.hip -- grouped expert GEMMs on CDNA4 MFMA (prefill and batched decode).
+//
+// For each tile of up to kGemmMTile tokens routed to one expert (the permutation's row tiles)
+// and each kGemmNTile-row slice of that expert's weight matrix, a 256-thread workgroup
+// computes C[tokens, rows] = A[tokens, K] . W[rows, K]^T with v_mfma_f32_16x16x32_bf16:
+//
+//  * B (weights) streams from HBM straight into registers in the on-disk layout: W is row-major
+//    with K contiguous, which is the MFMA B-fragment order.  Lane l of a wave owns weight row
+//    l % 16 and 32 consecutive k (one MX block: 16 B of E2M1, 32 B of E4M3 or 64 B of BF16),
+//    decodes it in registers with the scaled CDNA4 conversions (v_cvt_scalef32_pk_bf16_fp4/fp8,
+//    exact: E2M1 or E4M3 times 2^k is a BF16 value) and feeds four MFMAs, the j-th taking
+//    k = 32 q + 8 j + [0, 8) of lane group q = l / 16.
+//  * A (activations, f32) is gathered through the permutation, split into hi + lo BF16 halves
+//    (hi = bf16(a), lo = bf16(a - hi): the product keeps 16 significant bits of a) and staged
+//    in LDS in the same permuted k order; the lo MFMAs are skipped for a K step whose lo half
+//    is all zero (BF16-valued activations).
+//  * Accumulation is f32 in the MFMA; the epilogue is the same as the decode kernels'.
+#include "urb_device.hpp"
+#include "urb_kernels.hpp"
+
+namespace urb {
+
+enum { kFmtBF16 = 0, kFmtMXFP4 = 1, kFmtMXFP8 = 2 };
+
+constexpr int kMT = kGemmMTile;   // 32 tokens: two 16-row MFMA blocks
+constexpr int kNT = kGemmNTile;   // 64 weight rows: 16 per wave
+constexpr int kKS = kGemmKStep;   // 128 k per step: four 32-k MX blocks
+constexpr int kALd = kKS + 8;     // LDS row pitch in bf16 (16 B pad against bank conflicts)
+
+typedef unsigned short u16;
+
+__device__ __forceinline__ u16 bf16_rne_bits(float v) {
+  uint32_t b = f2u(v);
+  return (u16)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+// Raw B fragment of one lane for one K step: the lane's 32 consecutive k of its row.
+template <int FMT>
+struct BRaw;
+template <>
+struct BRaw<kFmtBF16> { uint4 q[4]; };
+template <>
+struct BRaw<kFmtMXFP4> { uint4 q; uint32_t s; };
+template <>
+struct BRaw<kFmtMXFP8> { uint4 q[2]; uint32_t s; };
+
+template <int FMT>
+__device__ __forceinline__ void load_b(BRaw<FMT>& r, const uint8_t* __restrict__ row,
+                                       const uint8_t* __restrict__ srow, int kblk) {
+  // kblk: index of the lane's 32-column block along K
+  if constexpr (FMT == kFmtBF16) {
+    const uint4* p = reinterpret_cast<const uint4*>(row + (size_t)kblk * 64);
+    r.q[0] = p[0]; r.q[1] = p[1]; r.q[2] = p[2]; r.q[3] = p[3];
+  } else if constexpr (FMT == kFmtMXFP4) {
+    r.q = *reinterpret_cast<const uint4*>(row + (size_t)kblk * 16);
+    r.s = srow[kblk];
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(row + (size_t)kblk * 32);
+    r.q[0] = p[0]; r.q[1] = p[1];
+    r.s = srow[kblk];
+  }
+}
+
+// Decoded B fragment: four bf16x8 MFMA operands (j = 0..3).
+struct BFrag { bf16x8 v[4]; };
+
+__device__ __forceinline__ bf16x8 pack8(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) {
+  bf16x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+  return r;
+}
+
+template <int FMT>
+__device__ __forceinline__ void decode_b(const BRaw<FMT>& r, BFrag& f) {
+  if constexpr (FMT == kFmtBF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.v[j] = __builtin_bit_cast(bf16x8, r.q[j]);
+  } else if constexpr (FMT == kFmtMXFP4) {
+    const float sc = e8m0_to_f32(r.s);
+    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      f.v[j] = pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 0),
+                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 1),
+                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 2),
+                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 3));
+  } else {
+    const float sc = e8m0_to_f32(r.s);
+    const uint32_t w[8] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w,
+                           r.q[1].x, r.q[1].y, r.q[1].z, r.q[1].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      f.v[j] = pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j], sc, false),
+                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j], sc, true),
+                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], sc, false),
+                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], sc, true));
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ size_t gemm_row_bytes(int K) {
+  return FMT == kFmtBF16 ? (size_t)K * 2 : (FMT == kFmtMXFP4 ? (size_t)K / 2 : (size_t)K);
+}
+
+// A staging: thread t covers row t/8 and 16 consecutive k at 16*(t%8) of the K step.
+struct AStage { float4 v[4]; };
+
+__device__ __forceinline__ void load_a(AStage& a, const float* __restrict__ src, bool valid,
+                                       int k0) {
+  const int kc = (threadIdx.x & 7) * 16;
+  if (valid) {
+    const float4* p = reinterpret_cast<const float4*>(src + k0 + kc);
+    a.v[0] = p[0]; a.v[1] = p[1]; a.v[2] = p[2]; a.v[3] = p[3];
+  } else {
+    a.v[0] = a.v[1] = a.v[2] = a.v[3] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// Writes hi/lo BF16 halves of the staged values; returns whether any lo half is non-zero.
+__device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo) {
+  const int m = threadIdx.x >> 3, kc = (threadIdx.x & 7) * 16;
+  const float* v = reinterpret_cast<const float*>(a.v);
+  u16 h[16], l[16];
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    h[i] = bf16_rne_bits(v[i]);
+    float rest = v[i] - u2f((uint32_t)h[i] << 16);
+    l[i] = bf16_rne_bits(rest);
+    any |= (l[i] & 0x7fff) != 0;
+  }
+  uint4* dh = reinterpret_cast<uint4*>(hi + m * kALd + kc);
+  uint4* dl = reinterpret_cast<uint4*>(lo + m * kALd + kc);
+  dh[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+  dh[1] = make_uint4(h[8] | (h[9] << 16), h[10] | (h[11] << 16), h[12] | (h[13] << 16), h[14] | (h[15] << 16));
+  dl[0] = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+  dl[1] = make_uint4(l[8] | (l[9] << 16), l[10] | (l[11] << 16), l[12] | (l[13] << 16), l[14] | (l[15] << 16));
+  return any;
+}
+
+__device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + m * kALd + k));
+}
+
+template <int FMT, bool PAIR>
+__global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
+                                                      Perm perm, int rows, int K,
+                                                      const float* __restrict__ in,
+                                                      float* __restrict__ out, int qwen,
+                                                      int* status) {
+  __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
+  __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
+
+  // ---- which tile
+  const int w = blockIdx.y;
+  int expert, base, count, m0;
+  if (perm.dense_tokens > 0) {
+    expert = 0;
+    base = 0;
+    count = perm.dense_tokens;
+    m0 = w * kMT;
+    if (m0 >= count) return;
+  } else {
+    if (w >= perm.meta[1]) return;
+    expert = perm.tiles[2 * w];
+    m0 = perm.tiles[2 * w + 1];
+    base = perm.offsets[expert];
+    count = perm.counts[expert];
+  }
+  const int mrows = min(kMT, count - m0);
+  const ExpertMats m = mats[expert];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ln = lane & 15, lq = lane >> 4;
+  const int n0 = blockIdx.x * kNT + wave * 16;
+  const int row = n0 + ln;
+  const size_t rb = gemm_row_bytes<FMT>(K);
+  const int sb = K / 32;
+
+  const uint8_t* b_row0 = m.data[PAIR ? 0 : 2] + (size_t)row * rb;
+  const uint8_t* b_s0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + (size_t)row * sb;
+  const uint8_t* b_row1 = PAIR ? m.data[1] + (size_t)row * rb : nullptr;
+  const uint8_t* b_s1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + (size_t)row * sb : nullptr;
+
+  // ---- A source row of this thread's staging slot
+  const int am = threadIdx.x >> 3;
+  const bool a_valid = am < mrows;
+  const float* a_src = in;
+  if (a_valid) {
+    const int p = base + m0 + am;
+    const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
+    a_src = in + (size_t)src_row * K;
+  }
+
+  f32x4 acc0[2], acc1[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    acc0[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int steps = K / kKS;
+  BRaw<FMT> r0, r1;
+  AStage as;
+  load_b<FMT>(r0, b_row0, b_s0, lq);
+  if constexpr (PAIR) load_b<FMT>(r1, b_row1, b_s1, lq);
+  load_a(as, a_src, a_valid, 0);
+  bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
+
+  for (int s = 0; s < steps; ++s) {
+    const int buf = s & 1;
+    const bool more = s + 1 < steps;
+    BFrag f0, f1;
+    decode_b<FMT>(r0, f0);
+    if constexpr (PAIR) decode_b<FMT>(r1, f1);
+    if (more) {  // prefetch the next K step: weights to registers, activations to registers
+      const int kb = (s + 1) * (kKS / 32) + lq;
+      load_b<FMT>(r0, b_row0, b_s0, kb);
+      if constexpr (PAIR) load_b<FMT>(r1, b_row1, b_s1, kb);
+      load_a(as, a_src, a_valid, (s + 1) * kKS);
+    }
+    const u16* hi = a_hi[buf];
+    const u16* lo = a_lo[buf];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const bf16x8 ah = lds_frag(hi, mb * 16 + ln, 32 * lq + 8 * j);
+        acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0.v[j], acc0[mb], 0, 0, 0);
+        if constexpr (PAIR)
+          acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1.v[j], acc1[mb], 0, 0, 0);
+        if (lo_any) {
+          const bf16x8 al = lds_frag(lo, mb * 16 + ln, 32 * lq + 8 * j);
+          acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0.v[j], acc0[mb], 0, 0, 0);
+          if constexpr (PAIR)
+            acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1.v[j], acc1[mb], 0, 0, 0);
+        }
+      }
+    }
+    if (more) lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
+  }
+
+  // ---- epilogue: lane holds column `row`, rows 4*lq + i of each 16-row block
+  bool bad = false;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int mm = mb * 16 + 4 * lq + i;
+      if (mm >= mrows) continue;
+      const size_t p = (size_t)(base + m0 + mm);
+      if constexpr (PAIR) {
+        const float g0 = acc0[mb][i], u0 = acc1[mb][i];
+        float act;
+        if (qwen) {
+          float g, u, ag;
+          bool ok = rne_bf16(g0, &g) && rne_bf16(u0, &u) && rne_bf16(silu(g), &ag);
+          float v = ag * u;
+          ok = ok && rne_bf16(v, &act);
+          if (!ok) { bad = true; act = v; }
+        } else {
+          act = silu(g0) * u0;
+          if (!finite(act)) bad = true;
+        }
+        out[p * rows + row] = act;
+      } else {
+        float y = acc0[mb][i];
+        if (qwen) {
+          float r;
+          if (!rne_bf16(y, &r)) bad = true; else y = r;
+        } else if (FMT == kFmtMXFP8 && !finite(y)) {
+          bad = true;
+        }
+        out[p * rows + row] = y;
+      }
+    }
+  }
+  if (bad) flag(status, kStatusNonFinite);
+}
+
+template <int FMT, bool PAIR>
+static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
+                   const float* in, float* out, int qwen, int* status, hipStream_t s) {
+  dim3 grid(rows / kNT, max_tiles);
+  gemm_kernel<FMT, PAIR><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, qwen, status);
+}
+
+void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
+                         int I, const float* x, float* act, int qwen, int* status,
+                         hipStream_t s) {
+  if (fmt == kFmtBF16) launch<kFmtBF16, true>(mats, perm, max_tiles, I, H, x, act, qwen, status, s);
+  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, true>(mats, perm, max_tiles, I, H, x, act, qwen, status, s);
+  else launch<kFmtMXFP8, true>(mats, perm, max_tiles, I, H, x, act, qwen, status, s);
+}
+
+void launch_gemm_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
+                      int I, const float* act, float* y, int qwen, int* status, hipStream_t s) {
+  if (fmt == kFmtBF16) launch<kFmtBF16, false>(mats, perm, max_tiles, H, I, act, y, qwen, status, s);
+  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, false>(mats, perm, max_tiles, H, I, act, y, qwen, status, s);
+  else launch<kFmtMXFP8, false>(mats, perm, max_tiles, H, I, act, y, qwen, status, s);
+}
+
+}  // namespace urb

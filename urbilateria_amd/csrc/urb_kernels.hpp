@@ -18,13 +18,32 @@ struct ExpertMats {
 // Token -> expert permutation for one forward chunk.  Stable (expert, token) order, the
 // execute_batched_moe grouping (src/models/qwen3_6/runtime.rs:1123-1132).
 struct Perm {
-  const int32_t* meta;        // meta[0] = number of active experts
+  const int32_t* meta;        // meta[0] = active experts, meta[1] = GEMM row tiles
   const int32_t* active;      // active expert ids, ascending
   const int32_t* offsets;     // [E + 1] first permuted position of each expert
   const int32_t* counts;      // [E] tokens routed to each expert
   const int32_t* perm_token;  // [T * k] token of each permuted position
   int dense_tokens;           // > 0: one dense expert (table entry 0) over tokens 0..n-1
+  const int32_t* tiles;       // [2 * tiles] (expert, first row) of each kGemmMTile-row tile
 };
+
+// Grouped GEMM (MFMA) tiling: tokens per tile, weight rows per tile, K per step.
+constexpr int kGemmMTile = 32;
+constexpr int kGemmNTile = 64;
+constexpr int kGemmKStep = 128;
+inline bool gemm_supported(int rows, int K) {
+  return rows % kGemmNTile == 0 && K % kGemmKStep == 0;
+}
+// Upper bound of row tiles for n tokens routed k ways over E experts.
+inline int gemm_max_tiles(int n, int k, int E) {
+  int a = n * k < E ? n * k : E;
+  return a + (n * k + kGemmMTile - 1) / kGemmMTile;
+}
+void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
+                         int I, const float* x, float* act, int qwen, int* status,
+                         hipStream_t s);
+void launch_gemm_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
+                      int I, const float* act, float* y, int qwen, int* status, hipStream_t s);
 
 struct RouteParams {
   int router;        // 0 softmax top-k, 1 sigmoid noaux_tc
@@ -47,7 +66,7 @@ void launch_route(const float* logits, int T, int E, int K, const RouteParams& p
 constexpr int kMaxChunkTokens = 1024;
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
-                    hipStream_t s);
+                    int32_t* tiles, hipStream_t s);
 // Decode projections (GEMV family): gate+up with the SwiGLU epilogue, then down.
 // `qwen` selects the BF16 boundaries of Qwen38Expert; otherwise GatedMlp's f32 path.
 void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,

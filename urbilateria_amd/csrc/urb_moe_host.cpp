@@ -38,6 +38,7 @@ struct Workspace {
   int32_t* counts = nullptr;
   int32_t* perm_token = nullptr;
   int32_t* pos_of_slot = nullptr;
+  int32_t* tiles = nullptr;
   float* act = nullptr;
   float* y_perm = nullptr;
   float* shared_act = nullptr;
@@ -207,6 +208,7 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   w.counts = b.take<int32_t>(E);
   w.perm_token = b.take<int32_t>(C * K);
   w.pos_of_slot = b.take<int32_t>(C * K);
+  w.tiles = b.take<int32_t>(2 * (size_t)urb::gemm_max_tiles((int)C, (int)K, (int)E));
   w.act = b.take<float>(C * K * I);
   w.y_perm = b.take<float>(C * K * H);
   w.shared_act = b.take<float>(C * std::max<size_t>(d.shared_intermediate, 1));
@@ -418,16 +420,25 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       // routes: it runs on the side stream while the router, top-k and permutation run here.
       URB_HIP(hipEventRecord(c->fork, s));
       URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
-      Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n};
+      Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr};
+      const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
       {
         Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
-        urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, xc,
-                                 ws.shared_act, 0, ws.status, c->side);
+        if (n > 1 && urb::gemm_supported(Is, H))
+          urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                                   xc, ws.shared_act, 0, ws.status, c->side);
+        else
+          urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, xc,
+                                   ws.shared_act, 0, ws.status, c->side);
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, c->side);
-        urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_act,
-                              ws.shared_out, 0, ws.status, c->side);
+        if (n > 1 && urb::gemm_supported(H, Is))
+          urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                                ws.shared_act, ws.shared_out, 0, ws.status, c->side);
+        else
+          urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is,
+                                ws.shared_act, ws.shared_out, 0, ws.status, c->side);
       }
       URB_HIP(hipEventRecord(c->join, c->side));
     }
@@ -435,19 +446,29 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     {
       Span span(c, URB_STAGE_PERMUTE, s);
       urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts,
-                          ws.perm_token, ws.pos_of_slot, s);
+                          ws.perm_token, ws.pos_of_slot, ws.tiles, s);
     }
-    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0};
+    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles};
     const int max_active = std::min(E, n * K);
+    const int max_tiles = urb::gemm_max_tiles(n, K, E);
+    // One token: row-parallel GEMV.  Several: grouped MFMA GEMM over the row tiles.
     {
       Span span(c, URB_STAGE_GATE_UP, s);
-      urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, xc, ws.act,
-                               qwen ? 1 : 0, ws.status, s);
+      if (n > 1 && urb::gemm_supported(I, H))
+        urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act,
+                                 qwen ? 1 : 0, ws.status, s);
+      else
+        urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, xc, ws.act,
+                                 qwen ? 1 : 0, ws.status, s);
     }
     {
       Span span(c, URB_STAGE_DOWN, s);
-      urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act,
-                            ws.y_perm, qwen ? 1 : 0, ws.status, s);
+      if (n > 1 && urb::gemm_supported(H, I))
+        urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act,
+                              ws.y_perm, qwen ? 1 : 0, ws.status, s);
+      else
+        urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act,
+                              ws.y_perm, qwen ? 1 : 0, ws.status, s);
     }
     if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {

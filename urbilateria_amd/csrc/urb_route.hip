@@ -345,13 +345,45 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 // Permutation (one workgroup, T <= 1024): a token bitmap per expert in LDS gives each
 // (token, route) its stable position: offsets[e] + #earlier tokens routed to e.
 // ------------------------------------------------------------------------------------------
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+  for (int o = 1; o < 64; o <<= 1) {
+    int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive prefix sum over a 1024-thread block; *total receives the block sum.
+__device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
+  const int incl = wave_incl_scan(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int w = 0; w < 16; ++w) {
+      int t = wsum[w];
+      wsum[w] = acc;
+      acc += t;
+    }
+    wsum[16] = acc;
+  }
+  __syncthreads();
+  const int r = incl - v + wsum[wave];
+  *total = wsum[16];
+  __syncthreads();
+  return r;
+}
+
 __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict__ ids, int T,
                                                        int E, int K, int32_t* meta,
                                                        int32_t* active, int32_t* offsets,
                                                        int32_t* counts, int32_t* perm_token,
-                                                       int32_t* pos_of_slot) {
+                                                       int32_t* pos_of_slot, int32_t* tiles) {
   extern __shared__ uint32_t bm[];  // [E][W]
   __shared__ int32_t off_s[kMaxExperts + 1];
+  __shared__ int32_t wsum[17];
   const int W = (T + 31) / 32;
   const int n = T * K;
   for (int i = threadIdx.x; i < E * W; i += blockDim.x) bm[i] = 0u;
@@ -361,25 +393,30 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
     atomicOr(&bm[e * W + (t >> 5)], 1u << (t & 31));
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int c = 0;
+  // one expert per thread (E <= 512 < 1024): counts, offsets, active list, GEMM row tiles
+  const int e = threadIdx.x;
+  int c = 0;
+  if (e < E)
     for (int w = 0; w < W; ++w) c += __popc(bm[e * W + w]);
-    off_s[e + 1] = c;
+  int total = 0, n_active = 0, n_tiles = 0;
+  const int off = block_excl_scan(c, wsum, &total);
+  const int slot = block_excl_scan(c > 0 ? 1 : 0, wsum, &n_active);
+  const int nt = (c + kGemmMTile - 1) / kGemmMTile;
+  const int toff = block_excl_scan(nt, wsum, &n_tiles);
+  if (e < E) {
     counts[e] = c;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0, na = 0;
-    off_s[0] = 0;
-    for (int e = 0; e < E; ++e) {
-      int c = off_s[e + 1];
-      offsets[e] = acc;
-      if (c) active[na++] = e;
-      acc += c;
-      off_s[e + 1] = acc;
+    offsets[e] = off;
+    off_s[e] = off;
+    if (c) active[slot] = e;
+    for (int j = 0; j < nt; ++j) {
+      tiles[2 * (toff + j)] = e;
+      tiles[2 * (toff + j) + 1] = j * kGemmMTile;
     }
-    offsets[E] = acc;
-    meta[0] = na;
+  }
+  if (threadIdx.x == 0) {
+    offsets[E] = total;
+    meta[0] = n_active;
+    meta[1] = n_tiles;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
@@ -421,10 +458,10 @@ void launch_route(const float* logits, int T, int E, int K, const RouteParams& p
 
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
-                    hipStream_t s) {
+                    int32_t* tiles, hipStream_t s) {
   size_t lds = (size_t)E * ((T + 31) / 32) * sizeof(uint32_t);
   permute_kernel<<<1, 1024, lds, s>>>(ids, T, E, K, meta, active, offsets, counts, perm_token,
-                                      pos_of_slot);
+                                      pos_of_slot, tiles);
 }
 
 }  // namespace urb

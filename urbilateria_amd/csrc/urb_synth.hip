@@ -75,6 +75,39 @@ __global__ void e8m0_kernel(uint64_t seed, size_t n, uint8_t* out) {
     out[i] = (uint8_t)(119 + splitmix(seed, i) % 7);
 }
 
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+// One v_mfma_f32_16x16x32_bf16 with operands placed by the lane layout the GEMM kernels
+// assume: A lane l holds row l%16, k = 8*(l/16) + [0,8); B lane l holds column l%16, the same
+// k range; C lane l holds column l%16, rows 4*(l/16) + [0,4).
+__global__ void mfma_layout_kernel(const float* A, const float* B, float* C) {
+  const int l = threadIdx.x;
+  bf16x8_t a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (__bf16)A[(l % 16) * 32 + 8 * (l / 16) + i];
+    b[i] = (__bf16)B[(8 * (l / 16) + i) * 16 + (l % 16)];
+  }
+  f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  for (int i = 0; i < 4; ++i) C[(4 * (l / 16) + i) * 16 + (l % 16)] = c[i];
+}
+
+// Scaled conversions to BF16 as the GEMM B-operand path uses them: element i of `codes`
+// (E2M1 nibble in the low 4 bits for fmt 1, E4M3 byte for fmt 2) times E8M0 scale `scales[i]`.
+__global__ void cvt_bf16_kernel(int fmt, const uint8_t* codes, const uint8_t* scales, int n,
+                                uint16_t* out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint32_t sb = (uint32_t)scales[i] << 23;
+  float scale = __uint_as_float(sb ? sb : 0x00400000u);
+  bf16x2_t v;
+  if (fmt == 1) v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4((uint32_t)codes[i] & 0xf, scale, 0);
+  else v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)codes[i], scale, false);
+  out[i] = __builtin_bit_cast(uint16_t, v[0]);
+}
+
 int grid_for(size_t n) {
   size_t b = (n + 255) / 256;
   return (int)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
@@ -107,6 +140,19 @@ int urb_synth_fp8(uint64_t seed, size_t n, void* out, void* stream) {
 // E8M0 scales 119 + draw % 7.
 int urb_synth_e8m0(uint64_t seed, size_t n, void* out, void* stream) {
   e8m0_kernel<<<grid_for(n), 256, 0, (hipStream_t)stream>>>(seed, n, (uint8_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// Diagnostics: C[16,16] = A[16,32] . B[32,16] through one MFMA (device f32 arrays).
+int urb_probe_mfma_16x16x32(const float* A, const float* B, float* C, void* stream) {
+  mfma_layout_kernel<<<1, 64, 0, (hipStream_t)stream>>>(A, B, C);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+// Diagnostics: BF16 bits of code[i] * E8M0 scale[i] via the scaled conversion instructions.
+int urb_probe_cvt_bf16(int fmt, const void* codes, const void* scales, int n, void* out,
+                       void* stream) {
+  cvt_bf16_kernel<<<(n + 255) / 256, 256, 0, (hipStream_t)stream>>>(
+      fmt, (const uint8_t*)codes, (const uint8_t*)scales, n, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

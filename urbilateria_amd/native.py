@@ -25,7 +25,7 @@ EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_rout
 STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
-                 "urb_synth_e8m0")
+                 "urb_synth_e8m0", "urb_probe_mfma_16x16x32", "urb_probe_cvt_bf16")
 
 
 class UrbError(RuntimeError):
@@ -116,6 +116,8 @@ def synth_lib() -> ctypes.CDLL:
         lib.urb_synth_fp4.argtypes = [u64, sz, P, P]
         lib.urb_synth_fp8.argtypes = [u64, sz, P, P]
         lib.urb_synth_e8m0.argtypes = [u64, sz, P, P]
+        lib.urb_probe_mfma_16x16x32.argtypes = [P, P, P, P]
+        lib.urb_probe_cvt_bf16.argtypes = [ctypes.c_int, P, P, ctypes.c_int, P, P]
         for f in SYNTH_EXPORTS:
             getattr(lib, f).restype = ctypes.c_int
         _synth = lib
