@@ -191,8 +191,11 @@ def test_router_logits_match_oracle(name):
         # the 8-lane FP32 tree is reproduced exactly, BF16 logits are bit-identical
         assert np.array_equal(logits.view(np.uint32), ref.logits.view(np.uint32))
     else:
-        ulp = np.abs(logits.view(np.int32).astype(np.int64) - ref.logits.view(np.int32))
-        assert ulp.max() <= 1
+        # f64 accumulation in another order (GEMV, < 16 tokens) or f32 MFMA partials of 32
+        # products folded into f64 (GEMM): the error stays far inside the 1e-6 near-tie gap
+        # that top-k parity allows.
+        err = np.abs(logits.astype(np.float64) - ref.logits.astype(np.float64))
+        assert err.max() <= 2e-7 + 2 * np.spacing(np.abs(ref.logits)).max()
     assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
     layer.close()
 

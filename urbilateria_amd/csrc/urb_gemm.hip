@@ -278,6 +278,95 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   if (bad) flag(status, kStatusNonFinite);
 }
 
+// ------------------------------------------------------------------------------------------
+// Router GEMM for many tokens: logits[t, e] = sum_k w[e, k] x[t, k] (`router.matvec`,
+// src/model/bf16.rs:121-216, ordered f64).  BF16 weight times the hi/lo BF16 halves of x are
+// exact products; each MFMA sums 32 of them in f32 and that partial is added into an f64
+// accumulator, so the f32 logit is the correctly rounded sum up to a few units in the last
+// place.  Tiles: 32 tokens x 64 experts (experts past E are clamped and not stored).
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __restrict__ w,
+                                                             int E, int H,
+                                                             const float* __restrict__ x, int T,
+                                                             float* __restrict__ logits,
+                                                             int* status) {
+  __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
+  __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
+  const int m0 = blockIdx.y * kMT;
+  const int mrows = min(kMT, T - m0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ln = lane & 15, lq = lane >> 4;
+  const int e = blockIdx.x * kNT + wave * 16 + ln;
+  const uint8_t* b_row = reinterpret_cast<const uint8_t*>(w + (size_t)min(e, E - 1) * H);
+  const int am = threadIdx.x >> 3;
+  const bool a_valid = am < mrows;
+  const float* a_src = x + (size_t)(m0 + (a_valid ? am : 0)) * H;
+
+  double acc[2][4];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[mb][i] = 0.0;
+
+  const int steps = H / kKS;
+  BRaw<kFmtBF16> r;
+  AStage as;
+  load_b<kFmtBF16>(r, b_row, nullptr, lq);
+  load_a(as, a_src, a_valid, 0);
+  bool bad = false;
+  {
+    const float* v = reinterpret_cast<const float*>(as.v);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bad |= !finite(v[i]);
+  }
+  bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < steps; ++s) {
+    const int buf = s & 1;
+    const bool more = s + 1 < steps;
+    BFrag f;
+    decode_b<kFmtBF16>(r, f);
+    if (more) {
+      load_b<kFmtBF16>(r, b_row, nullptr, (s + 1) * (kKS / 32) + lq);
+      load_a(as, a_src, a_valid, (s + 1) * kKS);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            lds_frag(a_hi[buf], mb * 16 + ln, 32 * lq + 8 * j), f.v[j], zero, 0, 0, 0);
+        if (lo_any)
+          part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              lds_frag(a_lo[buf], mb * 16 + ln, 32 * lq + 8 * j), f.v[j], part, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mb][i] += (double)part[i];
+      }
+    }
+    if (more) {
+      const float* v = reinterpret_cast<const float*>(as.v);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) bad |= !finite(v[i]);
+      lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
+    }
+  }
+  if (bad && blockIdx.x == 0) flag(status, kStatusNonFinite);
+  if (e >= E) return;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int mm = mb * 16 + 4 * lq + i;
+      if (mm < mrows) logits[(size_t)(m0 + mm) * E + e] = (float)acc[mb][i];
+    }
+}
+
+void launch_router_gemm(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
+                        int* status, hipStream_t s) {
+  dim3 grid((E + kNT - 1) / kNT, (T + kMT - 1) / kMT);
+  router_gemm_kernel<<<grid, 256, 0, s>>>(w, E, H, x, T, logits, status);
+}
+
 template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                    const float* in, float* out, int qwen, int* status, hipStream_t s) {

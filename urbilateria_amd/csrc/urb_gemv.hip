@@ -34,13 +34,41 @@ struct Fmt<kFmtMXFP8> {
   __device__ static size_t row_bytes(int cols) { return (size_t)cols; }
 };
 
-// acc += chunk(row, g) . xs[g * kCols ...]
+// One lane's chunk of a weight row, loaded ahead of its use.
 template <int FMT>
-__device__ __forceinline__ void chunk_fma(const uint8_t* __restrict__ row,
-                                          const uint8_t* __restrict__ srow, int g,
+struct Chunk;
+template <>
+struct Chunk<kFmtBF16> { uint4 q; };
+template <>
+struct Chunk<kFmtMXFP4> { uint4 q; uint32_t s; };
+template <>
+struct Chunk<kFmtMXFP8> { uint4 q0, q1; uint32_t s; };
+// Chunks a lane loads before computing on them (a batch of independent 128-bit loads).
+template <int FMT>
+constexpr int kBatch = FMT == kFmtBF16 ? 8 : 4;
+
+template <int FMT>
+__device__ __forceinline__ void chunk_load(Chunk<FMT>& c, const uint8_t* __restrict__ row,
+                                           const uint8_t* __restrict__ srow, int g) {
+  if constexpr (FMT == kFmtBF16) {
+    c.q = *reinterpret_cast<const uint4*>(row + (size_t)g * 16);
+  } else if constexpr (FMT == kFmtMXFP4) {
+    c.q = *reinterpret_cast<const uint4*>(row + (size_t)g * 16);
+    c.s = srow[g];
+  } else {
+    const uint4* qp = reinterpret_cast<const uint4*>(row + (size_t)g * 32);
+    c.q0 = qp[0];
+    c.q1 = qp[1];
+    c.s = srow[g];
+  }
+}
+
+// acc += chunk . xs[g * kCols ...]
+template <int FMT>
+__device__ __forceinline__ void chunk_dot(const Chunk<FMT>& c, int g,
                                           const float* __restrict__ xs, float& acc) {
   if constexpr (FMT == kFmtBF16) {
-    uint4 q = *reinterpret_cast<const uint4*>(row + (size_t)g * 16);
+    const uint4 q = c.q;
     const float4* xv = reinterpret_cast<const float4*>(xs + g * 8);
     float4 a = xv[0], b = xv[1];
     float p0 = bf16_lo(q.x) * a.x, p1 = bf16_hi(q.x) * a.y;
@@ -52,10 +80,9 @@ __device__ __forceinline__ void chunk_fma(const uint8_t* __restrict__ row,
     p1 = fmaf(bf16_hi(q.w), b.w, p1);
     acc += p0 + p1;
   } else if constexpr (FMT == kFmtMXFP4) {
-    uint4 q = *reinterpret_cast<const uint4*>(row + (size_t)g * 16);
-    float scale = e8m0_to_f32(srow[g]);
+    const float scale = e8m0_to_f32(c.s);
     const float4* xv = reinterpret_cast<const float4*>(xs + g * 32);
-    uint32_t words[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t words[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
     float part[4];
 #pragma unroll
     for (int wd = 0; wd < 4; ++wd) {
@@ -74,11 +101,9 @@ __device__ __forceinline__ void chunk_fma(const uint8_t* __restrict__ row,
     }
     acc = fmaf((part[0] + part[1]) + (part[2] + part[3]), scale, acc);
   } else {
-    const uint4* qp = reinterpret_cast<const uint4*>(row + (size_t)g * 32);
-    uint4 q0 = qp[0], q1 = qp[1];
-    float scale = e8m0_to_f32(srow[g]);
+    const float scale = e8m0_to_f32(c.s);
     const float4* xv = reinterpret_cast<const float4*>(xs + g * 32);
-    uint32_t words[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const uint32_t words[8] = {c.q0.x, c.q0.y, c.q0.z, c.q0.w, c.q1.x, c.q1.y, c.q1.z, c.q1.w};
     float part[4];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -150,29 +175,61 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict_
   const int r_begin = rb * rows_per_block;
   const int r_end = min(rows, r_begin + rows_per_block);
   bool bad = false;
+  constexpr int NB = kBatch<FMT>;
+  const int r_first = r_begin + wave * kGroups + sub;
   for (int q = 0; q < count; ++q) {
     const int p = base + q;
     const float* src = PAIR ? in + (size_t)perm_token(perm, p) * cols : in + (size_t)p * cols;
+    // The first batch of this lane's weights is requested before the input vector is staged,
+    // so the two memory latencies overlap.
+    Chunk<FMT> c0[NB], c1[NB];
+    bool have = r_first < r_end;
+    if (have) {
+      const uint8_t* row0 = m.data[PAIR ? 0 : 2] + (size_t)r_first * rbytes;
+      const uint8_t* s0 =
+          FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + (size_t)r_first * sbytes;
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        const int g = li + u * LPR;
+        if (g < G) {
+          chunk_load<FMT>(c0[u], row0, s0, g);
+          if constexpr (PAIR)
+            chunk_load<FMT>(c1[u], m.data[1] + (size_t)r_first * rbytes,
+                            FMT == kFmtBF16 ? nullptr
+                                            : m.scales[1] + (size_t)r_first * sbytes,
+                            g);
+        }
+      }
+    }
     __syncthreads();
     stage(src, cols, xs);
     __syncthreads();
-    for (int r = r_begin + wave * kGroups + sub; r < r_end; r += 4 * kGroups) {
+    for (int r = r_first; r < r_end; r += 4 * kGroups) {
       float acc0 = 0.0f, acc1 = 0.0f;
-      if constexpr (PAIR) {
-        const uint8_t* g_row = m.data[0] + (size_t)r * rbytes;
-        const uint8_t* u_row = m.data[1] + (size_t)r * rbytes;
-        const uint8_t* g_s = FMT == kFmtBF16 ? nullptr : m.scales[0] + (size_t)r * sbytes;
-        const uint8_t* u_s = FMT == kFmtBF16 ? nullptr : m.scales[1] + (size_t)r * sbytes;
-#pragma unroll 4
-        for (int g = li; g < G; g += LPR) {
-          chunk_fma<FMT>(g_row, g_s, g, xs, acc0);
-          chunk_fma<FMT>(u_row, u_s, g, xs, acc1);
+      const uint8_t* row0 = m.data[PAIR ? 0 : 2] + (size_t)r * rbytes;
+      const uint8_t* s0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + (size_t)r * sbytes;
+      const uint8_t* row1 = PAIR ? m.data[1] + (size_t)r * rbytes : nullptr;
+      const uint8_t* s1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + (size_t)r * sbytes : nullptr;
+      for (int g0 = li; g0 < G; g0 += NB * LPR) {
+        if (!have) {
+#pragma unroll
+          for (int u = 0; u < NB; ++u) {
+            const int g = g0 + u * LPR;
+            if (g < G) {
+              chunk_load<FMT>(c0[u], row0, s0, g);
+              if constexpr (PAIR) chunk_load<FMT>(c1[u], row1, s1, g);
+            }
+          }
         }
-      } else {
-        const uint8_t* d_row = m.data[2] + (size_t)r * rbytes;
-        const uint8_t* d_s = FMT == kFmtBF16 ? nullptr : m.scales[2] + (size_t)r * sbytes;
-#pragma unroll 4
-        for (int g = li; g < G; g += LPR) chunk_fma<FMT>(d_row, d_s, g, xs, acc0);
+        have = false;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+          const int g = g0 + u * LPR;
+          if (g < G) {
+            chunk_dot<FMT>(c0[u], g, xs, acc0);
+            if constexpr (PAIR) chunk_dot<FMT>(c1[u], g, xs, acc1);
+          }
+        }
       }
       acc0 = wave_sum_f32(acc0, LPR);
       if constexpr (PAIR) acc1 = wave_sum_f32(acc1, LPR);
@@ -217,8 +274,16 @@ static void launch_gemv(const ExpertMats* mats, const Perm& perm, int max_active
   // Lanes per row: the widest split that leaves every lane at least 2 chunks.
   int lpr = 64;
   while (lpr > 16 && G < 2 * lpr) lpr /= 2;
-  const int rows_per_wave_pass = 64 / lpr;
-  const int rows_per_block = 4 * rows_per_wave_pass * (PAIR ? 8 : 4);
+  // Rows per workgroup: ~2048 workgroups to cover every CU several times, with at least 2x the
+  // staged input vector's bytes of weights per workgroup and at most 8 row passes per wave.
+  const int rows_per_pass = 4 * (64 / lpr);
+  const long row_bytes = (long)cols * (FMT == kFmtBF16 ? 2 : 1) / (FMT == kFmtMXFP4 ? 2 : 1) *
+                         (PAIR ? 2 : 1);
+  const long reuse_rows = (2L * cols * 4 + row_bytes - 1) / row_bytes;
+  const long spread_rows = ((long)rows * max_active + 2047) / 2048;
+  const long want = std::max(reuse_rows, spread_rows);
+  const int passes = (int)std::max(1L, std::min(8L, (want + rows_per_pass - 1) / rows_per_pass));
+  const int rows_per_block = rows_per_pass * passes;
   const int nrb = (rows + rows_per_block - 1) / rows_per_block;
   dim3 grid(max_active * nrb);
   size_t lds = (size_t)cols * sizeof(float);
@@ -260,6 +325,7 @@ void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max
 // GLM (src/models/glm/runtime/moe.rs:162-171): acc = f64(shared) (or 0), then in ranking
 //   order acc += f64(w) * f64(y); out = f32(acc).
 // ------------------------------------------------------------------------------------------
+template <int KMAX>
 __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restrict__ y,
                                                            const int32_t* __restrict__ pos,
                                                            const float* __restrict__ w,
@@ -270,26 +336,40 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
   const int h4 = blockIdx.x * blockDim.x + threadIdx.x;
   const int t = blockIdx.y;
   if (h4 * 4 >= H) return;
+  // all route metadata first, then every expert row: two dependent round trips in total
+  int rk[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) rk[j] = j < K ? asc[(size_t)t * K + j] : 0;
+  float wt[KMAX];
+  float4 v[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < K) {
+      wt[j] = w[(size_t)t * K + rk[j]];
+      const int p = pos[(size_t)t * K + rk[j]];
+      v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
+    }
+  }
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   bool bad = false;
-  for (int j = 0; j < K; ++j) {
-    const int r = asc[(size_t)t * K + j];
-    const float wt = w[(size_t)t * K + r];
-    const int p = pos[(size_t)t * K + r];
-    float4 v = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
-    float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      float c;
-      if (!rne_bf16(wt * vv[u], &c)) { bad = true; c = wt * vv[u]; }
-      float s = acc[u] + c;
-      if (!rne_bf16(s, &acc[u])) { bad = true; acc[u] = s; }
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < K) {
+      const float vv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float c;
+        if (!rne_bf16(wt[j] * vv[u], &c)) { bad = true; c = wt[j] * vv[u]; }
+        const float s = acc[u] + c;
+        if (!rne_bf16(s, &acc[u])) { bad = true; acc[u] = s; }
+      }
     }
   }
   if (bad) flag(status, kStatusNonFinite);
   reinterpret_cast<float4*>(out + (size_t)t * H)[h4] = make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
 
+template <int KMAX>
 __global__ __launch_bounds__(256) void combine_glm_kernel(const float* __restrict__ y,
                                                           const int32_t* __restrict__ pos,
                                                           const float* __restrict__ w,
@@ -299,19 +379,30 @@ __global__ __launch_bounds__(256) void combine_glm_kernel(const float* __restric
   const int h4 = blockIdx.x * blockDim.x + threadIdx.x;
   const int t = blockIdx.y;
   if (h4 * 4 >= H) return;
+  float wt[KMAX];
+  float4 v[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < K) {
+      wt[j] = w[(size_t)t * K + j];
+      const int p = pos[(size_t)t * K + j];
+      v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
+    }
+  }
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
   if (shared) {
-    float4 s = reinterpret_cast<const float4*>(shared + (size_t)t * H)[h4];
+    const float4 s = reinterpret_cast<const float4*>(shared + (size_t)t * H)[h4];
     acc[0] = s.x; acc[1] = s.y; acc[2] = s.z; acc[3] = s.w;
   }
-  for (int j = 0; j < K; ++j) {
-    const double wt = (double)w[(size_t)t * K + j];
-    const int p = pos[(size_t)t * K + j];
-    float4 v = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
-    acc[0] += wt * (double)v.x;
-    acc[1] += wt * (double)v.y;
-    acc[2] += wt * (double)v.z;
-    acc[3] += wt * (double)v.w;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < K) {
+      const double wd = (double)wt[j];
+      acc[0] += wd * (double)v[j].x;
+      acc[1] += wd * (double)v[j].y;
+      acc[2] += wd * (double)v[j].z;
+      acc[3] += wd * (double)v[j].w;
+    }
   }
   reinterpret_cast<float4*>(out + (size_t)t * H)[h4] =
       make_float4((float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]);
@@ -321,14 +412,22 @@ void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const 
                          const int32_t* asc, int T, int K, int H, float* out, int* status,
                          hipStream_t s) {
   dim3 grid((H / 4 + 255) / 256, T);
-  combine_qwen_kernel<<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H, out,
-                                           status);
+  if (K <= 8)
+    combine_qwen_kernel<8><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H, out,
+                                                status);
+  else
+    combine_qwen_kernel<32><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H, out,
+                                                 status);
 }
 
 void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                         const float* shared, int T, int K, int H, float* out, hipStream_t s) {
   dim3 grid((H / 4 + 255) / 256, T);
-  combine_glm_kernel<<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, shared, T, K, H, out);
+  if (K <= 8)
+    combine_glm_kernel<8><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, shared, T, K, H, out);
+  else
+    combine_glm_kernel<32><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, shared, T, K, H,
+                                                out);
 }
 
 // ------------------------------------------------------------------------------------------

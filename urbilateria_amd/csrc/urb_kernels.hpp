@@ -58,6 +58,10 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
                          int* status, hipStream_t s);
 void launch_router_f64(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
                        int* status, hipStream_t s);
+// Router logits for many tokens (GLM): MFMA BF16 with f64 accumulation of 32-k partials.
+void launch_router_gemm(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
+                        int* status, hipStream_t s);
+constexpr int kRouterGemmMinTokens = 16;
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s);
 // Top-k routing, one wavefront per token.
 void launch_route(const float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,

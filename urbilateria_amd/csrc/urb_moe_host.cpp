@@ -232,8 +232,9 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
         return URB_ERR_ARGUMENT;
   URB_HIP(hipGetDevice(&c->device));
   c->desc = *d;
-  // The permutation keeps an [E][chunk/32] token bitmap in LDS: cap it at 60 KiB.
-  const uint32_t bitmap_chunk = (uint32_t)(60 * 1024 / (4 * E)) * 32;
+  // The permutation keeps [E][chunk/64] 64-bit token bitmaps and u16 prefix counts in LDS:
+  // cap them at 60 KiB.
+  const uint32_t bitmap_chunk = (uint32_t)(60 * 1024 / (10 * E)) * 64;
   c->chunk = std::min<uint32_t>({d->max_tokens, (uint32_t)urb::kMaxChunkTokens, bitmap_chunk});
 
   const bool borrow = src == URB_SOURCE_DEVICE_BORROW;
@@ -386,6 +387,8 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logi
   {
     Span span(c, URB_STAGE_ROUTER, s);
     if (qwen) urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, c->ws.status, s);
+    else if (n >= urb::kRouterGemmMinTokens && H % urb::kGemmKStep == 0)
+      urb::launch_router_gemm(c->router, E, H, x, n, logits, c->ws.status, s);
     else urb::launch_router_f64(c->router, E, H, x, n, logits, c->ws.status, s);
   }
   urb::RouteParams rp{(int)d.router, qwen ? 1 : 0, (int)d.n_group, (int)d.topk_group,

@@ -13,7 +13,6 @@ namespace urb {
 // The weights are re-laid out once at create time so that each chain is contiguous:
 //   w8[e][j][i] = w[e][8 i + j] for i < H/8, then the H % 8 tail columns of row e.
 // ------------------------------------------------------------------------------------------
-constexpr int kLane8Tokens = 4;
 
 __global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E, int H,
                                       uint16_t* __restrict__ w8) {
@@ -28,6 +27,7 @@ __global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E, int
   }
 }
 
+template <int kLane8Tokens>
 __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __restrict__ w8,
                                                           int E, int H,
                                                           const float* __restrict__ x, int T,
@@ -38,32 +38,62 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
   const int t0 = blockIdx.y * kLane8Tokens;
   const int nt = min(kLane8Tokens, T - t0);
   float* xt = xs + kLane8Tokens * 8 * H8p;
-  for (int i = threadIdx.x; i < nt * H; i += blockDim.x) {
-    int tt = i / H, c = i - tt * H;
-    float v = x[(size_t)(t0 + tt) * H + c];
-    if (!finite(v)) flag(status, kStatusNonFinite);
-    if (c < 8 * H8) xs[(tt * 8 + (c & 7)) * H8p + (c >> 3)] = v;
-    else xt[tt * tail + (c - 8 * H8)] = v;
-  }
-  __syncthreads();
   const int el = threadIdx.x >> 3, j = threadIdx.x & 7;
   const int e = blockIdx.x * 8 + el;
-  float acc[kLane8Tokens] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* chain = w8 + (size_t)min(e, E - 1) * H + (size_t)j * H8;
+  const bool vec = (H8 & 63) == 0;
+  // First 64 chain elements go to registers before the activations are staged.
+  uint4 wq[8];
+  if (vec) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) wq[u] = reinterpret_cast<const uint4*>(chain)[u];
+  }
+  // Stage x with coalesced float4 loads, transposed into per-lane chains.
+  bool bad = false;
+  const int n4 = nt * H / 4;
+  for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+    const float4 v4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H)[i];
+    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int flat = 4 * i + u, tt = flat / H, c = flat - tt * H;
+      bad |= !finite(vv[u]);
+      if (c < 8 * H8) xs[(tt * 8 + (c & 7)) * H8p + (c >> 3)] = vv[u];
+      else xt[tt * tail + (c - 8 * H8)] = vv[u];
+    }
+  }
+  if (bad) flag(status, kStatusNonFinite);
+  __syncthreads();
+  float acc[kLane8Tokens];
+#pragma unroll
+  for (int tt = 0; tt < kLane8Tokens; ++tt) acc[tt] = 0.0f;
   if (e < E) {
-    const uint16_t* chain = w8 + (size_t)e * H + (size_t)j * H8;
     const float* xj = xs + j * H8p;
-    if ((H8 & 7) == 0) {
-      for (int i = 0; i < H8; i += 8) {
-        uint4 q = *reinterpret_cast<const uint4*>(chain + i);
-        float wv[8] = {bf16_lo(q.x), bf16_hi(q.x), bf16_lo(q.y), bf16_hi(q.y),
-                       bf16_lo(q.z), bf16_hi(q.z), bf16_lo(q.w), bf16_hi(q.w)};
+    if (vec) {
+      for (int i0 = 0; i0 < H8; i0 += 64) {
+        uint4 nq[8];
+        const bool more = i0 + 64 < H8;
+        if (more) {
 #pragma unroll
-        for (int tt = 0; tt < kLane8Tokens; ++tt) {
-          if (tt < nt) {
-            const float* xv = xj + tt * 8 * H8p + i;
+          for (int u = 0; u < 8; ++u) nq[u] = reinterpret_cast<const uint4*>(chain + i0 + 64)[u];
+        }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc[tt] = fmaf(wv[u], xv[u], acc[tt]);
+        for (int u = 0; u < 8; ++u) {
+          const uint4 q = wq[u];
+          const float wv[8] = {bf16_lo(q.x), bf16_hi(q.x), bf16_lo(q.y), bf16_hi(q.y),
+                               bf16_lo(q.z), bf16_hi(q.z), bf16_lo(q.w), bf16_hi(q.w)};
+#pragma unroll
+          for (int tt = 0; tt < kLane8Tokens; ++tt) {
+            if (tt < nt) {
+              const float* xv = xj + tt * 8 * H8p + i0 + 8 * u;
+#pragma unroll
+              for (int k = 0; k < 8; ++k) acc[tt] = fmaf(wv[k], xv[k], acc[tt]);
+            }
           }
+        }
+        if (more) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) wq[u] = nq[u];
         }
       }
     } else {
@@ -151,27 +181,58 @@ __global__ __launch_bounds__(256) void router_f64_kernel(const uint16_t* __restr
 }
 
 // ------------------------------------------------------------------------------------------
-// Top-k routing: one wavefront per token, experts spread over lanes (lane l holds experts
-// l, l + 64, ...).  Ranking is iterated wave arg-max on (total-order key desc, expert id asc),
-// the reference's sort comparator.  Sums the reference performs sequentially are performed
-// sequentially here too (uniformly in every lane, reading from LDS).
+// Top-k routing: one wavefront per token, expert e in lane e % 64, slot e / 64.  Ranking is
+// iterated wave arg-max on (total-order key desc, expert id asc) -- the reference's sort
+// comparator -- with DPP reductions.  Round r's winner is kept by lane r.  Sums the reference
+// performs sequentially are performed sequentially here too (lane by lane via readlane).
 // ------------------------------------------------------------------------------------------
 constexpr int kMaxExperts = 512;
-constexpr int kEPL = kMaxExperts / 64;
 constexpr int kMaxTopK = 32;
 
-// Packs (key desc, id asc) into one u64 whose maximum is the reference's first-ranked element.
-__device__ __forceinline__ uint64_t rank_key(float v, int id) {
-  return ((uint64_t)((uint32_t)total_key(v) ^ 0x80000000u) << 32) | (uint32_t)(0xffffffffu - id);
+__device__ __forceinline__ int dpp_max_i32(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xf, 0xf, false));  // row_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast15
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast31
+  return __builtin_amdgcn_readlane(v, 63);
 }
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t other = __shfl_xor(v, o, 64);
-    v = other > v ? other : v;
-  }
-  return v;
+__device__ __forceinline__ int dpp_min_i32(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ float rdl(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// One ranking round over the lane's untaken slots: returns the winner id (uniform) and sets
+// `val` (uniform) to the winner's `score2` value.
+template <int EPL>
+__device__ __forceinline__ int argmax_round(const int32_t (&key)[EPL], const float (&score2)[EPL],
+                                            bool (&open)[EPL], float& val) {
+  const int lane = threadIdx.x & 63;
+  int32_t bk = INT32_MIN;
+  int bid = INT32_MAX;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    if (open[i] && key[i] > bk) { bk = key[i]; bid = lane + 64 * i; }
+  const int kmax = dpp_max_i32(bk);
+  const int id = dpp_min_i32(bk == kmax ? bid : INT32_MAX);
+  float mine = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    if (lane + 64 * i == id) { open[i] = false; mine = score2[i]; }
+  val = rdl(mine, id & 63);
+  return id;
+}
+
+template <int EPL, bool SOFTMAX>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int T,
                                                     int E, int K, RouteParams rp,
                                                     int32_t* __restrict__ ids,
@@ -182,161 +243,131 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
-  float* sh = lds[wave];
   const float* lt = logits + (size_t)t * E;
-  float v[kEPL];
-  bool valid[kEPL], taken[kEPL];
+  float v[EPL];
+  bool open[EPL];
   bool bad = false;
 #pragma unroll
-  for (int i = 0; i < kEPL; ++i) {
-    int e = lane + 64 * i;
-    valid[i] = e < E;
-    taken[i] = false;
-    v[i] = valid[i] ? lt[e] : 0.0f;
-    if (valid[i] && !finite(v[i])) bad = true;
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    open[i] = e < E;
+    v[i] = open[i] ? lt[e] : 0.0f;
+    if (open[i] && !finite(v[i])) bad = true;
   }
-  int out_ids[kMaxTopK];
-  float out_w[kMaxTopK];
-
-  if (rp.router == 0) {
+  int my_id = 0;
+  float my_val = 0.0f;
+  float w = 0.0f;
+  if constexpr (SOFTMAX) {
     // route_softmax_top_k (src/models/qwen3_8/moe.rs:91-159).
-    float m = -INFINITY;
+    int32_t mk = INT32_MIN;
 #pragma unroll
-    for (int i = 0; i < kEPL; ++i)
-      if (valid[i]) m = fmaxf(m, v[i]);
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    float p[kEPL];
+    for (int i = 0; i < EPL; ++i)
+      if (open[i]) mk = max(mk, total_key(v[i]));
+    // total-order key of the maximum; logits are finite here, so it is the float maximum
+    int32_t kmax = dpp_max_i32(mk);
+    const float m = __int_as_float(kmax ^ (int32_t)(((uint32_t)(kmax >> 31)) >> 1));
+    float p[EPL];
 #pragma unroll
-    for (int i = 0; i < kEPL; ++i) {
-      p[i] = valid[i] ? exp_f32(v[i] - m) : 0.0f;
-      if (valid[i]) sh[lane + 64 * i] = p[i];
+    for (int i = 0; i < EPL; ++i) p[i] = open[i] ? exp_f32(v[i] - m) : 0.0f;
+    float den = 0.0f;  // sequential in expert order e = 64 i + lane
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int n_here = min(64, E - 64 * i);
+      for (int l = 0; l < n_here; ++l) den = __fadd_rn(den, rdl(p[i], l));
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    float den = 0.0f;  // sequential, expert order
-    for (int e = 0; e < E; ++e) den = __fadd_rn(den, sh[e]);
     if (!finite(den) || den <= 0.0f) bad = true;
+    int32_t key[EPL];
 #pragma unroll
-    for (int i = 0; i < kEPL; ++i) {
-      if (valid[i]) {
-        p[i] = p[i] / den;
-        if (!finite(p[i])) bad = true;
-      }
+    for (int i = 0; i < EPL; ++i) {
+      p[i] = p[i] / den;
+      if (open[i] && !finite(p[i])) bad = true;
+      key[i] = total_key(p[i]);
     }
-    float sel_sum = 0.0f;
     for (int r = 0; r < K; ++r) {
-      uint64_t best = 0;
-#pragma unroll
-      for (int i = 0; i < kEPL; ++i)
-        if (valid[i] && !taken[i]) {
-          uint64_t k = rank_key(p[i], lane + 64 * i);
-          best = k > best ? k : best;
-        }
-      best = wave_max_u64(best);
-      int id = (int)(0xffffffffu - (uint32_t)best);
-      float pv = 0.0f;
-#pragma unroll
-      for (int i = 0; i < kEPL; ++i)
-        if (lane + 64 * i == id) { taken[i] = true; pv = p[i]; }
-      pv = __shfl(pv, id & 63, 64);
-      out_ids[r] = id;
-      out_w[r] = pv;
-      sel_sum = __fadd_rn(sel_sum, pv);
+      float val;
+      const int id = argmax_round<EPL>(key, p, open, val);
+      if (lane == r) { my_id = id; my_val = val; }
     }
+    float sel_sum = 0.0f;  // sequential in ranking order
+    for (int r = 0; r < K; ++r) sel_sum = __fadd_rn(sel_sum, rdl(my_val, r));
     if (!finite(sel_sum) || sel_sum <= 0.0f) bad = true;
-    for (int r = 0; r < K; ++r) {
-      float w = out_w[r] / sel_sum;
+    w = my_val / sel_sum;
+    if (lane < K) {
       if (!finite(w)) bad = true;
       if (rp.qwen) {  // qwen3_6/runtime.rs:1233-1238: route weights materialised in BF16
         float q;
-        if (!rne_bf16(w, &q)) { bad = true; q = w; }
-        w = q;
+        if (!rne_bf16(w, &q)) bad = true; else w = q;
       }
-      out_w[r] = w;
     }
   } else {
     // route_noaux_tc (src/math/routing.rs:38-155).
-    float g[kEPL], s[kEPL];
+    float g[EPL], sc[EPL];
+    int32_t key[EPL];
+    float* sh = lds[wave];
 #pragma unroll
-    for (int i = 0; i < kEPL; ++i) {
-      int e = lane + 64 * i;
-      g[i] = valid[i] ? 1.0f / (1.0f + exp_f32(-v[i])) : 0.0f;
-      float b = (valid[i] && rp.bias) ? rp.bias[e] : 0.0f;
-      s[i] = __fadd_rn(g[i], b);
-      if (valid[i]) sh[e] = s[i];
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      g[i] = open[i] ? 1.0f / (1.0f + exp_f32(-v[i])) : 0.0f;
+      const float b = (open[i] && rp.bias) ? rp.bias[e] : 0.0f;
+      sc[i] = __fadd_rn(g[i], b);
+      key[i] = total_key(sc[i]);
+      if (open[i]) sh[e] = sc[i];
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const int per = E / rp.n_group;
-    // group score = sum of the two largest selection scores (:104-111)
-    if (lane < rp.n_group) {
-      int32_t k1 = INT32_MIN, k2 = INT32_MIN;
-      float b1 = 0.0f, b2 = 0.0f;
-      for (int i = 0; i < per; ++i) {
-        float sv = sh[lane * per + i];
-        int32_t k = total_key(sv);
-        if (k > k1) { k2 = k1; b2 = b1; k1 = k; b1 = sv; }
-        else if (k > k2) { k2 = k; b2 = sv; }
-      }
-      grp[wave][lane] = __fadd_rn(b1, b2);
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    // keep the top `topk_group` groups (score desc, id asc)
-    bool gsel = false;
-    float gs = lane < rp.n_group ? grp[wave][lane] : 0.0f;
-    for (int r = 0; r < rp.topk_group; ++r) {
-      uint64_t k = (lane < rp.n_group && !gsel) ? rank_key(gs, lane) : 0;
-      k = wave_max_u64(k);
-      int id = (int)(0xffffffffu - (uint32_t)k);
-      if (lane == id) gsel = true;
-    }
-    uint64_t gmask = __ballot(gsel);
-    for (int r = 0; r < K; ++r) {
-      uint64_t best = 0;
-#pragma unroll
-      for (int i = 0; i < kEPL; ++i) {
-        int e = lane + 64 * i;
-        if (valid[i] && !taken[i] && ((gmask >> (e / per)) & 1ull)) {
-          uint64_t k = rank_key(s[i], e);
-          best = k > best ? k : best;
+    if (rp.topk_group < rp.n_group) {
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      const int per = E / rp.n_group;
+      // group score = sum of the two largest selection scores (:104-111)
+      if (lane < rp.n_group) {
+        int32_t k1 = INT32_MIN, k2 = INT32_MIN;
+        float b1 = 0.0f, b2 = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < per; ++i) {
+          const float sv = sh[lane * per + i];
+          const int32_t k = total_key(sv);
+          if (k > k1) { k2 = k1; b2 = b1; k1 = k; b1 = sv; }
+          else if (k > k2) { k2 = k; b2 = sv; }
         }
+        grp[wave][lane] = __fadd_rn(b1, b2);
       }
-      best = wave_max_u64(best);
-      int id = (int)(0xffffffffu - (uint32_t)best);
-      float gv = 0.0f;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      // keep the top `topk_group` groups (score desc, id asc)
+      const bool is_group = lane < rp.n_group;
+      const int32_t gk = is_group ? total_key(grp[wave][lane]) : INT32_MIN;
+      bool gopen = is_group, gsel = false;
+      for (int r = 0; r < rp.topk_group; ++r) {
+        const int32_t cand = gopen ? gk : INT32_MIN;
+        const int32_t kmax = dpp_max_i32(cand);
+        const int gid = dpp_min_i32(gopen && gk == kmax ? lane : INT32_MAX);
+        if (lane == gid) { gopen = false; gsel = true; }
+      }
+      const uint64_t gmask = __ballot(gsel);
 #pragma unroll
-      for (int i = 0; i < kEPL; ++i)
-        if (lane + 64 * i == id) { taken[i] = true; gv = g[i]; }
-      gv = __shfl(gv, id & 63, 64);
-      out_ids[r] = id;
-      out_w[r] = gv;
+      for (int i = 0; i < EPL; ++i)
+        if (open[i] && !((gmask >> ((lane + 64 * i) / per)) & 1ull)) open[i] = false;
     }
-    float den = -0.0f;
-    for (int r = 0; r < K; ++r) den = __fadd_rn(den, out_w[r]);
+    for (int r = 0; r < K; ++r) {
+      float val;
+      const int id = argmax_round<EPL>(key, g, open, val);
+      if (lane == r) { my_id = id; my_val = val; }
+    }
+    float den = -0.0f;  // Iterator::sum in ranking order, plus the 1e-20 epsilon
+    for (int r = 0; r < K; ++r) den = __fadd_rn(den, rdl(my_val, r));
     den = __fadd_rn(den, 1e-20f);
     if (rp.normalize && !finite(den)) bad = true;
-    for (int r = 0; r < K; ++r) {
-      float w = rp.normalize ? out_w[r] / den : out_w[r];
-      out_w[r] = __fmul_rn(w, rp.scale);
-    }
+    w = __fmul_rn(rp.normalize ? my_val / den : my_val, rp.scale);
   }
   if (bad) flag(status, kStatusNonFinite);
-  if (lane == 0) {
-    for (int r = 0; r < K; ++r) {
-      ids[(size_t)t * K + r] = out_ids[r];
-      weights[(size_t)t * K + r] = out_w[r];
-    }
+  if (lane < K) {
+    ids[(size_t)t * K + lane] = my_id;
+    weights[(size_t)t * K + lane] = w;
     if (asc) {
-      // ranking positions ordered by ascending expert id (qwen3_6/runtime.rs:1239-1240)
-      int order[kMaxTopK];
-      for (int r = 0; r < K; ++r) order[r] = r;
-      for (int a = 1; a < K; ++a) {
-        int cur = order[a], b = a - 1;
-        while (b >= 0 && out_ids[order[b]] > out_ids[cur]) { order[b + 1] = order[b]; --b; }
-        order[b + 1] = cur;
-      }
-      for (int r = 0; r < K; ++r) asc[(size_t)t * K + r] = order[r];
+      // ranking position `lane` goes to its place in ascending expert id order
+      // (qwen3_6/runtime.rs:1239-1240; the ids of one token are distinct)
+      int before = 0;
+      for (int r = 0; r < K; ++r) before += __builtin_amdgcn_readlane(my_id, r) < my_id;
+      asc[(size_t)t * K + before] = lane;
     }
   }
 }
@@ -381,23 +412,29 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
                                                        int32_t* active, int32_t* offsets,
                                                        int32_t* counts, int32_t* perm_token,
                                                        int32_t* pos_of_slot, int32_t* tiles) {
-  extern __shared__ uint32_t bm[];  // [E][W]
+  // LDS: bm[E][W] token bitmaps (64 tokens per word), then pre[E][W] = tokens routed to the
+  // expert in the words before (u16), so a token's rank inside its expert is O(1).
+  extern __shared__ uint64_t bm[];
   __shared__ int32_t off_s[kMaxExperts + 1];
   __shared__ int32_t wsum[17];
-  const int W = (T + 31) / 32;
+  const int W = (T + 63) / 64;
+  uint16_t* pre = reinterpret_cast<uint16_t*>(bm + (size_t)E * W);
   const int n = T * K;
-  for (int i = threadIdx.x; i < E * W; i += blockDim.x) bm[i] = 0u;
+  for (int i = threadIdx.x; i < E * W; i += blockDim.x) bm[i] = 0ull;
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    int e = ids[i], t = i / K;
-    atomicOr(&bm[e * W + (t >> 5)], 1u << (t & 31));
+    const int e = ids[i], t = i / K;
+    atomicOr(reinterpret_cast<unsigned long long*>(&bm[e * W + (t >> 6)]), 1ull << (t & 63));
   }
   __syncthreads();
   // one expert per thread (E <= 512 < 1024): counts, offsets, active list, GEMM row tiles
   const int e = threadIdx.x;
   int c = 0;
   if (e < E)
-    for (int w = 0; w < W; ++w) c += __popc(bm[e * W + w]);
+    for (int w = 0; w < W; ++w) {
+      pre[e * W + w] = (uint16_t)c;
+      c += __popcll(bm[e * W + w]);
+    }
   int total = 0, n_active = 0, n_tiles = 0;
   const int off = block_excl_scan(c, wsum, &total);
   const int slot = block_excl_scan(c > 0 ? 1 : 0, wsum, &n_active);
@@ -420,11 +457,9 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
   }
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    int e = ids[i], t = i / K;
-    const uint32_t* row = bm + e * W;
-    int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
-    for (int w = 0; w < (t >> 5); ++w) rank += __popc(row[w]);
-    int p = off_s[e] + rank;
+    const int ex = ids[i], t = i / K, w = t >> 6;
+    const uint64_t below = bm[ex * W + w] & ((1ull << (t & 63)) - 1ull);
+    const int p = off_s[ex] + pre[ex * W + w] + __popcll(below);
     pos_of_slot[i] = p;
     perm_token[p] = t;
   }
@@ -439,10 +474,18 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int* status, hipStream_t s) {
+  // Each thread runs one 8-lane chain per token; up to 512 tokens, one token per workgroup
+  // gives the most independent waves, beyond that four tokens share each weight chain load.
   const int H8 = H / 8, tail = H - 8 * H8;
-  size_t lds = (size_t)kLane8Tokens * (8 * (H8 + 1) + tail) * sizeof(float);
-  dim3 grid((E + 7) / 8, (T + kLane8Tokens - 1) / kLane8Tokens);
-  router_lane8_kernel<<<grid, 64, lds, s>>>(w8, E, H, x, T, logits, status);
+  if (T <= 512) {
+    size_t lds = (size_t)(8 * (H8 + 1) + tail) * sizeof(float);
+    dim3 grid((E + 7) / 8, T);
+    router_lane8_kernel<1><<<grid, 64, lds, s>>>(w8, E, H, x, T, logits, status);
+  } else {
+    size_t lds = (size_t)4 * (8 * (H8 + 1) + tail) * sizeof(float);
+    dim3 grid((E + 7) / 8, (T + 3) / 4);
+    router_lane8_kernel<4><<<grid, 64, lds, s>>>(w8, E, H, x, T, logits, status);
+  }
 }
 
 void launch_router_f64(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
@@ -451,15 +494,31 @@ void launch_router_f64(const uint16_t* w, int E, int H, const float* x, int T, f
   router_f64_kernel<<<grid, 256, 0, s>>>(w, E, H, x, T, logits, status);
 }
 
+template <int EPL>
+static void launch_route_epl(const float* logits, int T, int E, int K, const RouteParams& p,
+                             int32_t* ids, float* weights, int32_t* asc, int* status,
+                             hipStream_t s) {
+  if (p.router == 0)
+    route_kernel<EPL, true><<<(T + 3) / 4, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc,
+                                                        status);
+  else
+    route_kernel<EPL, false><<<(T + 3) / 4, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc,
+                                                         status);
+}
+
 void launch_route(const float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
                   float* weights, int32_t* asc, int* status, hipStream_t s) {
-  route_kernel<<<(T + 3) / 4, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc, status);
+  const int epl = (E + 63) / 64;
+  if (epl <= 1) launch_route_epl<1>(logits, T, E, K, p, ids, weights, asc, status, s);
+  else if (epl <= 2) launch_route_epl<2>(logits, T, E, K, p, ids, weights, asc, status, s);
+  else if (epl <= 4) launch_route_epl<4>(logits, T, E, K, p, ids, weights, asc, status, s);
+  else launch_route_epl<8>(logits, T, E, K, p, ids, weights, asc, status, s);
 }
 
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
                     int32_t* tiles, hipStream_t s) {
-  size_t lds = (size_t)E * ((T + 31) / 32) * sizeof(uint32_t);
+  size_t lds = (size_t)E * ((T + 63) / 64) * (sizeof(uint64_t) + sizeof(uint16_t));
   permute_kernel<<<1, 1024, lds, s>>>(ids, T, E, K, meta, active, offsets, counts, perm_token,
                                       pos_of_slot, tiles);
 }
