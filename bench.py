@@ -46,6 +46,9 @@ def parse():
                     help="CPU-baseline budget per run (headline run gets 2.5x)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run a device-to-device copy of this many MiB (a known-size "
+                         "kernel for calibrating HBM byte counters)")
     return ap.parse_args()
 
 
@@ -210,6 +213,15 @@ def main():
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {args.copy_probe_mib} MiB device-to-device")
+        del src, dst
     runs = RUNS if args.configs == "all" else [
         (c.split(":")[0], int(c.split(":")[1])) for c in args.configs.split(",")]
     results = []
