@@ -45,11 +45,16 @@ typedef enum { URB_ROUTER_SOFTMAX_TOPK = 0, URB_ROUTER_SIGMOID_NOAUX_TC = 1 } ur
  *          GatedMlp experts, f64 combine in ranking order on top of the shared expert. */
 typedef enum { URB_COMPOSE_QWEN36 = 0, URB_COMPOSE_GLM = 1 } urb_composition;
 
-/* Where urb_moe_create reads the weights from. */
+/* Where urb_moe_create reads the weights from.  The context streams expert and shared-expert
+ * matrices in the panel layout (see urb_pack_matrix); HOST and DEVICE_COPY sources are in the
+ * row-major checkpoint layout below and are converted while they are copied into the context's
+ * HBM arena.  DEVICE_BORROW matrices must already be in the panel layout; they are used in
+ * place and must outlive the context.  The router weight and bias are always row-major and
+ * always copied. */
 typedef enum {
-  URB_SOURCE_HOST = 0,          /* host memory: copied verbatim into HBM                    */
-  URB_SOURCE_DEVICE_COPY = 1,   /* device memory: copied into the context's own HBM arena  */
-  URB_SOURCE_DEVICE_BORROW = 2  /* device memory: used in place; must outlive the context   */
+  URB_SOURCE_HOST = 0,
+  URB_SOURCE_DEVICE_COPY = 1,
+  URB_SOURCE_DEVICE_BORROW = 2
 } urb_weight_source;
 
 /* One matrix in its on-disk layout (row-major [rows, cols]):
@@ -62,7 +67,9 @@ typedef struct {
   const uint8_t *scales;
 } urb_matrix;
 
-/* Layer geometry: MoeGeometry (src/models/glm/moe_geometry.rs:3-9) plus projection formats. */
+/* Layer geometry: MoeGeometry (src/models/glm/moe_geometry.rs:3-9) plus projection formats.
+ * hidden, intermediate and shared_intermediate must be multiples of 128 and at most 12288
+ * (URB_ERR_SHAPE otherwise); top_k <= 32, n_experts <= 512. */
 typedef struct {
   uint32_t hidden;               /* H */
   uint32_t n_experts;            /* E */
@@ -88,7 +95,7 @@ typedef struct {
 
 typedef struct urb_moe_ctx urb_moe_ctx;
 
-/* Builds a layer: shape/geometry checks, verbatim upload, one validation pass over every payload
+/* Builds a layer: shape/geometry checks, upload (panel layout), one validation pass over every payload
  * (E8M0 0xFF -> URB_ERR_INVALID_SCALE; E4M3 0x7F/0xFF or non-finite BF16 -> URB_ERR_NONFINITE).
  * Replaces RuntimeMoeLayer::new (src/models/glm/runtime/moe.rs:78-125) together with the
  * payload checks of MxFp4Matrix::from_packed (src/math/mxfp.rs:1371-1443), MxFp8Matrix::
@@ -124,6 +131,19 @@ urb_status urb_moe_sync(urb_moe_ctx *ctx, void *stream);
 urb_status urb_dequant_rows(urb_format format, const void *data, const uint8_t *scales,
                             uint32_t rows, uint32_t cols, uint32_t row0, uint32_t count,
                             float *out, void *stream);
+
+/* Converts one row-major matrix (device, the urb_matrix layout) into the panel layout the
+ * context streams (device; same byte counts: packed_data as large as data, packed_scales as
+ * large as scales).  rows % 16 == 0 and cols % 128 == 0, else URB_ERR_SHAPE.  A panel is 16
+ * consecutive rows; its bytes are reordered so that 1 KiB slab t holds, in 16-byte unit
+ * l = ln + 16 lq, row ln's columns 32t+8lq..+8 (BF16), MX block 4t+lq (MXFP4), or half t%2 of
+ * MX block 4(t/2)+lq (MXFP8); scales per panel are 64-byte slabs, byte l of slab s being row
+ * ln's scale of block 4s+lq.  No reference counterpart: the reference keeps the checkpoint
+ * layout (MxFp4Matrix::from_packed, src/math/mxfp.rs:1362-1443); this is the HBM layout for
+ * callers that borrow pre-converted weights. */
+urb_status urb_pack_matrix(urb_format format, const void *data, const uint8_t *scales,
+                           uint32_t rows, uint32_t cols, void *packed_data,
+                           uint8_t *packed_scales, void *stream);
 
 /* Device-time spans per stage of a layer call: the counterpart of the reference's profiling
  * spans (ProfileStage, src/profiling.rs:75-136; span_with_work, src/profiling.rs:581-600).

@@ -156,7 +156,7 @@ def test_scaled_bf16_conversion_matches_dequantised_weights(fmt):
 SMALL = [(name, T) for name in C.WORKLOADS for T in (1, 3, 40)]
 
 
-def _small_layer(name, hidden=256, n_experts=16, intermediate=64):
+def _small_layer(name, hidden=256, n_experts=16, intermediate=128):
     w = C.WORKLOADS[name]
     spec = C.small_spec(w.spec, hidden=hidden, n_experts=n_experts, intermediate=intermediate)
     bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.05) if w.zipf_s else None
@@ -201,7 +201,7 @@ def test_router_logits_match_oracle(name):
 
 
 def test_forward_is_deterministic_and_chunked_calls_equal_tokenwise():
-    host = _small_layer("c5_mxfp4_zipf_prefill", hidden=128, n_experts=16, intermediate=64)
+    host = _small_layer("c5_mxfp4_zipf_prefill", hidden=128, n_experts=16, intermediate=128)
     T = 1100  # > one 1024-token internal chunk
     x = torch.from_numpy(synth.activations("x.chunk", T, 128)).cuda()
     layer = moe_mod().MoeLayer(host, max_tokens=T)
@@ -215,6 +215,66 @@ def test_forward_is_deterministic_and_chunked_calls_equal_tokenwise():
         assert rel_l2(ys.cpu().numpy(), y1[t:t + 1].cpu().numpy()) < 1e-5
     layer.close()
     single.close()
+
+
+# ------------------------------------------------------------------------------- panel layout
+def _panel_pack_np(fmt, data, scales):
+    """Restates the panel layout on the host: slab t of a 16-row panel, 16-byte unit
+    l = ln + 16 lq <- row ln's bytes at 64 t + 16 lq (BF16, MXFP4) or
+    128 (t // 2) + 32 lq + 16 (t % 2) (MXFP8); scale slab s, byte l <- row ln, block 4 s + lq."""
+    raw = np.ascontiguousarray(data).view(np.uint8)
+    rows = raw.shape[0]
+    rb = raw.size // rows
+    units = raw.reshape(rows // 16, 16, rb // 16, 16)          # [panel, row, unit, byte]
+    out = np.empty((rows // 16, rb // 64, 64, 16), np.uint8)  # [panel, slab, lane, byte]
+    for t in range(rb // 64):
+        for lq in range(4):
+            off = (t // 2) * 128 + 32 * lq + 16 * (t % 2) if fmt == C.FMT_MXFP8 else 64 * t + 16 * lq
+            out[:, t, 16 * lq:16 * lq + 16, :] = units[:, :, off // 16, :]
+    packed_scales = None
+    if scales is not None:
+        sc = np.ascontiguousarray(scales).reshape(rows // 16, 16, -1)  # [panel, row, block]
+        nb = sc.shape[2]
+        ps = np.empty((rows // 16, nb // 4, 64), np.uint8)
+        for lq in range(4):
+            ps[:, :, 16 * lq:16 * lq + 16] = sc[:, :, lq::4].transpose(0, 2, 1)
+        packed_scales = ps.ravel()
+    return out.ravel(), packed_scales
+
+
+@pytest.mark.parametrize("fmt", [C.FMT_BF16, C.FMT_MXFP4, C.FMT_MXFP8])
+def test_pack_matrix_matches_host_restatement(fmt):
+    spec = C.small_spec(C.WORKLOADS["c4_mxfp8"].spec, hidden=256, n_experts=2, intermediate=384)
+    from dataclasses import replace
+    spec = replace(spec, expert_format=fmt)
+    host = C.make_host_layer(spec)
+    for m, (rows, cols) in enumerate(((384, 256), (384, 256), (256, 384))):
+        d, s = host.experts[1][m]
+        dd = torch.from_numpy(np.ascontiguousarray(d).view(np.uint8).copy()).cuda()
+        ss = None if s is None else torch.from_numpy(np.ascontiguousarray(s).copy()).cuda()
+        pd, ps = moe_mod().pack_matrix(fmt, dd, ss, rows, cols)
+        torch.cuda.synchronize()
+        want_d, want_s = _panel_pack_np(fmt, d, s)
+        assert np.array_equal(pd.cpu().numpy().view(np.uint8).ravel(), want_d)
+        if s is not None:
+            assert np.array_equal(ps.cpu().numpy().ravel(), want_s)
+
+
+def test_borrowed_panel_layer_equals_copied_layer():
+    for name in ("c2_bf16_prefill", "c3_mxfp4_decode", "c4_mxfp8"):
+        host = _small_layer(name)
+        dev = moe_mod().DeviceLayer.from_host(host)
+        x = torch.from_numpy(synth.activations("x.borrow", 5, host.spec.hidden)).cuda()
+        copied = moe_mod().MoeLayer(dev, max_tokens=5)
+        borrowed = moe_mod().MoeLayer(moe_mod().packed_layer(dev), max_tokens=5,
+                                      source=N.SOURCE_DEVICE_BORROW)
+        for T in (1, 5):
+            y1, i1, w1 = copied.forward(x[:T].contiguous())
+            y2, i2, w2 = borrowed.forward(x[:T].contiguous())
+            assert torch.equal(y1, y2) and torch.equal(i1, i2) and torch.equal(w1, w2)
+        assert borrowed.memory()[0] == 0
+        copied.close()
+        borrowed.close()
 
 
 # ------------------------------------------------------------------------------- errors
@@ -263,6 +323,12 @@ def test_shape_and_geometry_errors():
     with pytest.raises(N.UrbError) as e:
         moe_mod().MoeLayer(h2, max_tokens=1)
     assert e.value.status == N.ERR_INVALID_GEOMETRY
+    for dims in ({"hidden": 192}, {"intermediate": 96}, {"hidden": 12288 + 128}):
+        bad = dataclasses.replace(host.spec, **dims)
+        h3 = C.HostLayer(bad, host.router_weight, host.experts, host.shared)
+        with pytest.raises(N.UrbError) as e:
+            moe_mod().MoeLayer(h3, max_tokens=1)
+        assert e.value.status == N.ERR_SHAPE
     layer = moe_mod().MoeLayer(host, max_tokens=2)
     x = torch.zeros((3, host.spec.hidden), device="cuda")
     with pytest.raises(N.UrbError) as e:

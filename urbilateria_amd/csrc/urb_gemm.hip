@@ -1,30 +1,30 @@
 // urb_gemm.hip -- grouped expert GEMMs on CDNA4 MFMA (prefill and batched decode).
 //
 // For each tile of up to kGemmMTile tokens routed to one expert (the permutation's row tiles)
-// and each kGemmNTile-row slice of that expert's weight matrix, a 256-thread workgroup
+// and each group of four 16-row weight panels of that expert's matrix, a 256-thread workgroup
 // computes C[tokens, rows] = A[tokens, K] . W[rows, K]^T with v_mfma_f32_16x16x32_bf16:
 //
-//  * B (weights) streams from HBM straight into registers in the on-disk layout: W is row-major
-//    with K contiguous, which is the MFMA B-fragment order.  Lane l of a wave owns weight row
-//    l % 16 and 32 consecutive k (one MX block: 16 B of E2M1, 32 B of E4M3 or 64 B of BF16),
-//    decodes it in registers with the scaled CDNA4 conversions (v_cvt_scalef32_pk_bf16_fp4/fp8,
-//    exact: E2M1 or E4M3 times 2^k is a BF16 value) and feeds four MFMAs, the j-th taking
-//    k = 32 q + 8 j + [0, 8) of lane group q = l / 16.
+//  * B (weights) streams from HBM straight into registers in the panel layout
+//    (urb_kernels.hpp): wave w sweeps panel 4 x + w front to back, one 1 KiB slab per load
+//    instruction, DEPTH K steps ahead of the MFMAs.  Lane l = ln + 16 lq holds row ln; for
+//    BF16 its 16 B are MFMA j's operand directly (k = 32 j + 8 lq), for the MX formats they
+//    are one whole 32-column block (k = 32 lq + [0, 32)), decoded in registers with the scaled
+//    CDNA4 conversions (v_cvt_scalef32_pk_bf16_fp4/fp8, exact: E2M1 or E4M3 times 2^k is a
+//    BF16 value) into the operands of four MFMAs (MFMA j takes k = 32 lq + 8 j + [0, 8)).
 //  * A (activations, f32) is gathered through the permutation, split into hi + lo BF16 halves
 //    (hi = bf16(a), lo = bf16(a - hi): the product keeps 16 significant bits of a) and staged
-//    in LDS in the same permuted k order; the lo MFMAs are skipped for a K step whose lo half
-//    is all zero (BF16-valued activations).
+//    in LDS one K step ahead; the lo MFMAs are skipped for a K step whose lo half is all zero
+//    (BF16-valued activations), and the second 16-token MFMA block for tiles of <= 16 tokens.
 //  * Accumulation is f32 in the MFMA; the epilogue is the same as the decode kernels'.
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
+#include "urb_panel.hpp"
 
 namespace urb {
 
-enum { kFmtBF16 = 0, kFmtMXFP4 = 1, kFmtMXFP8 = 2 };
-
 constexpr int kMT = kGemmMTile;   // 32 tokens: two 16-row MFMA blocks
-constexpr int kNT = kGemmNTile;   // 64 weight rows: 16 per wave
-constexpr int kKS = kGemmKStep;   // 128 k per step: four 32-k MX blocks
+constexpr int kNT = kGemmNTile;   // 64 weight rows: one 16-row panel per wave
+constexpr int kKS = kGemmKStep;   // 128 k per step
 constexpr int kALd = kKS + 8;     // LDS row pitch in bf16 (16 B pad against bank conflicts)
 
 typedef unsigned short u16;
@@ -34,31 +34,10 @@ __device__ __forceinline__ u16 bf16_rne_bits(float v) {
   return (u16)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
 }
 
-// Raw B fragment of one lane for one K step: the lane's 32 consecutive k of its row.
+// k offset (within the K step) of MFMA j's operands for lane group lq.
 template <int FMT>
-struct BRaw;
-template <>
-struct BRaw<kFmtBF16> { uint4 q[4]; };
-template <>
-struct BRaw<kFmtMXFP4> { uint4 q; uint32_t s; };
-template <>
-struct BRaw<kFmtMXFP8> { uint4 q[2]; uint32_t s; };
-
-template <int FMT>
-__device__ __forceinline__ void load_b(BRaw<FMT>& r, const uint8_t* __restrict__ row,
-                                       const uint8_t* __restrict__ srow, int kblk) {
-  // kblk: index of the lane's 32-column block along K
-  if constexpr (FMT == kFmtBF16) {
-    const uint4* p = reinterpret_cast<const uint4*>(row + (size_t)kblk * 64);
-    r.q[0] = p[0]; r.q[1] = p[1]; r.q[2] = p[2]; r.q[3] = p[3];
-  } else if constexpr (FMT == kFmtMXFP4) {
-    r.q = *reinterpret_cast<const uint4*>(row + (size_t)kblk * 16);
-    r.s = srow[kblk];
-  } else {
-    const uint4* p = reinterpret_cast<const uint4*>(row + (size_t)kblk * 32);
-    r.q[0] = p[0]; r.q[1] = p[1];
-    r.s = srow[kblk];
-  }
+__device__ __forceinline__ int frag_k(int j, int lq) {
+  return FMT == kFmtBF16 ? 32 * j + 8 * lq : 32 * lq + 8 * j;
 }
 
 // Decoded B fragment: four bf16x8 MFMA operands (j = 0..3).
@@ -96,11 +75,6 @@ __device__ __forceinline__ void decode_b(const BRaw<FMT>& r, BFrag& f) {
                      __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], sc, false),
                      __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], sc, true));
   }
-}
-
-template <int FMT>
-__device__ __forceinline__ size_t gemm_row_bytes(int K) {
-  return FMT == kFmtBF16 ? (size_t)K * 2 : (FMT == kFmtMXFP4 ? (size_t)K / 2 : (size_t)K);
 }
 
 // A staging: thread t covers row t/8 and 16 consecutive k at 16*(t%8) of the K step.
@@ -143,7 +117,10 @@ __device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + m * kALd + k));
 }
 
-template <int FMT, bool PAIR>
+template <int N>
+using Int = std::integral_constant<int, N>;
+
+template <int FMT, bool PAIR, int DEPTH>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
                                                       Perm perm, int rows, int K,
                                                       const float* __restrict__ in,
@@ -172,15 +149,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   const ExpertMats m = mats[expert];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lq = lane >> 4;
-  const int n0 = blockIdx.x * kNT + wave * 16;
-  const int row = n0 + ln;
-  const size_t rb = gemm_row_bytes<FMT>(K);
-  const int sb = K / 32;
+  const int panel = blockIdx.x * 4 + wave;
+  const int row = panel * kPanelRows + ln;
+  const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(K);
+  const size_t pscales = (size_t)kPanelRows * (K / 32);
 
-  const uint8_t* b_row0 = m.data[PAIR ? 0 : 2] + (size_t)row * rb;
-  const uint8_t* b_s0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + (size_t)row * sb;
-  const uint8_t* b_row1 = PAIR ? m.data[1] + (size_t)row * rb : nullptr;
-  const uint8_t* b_s1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + (size_t)row * sb : nullptr;
+  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + panel * pbytes + 16 * lane;
+  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + panel * pscales + lane;
+  const uint8_t* pd1 = PAIR ? m.data[1] + panel * pbytes + 16 * lane : nullptr;
+  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + panel * pscales + lane : nullptr;
 
   // ---- A source row of this thread's staging slot
   const int am = threadIdx.x >> 3;
@@ -200,45 +177,58 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   }
 
   const int steps = K / kKS;
-  BRaw<FMT> r0, r1;
-  AStage as;
-  load_b<FMT>(r0, b_row0, b_s0, lq);
-  if constexpr (PAIR) load_b<FMT>(r1, b_row1, b_s1, lq);
-  load_a(as, a_src, a_valid, 0);
-  bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
-
-  for (int s = 0; s < steps; ++s) {
-    const int buf = s & 1;
-    const bool more = s + 1 < steps;
-    BFrag f0, f1;
-    decode_b<FMT>(r0, f0);
-    if constexpr (PAIR) decode_b<FMT>(r1, f1);
-    if (more) {  // prefetch the next K step: weights to registers, activations to registers
-      const int kb = (s + 1) * (kKS / 32) + lq;
-      load_b<FMT>(r0, b_row0, b_s0, kb);
-      if constexpr (PAIR) load_b<FMT>(r1, b_row1, b_s1, kb);
-      load_a(as, a_src, a_valid, (s + 1) * kKS);
-    }
-    const u16* hi = a_hi[buf];
-    const u16* lo = a_lo[buf];
+  auto body = [&](auto nmb) {
+    constexpr int NMB = decltype(nmb)::value;  // 16-token MFMA blocks this tile needs
+    BRaw<FMT> r0[DEPTH], r1[DEPTH];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int d = 0; d < DEPTH; ++d)
+      if (d < steps) {
+        load_b<FMT>(r0[d], pd0, ps0, d);
+        if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, d);
+      }
+    AStage as;
+    load_a(as, a_src, a_valid, 0);
+    bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
+    for (int s0 = 0; s0 < steps; s0 += DEPTH) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const bf16x8 ah = lds_frag(hi, mb * 16 + ln, 32 * lq + 8 * j);
-        acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0.v[j], acc0[mb], 0, 0, 0);
-        if constexpr (PAIR)
-          acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1.v[j], acc1[mb], 0, 0, 0);
-        if (lo_any) {
-          const bf16x8 al = lds_frag(lo, mb * 16 + ln, 32 * lq + 8 * j);
-          acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0.v[j], acc0[mb], 0, 0, 0);
-          if constexpr (PAIR)
-            acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1.v[j], acc1[mb], 0, 0, 0);
+      for (int d = 0; d < DEPTH; ++d) {
+        const int s = s0 + d;
+        if (s >= steps) break;
+        const int buf = s & 1;
+        const bool more = s + 1 < steps;
+        if (more) load_a(as, a_src, a_valid, (s + 1) * kKS);
+        BFrag f0, f1;
+        decode_b<FMT>(r0[d], f0);
+        if constexpr (PAIR) decode_b<FMT>(r1[d], f1);
+        if (s + DEPTH < steps) {  // refill this ring slot DEPTH steps ahead
+          load_b<FMT>(r0[d], pd0, ps0, s + DEPTH);
+          if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, s + DEPTH);
         }
+        const u16* hi = a_hi[buf];
+        const u16* lo = a_lo[buf];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int kf = frag_k<FMT>(j, lq);
+#pragma unroll
+          for (int mb = 0; mb < NMB; ++mb) {
+            const bf16x8 ah = lds_frag(hi, mb * 16 + ln, kf);
+            acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0.v[j], acc0[mb], 0, 0, 0);
+            if constexpr (PAIR)
+              acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1.v[j], acc1[mb], 0, 0, 0);
+            if (lo_any) {
+              const bf16x8 al = lds_frag(lo, mb * 16 + ln, kf);
+              acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0.v[j], acc0[mb], 0, 0, 0);
+              if constexpr (PAIR)
+                acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1.v[j], acc1[mb], 0, 0, 0);
+            }
+          }
+        }
+        if (more) lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
       }
     }
-    if (more) lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
-  }
+  };
+  if (mrows > 16) body(Int<2>{});
+  else body(Int<1>{});
 
   // ---- epilogue: lane holds column `row`, rows 4*lq + i of each 16-row block
   bool bad = false;
@@ -285,6 +275,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
 // accumulator, so the f32 logit is the correctly rounded sum up to a few units in the last
 // place.  Tiles: 32 tokens x 64 experts (experts past E are clamped and not stored).
 // ------------------------------------------------------------------------------------------
+// Router weights stay row-major [E, H]: lane (ln, lq) reads its row's 32-column block kblk.
+__device__ __forceinline__ void load_row_block(uint4 (&q)[4], const uint8_t* __restrict__ row,
+                                               int kblk) {
+  const uint4* p = reinterpret_cast<const uint4*>(row + (size_t)kblk * 64);
+  q[0] = p[0]; q[1] = p[1]; q[2] = p[2]; q[3] = p[3];
+}
+
 __global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __restrict__ w,
                                                              int E, int H,
                                                              const float* __restrict__ x, int T,
@@ -309,9 +306,9 @@ __global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __r
     for (int i = 0; i < 4; ++i) acc[mb][i] = 0.0;
 
   const int steps = H / kKS;
-  BRaw<kFmtBF16> r;
+  uint4 r[4];
   AStage as;
-  load_b<kFmtBF16>(r, b_row, nullptr, lq);
+  load_row_block(r, b_row, lq);
   load_a(as, a_src, a_valid, 0);
   bool bad = false;
   {
@@ -325,9 +322,10 @@ __global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __r
     const int buf = s & 1;
     const bool more = s + 1 < steps;
     BFrag f;
-    decode_b<kFmtBF16>(r, f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.v[j] = __builtin_bit_cast(bf16x8, r[j]);
     if (more) {
-      load_b<kFmtBF16>(r, b_row, nullptr, (s + 1) * (kKS / 32) + lq);
+      load_row_block(r, b_row, (s + 1) * (kKS / 32) + lq);
       load_a(as, a_src, a_valid, (s + 1) * kKS);
     }
 #pragma unroll
@@ -367,11 +365,18 @@ void launch_router_gemm(const uint16_t* w, int E, int H, const float* x, int T, 
   router_gemm_kernel<<<grid, 256, 0, s>>>(w, E, H, x, T, logits, status);
 }
 
+// Weight steps in flight per wave: enough 1 KiB slabs to cover HBM latency.
+template <int FMT, bool PAIR>
+constexpr int gemm_depth() {
+  return FMT == kFmtBF16 ? (PAIR ? 2 : 1) : (FMT == kFmtMXFP4 ? 4 : 2);
+}
+
 template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                    const float* in, float* out, int qwen, int* status, hipStream_t s) {
   dim3 grid(rows / kNT, max_tiles);
-  gemm_kernel<FMT, PAIR><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, qwen, status);
+  gemm_kernel<FMT, PAIR, gemm_depth<FMT, PAIR>()><<<grid, 256, 0, s>>>(mats, perm, rows, K, in,
+                                                                        out, qwen, status);
 }
 
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,

@@ -1,116 +1,67 @@
 // urb_gemv.hip -- decode-path expert projections, combines, validation and dequantisation.
 //
-// Decode projections are matrix-vector products over the rows of each active expert.  A
-// wavefront splits into 64/LPR row groups of LPR lanes; each lane walks the row in "chunks"
-// (BF16: 8 columns = 16 B; MXFP4: 32 columns = 16 B of nibbles + one E8M0 byte; MXFP8: 32
-// columns = 32 B + one E8M0 byte) with 128-bit loads, decodes in registers (CDNA4
-// v_cvt_scalef32_pk_f32_fp4/fp8), and FMA-accumulates against the input vector staged in LDS.
-// MX chunks accumulate sum(code * x) in f32 and apply the power-of-two scale once per chunk,
-// which is exact multiplication by 2^k of the chunk partial.
+// Decode projections (one token per active expert) stream the panel layout
+// (urb_kernels.hpp).  A 256-thread workgroup is 4 / KSPLIT panels x KSPLIT parts of K; each
+// wave sweeps its part of one panel front to back, DEPTH K steps of 1 KiB slabs in flight.
+// Lane l = ln + 16 lq accumulates panel row ln over the columns its 16-byte units hold
+// (BF16: 8 columns per unit; MX: one whole 32-column block, decoded with the CDNA4
+// v_cvt_scalef32_pk_f32_fp4/fp8 conversions and scaled once per block, which is exact
+// multiplication by 2^k of the block partial), against the input vector staged in LDS.  The
+// four lq lanes are summed by shuffles and the K parts through LDS, in a fixed order.
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
+#include "urb_panel.hpp"
 
 #include <algorithm>
 
 namespace urb {
 
-enum { kFmtBF16 = 0, kFmtMXFP4 = 1, kFmtMXFP8 = 2 };
+// Staged input vectors carry 4 floats of padding after every 32, so the four lane groups'
+// 32-column blocks (128 B apart) start in different LDS banks.
+__device__ __forceinline__ int xs_index(int k) { return k + 4 * (k >> 5); }
+__host__ __device__ constexpr size_t xs_floats(int K) { return (size_t)K + (size_t)K / 8; }
 
+// acc += lane's units of one K step . x.  BF16 unit j covers k = 128 s + 32 j + 8 lq + [0, 8);
+// an MX unit covers k = 128 s + 32 lq + [0, 32).
 template <int FMT>
-struct Fmt;
-template <>
-struct Fmt<kFmtBF16> {
-  static constexpr int kCols = 8;  // columns per chunk
-  __device__ static size_t row_bytes(int cols) { return (size_t)cols * 2; }
-};
-template <>
-struct Fmt<kFmtMXFP4> {
-  static constexpr int kCols = 32;
-  __device__ static size_t row_bytes(int cols) { return (size_t)cols / 2; }
-};
-template <>
-struct Fmt<kFmtMXFP8> {
-  static constexpr int kCols = 32;
-  __device__ static size_t row_bytes(int cols) { return (size_t)cols; }
-};
-
-// One lane's chunk of a weight row, loaded ahead of its use.
-template <int FMT>
-struct Chunk;
-template <>
-struct Chunk<kFmtBF16> { uint4 q; };
-template <>
-struct Chunk<kFmtMXFP4> { uint4 q; uint32_t s; };
-template <>
-struct Chunk<kFmtMXFP8> { uint4 q0, q1; uint32_t s; };
-// Chunks a lane loads before computing on them (a batch of independent 128-bit loads).
-template <int FMT>
-constexpr int kBatch = FMT == kFmtBF16 ? 8 : 4;
-
-template <int FMT>
-__device__ __forceinline__ void chunk_load(Chunk<FMT>& c, const uint8_t* __restrict__ row,
-                                           const uint8_t* __restrict__ srow, int g) {
+__device__ __forceinline__ void raw_dot(const BRaw<FMT>& r, int step, int lq,
+                                        const float* __restrict__ xs, float& acc) {
   if constexpr (FMT == kFmtBF16) {
-    c.q = *reinterpret_cast<const uint4*>(row + (size_t)g * 16);
-  } else if constexpr (FMT == kFmtMXFP4) {
-    c.q = *reinterpret_cast<const uint4*>(row + (size_t)g * 16);
-    c.s = srow[g];
-  } else {
-    const uint4* qp = reinterpret_cast<const uint4*>(row + (size_t)g * 32);
-    c.q0 = qp[0];
-    c.q1 = qp[1];
-    c.s = srow[g];
-  }
-}
-
-// acc += chunk . xs[g * kCols ...]
-template <int FMT>
-__device__ __forceinline__ void chunk_dot(const Chunk<FMT>& c, int g,
-                                          const float* __restrict__ xs, float& acc) {
-  if constexpr (FMT == kFmtBF16) {
-    const uint4 q = c.q;
-    const float4* xv = reinterpret_cast<const float4*>(xs + g * 8);
-    float4 a = xv[0], b = xv[1];
-    float p0 = bf16_lo(q.x) * a.x, p1 = bf16_hi(q.x) * a.y;
-    p0 = fmaf(bf16_lo(q.y), a.z, p0);
-    p1 = fmaf(bf16_hi(q.y), a.w, p1);
-    p0 = fmaf(bf16_lo(q.z), b.x, p0);
-    p1 = fmaf(bf16_hi(q.z), b.y, p1);
-    p0 = fmaf(bf16_lo(q.w), b.z, p0);
-    p1 = fmaf(bf16_hi(q.w), b.w, p1);
-    acc += p0 + p1;
-  } else if constexpr (FMT == kFmtMXFP4) {
-    const float scale = e8m0_to_f32(c.s);
-    const float4* xv = reinterpret_cast<const float4*>(xs + g * 32);
-    const uint32_t words[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
-    float part[4];
 #pragma unroll
-    for (int wd = 0; wd < 4; ++wd) {
-      float v[8];
-      decode_fp4x8(words[wd], v);
-      float4 a = xv[2 * wd], b = xv[2 * wd + 1];
-      float p = v[0] * a.x;
-      p = fmaf(v[1], a.y, p);
-      p = fmaf(v[2], a.z, p);
-      p = fmaf(v[3], a.w, p);
-      p = fmaf(v[4], b.x, p);
-      p = fmaf(v[5], b.y, p);
-      p = fmaf(v[6], b.z, p);
-      p = fmaf(v[7], b.w, p);
-      part[wd] = p;
+    for (int j = 0; j < 4; ++j) {
+      const uint4 q = r.q[j];
+      const float4* xv = reinterpret_cast<const float4*>(xs + xs_index(128 * step + 32 * j + 8 * lq));
+      const float4 a = xv[0], b = xv[1];
+      float p0 = bf16_lo(q.x) * a.x, p1 = bf16_hi(q.x) * a.y;
+      p0 = fmaf(bf16_lo(q.y), a.z, p0);
+      p1 = fmaf(bf16_hi(q.y), a.w, p1);
+      p0 = fmaf(bf16_lo(q.z), b.x, p0);
+      p1 = fmaf(bf16_hi(q.z), b.y, p1);
+      p0 = fmaf(bf16_lo(q.w), b.z, p0);
+      p1 = fmaf(bf16_hi(q.w), b.w, p1);
+      acc += p0 + p1;
     }
-    acc = fmaf((part[0] + part[1]) + (part[2] + part[3]), scale, acc);
   } else {
-    const float scale = e8m0_to_f32(c.s);
-    const float4* xv = reinterpret_cast<const float4*>(xs + g * 32);
-    const uint32_t words[8] = {c.q0.x, c.q0.y, c.q0.z, c.q0.w, c.q1.x, c.q1.y, c.q1.z, c.q1.w};
+    const float scale = e8m0_to_f32(r.s);
+    const float4* xv = reinterpret_cast<const float4*>(xs + xs_index(128 * step + 32 * lq));
+    uint32_t words[8];
+    if constexpr (FMT == kFmtMXFP4) {
+      words[0] = r.q.x; words[1] = r.q.y; words[2] = r.q.z; words[3] = r.q.w;
+    } else {
+      words[0] = r.q[0].x; words[1] = r.q[0].y; words[2] = r.q[0].z; words[3] = r.q[0].w;
+      words[4] = r.q[1].x; words[5] = r.q[1].y; words[6] = r.q[1].z; words[7] = r.q[1].w;
+    }
     float part[4];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
+    for (int h = 0; h < 4; ++h) {  // 8 columns each
       float v[8];
-      decode_fp8x4(words[2 * h], v);
-      decode_fp8x4(words[2 * h + 1], v + 4);
-      float4 a = xv[2 * h], b = xv[2 * h + 1];
+      if constexpr (FMT == kFmtMXFP4) {
+        decode_fp4x8(words[h], v);
+      } else {
+        decode_fp8x4(words[2 * h], v);
+        decode_fp8x4(words[2 * h + 1], v + 4);
+      }
+      const float4 a = xv[2 * h], b = xv[2 * h + 1];
       float p = v[0] * a.x;
       p = fmaf(v[1], a.y, p);
       p = fmaf(v[2], a.z, p);
@@ -125,7 +76,7 @@ __device__ __forceinline__ void chunk_dot(const Chunk<FMT>& c, int g,
   }
 }
 
-// Resolves (active slot, token ordinal) -> expert, permuted position and token.
+// Resolves an active slot -> expert and its first permuted position.
 __device__ __forceinline__ bool perm_expert(const Perm& perm, int a, int& expert, int& base,
                                             int& count) {
   if (perm.dense_tokens > 0) {
@@ -141,166 +92,149 @@ __device__ __forceinline__ bool perm_expert(const Perm& perm, int a, int& expert
   count = perm.counts[expert];
   return true;
 }
-__device__ __forceinline__ int perm_token(const Perm& perm, int p) {
-  return perm.dense_tokens > 0 ? p : perm.perm_token[p];
-}
 
-__device__ __forceinline__ void stage(const float* __restrict__ src, int n, float* xs) {
-  const float4* s4 = reinterpret_cast<const float4*>(src);
-  float4* d4 = reinterpret_cast<float4*>(xs);
-  for (int i = threadIdx.x; i < n / 4; i += blockDim.x) d4[i] = s4[i];
-}
-
-// PAIR = gate+up rows with the SwiGLU epilogue (rows I, cols H, input x[token]);
-// otherwise down rows (rows H, cols I, input act[position]).
-template <int FMT, int LPR, bool PAIR>
+// PAIR = gate+up rows with the SwiGLU epilogue (rows I, cols H, input x[token]); otherwise
+// down rows (rows H, cols I, input act[position]).  Every active expert has one token.
+template <int FMT, bool PAIR, int DEPTH>
 __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict__ mats,
-                                                   Perm perm, int rows, int cols,
-                                                   int rows_per_block,
+                                                   Perm perm, int rows, int cols, int ksplit,
                                                    const float* __restrict__ in,
                                                    float* __restrict__ out, int qwen,
                                                    int* status) {
-  extern __shared__ float xs[];
-  const int nrb = (rows + rows_per_block - 1) / rows_per_block;
-  const int a = blockIdx.x / nrb, rb = blockIdx.x - a * nrb;
+  extern __shared__ float xs[];  // xs_floats(cols) staged input + [4][16][2] part sums
   int expert, base, count;
-  if (!perm_expert(perm, a, expert, base, count)) return;
+  if (!perm_expert(perm, blockIdx.y, expert, base, count)) return;
   const ExpertMats m = mats[expert];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane / LPR, li = lane % LPR;
-  constexpr int kGroups = 64 / LPR;
-  const int G = cols / Fmt<FMT>::kCols;
-  const size_t rbytes = Fmt<FMT>::row_bytes(cols);
-  const int sbytes = cols / 32;
-  const int r_begin = rb * rows_per_block;
-  const int r_end = min(rows, r_begin + rows_per_block);
-  bool bad = false;
-  constexpr int NB = kBatch<FMT>;
-  const int r_first = r_begin + wave * kGroups + sub;
-  for (int q = 0; q < count; ++q) {
-    const int p = base + q;
-    const float* src = PAIR ? in + (size_t)perm_token(perm, p) * cols : in + (size_t)p * cols;
-    // The first batch of this lane's weights is requested before the input vector is staged,
-    // so the two memory latencies overlap.
-    Chunk<FMT> c0[NB], c1[NB];
-    bool have = r_first < r_end;
-    if (have) {
-      const uint8_t* row0 = m.data[PAIR ? 0 : 2] + (size_t)r_first * rbytes;
-      const uint8_t* s0 =
-          FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + (size_t)r_first * sbytes;
+  const int ln = lane & 15, lq = lane >> 4;
+  const int part = wave % ksplit;
+  const int panel = blockIdx.x * (4 / ksplit) + wave / ksplit;
+  const bool valid = panel < rows / kPanelRows;
+  const int steps = cols / kGemmKStep;
+  const int s_begin = steps * part / ksplit, s_end = steps * (part + 1) / ksplit;
+  const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(cols);
+  const size_t pscales = (size_t)kPanelRows * (cols / 32);
+  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + (size_t)panel * pbytes + 16 * lane;
+  const uint8_t* ps0 =
+      FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + (size_t)panel * pscales + lane;
+  const uint8_t* pd1 = PAIR ? m.data[1] + (size_t)panel * pbytes + 16 * lane : nullptr;
+  const uint8_t* ps1 =
+      (PAIR && FMT != kFmtBF16) ? m.scales[1] + (size_t)panel * pscales + lane : nullptr;
+
+  // The first DEPTH steps of weights are requested before the input vector is staged, so the
+  // two memory latencies overlap.
+  BRaw<FMT> r0[DEPTH], r1[DEPTH];
+  if (valid) {
 #pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const int g = li + u * LPR;
-        if (g < G) {
-          chunk_load<FMT>(c0[u], row0, s0, g);
-          if constexpr (PAIR)
-            chunk_load<FMT>(c1[u], m.data[1] + (size_t)r_first * rbytes,
-                            FMT == kFmtBF16 ? nullptr
-                                            : m.scales[1] + (size_t)r_first * sbytes,
-                            g);
-        }
+    for (int d = 0; d < DEPTH; ++d)
+      if (s_begin + d < s_end) {
+        load_b<FMT>(r0[d], pd0, ps0, s_begin + d);
+        if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, s_begin + d);
       }
-    }
-    __syncthreads();
-    stage(src, cols, xs);
-    __syncthreads();
-    for (int r = r_first; r < r_end; r += 4 * kGroups) {
-      float acc0 = 0.0f, acc1 = 0.0f;
-      const uint8_t* row0 = m.data[PAIR ? 0 : 2] + (size_t)r * rbytes;
-      const uint8_t* s0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + (size_t)r * sbytes;
-      const uint8_t* row1 = PAIR ? m.data[1] + (size_t)r * rbytes : nullptr;
-      const uint8_t* s1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + (size_t)r * sbytes : nullptr;
-      for (int g0 = li; g0 < G; g0 += NB * LPR) {
-        if (!have) {
+  }
+  const int p = base;  // the expert's one permuted position
+  const float* src = PAIR ? in + (size_t)(perm.dense_tokens > 0 ? p : perm.perm_token[p]) * cols
+                          : in + (size_t)p * cols;
+  {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    for (int i = threadIdx.x; i < cols / 4; i += blockDim.x)
+      *reinterpret_cast<float4*>(xs + xs_index(4 * i)) = s4[i];
+  }
+  __syncthreads();
+
+  float acc0 = 0.0f, acc1 = 0.0f;
+  if (valid) {
+    for (int s0 = s_begin; s0 < s_end; s0 += DEPTH) {
 #pragma unroll
-          for (int u = 0; u < NB; ++u) {
-            const int g = g0 + u * LPR;
-            if (g < G) {
-              chunk_load<FMT>(c0[u], row0, s0, g);
-              if constexpr (PAIR) chunk_load<FMT>(c1[u], row1, s1, g);
-            }
-          }
+      for (int d = 0; d < DEPTH; ++d) {
+        const int s = s0 + d;
+        if (s >= s_end) break;
+        BRaw<FMT> c0 = r0[d], c1;
+        if constexpr (PAIR) c1 = r1[d];
+        if (s + DEPTH < s_end) {
+          load_b<FMT>(r0[d], pd0, ps0, s + DEPTH);
+          if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, s + DEPTH);
         }
-        have = false;
-#pragma unroll
-        for (int u = 0; u < NB; ++u) {
-          const int g = g0 + u * LPR;
-          if (g < G) {
-            chunk_dot<FMT>(c0[u], g, xs, acc0);
-            if constexpr (PAIR) chunk_dot<FMT>(c1[u], g, xs, acc1);
-          }
-        }
-      }
-      acc0 = wave_sum_f32(acc0, LPR);
-      if constexpr (PAIR) acc1 = wave_sum_f32(acc1, LPR);
-      if (li == 0) {
-        if constexpr (PAIR) {
-          // Qwen38Expert (src/models/qwen3_8/expert.rs:137-207): g, u, silu(g), g*u in BF16.
-          // GatedMlp (src/model/mlp.rs:90-99): silu(g) * u in f32; a non-finite activation
-          // is rejected by the down projection's input check.
-          float act;
-          if (qwen) {
-            float g, u, ag, v;
-            bool ok = rne_bf16(acc0, &g) && rne_bf16(acc1, &u) && rne_bf16(silu(g), &ag);
-            v = ag * u;
-            ok = ok && rne_bf16(v, &act);
-            if (!ok) { bad = true; act = v; }
-          } else {
-            act = silu(acc0) * acc1;
-            if (!finite(act)) bad = true;
-          }
-          out[(size_t)p * rows + r] = act;
-        } else {
-          float y = acc0;
-          if (qwen) {
-            float rr;
-            if (!rne_bf16(y, &rr)) bad = true; else y = rr;
-          } else if (FMT == kFmtMXFP8 && !finite(y)) {
-            bad = true;  // MxFp8Matrix::matvec_rows rejects non-finite outputs (mxfp.rs:779-781)
-          }
-          out[(size_t)p * rows + r] = y;
-        }
+        raw_dot<FMT>(c0, s, lq, xs, acc0);
+        if constexpr (PAIR) raw_dot<FMT>(c1, s, lq, xs, acc1);
       }
     }
   }
+  acc0 += __shfl_xor(acc0, 16);
+  acc0 += __shfl_xor(acc0, 32);
+  if constexpr (PAIR) {
+    acc1 += __shfl_xor(acc1, 16);
+    acc1 += __shfl_xor(acc1, 32);
+  }
+  if (ksplit > 1) {
+    float* red = xs + xs_floats(cols);
+    if (lane < 16) {
+      red[(wave * 16 + lane) * 2] = acc0;
+      red[(wave * 16 + lane) * 2 + 1] = acc1;
+    }
+    __syncthreads();
+    if (part == 0 && lane < 16) {
+      acc0 = 0.0f;
+      acc1 = 0.0f;
+      for (int q = 0; q < ksplit; ++q) {
+        acc0 += red[((wave + q) * 16 + lane) * 2];
+        acc1 += red[((wave + q) * 16 + lane) * 2 + 1];
+      }
+    }
+  }
+  if (!valid || part != 0 || lane >= 16) return;
+  const int r = panel * kPanelRows + ln;
+  bool bad = false;
+  if constexpr (PAIR) {
+    // Qwen38Expert (src/models/qwen3_8/expert.rs:137-207): g, u, silu(g), g*u in BF16.
+    // GatedMlp (src/model/mlp.rs:90-99): silu(g) * u in f32; a non-finite activation is
+    // rejected by the down projection's input check.
+    float act;
+    if (qwen) {
+      float g, u, ag, v;
+      bool ok = rne_bf16(acc0, &g) && rne_bf16(acc1, &u) && rne_bf16(silu(g), &ag);
+      v = ag * u;
+      ok = ok && rne_bf16(v, &act);
+      if (!ok) { bad = true; act = v; }
+    } else {
+      act = silu(acc0) * acc1;
+      if (!finite(act)) bad = true;
+    }
+    out[(size_t)p * rows + r] = act;
+  } else {
+    float y = acc0;
+    if (qwen) {
+      float rr;
+      if (!rne_bf16(y, &rr)) bad = true; else y = rr;
+    } else if (FMT == kFmtMXFP8 && !finite(y)) {
+      bad = true;  // MxFp8Matrix::matvec_rows rejects non-finite outputs (mxfp.rs:779-781)
+    }
+    out[(size_t)p * rows + r] = y;
+  }
   if (bad) flag(status, kStatusNonFinite);
+}
+
+// Weight steps in flight per wave (~8 KiB per matrix).
+template <int FMT>
+constexpr int gemv_depth() {
+  return FMT == kFmtBF16 ? 2 : (FMT == kFmtMXFP4 ? 8 : 4);
 }
 
 template <int FMT, bool PAIR>
 static void launch_gemv(const ExpertMats* mats, const Perm& perm, int max_active, int rows,
                         int cols, const float* in, float* out, int qwen, int* status,
                         hipStream_t s) {
-  const int G = cols / Fmt<FMT>::kCols;
-  // Lanes per row: the widest split that leaves every lane at least 2 chunks.
-  int lpr = 64;
-  while (lpr > 16 && G < 2 * lpr) lpr /= 2;
-  // Rows per workgroup: ~2048 workgroups to cover every CU several times, with at least 2x the
-  // staged input vector's bytes of weights per workgroup and at most 8 row passes per wave.
-  const int rows_per_pass = 4 * (64 / lpr);
-  const long row_bytes = (long)cols * (FMT == kFmtBF16 ? 2 : 1) / (FMT == kFmtMXFP4 ? 2 : 1) *
-                         (PAIR ? 2 : 1);
-  const long reuse_rows = (2L * cols * 4 + row_bytes - 1) / row_bytes;
-  const long spread_rows = ((long)rows * max_active + 2047) / 2048;
-  const long want = std::max(reuse_rows, spread_rows);
-  const int passes = (int)std::max(1L, std::min(8L, (want + rows_per_pass - 1) / rows_per_pass));
-  const int rows_per_block = rows_per_pass * passes;
-  const int nrb = (rows + rows_per_block - 1) / rows_per_block;
-  dim3 grid(max_active * nrb);
-  size_t lds = (size_t)cols * sizeof(float);
-  switch (lpr) {
-    case 64:
-      gemv_kernel<FMT, 64, PAIR><<<grid, 256, lds, s>>>(mats, perm, rows, cols, rows_per_block,
-                                                        in, out, qwen, status);
-      break;
-    case 32:
-      gemv_kernel<FMT, 32, PAIR><<<grid, 256, lds, s>>>(mats, perm, rows, cols, rows_per_block,
-                                                        in, out, qwen, status);
-      break;
-    default:
-      gemv_kernel<FMT, 16, PAIR><<<grid, 256, lds, s>>>(mats, perm, rows, cols, rows_per_block,
-                                                        in, out, qwen, status);
-      break;
-  }
+  constexpr int D = gemv_depth<FMT>();
+  const int panels = rows / kPanelRows, steps = cols / kGemmKStep;
+  // Split K until the launch has ~4096 waves, keeping at least DEPTH steps per part.
+  int ksplit = 1;
+  while (ksplit < 4 && (long)panels * max_active * ksplit < 4096 && steps / (2 * ksplit) >= D)
+    ksplit *= 2;
+  const int ppw = 4 / ksplit;
+  dim3 grid((panels + ppw - 1) / ppw, max_active);
+  const size_t lds = (xs_floats(cols) + 4 * 16 * 2) * sizeof(float);
+  gemv_kernel<FMT, PAIR, D><<<grid, 256, lds, s>>>(mats, perm, rows, cols, ksplit, in, out, qwen,
+                                                   status);
 }
 
 void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,

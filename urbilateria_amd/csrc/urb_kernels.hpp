@@ -9,7 +9,25 @@ namespace urb {
 // Error bits written to the per-context status word (the host maps them to urb_status).
 constexpr int kStatusNonFinite = 1;
 
-// One expert's three projections in HBM (gate [I,H], up [I,H], down [H,I]).
+// Panel layout of a [rows, cols] weight matrix in HBM (rows % 16 == 0, cols % 128 == 0).
+// The matrix is a sequence of 16-row panels, each holding exactly the bytes of its 16 rows.
+// A panel is a run of 1 KiB slabs; 16-byte unit l = ln + 16 lq of slab t belongs to panel row
+// ln and holds
+//   BF16:  columns 32 t + 8 lq + [0, 8)                        (cols / 32 slabs)
+//   MXFP4: MX block 4 t + lq, i.e. columns 128 t + 32 lq + [0, 32)  (cols / 128 slabs)
+//   MXFP8: half t % 2 of MX block 4 (t / 2) + lq                (cols / 64 slabs)
+// so one wavefront load instruction (64 lanes x 16 B) reads one slab, and a wavefront that
+// sweeps a panel reads it front to back.  E8M0 scales: per panel, cols / 128 slabs of 64 B;
+// byte l of scale slab s is the scale of row ln, block 4 s + lq.
+constexpr int kPanelRows = 16;
+constexpr int kPanelCols = 128;
+inline bool panel_shape_ok(size_t rows, size_t cols) {
+  return rows % kPanelRows == 0 && cols % kPanelCols == 0 && rows > 0 && cols > 0;
+}
+void launch_pack(int fmt, const uint8_t* data, const uint8_t* scales, int rows, int cols,
+                 uint8_t* packed, uint8_t* packed_scales, hipStream_t s);
+
+// One expert's three projections in HBM (gate [I,H], up [I,H], down [H,I]), panel layout.
 struct ExpertMats {
   const uint8_t* data[3];
   const uint8_t* scales[3];
@@ -27,13 +45,11 @@ struct Perm {
   const int32_t* tiles;       // [2 * tiles] (expert, first row) of each kGemmMTile-row tile
 };
 
-// Grouped GEMM (MFMA) tiling: tokens per tile, weight rows per tile, K per step.
+// Grouped GEMM (MFMA) tiling: tokens per tile, weight rows per workgroup (four panels), K per
+// step.
 constexpr int kGemmMTile = 32;
 constexpr int kGemmNTile = 64;
 constexpr int kGemmKStep = 128;
-inline bool gemm_supported(int rows, int K) {
-  return rows % kGemmNTile == 0 && K % kGemmKStep == 0;
-}
 // Upper bound of row tiles for n tokens routed k ways over E experts.
 inline int gemm_max_tiles(int n, int k, int E) {
   int a = n * k < E ? n * k : E;
@@ -71,8 +87,9 @@ constexpr int kMaxChunkTokens = 1024;
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
                     int32_t* tiles, hipStream_t s);
-// Decode projections (GEMV family): gate+up with the SwiGLU epilogue, then down.
-// `qwen` selects the BF16 boundaries of Qwen38Expert; otherwise GatedMlp's f32 path.
+// Decode projections (GEMV family, one token per active expert): gate+up with the SwiGLU
+// epilogue, then down.  `qwen` selects the BF16 boundaries of Qwen38Expert; otherwise
+// GatedMlp's f32 path.
 void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
                          int H, int I, const float* x, float* act, int qwen, int* status,
                          hipStream_t s);

@@ -142,6 +142,8 @@ const char* urb_status_string(urb_status s) {
 
 }  // extern "C"
 
+constexpr uint32_t kMaxDim = 12288;
+
 static bool finite_host(float v) { return v == v && v <= 3.4028235e38f && v >= -3.4028235e38f; }
 
 static urb_status check_desc(const urb_moe_desc* d) {
@@ -151,10 +153,10 @@ static urb_status check_desc(const urb_moe_desc* d) {
   if (d->top_k > 32 || d->n_experts > 512) return URB_ERR_ARGUMENT;
   for (urb_format f : {d->expert_format, d->shared_format})
     if (f != URB_FMT_BF16 && f != URB_FMT_MXFP4 && f != URB_FMT_MXFP8) return URB_ERR_ARGUMENT;
-  // 128-bit row chunks: H a multiple of 32 (the MX block), I of 32 (MX) or 8 (BF16).
-  if (d->hidden % 32) return URB_ERR_SHAPE;
-  if (d->intermediate % (d->expert_format == URB_FMT_BF16 ? 8 : 32)) return URB_ERR_SHAPE;
-  if (d->shared_intermediate % (d->shared_format == URB_FMT_BF16 ? 8 : 32)) return URB_ERR_SHAPE;
+  // Panel layout: every projection dimension a multiple of 128 columns (16-row panels follow).
+  // The decode kernels stage one input vector in LDS: at most kMaxDim columns.
+  for (uint32_t dim : {d->hidden, d->intermediate, d->shared_intermediate})
+    if (dim % urb::kPanelCols || dim > kMaxDim) return URB_ERR_SHAPE;
   if (d->composition == URB_COMPOSE_QWEN36) {
     // The Qwen3.6 composition reproduced here: BF16 experts, softmax router, no shared expert.
     if (d->expert_format != URB_FMT_BF16 || d->shared_intermediate != 0 ||
@@ -240,6 +242,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   const bool borrow = src == URB_SOURCE_DEVICE_BORROW;
   const hipMemcpyKind kind = src == URB_SOURCE_HOST ? hipMemcpyHostToDevice
                                                     : hipMemcpyDeviceToDevice;
+  if (!borrow) URB_HIP(hipDeviceSynchronize());  // device sources may come from any stream
   // Matrix geometry: gate [I, H], up [I, H], down [H, I].
   const size_t dims[3][2] = {{I, H}, {I, H}, {H, I}};
   const size_t sdims[3][2] = {{Is, H}, {Is, H}, {H, Is}};
@@ -274,6 +277,26 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
     c->bias = bias;
   }
 
+  // Payloads enter HBM in the panel layout.  Host sources go through one staging buffer the
+  // size of the largest matrix; device sources are converted directly.  Borrowed memory must
+  // already be in the panel layout (urb_pack_matrix).
+  void* staging = nullptr;
+  if (src == URB_SOURCE_HOST) {
+    size_t most = 0;
+    for (int m = 0; m < 3; ++m) {
+      size_t sb, db = matrix_bytes(d->expert_format, dims[m][0], dims[m][1], &sb);
+      most = std::max(most, align_up(db) + sb);
+      if (has_shared) {
+        db = matrix_bytes(d->shared_format, sdims[m][0], sdims[m][1], &sb);
+        most = std::max(most, align_up(db) + sb);
+      }
+    }
+    URB_HIP(hipMalloc(&staging, most));
+  }
+  struct StagingFree {
+    void* p;
+    ~StagingFree() { if (p) { (void)hipDeviceSynchronize(); (void)hipFree(p); } }
+  } staging_free{staging};
   std::vector<ExpertMats> table(E);
   auto place = [&](urb_format f, size_t rows, size_t cols, const urb_matrix& mat,
                    const uint8_t** data, const uint8_t** scales) -> urb_status {
@@ -285,8 +308,18 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
     }
     uint8_t* dd = ab.take<uint8_t>(db);
     uint8_t* ss = sb ? ab.take<uint8_t>(sb) : nullptr;
-    URB_HIP(hipMemcpy(dd, mat.data, db, kind));
-    if (sb) URB_HIP(hipMemcpy(ss, mat.scales, sb, kind));
+    const uint8_t* from = static_cast<const uint8_t*>(mat.data);
+    const uint8_t* from_scales = mat.scales;
+    if (staging) {
+      uint8_t* st = static_cast<uint8_t*>(staging);
+      URB_HIP(hipMemcpy(st, mat.data, db, hipMemcpyHostToDevice));
+      if (sb) URB_HIP(hipMemcpy(st + align_up(db), mat.scales, sb, hipMemcpyHostToDevice));
+      from = st;
+      from_scales = sb ? st + align_up(db) : nullptr;
+    }
+    urb::launch_pack(f, from, from_scales, (int)rows, (int)cols, dd, ss, nullptr);
+    URB_HIP(hipGetLastError());
+    if (staging) URB_HIP(hipDeviceSynchronize());  // the staging buffer is reused
     *data = dd;
     *scales = ss;
     return URB_OK;
@@ -427,7 +460,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
       {
         Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
-        if (n > 1 && urb::gemm_supported(Is, H))
+        if (n > 1)
           urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
                                    xc, ws.shared_act, 0, ws.status, c->side);
         else
@@ -436,7 +469,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, c->side);
-        if (n > 1 && urb::gemm_supported(H, Is))
+        if (n > 1)
           urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
                                 ws.shared_act, ws.shared_out, 0, ws.status, c->side);
         else
@@ -457,7 +490,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     // One token: row-parallel GEMV.  Several: grouped MFMA GEMM over the row tiles.
     {
       Span span(c, URB_STAGE_GATE_UP, s);
-      if (n > 1 && urb::gemm_supported(I, H))
+      if (n > 1)
         urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act,
                                  qwen ? 1 : 0, ws.status, s);
       else
@@ -466,7 +499,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     }
     {
       Span span(c, URB_STAGE_DOWN, s);
-      if (n > 1 && urb::gemm_supported(H, I))
+      if (n > 1)
         urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act,
                               ws.y_perm, qwen ? 1 : 0, ws.status, s);
       else
@@ -558,6 +591,21 @@ urb_status urb_dequant_rows(urb_format format, const void* data, const uint8_t* 
   if (count == 0) return URB_OK;
   urb::launch_dequant(format, static_cast<const uint8_t*>(data), scales, (int)rows, (int)cols,
                       (int)row0, (int)count, out, static_cast<hipStream_t>(stream));
+  URB_HIP(hipGetLastError());
+  return URB_OK;
+}
+
+urb_status urb_pack_matrix(urb_format format, const void* data, const uint8_t* scales,
+                           uint32_t rows, uint32_t cols, void* packed_data,
+                           uint8_t* packed_scales, void* stream) {
+  if (format != URB_FMT_BF16 && format != URB_FMT_MXFP4 && format != URB_FMT_MXFP8)
+    return URB_ERR_ARGUMENT;
+  const bool mx = format != URB_FMT_BF16;
+  if (!data || !packed_data || (mx && (!scales || !packed_scales))) return URB_ERR_ARGUMENT;
+  if (!urb::panel_shape_ok(rows, cols)) return URB_ERR_SHAPE;
+  urb::launch_pack(format, static_cast<const uint8_t*>(data), scales, (int)rows, (int)cols,
+                   static_cast<uint8_t*>(packed_data), packed_scales,
+                   static_cast<hipStream_t>(stream));
   URB_HIP(hipGetLastError());
   return URB_OK;
 }

@@ -146,12 +146,13 @@ class MoeLayer:
         spec: C.LayerSpec = layer.spec
         self.spec = spec
         self.max_tokens = max_tokens
-        self._layer = layer  # keeps borrowed / host buffers alive
         lib = N.moe_lib()
         E = spec.n_experts
         host = isinstance(layer, C.HostLayer)
         if source is None:
-            source = N.SOURCE_HOST if host else N.SOURCE_DEVICE_BORROW
+            source = N.SOURCE_HOST if host else N.SOURCE_DEVICE_COPY
+        # borrowed (panel-layout) buffers must outlive the context; copies do not
+        self._layer = layer if source == N.SOURCE_DEVICE_BORROW else None
         mats = (N.Matrix * (3 * E))()
         for e in range(E):
             for m in range(3):
@@ -232,6 +233,32 @@ class MoeLayer:
             self.close()
         except Exception:
             pass
+
+
+def pack_matrix(fmt: int, data, scales, rows: int, cols: int):
+    """Row-major device matrix -> (data, scales) in the panel layout the context streams."""
+    pd = torch.empty_like(data)
+    ps = None if scales is None else torch.empty_like(scales)
+    N.check(N.moe_lib().urb_pack_matrix(fmt, _ptr(data), _ptr(scales), rows, cols, _ptr(pd),
+                                        _ptr(ps), _stream_handle()), "urb_pack_matrix")
+    return pd, ps
+
+
+def packed_layer(layer: "DeviceLayer") -> "DeviceLayer":
+    """The same layer with every expert and shared matrix converted to the panel layout, for
+    URB_SOURCE_DEVICE_BORROW."""
+    spec = layer.spec
+    H, I, Is = spec.hidden, spec.intermediate, spec.shared_intermediate
+    dims = ((I, H), (I, H), (H, I))
+    sdims = ((Is, H), (Is, H), (H, Is))
+    ex = [[pack_matrix(spec.expert_format, d, sc, *dims[m]) for m, (d, sc) in enumerate(trip)]
+          for trip in layer.experts]
+    sh = None
+    if layer.shared is not None:
+        sh = [pack_matrix(spec.shared_format, d, sc, *sdims[m])
+              for m, (d, sc) in enumerate(layer.shared)]
+    torch.cuda.current_stream().synchronize()
+    return DeviceLayer(spec, layer.router_weight, ex, sh, layer.correction_bias, None)
 
 
 def dequant_rows(fmt: int, data, scales, rows: int, cols: int, row0: int = 0,
