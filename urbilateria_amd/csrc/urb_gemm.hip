@@ -40,9 +40,6 @@ __device__ __forceinline__ int frag_k(int j, int lq) {
   return FMT == kFmtBF16 ? 32 * j + 8 * lq : 32 * lq + 8 * j;
 }
 
-// Decoded B fragment: four bf16x8 MFMA operands (j = 0..3).
-struct BFrag { bf16x8 v[4]; };
-
 __device__ __forceinline__ bf16x8 pack8(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) {
   bf16x8 r;
   r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
@@ -50,30 +47,26 @@ __device__ __forceinline__ bf16x8 pack8(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) 
   return r;
 }
 
+// MFMA j's B operand from the raw step data (j is a compile-time constant after unrolling).
 template <int FMT>
-__device__ __forceinline__ void decode_b(const BRaw<FMT>& r, BFrag& f) {
+__device__ __forceinline__ bf16x8 decode_b(const BRaw<FMT>& r, int j) {
   if constexpr (FMT == kFmtBF16) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f.v[j] = __builtin_bit_cast(bf16x8, r.q[j]);
+    return __builtin_bit_cast(bf16x8, r.q[j]);
   } else if constexpr (FMT == kFmtMXFP4) {
     const float sc = e8m0_to_f32(r.s);
-    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      f.v[j] = pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 0),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 1),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 2),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], sc, 3));
+    const uint32_t w = j == 0 ? r.q.x : j == 1 ? r.q.y : j == 2 ? r.q.z : r.q.w;
+    return pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
   } else {
     const float sc = e8m0_to_f32(r.s);
-    const uint32_t w[8] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w,
-                           r.q[1].x, r.q[1].y, r.q[1].z, r.q[1].w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      f.v[j] = pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j], sc, false),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j], sc, true),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], sc, false),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], sc, true));
+    const uint4 q = r.q[j >> 1];
+    const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
+    return pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, false),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true));
   }
 }
 
@@ -120,7 +113,9 @@ __device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
 template <int N>
 using Int = std::integral_constant<int, N>;
 
-template <int FMT, bool PAIR, int DEPTH>
+// NP panels per wave (the workgroup covers 4 NP panels = 64 NP weight rows): every staged
+// activation fragment feeds NP (x2 for gate+up) MFMAs.
+template <int FMT, bool PAIR, int DEPTH, int NP>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
                                                       Perm perm, int rows, int K,
                                                       const float* __restrict__ in,
@@ -149,15 +144,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   const ExpertMats m = mats[expert];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lq = lane >> 4;
-  const int panel = blockIdx.x * 4 + wave;
-  const int row = panel * kPanelRows + ln;
+  const int panel0 = (blockIdx.x * 4 + wave) * NP;
   const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(K);
   const size_t pscales = (size_t)kPanelRows * (K / 32);
 
-  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + panel * pbytes + 16 * lane;
-  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + panel * pscales + lane;
-  const uint8_t* pd1 = PAIR ? m.data[1] + panel * pbytes + 16 * lane : nullptr;
-  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + panel * pscales + lane : nullptr;
+  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + panel0 * pbytes + 16 * lane;
+  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + panel0 * pscales + lane;
+  const uint8_t* pd1 = PAIR ? m.data[1] + panel0 * pbytes + 16 * lane : nullptr;
+  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + panel0 * pscales + lane : nullptr;
 
   // ---- A source row of this thread's staging slot
   const int am = threadIdx.x >> 3;
@@ -169,23 +163,29 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     a_src = in + (size_t)src_row * K;
   }
 
-  f32x4 acc0[2], acc1[2];
+  f32x4 acc0[NP][2], acc1[NP][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    acc0[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int q = 0; q < NP; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      acc0[q][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc1[q][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
   const int steps = K / kKS;
   auto body = [&](auto nmb) {
     constexpr int NMB = decltype(nmb)::value;  // 16-token MFMA blocks this tile needs
-    BRaw<FMT> r0[DEPTH], r1[DEPTH];
+    BRaw<FMT> r0[DEPTH][NP], r1[DEPTH][NP];
+    auto fetch = [&](int d, int s) {
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        load_b<FMT>(r0[d][q], pd0 + q * pbytes, ps0 + q * pscales, s);
+        if constexpr (PAIR) load_b<FMT>(r1[d][q], pd1 + q * pbytes, ps1 + q * pscales, s);
+      }
+    };
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
-      if (d < steps) {
-        load_b<FMT>(r0[d], pd0, ps0, d);
-        if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, d);
-      }
+      if (d < steps) fetch(d, d);
     AStage as;
     load_a(as, a_src, a_valid, 0);
     bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
@@ -197,29 +197,41 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
         const int buf = s & 1;
         const bool more = s + 1 < steps;
         if (more) load_a(as, a_src, a_valid, (s + 1) * kKS);
-        BFrag f0, f1;
-        decode_b<FMT>(r0[d], f0);
-        if constexpr (PAIR) decode_b<FMT>(r1[d], f1);
-        if (s + DEPTH < steps) {  // refill this ring slot DEPTH steps ahead
-          load_b<FMT>(r0[d], pd0, ps0, s + DEPTH);
-          if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, s + DEPTH);
+        BRaw<FMT> c0[NP], c1[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          c0[q] = r0[d][q];
+          if constexpr (PAIR) c1[q] = r1[d][q];
         }
+        if (s + DEPTH < steps) fetch(d, s + DEPTH);  // refill this ring slot DEPTH steps ahead
         const u16* hi = a_hi[buf];
         const u16* lo = a_lo[buf];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+          bf16x8 f0[NP], f1[NP];
+#pragma unroll
+          for (int q = 0; q < NP; ++q) {
+            f0[q] = decode_b<FMT>(c0[q], j);
+            if constexpr (PAIR) f1[q] = decode_b<FMT>(c1[q], j);
+          }
           const int kf = frag_k<FMT>(j, lq);
 #pragma unroll
           for (int mb = 0; mb < NMB; ++mb) {
             const bf16x8 ah = lds_frag(hi, mb * 16 + ln, kf);
-            acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0.v[j], acc0[mb], 0, 0, 0);
-            if constexpr (PAIR)
-              acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1.v[j], acc1[mb], 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0[q], acc0[q][mb], 0, 0, 0);
+              if constexpr (PAIR)
+                acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1[q], acc1[q][mb], 0, 0, 0);
+            }
             if (lo_any) {
               const bf16x8 al = lds_frag(lo, mb * 16 + ln, kf);
-              acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0.v[j], acc0[mb], 0, 0, 0);
-              if constexpr (PAIR)
-                acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1.v[j], acc1[mb], 0, 0, 0);
+#pragma unroll
+              for (int q = 0; q < NP; ++q) {
+                acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0[q], acc0[q][mb], 0, 0, 0);
+                if constexpr (PAIR)
+                  acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1[q], acc1[q][mb], 0, 0, 0);
+              }
             }
           }
         }
@@ -230,38 +242,42 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   if (mrows > 16) body(Int<2>{});
   else body(Int<1>{});
 
-  // ---- epilogue: lane holds column `row`, rows 4*lq + i of each 16-row block
+  // ---- epilogue: lane holds column `row` of panel q, rows 4*lq + i of each 16-row block
   bool bad = false;
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int q = 0; q < NP; ++q) {
+    const int row = (panel0 + q) * kPanelRows + ln;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int mm = mb * 16 + 4 * lq + i;
-      if (mm >= mrows) continue;
-      const size_t p = (size_t)(base + m0 + mm);
-      if constexpr (PAIR) {
-        const float g0 = acc0[mb][i], u0 = acc1[mb][i];
-        float act;
-        if (qwen) {
-          float g, u, ag;
-          bool ok = rne_bf16(g0, &g) && rne_bf16(u0, &u) && rne_bf16(silu(g), &ag);
-          float v = ag * u;
-          ok = ok && rne_bf16(v, &act);
-          if (!ok) { bad = true; act = v; }
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mm = mb * 16 + 4 * lq + i;
+        if (mm >= mrows) continue;
+        const size_t p = (size_t)(base + m0 + mm);
+        if constexpr (PAIR) {
+          const float g0 = acc0[q][mb][i], u0 = acc1[q][mb][i];
+          float act;
+          if (qwen) {
+            float g, u, ag;
+            bool ok = rne_bf16(g0, &g) && rne_bf16(u0, &u) && rne_bf16(silu(g), &ag);
+            float v = ag * u;
+            ok = ok && rne_bf16(v, &act);
+            if (!ok) { bad = true; act = v; }
+          } else {
+            act = silu(g0) * u0;
+            if (!finite(act)) bad = true;
+          }
+          out[p * rows + row] = act;
         } else {
-          act = silu(g0) * u0;
-          if (!finite(act)) bad = true;
+          float y = acc0[q][mb][i];
+          if (qwen) {
+            float r;
+            if (!rne_bf16(y, &r)) bad = true; else y = r;
+          } else if (FMT == kFmtMXFP8 && !finite(y)) {
+            bad = true;
+          }
+          out[p * rows + row] = y;
         }
-        out[p * rows + row] = act;
-      } else {
-        float y = acc0[mb][i];
-        if (qwen) {
-          float r;
-          if (!rne_bf16(y, &r)) bad = true; else y = r;
-        } else if (FMT == kFmtMXFP8 && !finite(y)) {
-          bad = true;
-        }
-        out[p * rows + row] = y;
       }
     }
   }
@@ -321,9 +337,9 @@ __global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __r
   for (int s = 0; s < steps; ++s) {
     const int buf = s & 1;
     const bool more = s + 1 < steps;
-    BFrag f;
+    bf16x8 f[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f.v[j] = __builtin_bit_cast(bf16x8, r[j]);
+    for (int j = 0; j < 4; ++j) f[j] = __builtin_bit_cast(bf16x8, r[j]);
     if (more) {
       load_row_block(r, b_row, (s + 1) * (kKS / 32) + lq);
       load_a(as, a_src, a_valid, (s + 1) * kKS);
@@ -333,10 +349,10 @@ __global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __r
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            lds_frag(a_hi[buf], mb * 16 + ln, 32 * lq + 8 * j), f.v[j], zero, 0, 0, 0);
+            lds_frag(a_hi[buf], mb * 16 + ln, 32 * lq + 8 * j), f[j], zero, 0, 0, 0);
         if (lo_any)
           part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              lds_frag(a_lo[buf], mb * 16 + ln, 32 * lq + 8 * j), f.v[j], part, 0, 0, 0);
+              lds_frag(a_lo[buf], mb * 16 + ln, 32 * lq + 8 * j), f[j], part, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[mb][i] += (double)part[i];
       }
@@ -365,18 +381,29 @@ void launch_router_gemm(const uint16_t* w, int E, int H, const float* x, int T, 
   router_gemm_kernel<<<grid, 256, 0, s>>>(w, E, H, x, T, logits, status);
 }
 
-// Weight steps in flight per wave: enough 1 KiB slabs to cover HBM latency.
-template <int FMT, bool PAIR>
-constexpr int gemm_depth() {
-  return FMT == kFmtBF16 ? (PAIR ? 2 : 1) : (FMT == kFmtMXFP4 ? 4 : 2);
+template <int FMT, bool PAIR, int DEPTH, int NP>
+static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
+                         const float* in, float* out, int qwen, int* status, hipStream_t s) {
+  dim3 grid(rows / (kNT * NP), max_tiles);
+  gemm_kernel<FMT, PAIR, DEPTH, NP><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, qwen,
+                                                          status);
 }
 
+// Weight steps in flight per wave (DEPTH) and panels per wave (NP), per format.  BF16 steps are
+// 4 KiB per panel, so one panel two steps deep; the MX formats stream 1-2 KiB per panel and
+// step and need more panels per staged activation tile (activations are 2-4x their bytes).
+// Rows are multiples of 128 (urb_moe_create), so NP = 2 always tiles them.
 template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                    const float* in, float* out, int qwen, int* status, hipStream_t s) {
-  dim3 grid(rows / kNT, max_tiles);
-  gemm_kernel<FMT, PAIR, gemm_depth<FMT, PAIR>()><<<grid, 256, 0, s>>>(mats, perm, rows, K, in,
-                                                                        out, qwen, status);
+  if constexpr (FMT == kFmtBF16)
+    launch_shape<FMT, PAIR, PAIR ? 2 : 1, 1>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+  else if constexpr (FMT == kFmtMXFP8)
+    launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+  else if (rows % (kNT * 4) == 0)
+    launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+  else
+    launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
 }
 
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
