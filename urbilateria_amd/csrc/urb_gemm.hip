@@ -20,6 +20,8 @@
 #include "urb_kernels.hpp"
 #include "urb_panel.hpp"
 
+#include <algorithm>
+
 namespace urb {
 
 constexpr int kMT = kGemmMTile;   // 32 tokens: two 16-row MFMA blocks
@@ -285,23 +287,21 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
 }
 
 // ------------------------------------------------------------------------------------------
-// Router GEMM for many tokens: logits[t, e] = sum_k w[e, k] x[t, k] (`router.matvec`,
-// src/model/bf16.rs:121-216, ordered f64).  BF16 weight times the hi/lo BF16 halves of x are
-// exact products; each MFMA sums 32 of them in f32 and that partial is added into an f64
-// accumulator, so the f32 logit is the correctly rounded sum up to a few units in the last
-// place.  Tiles: 32 tokens x 64 experts (experts past E are clamped and not stored).
+// Router logits (`router.matvec`, src/model/bf16.rs:121-216, ordered f64) for the GLM
+// composition: logits[t, e] = sum_k w[e, k] x[t, k].  BF16 weight times the hi/lo BF16 halves
+// of x are exact products; each MFMA sums 32 of them in f32 and that partial is added into an
+// f64 accumulator, so the f32 logit is the correctly rounded sum up to a few units in the last
+// place.  The router weight is in the panel layout with its rows padded to a multiple of 64
+// (zero rows).  Workgroup (x, y, z) covers experts [64 x, 64 x + 64), tokens [32 y, 32 y + 32)
+// and K steps [z * slice, (z + 1) * slice) and writes f64 partial sums part[z][t][e]; the
+// routing kernel adds the slices in order.
 // ------------------------------------------------------------------------------------------
-// Router weights stay row-major [E, H]: lane (ln, lq) reads its row's 32-column block kblk.
-__device__ __forceinline__ void load_row_block(uint4 (&q)[4], const uint8_t* __restrict__ row,
-                                               int kblk) {
-  const uint4* p = reinterpret_cast<const uint4*>(row + (size_t)kblk * 64);
-  q[0] = p[0]; q[1] = p[1]; q[2] = p[2]; q[3] = p[3];
-}
-
-__global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __restrict__ w,
-                                                             int E, int H,
-                                                             const float* __restrict__ x, int T,
-                                                             float* __restrict__ logits,
+template <int DEPTH>
+__global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __restrict__ wp,
+                                                             int Epad, int H,
+                                                             const float* __restrict__ x,
+                                                             int T, int slice,
+                                                             double* __restrict__ part,
                                                              int* status) {
   __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
   __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
@@ -309,8 +309,10 @@ __global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __r
   const int mrows = min(kMT, T - m0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lq = lane >> 4;
-  const int e = blockIdx.x * kNT + wave * 16 + ln;
-  const uint8_t* b_row = reinterpret_cast<const uint8_t*>(w + (size_t)min(e, E - 1) * H);
+  const int panel = blockIdx.x * 4 + wave;
+  const int steps = H / kKS;
+  const int s_begin = blockIdx.z * slice, s_end = min(steps, s_begin + slice);
+  const uint8_t* pd = wp + (size_t)panel * (kPanelRows * panel_row_bytes<kFmtBF16>(H)) + 16 * lane;
   const int am = threadIdx.x >> 3;
   const bool a_valid = am < mrows;
   const float* a_src = x + (size_t)(m0 + (a_valid ? am : 0)) * H;
@@ -321,64 +323,84 @@ __global__ __launch_bounds__(256, 2) void router_gemm_kernel(const uint16_t* __r
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[mb][i] = 0.0;
 
-  const int steps = H / kKS;
-  uint4 r[4];
-  AStage as;
-  load_row_block(r, b_row, lq);
-  load_a(as, a_src, a_valid, 0);
   bool bad = false;
-  {
+  auto check = [&](const AStage& as) {
     const float* v = reinterpret_cast<const float*>(as.v);
 #pragma unroll
     for (int i = 0; i < 16; ++i) bad |= !finite(v[i]);
-  }
-  bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < steps; ++s) {
-    const int buf = s & 1;
-    const bool more = s + 1 < steps;
-    bf16x8 f[4];
+  };
+  auto body = [&](auto nmb) {
+    constexpr int NMB = decltype(nmb)::value;
+    BRaw<kFmtBF16> r[DEPTH];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f[j] = __builtin_bit_cast(bf16x8, r[j]);
-    if (more) {
-      load_row_block(r, b_row, (s + 1) * (kKS / 32) + lq);
-      load_a(as, a_src, a_valid, (s + 1) * kKS);
-    }
+    for (int d = 0; d < DEPTH; ++d)
+      if (s_begin + d < s_end) load_b<kFmtBF16>(r[d], pd, nullptr, s_begin + d);
+    AStage as;
+    load_a(as, a_src, a_valid, s_begin * kKS);
+    check(as);
+    bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = s_begin; s0 < s_end; s0 += DEPTH) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+      for (int d = 0; d < DEPTH; ++d) {
+        const int s = s0 + d;
+        if (s >= s_end) break;
+        const int buf = (s - s_begin) & 1;
+        const bool more = s + 1 < s_end;
+        if (more) load_a(as, a_src, a_valid, (s + 1) * kKS);
+        const BRaw<kFmtBF16> c = r[d];
+        if (s + DEPTH < s_end) load_b<kFmtBF16>(r[d], pd, nullptr, s + DEPTH);
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            lds_frag(a_hi[buf], mb * 16 + ln, 32 * lq + 8 * j), f[j], zero, 0, 0, 0);
-        if (lo_any)
-          part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              lds_frag(a_lo[buf], mb * 16 + ln, 32 * lq + 8 * j), f[j], part, 0, 0, 0);
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 f = __builtin_bit_cast(bf16x8, c.q[j]);
+          const int kf = frag_k<kFmtBF16>(j, lq);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mb][i] += (double)part[i];
+          for (int mb = 0; mb < NMB; ++mb) {
+            f32x4 pp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                lds_frag(a_hi[buf], mb * 16 + ln, kf), f, zero, 0, 0, 0);
+            if (lo_any)
+              pp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  lds_frag(a_lo[buf], mb * 16 + ln, kf), f, pp, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mb][i] += (double)pp[i];
+          }
+        }
+        if (more) {
+          check(as);
+          lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
+        }
       }
     }
-    if (more) {
-      const float* v = reinterpret_cast<const float*>(as.v);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) bad |= !finite(v[i]);
-      lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
-    }
-  }
+  };
+  if (mrows > 16) body(Int<2>{});
+  else body(Int<1>{});
   if (bad && blockIdx.x == 0) flag(status, kStatusNonFinite);
-  if (e >= E) return;
+  const int e = panel * kPanelRows + ln;
+  double* out = part + (size_t)blockIdx.z * T * Epad;
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int mm = mb * 16 + 4 * lq + i;
-      if (mm < mrows) logits[(size_t)(m0 + mm) * E + e] = (float)acc[mb][i];
+      if (mm < mrows) out[(size_t)(m0 + mm) * Epad + e] = acc[mb][i];
     }
 }
 
-void launch_router_gemm(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
-                        int* status, hipStream_t s) {
-  dim3 grid((E + kNT - 1) / kNT, (T + kMT - 1) / kMT);
-  router_gemm_kernel<<<grid, 256, 0, s>>>(w, E, H, x, T, logits, status);
+int router_slices(int E, int H, int T) {
+  const int steps = H / kKS;
+  const int base = (router_rows(E) / kNT) * ((T + kMT - 1) / kMT);
+  int slices = std::min(kRouterMaxSlices, std::max(1, (512 + base - 1) / base));
+  slices = std::min(slices, std::max(1, steps / 2));
+  const int per = (steps + slices - 1) / slices;
+  return (steps + per - 1) / per;
+}
+
+void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
+                        int slices, int* status, hipStream_t s) {
+  const int steps = H / kKS;
+  const int per = (steps + slices - 1) / slices;
+  dim3 grid(router_rows(E) / kNT, (T + kMT - 1) / kMT, slices);
+  router_mfma_kernel<4><<<grid, 256, 0, s>>>(wp, router_rows(E), H, x, T, per, part, status);
 }
 
 template <int FMT, bool PAIR, int DEPTH, int NP>

@@ -67,20 +67,27 @@ struct RouteParams {
   int n_group, topk_group, normalize;
   float scale;
   const float* bias; // [E] or nullptr
+  // When set, the logits are the in-order sums of `slices` f64 partial slices
+  // part[z][t][e] (z < slices, row pitch router_rows(E)); the routing kernel writes them to
+  // `logits` as f32.
+  const double* part;
+  int slices;
 };
 
 // Router logits.
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int* status, hipStream_t s);
-void launch_router_f64(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
-                       int* status, hipStream_t s);
-// Router logits for many tokens (GLM): MFMA BF16 with f64 accumulation of 32-k partials.
-void launch_router_gemm(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
-                        int* status, hipStream_t s);
-constexpr int kRouterGemmMinTokens = 16;
+// GLM router logits: MFMA BF16 with f64 accumulation of 32-k partials, split over K into
+// f64 partial slices.  The router weight is packed in the panel layout with router_rows(E)
+// rows (zero padding).
+__host__ __device__ inline int router_rows(int E) { return (E + kGemmNTile - 1) / kGemmNTile * kGemmNTile; }
+constexpr int kRouterMaxSlices = 16;
+int router_slices(int E, int H, int T);
+void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
+                        int slices, int* status, hipStream_t s);
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s);
-// Top-k routing, one wavefront per token.
-void launch_route(const float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
+// Top-k routing, one wavefront per token (logits is an output when p.part is set).
+void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
                   float* weights, int32_t* asc, int* status, hipStream_t s);
 // Permutation for T <= kMaxChunkTokens tokens.
 constexpr int kMaxChunkTokens = 1024;

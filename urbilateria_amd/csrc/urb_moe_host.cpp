@@ -29,6 +29,7 @@ size_t matrix_bytes(urb_format f, size_t rows, size_t cols, size_t* scales) {
 
 struct Workspace {
   float* logits = nullptr;
+  double* router_part = nullptr;  // GLM router f64 partial slices
   int32_t* ids = nullptr;
   float* weights = nullptr;
   int32_t* asc = nullptr;
@@ -68,8 +69,9 @@ struct urb_moe_ctx {
   size_t arena_bytes = 0, weight_bytes = 0;
   void* work = nullptr;
   size_t work_bytes = 0;
-  const uint16_t* router = nullptr;    // [E, H] BF16
+  const uint16_t* router = nullptr;    // [E, H] BF16 (rows zero-padded to router_rows(E))
   uint16_t* router_lane8 = nullptr;    // per-lane chain layout (QWEN36)
+  uint8_t* router_panel = nullptr;     // panel layout of the padded router (GLM)
   const float* bias = nullptr;         // [E] or nullptr
   ExpertMats* table = nullptr;         // device [E]
   ExpertMats* shared_table = nullptr;  // device [1]
@@ -201,6 +203,12 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   Workspace& w = c->ws;
   w.status = b.take<int>(4);
   w.logits = b.take<float>(C * E);
+  if (d.composition == URB_COMPOSE_GLM) {
+    size_t most = 0;  // largest slices x tokens any call can need
+    for (size_t t = 1; t <= C; ++t)
+      most = std::max(most, (size_t)urb::router_slices((int)E, (int)H, (int)t) * t);
+    w.router_part = b.take<double>(most * urb::router_rows((int)E));
+  }
   w.ids = b.take<int32_t>(C * K);
   w.weights = b.take<float>(C * K);
   w.asc = b.take<int32_t>(C * K);
@@ -248,7 +256,9 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   const size_t sdims[3][2] = {{Is, H}, {Is, H}, {H, Is}};
 
   // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
-  size_t arena = align_up(E * H * 2) + (qwen ? align_up(E * H * 2) : 0) + align_up(E * 4);
+  const size_t Ep = urb::router_rows((int)E);
+  size_t arena = align_up(Ep * H * 2) + (qwen ? align_up(E * H * 2) : align_up(Ep * H * 2)) +
+                 align_up(E * 4);
   size_t wbytes = 0;
   if (!borrow) {
     for (int m = 0; m < 3; ++m) {
@@ -265,12 +275,15 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   c->arena_bytes = arena;
   c->weight_bytes = wbytes;
   Bump ab{static_cast<char*>(c->arena)};
-  uint16_t* router = ab.take<uint16_t>(E * H);
+  uint16_t* router = ab.take<uint16_t>(Ep * H);
   c->router_lane8 = qwen ? ab.take<uint16_t>(E * H) : nullptr;
+  c->router_panel = qwen ? nullptr : ab.take<uint8_t>(Ep * H * 2);
   float* bias = ab.take<float>(E);
   c->table = ab.take<ExpertMats>(E);
   c->shared_table = ab.take<ExpertMats>(1);
   URB_HIP(hipMemcpy(router, w->router_weight, E * H * 2, kind));
+  if (Ep > E) urb::launch_fill_i32(reinterpret_cast<int32_t*>(router + E * H), 0, (Ep - E) * H / 2,
+                                   nullptr);
   c->router = router;
   if (w->correction_bias) {
     URB_HIP(hipMemcpy(bias, w->correction_bias, E * 4, kind));
@@ -375,7 +388,11 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   if (host_flags[1] & 2) return URB_ERR_INVALID_SCALE;
   urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
 
-  if (qwen) urb::launch_relayout_lane8(router, (int)E, (int)H, c->router_lane8, nullptr);
+  if (qwen)
+    urb::launch_relayout_lane8(router, (int)E, (int)H, c->router_lane8, nullptr);
+  else
+    urb::launch_pack(URB_FMT_BF16, reinterpret_cast<const uint8_t*>(router), nullptr, (int)Ep,
+                     (int)H, c->router_panel, nullptr, nullptr);
   URB_HIP(hipGetLastError());
   URB_HIP(hipDeviceSynchronize());
 
@@ -417,15 +434,19 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logi
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
+  urb::RouteParams rp{(int)d.router, qwen ? 1 : 0, (int)d.n_group, (int)d.topk_group,
+                      d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias, nullptr, 0};
   {
     Span span(c, URB_STAGE_ROUTER, s);
-    if (qwen) urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, c->ws.status, s);
-    else if (n >= urb::kRouterGemmMinTokens && H % urb::kGemmKStep == 0)
-      urb::launch_router_gemm(c->router, E, H, x, n, logits, c->ws.status, s);
-    else urb::launch_router_f64(c->router, E, H, x, n, logits, c->ws.status, s);
+    if (qwen) {
+      urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, c->ws.status, s);
+    } else {
+      rp.slices = urb::router_slices(E, H, n);
+      rp.part = c->ws.router_part;
+      urb::launch_router_mfma(c->router_panel, E, H, x, n, c->ws.router_part, rp.slices,
+                              c->ws.status, s);
+    }
   }
-  urb::RouteParams rp{(int)d.router, qwen ? 1 : 0, (int)d.n_group, (int)d.topk_group,
-                      d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias};
   {
     Span span(c, URB_STAGE_ROUTE, s);
     urb::launch_route(logits, n, E, K, rp, ids, weights, qwen ? c->ws.asc : nullptr,

@@ -27,27 +27,34 @@ __global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E, int
   }
 }
 
+// 16-element chain batches in flight per lane (8 x 32 B = 64 VGPRs of weights).
+constexpr int kLane8Ring = 8;
+
 template <int kLane8Tokens>
 __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __restrict__ w8,
                                                           int E, int H,
                                                           const float* __restrict__ x, int T,
                                                           float* __restrict__ logits,
                                                           int* status) {
-  extern __shared__ float xs[];  // [tok][8][H8 + 1] transposed chains, then [tok][tail]
-  const int H8 = H / 8, tail = H - 8 * H8, H8p = H8 + 1;
+  // [tok][8][H8 + 4] transposed chains (the pad of 4 floats puts the 8 chains of a column in
+  // different LDS banks and keeps 16-byte alignment), then [tok][tail]
+  extern __shared__ float xs[];
+  const int H8 = H / 8, tail = H - 8 * H8, H8p = H8 + 4;
   const int t0 = blockIdx.y * kLane8Tokens;
   const int nt = min(kLane8Tokens, T - t0);
   float* xt = xs + kLane8Tokens * 8 * H8p;
   const int el = threadIdx.x >> 3, j = threadIdx.x & 7;
   const int e = blockIdx.x * 8 + el;
   const uint16_t* chain = w8 + (size_t)min(e, E - 1) * H + (size_t)j * H8;
-  const bool vec = (H8 & 63) == 0;
-  // First 64 chain elements go to registers before the activations are staged.
-  uint4 wq[8];
-  if (vec) {
+  const int nb = H8 / 16;  // H is a multiple of 128, so chains are whole batches
+  // The first kLane8Ring batches are requested before the activations are staged.
+  uint4 ring[kLane8Ring][2];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) wq[u] = reinterpret_cast<const uint4*>(chain)[u];
-  }
+  for (int d = 0; d < kLane8Ring; ++d)
+    if (d < nb) {
+      ring[d][0] = reinterpret_cast<const uint4*>(chain)[2 * d];
+      ring[d][1] = reinterpret_cast<const uint4*>(chain)[2 * d + 1];
+    }
   // Stage x with coalesced float4 loads, transposed into per-lane chains.
   bool bad = false;
   const int n4 = nt * H / 4;
@@ -69,37 +76,31 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
   for (int tt = 0; tt < kLane8Tokens; ++tt) acc[tt] = 0.0f;
   if (e < E) {
     const float* xj = xs + j * H8p;
-    if (vec) {
-      for (int i0 = 0; i0 < H8; i0 += 64) {
-        uint4 nq[8];
-        const bool more = i0 + 64 < H8;
-        if (more) {
+    for (int b0 = 0; b0 < nb; b0 += kLane8Ring) {
 #pragma unroll
-          for (int u = 0; u < 8; ++u) nq[u] = reinterpret_cast<const uint4*>(chain + i0 + 64)[u];
+      for (int d = 0; d < kLane8Ring; ++d) {
+        const int b = b0 + d;
+        if (b >= nb) break;
+        const uint4 qa = ring[d][0], qb = ring[d][1];
+        if (b + kLane8Ring < nb) {
+          ring[d][0] = reinterpret_cast<const uint4*>(chain)[2 * (b + kLane8Ring)];
+          ring[d][1] = reinterpret_cast<const uint4*>(chain)[2 * (b + kLane8Ring) + 1];
         }
+        const float wv[16] = {bf16_lo(qa.x), bf16_hi(qa.x), bf16_lo(qa.y), bf16_hi(qa.y),
+                              bf16_lo(qa.z), bf16_hi(qa.z), bf16_lo(qa.w), bf16_hi(qa.w),
+                              bf16_lo(qb.x), bf16_hi(qb.x), bf16_lo(qb.y), bf16_hi(qb.y),
+                              bf16_lo(qb.z), bf16_hi(qb.z), bf16_lo(qb.w), bf16_hi(qb.w)};
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const uint4 q = wq[u];
-          const float wv[8] = {bf16_lo(q.x), bf16_hi(q.x), bf16_lo(q.y), bf16_hi(q.y),
-                               bf16_lo(q.z), bf16_hi(q.z), bf16_lo(q.w), bf16_hi(q.w)};
+        for (int tt = 0; tt < kLane8Tokens; ++tt) {
+          if (tt < nt) {
+            const float4* xv = reinterpret_cast<const float4*>(xj + tt * 8 * H8p + 16 * b);
+            const float4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+            const float xf[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                                  x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
 #pragma unroll
-          for (int tt = 0; tt < kLane8Tokens; ++tt) {
-            if (tt < nt) {
-              const float* xv = xj + tt * 8 * H8p + i0 + 8 * u;
-#pragma unroll
-              for (int k = 0; k < 8; ++k) acc[tt] = fmaf(wv[k], xv[k], acc[tt]);
-            }
+            for (int k = 0; k < 16; ++k) acc[tt] = fmaf(wv[k], xf[k], acc[tt]);
           }
         }
-        if (more) {
-#pragma unroll
-          for (int u = 0; u < 8; ++u) wq[u] = nq[u];
-        }
-      }
-    } else {
-      for (int i = 0; i < H8; ++i) {
-        float wv = u2f((uint32_t)chain[i] << 16);
-        for (int tt = 0; tt < nt; ++tt) acc[tt] = fmaf(wv, xj[tt * 8 * H8p + i], acc[tt]);
       }
     }
   }
@@ -120,63 +121,6 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
       }
       logits[(size_t)(t0 + tt) * E + e] = r;
     }
-  }
-}
-
-// ------------------------------------------------------------------------------------------
-// GLM router: `router.matvec` = Bf16Matrix::matvec_rows, ordered f64 (src/model/bf16.rs:
-// 121-216).  Products bf16*f32 are exact in f64; the sum is reassociated across lanes (f64, so
-// the f32 logit differs from the ordered sum only in rare last-bit cases).  One wavefront per
-// expert, lanes over 8-column chunks, up to 8 tokens per block.
-// ------------------------------------------------------------------------------------------
-constexpr int kF64Tokens = 8;
-
-__global__ __launch_bounds__(256) void router_f64_kernel(const uint16_t* __restrict__ w, int E,
-                                                         int H, const float* __restrict__ x,
-                                                         int T, float* __restrict__ logits,
-                                                         int* status) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int e = blockIdx.x * 4 + wave;
-  const int t0 = blockIdx.y * kF64Tokens;
-  const int nt = min(kF64Tokens, T - t0);
-  if (e >= E) return;
-  double acc[kF64Tokens];
-#pragma unroll
-  for (int tt = 0; tt < kF64Tokens; ++tt) acc[tt] = 0.0;
-  const int H8 = H / 8;
-  const uint16_t* row = w + (size_t)e * H;
-  bool bad = false;
-  for (int ch = lane; ch < H8; ch += 64) {
-    uint4 q = *reinterpret_cast<const uint4*>(row + ch * 8);
-    float wv[8] = {bf16_lo(q.x), bf16_hi(q.x), bf16_lo(q.y), bf16_hi(q.y),
-                   bf16_lo(q.z), bf16_hi(q.z), bf16_lo(q.w), bf16_hi(q.w)};
-#pragma unroll
-    for (int tt = 0; tt < kF64Tokens; ++tt) {
-      if (tt < nt) {
-        const float4* xp = reinterpret_cast<const float4*>(x + (size_t)(t0 + tt) * H + ch * 8);
-        float4 a = xp[0], b = xp[1];
-        float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          bad |= !finite(xv[u]);
-          acc[tt] = fma((double)wv[u], (double)xv[u], acc[tt]);
-        }
-      }
-    }
-  }
-  for (int c = 8 * H8 + lane; c < H; c += 64) {
-    double wv = (double)u2f((uint32_t)row[c] << 16);
-    for (int tt = 0; tt < nt; ++tt) {
-      float xv = x[(size_t)(t0 + tt) * H + c];
-      bad |= !finite(xv);
-      acc[tt] = fma(wv, (double)xv, acc[tt]);
-    }
-  }
-  if (bad) flag(status, kStatusNonFinite);
-#pragma unroll
-  for (int tt = 0; tt < kF64Tokens; ++tt) {
-    double s = wave_sum_f64(acc[tt]);
-    if (lane == 0 && tt < nt) logits[(size_t)(t0 + tt) * E + e] = (float)s;
   }
 }
 
@@ -233,7 +177,7 @@ __device__ __forceinline__ int argmax_round(const int32_t (&key)[EPL], const flo
 }
 
 template <int EPL, bool SOFTMAX>
-__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, int T,
+__global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, int T,
                                                     int E, int K, RouteParams rp,
                                                     int32_t* __restrict__ ids,
                                                     float* __restrict__ weights,
@@ -243,17 +187,45 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
-  const float* lt = logits + (size_t)t * E;
+  float* lt = logits + (size_t)t * E;
   float v[EPL];
   bool open[EPL];
   bool bad = false;
+  if (rp.part) {
+    // logit = (f32) sum of the router's f64 partial slices, in slice order
+    const size_t pitch = (size_t)router_rows(E), slice = (size_t)T * pitch;
+    const double* pt = rp.part + (size_t)t * pitch;
+    double acc[EPL];
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int e = lane + 64 * i;
-    open[i] = e < E;
-    v[i] = open[i] ? lt[e] : 0.0f;
-    if (open[i] && !finite(v[i])) bad = true;
+    for (int i = 0; i < EPL; ++i) acc[i] = 0.0;
+    for (int z = 0; z < rp.slices; ++z) {
+      double pz[EPL];
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        const int e = lane + 64 * i;
+        pz[i] = e < E ? pt[z * slice + e] : 0.0;
+      }
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) acc[i] += pz[i];
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      open[i] = e < E;
+      v[i] = (float)acc[i];
+      if (open[i]) lt[e] = v[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      open[i] = e < E;
+      v[i] = open[i] ? lt[e] : 0.0f;
+    }
   }
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    if (open[i] && !finite(v[i])) bad = true;
   int my_id = 0;
   float my_val = 0.0f;
   float w = 0.0f;
@@ -474,28 +446,25 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int* status, hipStream_t s) {
-  // Each thread runs one 8-lane chain per token; up to 512 tokens, one token per workgroup
-  // gives the most independent waves, beyond that four tokens share each weight chain load.
+  // One token per block gives the most independent waves; with more tokens, 2 or 4 tokens
+  // share each weight chain (independent FMA chains interleave in the lane).
   const int H8 = H / 8, tail = H - 8 * H8;
-  if (T <= 512) {
-    size_t lds = (size_t)(8 * (H8 + 1) + tail) * sizeof(float);
-    dim3 grid((E + 7) / 8, T);
-    router_lane8_kernel<1><<<grid, 64, lds, s>>>(w8, E, H, x, T, logits, status);
+  const size_t per_tok = (size_t)(8 * (H8 + 4) + tail) * sizeof(float);
+  const dim3 block(64);
+  const int tb_lds = (int)(65536 / per_tok);  // tokens whose staged chains fit 64 KiB of LDS
+  if (T <= 32 || tb_lds < 2) {
+    router_lane8_kernel<1><<<dim3((E + 7) / 8, T), block, per_tok, s>>>(w8, E, H, x, T, logits, status);
+  } else if (T <= 256 || tb_lds < 4) {
+    router_lane8_kernel<2><<<dim3((E + 7) / 8, (T + 1) / 2), block, 2 * per_tok, s>>>(
+        w8, E, H, x, T, logits, status);
   } else {
-    size_t lds = (size_t)4 * (8 * (H8 + 1) + tail) * sizeof(float);
-    dim3 grid((E + 7) / 8, (T + 3) / 4);
-    router_lane8_kernel<4><<<grid, 64, lds, s>>>(w8, E, H, x, T, logits, status);
+    router_lane8_kernel<4><<<dim3((E + 7) / 8, (T + 3) / 4), block, 4 * per_tok, s>>>(
+        w8, E, H, x, T, logits, status);
   }
 }
 
-void launch_router_f64(const uint16_t* w, int E, int H, const float* x, int T, float* logits,
-                       int* status, hipStream_t s) {
-  dim3 grid((E + 3) / 4, (T + kF64Tokens - 1) / kF64Tokens);
-  router_f64_kernel<<<grid, 256, 0, s>>>(w, E, H, x, T, logits, status);
-}
-
 template <int EPL>
-static void launch_route_epl(const float* logits, int T, int E, int K, const RouteParams& p,
+static void launch_route_epl(float* logits, int T, int E, int K, const RouteParams& p,
                              int32_t* ids, float* weights, int32_t* asc, int* status,
                              hipStream_t s) {
   if (p.router == 0)
@@ -506,7 +475,7 @@ static void launch_route_epl(const float* logits, int T, int E, int K, const Rou
                                                          status);
 }
 
-void launch_route(const float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
+void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
                   float* weights, int32_t* asc, int* status, hipStream_t s) {
   const int epl = (E + 63) / 64;
   if (epl <= 1) launch_route_epl<1>(logits, T, E, K, p, ids, weights, asc, status, s);
