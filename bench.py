@@ -42,8 +42,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="all",
                     help="comma list of name:tokens (default: all seven runs)")
-    ap.add_argument("--cpu-seconds", type=float, default=4.0,
-                    help="CPU-baseline budget per run (headline run gets 2.5x)")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="CPU-baseline budget per run (the headline run gets 4x)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -86,6 +86,22 @@ def stage_bytes(spec, C, stage, tokens, distinct):
     return tokens * k * 16
 
 
+def measured_traffic(workload, tokens, stage):
+    """HBM bytes per launch of a stage's kernel from the committed counter measurement
+    (profiles/hbm_traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by
+    what the counter reads for a device copy of known size), or None when none matches."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            m = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for e in m.get("measurements", []):
+        if (e.get("workload"), e.get("tokens"), e.get("stage")) == (workload, tokens, stage):
+            return e.get("bytes_per_launch")
+    return None
+
+
 def cpu_baseline(name, spec, C, dev, x, budget_s, threads):
     """The CPU oracle (a C++ restatement of the reference's CPU path) timed on a bounded
     sample of the same workload's tokens, one worker per core."""
@@ -100,12 +116,17 @@ def cpu_baseline(name, spec, C, dev, x, budget_s, threads):
     O.moe_forward(spec, host.experts, host.router_weight, xs[:1], host.correction_bias,
                   host.shared, threads=threads)
     one = time.perf_counter() - t0
+    # tokens per call: the whole batch when a call fits the budget, else a prefix that does;
+    # whole calls repeat until the budget is spent
     n = int(max(1, min(T, budget_s / max(one, 1e-6))))
-    reps = 1 if n > 1 else int(max(1, min(20, budget_s / max(one, 1e-6))))
+    reps = 0
     t0 = time.perf_counter()
-    for _ in range(reps):
+    while True:
         O.moe_forward(spec, host.experts, host.router_weight, xs[:n], host.correction_bias,
                       host.shared, threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s or reps >= 5000:
+            break
     dt = (time.perf_counter() - t0) / reps
     return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{name}: first {n} of {T} tokens x{reps}, {dt * 1e3:.1f} ms per call, "
@@ -228,7 +249,7 @@ def main():
     for name, T in runs:
         log(f"run {name} T={T}")
         head = (name, T) == HEADLINE
-        budget = args.cpu_seconds * (2.5 if head else 1.0)
+        budget = args.cpu_seconds * (4.0 if head else 1.0)
         rec = run_one(name, T, args, not args.no_cpu, budget)
         log(f"  {rec['tokens_per_s']:.1f} tok/s, {rec['ms_per_call']:.3f} ms, "
             f"{rec['GBps']:.0f} GB/s ({100 * rec['hbm_frac']:.1f}% HBM), dominant "
@@ -256,7 +277,8 @@ def main():
         "roofline": {
             "kernel": head["dominant_stage"], "bound": "hbm",
             "achieved": dom.get("GBps"), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": (dom.get("GBps") or 0) / (HBM_PEAK / 1e9), "traffic": None,
+            "frac": (dom.get("GBps") or 0) / (HBM_PEAK / 1e9),
+            "traffic": measured_traffic(head["workload"], head["tokens"], head["dominant_stage"]),
             "bytes_per_launch": dom.get("bytes"), "avg_launch_us": dom.get("avg_us"),
         },
         "cpu_baseline": head.get("cpu_baseline"),

@@ -295,6 +295,32 @@ def test_gated_mlp_formula_kat():
     assert abs(y[1] - (first - second)) < k["tolerance"]
 
 
+def test_qwen_expert_bf16_boundaries():
+    # Qwen38Expert::forward_projections (src/models/qwen3_8/expert.rs:137-207): g and u are the
+    # 8-lane FP32 GEMV rounded to BF16, a = bf16(bf16(silu(g)) * u), y = bf16(down . a).
+    # Restated with torch's RNE bfloat16 casts and a float64-evaluated SiLU rounded to f32; a
+    # dropped or misplaced rounding changes most outputs, a 1-ulp expf difference very few.
+    import torch
+    H, I = 64, 32
+    spec = C.small_spec(C.WORKLOADS["c1_bf16_decode"].spec, hidden=H, n_experts=2, intermediate=I)
+    layer = C.make_host_layer(spec)
+    trip = layer.experts[1]
+    bf = lambda a: torch.from_numpy(np.asarray(a, np.float32)).bfloat16().float().numpy()
+    for t in range(4):
+        x = synth.activations(f"x.qwen.{t}", 1, H)[0]
+        got = O.qwen_expert(trip, H, I, x)[0]
+        g = bf(O.bf16_matvec_rows_fp32(trip[0][0], I, H, x))
+        u = bf(O.bf16_matvec_rows_fp32(trip[1][0], I, H, x))
+        g64 = g.astype(np.float64)
+        silu = (g64 / (1.0 + np.exp(-g64))).astype(np.float32)
+        a = bf(bf(silu) * u)
+        want = bf(O.bf16_matvec_rows_fp32(trip[2][0], H, I, a))
+        same = np.mean(got.view(np.uint32) == want.view(np.uint32))
+        assert same >= 0.95, same
+        ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32)) >> 16
+        assert ulp.max() <= 1
+
+
 # ---------------------------------------------------------------------- layer composition
 def _tokenwise(layer: C.HostLayer, x: np.ndarray):
     """Second formulation: route and execute every token on its own, in the loop-nest order
