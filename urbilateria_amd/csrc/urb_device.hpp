@@ -14,6 +14,19 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// Loads through pointers that were themselves read from memory (the per-expert matrix table)
+// are generic (flat) to the compiler; flat loads also count against the LDS wait counter, so a
+// wait for an LDS read would drain every weight load in flight.  These name the global address
+// space explicitly.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldg_u8(const void* p) {
+  return *(const __attribute__((address_space(1))) uint8_t*)p;
+}
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
 
 // BF16 (little-endian u16) -> f32: the high half of the f32 bit pattern

@@ -29,48 +29,8 @@ constexpr int kNT = kGemmNTile;   // 64 weight rows: one 16-row panel per wave
 constexpr int kKS = kGemmKStep;   // 128 k per step
 constexpr int kALd = kKS + 8;     // LDS row pitch in bf16 (16 B pad against bank conflicts)
 
-typedef unsigned short u16;
 
-__device__ __forceinline__ u16 bf16_rne_bits(float v) {
-  uint32_t b = f2u(v);
-  return (u16)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
-}
 
-// k offset (within the K step) of MFMA j's operands for lane group lq.
-template <int FMT>
-__device__ __forceinline__ int frag_k(int j, int lq) {
-  return FMT == kFmtBF16 ? 32 * j + 8 * lq : 32 * lq + 8 * j;
-}
-
-__device__ __forceinline__ bf16x8 pack8(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) {
-  bf16x8 r;
-  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
-  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
-  return r;
-}
-
-// MFMA j's B operand from the raw step data (j is a compile-time constant after unrolling).
-template <int FMT>
-__device__ __forceinline__ bf16x8 decode_b(const BRaw<FMT>& r, int j) {
-  if constexpr (FMT == kFmtBF16) {
-    return __builtin_bit_cast(bf16x8, r.q[j]);
-  } else if constexpr (FMT == kFmtMXFP4) {
-    const float sc = e8m0_to_f32(r.s);
-    const uint32_t w = j == 0 ? r.q.x : j == 1 ? r.q.y : j == 2 ? r.q.z : r.q.w;
-    return pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0),
-                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1),
-                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2),
-                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
-  } else {
-    const float sc = e8m0_to_f32(r.s);
-    const uint4 q = r.q[j >> 1];
-    const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
-    return pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, false),
-                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true),
-                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false),
-                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true));
-  }
-}
 
 // A staging: thread t covers row t/8 and 16 consecutive k at 16*(t%8) of the K step.
 struct AStage { float4 v[4]; };
@@ -412,14 +372,14 @@ static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles
 }
 
 // Weight steps in flight per wave (DEPTH) and panels per wave (NP), per format.  BF16 steps are
-// 4 KiB per panel, so one panel two steps deep; the MX formats stream 1-2 KiB per panel and
+// 4 KiB per panel, so one panel one step deep; the MX formats stream 1-2 KiB per panel and
 // step and need more panels per staged activation tile (activations are 2-4x their bytes).
 // Rows are multiples of 128 (urb_moe_create), so NP = 2 always tiles them.
 template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                    const float* in, float* out, int qwen, int* status, hipStream_t s) {
   if constexpr (FMT == kFmtBF16)
-    launch_shape<FMT, PAIR, PAIR ? 2 : 1, 1>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+    launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
   else if constexpr (FMT == kFmtMXFP8)
     launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
   else if (rows % (kNT * 4) == 0)

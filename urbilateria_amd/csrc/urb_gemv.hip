@@ -7,7 +7,8 @@
 // (BF16: 8 columns per unit; MX: one whole 32-column block, decoded with the CDNA4
 // v_cvt_scalef32_pk_f32_fp4/fp8 conversions and scaled once per block, which is exact
 // multiplication by 2^k of the block partial), against the input vector staged in LDS.  The
-// four lq lanes are summed by shuffles and the K parts through LDS, in a fixed order.
+// four lq lanes are summed by shuffles and the K parts through LDS, in a fixed order.  (FMA
+// lanes beat the matrix cores here: with one token, 15 of an MFMA's 16 rows would be zero.)
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
 #include "urb_panel.hpp"
@@ -93,8 +94,6 @@ __device__ __forceinline__ bool perm_expert(const Perm& perm, int a, int& expert
   return true;
 }
 
-// PAIR = gate+up rows with the SwiGLU epilogue (rows I, cols H, input x[token]); otherwise
-// down rows (rows H, cols I, input act[position]).  Every active expert has one token.
 template <int FMT, bool PAIR, int DEPTH>
 __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict__ mats,
                                                    Perm perm, int rows, int cols, int ksplit,
@@ -214,21 +213,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict_
   if (bad) flag(status, kStatusNonFinite);
 }
 
-// Weight steps in flight per wave (~8 KiB per matrix).
-template <int FMT>
+// Weight steps in flight per wave: 4 KiB BF16 steps one (gate+up) or two (down) deep, 1 KiB
+// MXFP4 and 2 KiB MXFP8 steps four deep.
+template <int FMT, bool PAIR>
 constexpr int gemv_depth() {
-  return FMT == kFmtBF16 ? 2 : (FMT == kFmtMXFP4 ? 8 : 4);
+  return FMT == kFmtBF16 ? (PAIR ? 1 : 2) : 4;
 }
 
 template <int FMT, bool PAIR>
 static void launch_gemv(const ExpertMats* mats, const Perm& perm, int max_active, int rows,
                         int cols, const float* in, float* out, int qwen, int* status,
                         hipStream_t s) {
-  constexpr int D = gemv_depth<FMT>();
+  constexpr int D = gemv_depth<FMT, PAIR>();
   const int panels = rows / kPanelRows, steps = cols / kGemmKStep;
-  // Split K until the launch has ~4096 waves, keeping at least DEPTH steps per part.
+  // Split K until the launch has ~2048 waves (8 per CU), keeping at least DEPTH steps per part.
   int ksplit = 1;
-  while (ksplit < 4 && (long)panels * max_active * ksplit < 4096 && steps / (2 * ksplit) >= D)
+  while (ksplit < 4 && (long)panels * max_active * ksplit < 2048 && steps / (2 * ksplit) >= D)
     ksplit *= 2;
   const int ppw = 4 / ksplit;
   dim3 grid((panels + ppw - 1) / ppw, max_active);

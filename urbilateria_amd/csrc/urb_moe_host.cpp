@@ -257,7 +257,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
 
   // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
   const size_t Ep = urb::router_rows((int)E);
-  size_t arena = align_up(Ep * H * 2) + (qwen ? align_up(E * H * 2) : align_up(Ep * H * 2)) +
+  size_t arena = align_up(Ep * H * 2) + (qwen ? align_up((E + 7) / 8 * 8 * H * 2) : align_up(Ep * H * 2)) +
                  align_up(E * 4);
   size_t wbytes = 0;
   if (!borrow) {
@@ -276,7 +276,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   c->weight_bytes = wbytes;
   Bump ab{static_cast<char*>(c->arena)};
   uint16_t* router = ab.take<uint16_t>(Ep * H);
-  c->router_lane8 = qwen ? ab.take<uint16_t>(E * H) : nullptr;
+  c->router_lane8 = qwen ? ab.take<uint16_t>((E + 7) / 8 * 8 * H) : nullptr;
   c->router_panel = qwen ? nullptr : ab.take<uint8_t>(Ep * H * 2);
   float* bias = ab.take<float>(E);
   c->table = ab.take<ExpertMats>(E);

@@ -7,23 +7,34 @@ namespace urb {
 // ------------------------------------------------------------------------------------------
 // Qwen router: `linear(router)` = Bf16Matrix::matvec_fp32 + BF16 (src/models/qwen3_8/math.rs:
 // 10-26).  The reference GEMV is the 8-lane FP32 FMA tree (src/model/bf16.rs:589-610): lane j
-// accumulates columns == j (mod 8) in order, lanes are summed 0..7, the tail is added with a
-// separate multiply and add.  One thread per (expert, lane) runs that exact chain, so the BF16
-// logits -- and hence their exact ties -- are bit-identical to the reference.
-// The weights are re-laid out once at create time so that each chain is contiguous:
-//   w8[e][j][i] = w[e][8 i + j] for i < H/8, then the H % 8 tail columns of row e.
+// accumulates columns == j (mod 8) in order, lanes are summed 0..7 (H is a multiple of 128
+// here, so there is no tail).  One thread per (expert, lane) runs that exact chain, so the
+// BF16 logits -- and hence their exact ties -- are bit-identical to the reference.  The
+// weights are re-laid out once at create time so that every load instruction of a wavefront
+// reads 1 KiB of consecutive chain elements.
 // ------------------------------------------------------------------------------------------
 
-__global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E, int H,
+// Lane-chain layout of the QWEN36 router: lane l = 8 el + j of the wavefront that owns experts
+// [8 g, 8 g + 8) accumulates chain (expert 8 g + el, lane j) = columns j, 8 + j, 16 + j, ...
+// of that expert.  Chain elements are stored so that each 16-element batch b of every lane is
+// two 1 KiB runs (halves h) in lane order: element 16 b + 8 h + k of lane l sits at
+// (((g * H / 128 + b) * 2 + h) * 64 + l) * 8 + k.  `w` has rows zero-padded to a multiple of 8.
+__global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E8, int H,
                                       uint16_t* __restrict__ w8) {
-  const int H8 = H / 8;
-  size_t n = (size_t)E * H;
+  const size_t n = (size_t)E8 * H;
+  const int nb = H / 128;
   for (size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x; idx < n;
        idx += (size_t)gridDim.x * blockDim.x) {
-    size_t e = idx / H;
-    int c = (int)(idx % H);
-    size_t dst = c < 8 * H8 ? e * H + (size_t)(c % 8) * H8 + c / 8 : idx;
-    w8[dst] = w[idx];
+    const int k = (int)(idx & 7);
+    const int l = (int)((idx >> 3) & 63);
+    const size_t rest = idx >> 9;  // (g * nb + b) * 2 + h
+    const int h = (int)(rest & 1);
+    const size_t gb = rest >> 1;
+    const int b = (int)(gb % nb);
+    const size_t g = gb / nb;
+    const size_t e = 8 * g + (l >> 3);
+    const int i = 16 * b + 8 * h + k;
+    w8[idx] = w[e * H + 8 * (size_t)i + (l & 7)];
   }
 }
 
@@ -36,37 +47,36 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
                                                           const float* __restrict__ x, int T,
                                                           float* __restrict__ logits,
                                                           int* status) {
-  // [tok][8][H8 + 4] transposed chains (the pad of 4 floats puts the 8 chains of a column in
-  // different LDS banks and keeps 16-byte alignment), then [tok][tail]
+  // [tok][8][H8 + 4] transposed chains: the pad of 4 floats puts the 8 chains of a column in
+  // different LDS banks and keeps 16-byte alignment.  H is a multiple of 128.
   extern __shared__ float xs[];
-  const int H8 = H / 8, tail = H - 8 * H8, H8p = H8 + 4;
+  const int H8 = H / 8, H8p = H8 + 4;
   const int t0 = blockIdx.y * kLane8Tokens;
   const int nt = min(kLane8Tokens, T - t0);
-  float* xt = xs + kLane8Tokens * 8 * H8p;
-  const int el = threadIdx.x >> 3, j = threadIdx.x & 7;
+  const int lane = threadIdx.x;
+  const int el = lane >> 3, j = lane & 7;
   const int e = blockIdx.x * 8 + el;
-  const uint16_t* chain = w8 + (size_t)min(e, E - 1) * H + (size_t)j * H8;
-  const int nb = H8 / 16;  // H is a multiple of 128, so chains are whole batches
+  const uint16_t* chains = w8 + (size_t)blockIdx.x * 8 * H + 8 * lane;
+  const int nb = H8 / 16;
   // The first kLane8Ring batches are requested before the activations are staged.
   uint4 ring[kLane8Ring][2];
 #pragma unroll
   for (int d = 0; d < kLane8Ring; ++d)
     if (d < nb) {
-      ring[d][0] = reinterpret_cast<const uint4*>(chain)[2 * d];
-      ring[d][1] = reinterpret_cast<const uint4*>(chain)[2 * d + 1];
+      ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d) * 512);
+      ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d + 1) * 512);
     }
   // Stage x with coalesced float4 loads, transposed into per-lane chains.
   bool bad = false;
   const int n4 = nt * H / 4;
-  for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+  for (int i = lane; i < n4; i += 64) {
     const float4 v4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H)[i];
     const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int flat = 4 * i + u, tt = flat / H, c = flat - tt * H;
       bad |= !finite(vv[u]);
-      if (c < 8 * H8) xs[(tt * 8 + (c & 7)) * H8p + (c >> 3)] = vv[u];
-      else xt[tt * tail + (c - 8 * H8)] = vv[u];
+      xs[(tt * 8 + (c & 7)) * H8p + (c >> 3)] = vv[u];
     }
   }
   if (bad) flag(status, kStatusNonFinite);
@@ -74,46 +84,41 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
   float acc[kLane8Tokens];
 #pragma unroll
   for (int tt = 0; tt < kLane8Tokens; ++tt) acc[tt] = 0.0f;
-  if (e < E) {
-    const float* xj = xs + j * H8p;
-    for (int b0 = 0; b0 < nb; b0 += kLane8Ring) {
+  const float* xj = xs + j * H8p;
+  for (int b0 = 0; b0 < nb; b0 += kLane8Ring) {
 #pragma unroll
-      for (int d = 0; d < kLane8Ring; ++d) {
-        const int b = b0 + d;
-        if (b >= nb) break;
-        const uint4 qa = ring[d][0], qb = ring[d][1];
-        if (b + kLane8Ring < nb) {
-          ring[d][0] = reinterpret_cast<const uint4*>(chain)[2 * (b + kLane8Ring)];
-          ring[d][1] = reinterpret_cast<const uint4*>(chain)[2 * (b + kLane8Ring) + 1];
-        }
-        const float wv[16] = {bf16_lo(qa.x), bf16_hi(qa.x), bf16_lo(qa.y), bf16_hi(qa.y),
-                              bf16_lo(qa.z), bf16_hi(qa.z), bf16_lo(qa.w), bf16_hi(qa.w),
-                              bf16_lo(qb.x), bf16_hi(qb.x), bf16_lo(qb.y), bf16_hi(qb.y),
-                              bf16_lo(qb.z), bf16_hi(qb.z), bf16_lo(qb.w), bf16_hi(qb.w)};
+    for (int d = 0; d < kLane8Ring; ++d) {
+      const int b = b0 + d;
+      if (b >= nb) break;
+      const uint4 qa = ring[d][0], qb = ring[d][1];
+      if (b + kLane8Ring < nb) {
+        ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + kLane8Ring)) * 512);
+        ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + kLane8Ring) + 1) * 512);
+      }
+      const float wv[16] = {bf16_lo(qa.x), bf16_hi(qa.x), bf16_lo(qa.y), bf16_hi(qa.y),
+                            bf16_lo(qa.z), bf16_hi(qa.z), bf16_lo(qa.w), bf16_hi(qa.w),
+                            bf16_lo(qb.x), bf16_hi(qb.x), bf16_lo(qb.y), bf16_hi(qb.y),
+                            bf16_lo(qb.z), bf16_hi(qb.z), bf16_lo(qb.w), bf16_hi(qb.w)};
 #pragma unroll
-        for (int tt = 0; tt < kLane8Tokens; ++tt) {
-          if (tt < nt) {
-            const float4* xv = reinterpret_cast<const float4*>(xj + tt * 8 * H8p + 16 * b);
-            const float4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
-            const float xf[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
-                                  x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+      for (int tt = 0; tt < kLane8Tokens; ++tt) {
+        if (tt < nt) {
+          const float4* xv = reinterpret_cast<const float4*>(xj + tt * 8 * H8p + 16 * b);
+          const float4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
+          const float xf[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                                x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
 #pragma unroll
-            for (int k = 0; k < 16; ++k) acc[tt] = fmaf(wv[k], xf[k], acc[tt]);
-          }
+          for (int k = 0; k < 16; ++k) acc[tt] = fmaf(wv[k], xf[k], acc[tt]);
         }
       }
     }
   }
-  // Lane sum in lane order 0..7, then the tail with separate multiply and add.
+  // Lane sum in lane order 0..7 (the reference's horizontal sum of the 8 FMA lanes).
   const int base = el * 8;
   for (int tt = 0; tt < kLane8Tokens; ++tt) {
     float sum = __shfl(acc[tt], base + 0, 64);
 #pragma unroll
     for (int u = 1; u < 8; ++u) sum = __fadd_rn(sum, __shfl(acc[tt], base + u, 64));
     if (e < E && j == 0 && tt < nt) {
-      const uint16_t* tw = w8 + (size_t)e * H + 8 * H8;
-      for (int c = 0; c < tail; ++c)
-        sum = __fadd_rn(sum, __fmul_rn(u2f((uint32_t)tw[c] << 16), xt[tt * tail + c]));
       float r;
       if (!rne_bf16(sum, &r)) {
         flag(status, kStatusNonFinite);
@@ -198,15 +203,22 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
     double acc[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) acc[i] = 0.0;
-    for (int z = 0; z < rp.slices; ++z) {
-      double pz[EPL];
+    // ZB slices' loads in flight at once, then added in slice order
+    constexpr int ZB = EPL >= 8 ? 4 : (EPL >= 4 ? 8 : 16);
+    for (int z0 = 0; z0 < rp.slices; z0 += ZB) {
+      double pz[ZB][EPL];
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        const int e = lane + 64 * i;
-        pz[i] = e < E ? pt[z * slice + e] : 0.0;
-      }
+      for (int zz = 0; zz < ZB; ++zz)
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) acc[i] += pz[i];
+        for (int i = 0; i < EPL; ++i) {
+          const int e = lane + 64 * i;
+          pz[zz][i] = (z0 + zz < rp.slices && e < E) ? pt[(size_t)(z0 + zz) * slice + e] : 0.0;
+        }
+#pragma unroll
+      for (int zz = 0; zz < ZB; ++zz)
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          if (z0 + zz < rp.slices) acc[i] += pz[zz][i];
     }
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
@@ -437,22 +449,22 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
   }
 }
 
-// ------------------------------------------------------------------------------------------
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s) {
-  size_t n = (size_t)E * H;
-  int blocks = (int)std::min<size_t>((n + 255) / 256, 65535);
-  relayout_lane8_kernel<<<blocks, 256, 0, s>>>(w, E, H, w8);
+  const int E8 = (E + 7) / 8 * 8;
+  const size_t n = (size_t)E8 * H;
+  const int blocks = (int)std::min<size_t>((n + 255) / 256, 65535);
+  relayout_lane8_kernel<<<blocks, 256, 0, s>>>(w, E8, H, w8);
 }
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int* status, hipStream_t s) {
-  // One token per block gives the most independent waves; with more tokens, 2 or 4 tokens
+  // One token per block gives the most independent waves; beyond 512 tokens, 2 or 4 tokens
   // share each weight chain (independent FMA chains interleave in the lane).
-  const int H8 = H / 8, tail = H - 8 * H8;
-  const size_t per_tok = (size_t)(8 * (H8 + 4) + tail) * sizeof(float);
+  const int H8 = H / 8;
+  const size_t per_tok = (size_t)8 * (H8 + 4) * sizeof(float);
   const dim3 block(64);
   const int tb_lds = (int)(65536 / per_tok);  // tokens whose staged chains fit 64 KiB of LDS
-  if (T <= 32 || tb_lds < 2) {
+  if (T <= 512 || tb_lds < 2) {
     router_lane8_kernel<1><<<dim3((E + 7) / 8, T), block, per_tok, s>>>(w8, E, H, x, T, logits, status);
   } else if (T <= 256 || tb_lds < 4) {
     router_lane8_kernel<2><<<dim3((E + 7) / 8, (T + 1) / 2), block, 2 * per_tok, s>>>(
