@@ -87,6 +87,13 @@ __device__ __forceinline__ bool perm_expert(const Perm& perm, int a, int& expert
     count = perm.dense_tokens;
     return true;
   }
+  if (perm.direct) {
+    if (a >= perm.direct_k) return false;
+    expert = perm.direct[a];
+    base = a;
+    count = 1;
+    return true;
+  }
   if (a >= perm.meta[0]) return false;
   expert = perm.active[a];
   base = perm.offsets[expert];
@@ -132,7 +139,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict_
       }
   }
   const int p = base;  // the expert's one permuted position
-  const float* src = PAIR ? in + (size_t)(perm.dense_tokens > 0 ? p : perm.perm_token[p]) * cols
+  const int token = perm.dense_tokens > 0 ? p : (perm.direct ? 0 : perm.perm_token[p]);
+  const float* src = PAIR ? in + (size_t)token * cols
                           : in + (size_t)p * cols;
   {
     const float4* s4 = reinterpret_cast<const float4*>(src);
@@ -213,11 +221,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict_
   if (bad) flag(status, kStatusNonFinite);
 }
 
-// Weight steps in flight per wave: 4 KiB BF16 steps one (gate+up) or two (down) deep, 1 KiB
-// MXFP4 and 2 KiB MXFP8 steps four deep.
+// Weight steps in flight per wave: one 4 KiB BF16 step or two 1-2 KiB MX steps (more only
+// costs registers: measured on MI355X, deeper rings were slower).
 template <int FMT, bool PAIR>
 constexpr int gemv_depth() {
-  return FMT == kFmtBF16 ? (PAIR ? 1 : 2) : 4;
+  return FMT == kFmtBF16 ? 1 : 2;
 }
 
 template <int FMT, bool PAIR>
@@ -226,9 +234,9 @@ static void launch_gemv(const ExpertMats* mats, const Perm& perm, int max_active
                         hipStream_t s) {
   constexpr int D = gemv_depth<FMT, PAIR>();
   const int panels = rows / kPanelRows, steps = cols / kGemmKStep;
-  // Split K until the launch has ~2048 waves (8 per CU), keeping at least DEPTH steps per part.
+  // Split K until the launch has ~4096 waves (16 per CU), keeping at least DEPTH steps per part.
   int ksplit = 1;
-  while (ksplit < 4 && (long)panels * max_active * ksplit < 2048 && steps / (2 * ksplit) >= D)
+  while (ksplit < 4 && (long)panels * max_active * ksplit < 4096 && steps / (2 * ksplit) >= D)
     ksplit *= 2;
   const int ppw = 4 / ksplit;
   dim3 grid((panels + ppw - 1) / ppw, max_active);
@@ -280,7 +288,7 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
   for (int j = 0; j < KMAX; ++j) {
     if (j < K) {
       wt[j] = w[(size_t)t * K + rk[j]];
-      const int p = pos[(size_t)t * K + rk[j]];
+      const int p = pos ? pos[(size_t)t * K + rk[j]] : rk[j];
       v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
     }
   }
@@ -319,7 +327,7 @@ __global__ __launch_bounds__(256) void combine_glm_kernel(const float* __restric
   for (int j = 0; j < KMAX; ++j) {
     if (j < K) {
       wt[j] = w[(size_t)t * K + j];
-      const int p = pos[(size_t)t * K + j];
+      const int p = pos ? pos[(size_t)t * K + j] : j;
       v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
     }
   }

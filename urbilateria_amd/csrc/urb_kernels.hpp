@@ -43,6 +43,10 @@ struct Perm {
   const int32_t* perm_token;  // [T * k] token of each permuted position
   int dense_tokens;           // > 0: one dense expert (table entry 0) over tokens 0..n-1
   const int32_t* tiles;       // [2 * tiles] (expert, first row) of each kGemmMTile-row tile
+  // One token (decode): the token's ranked expert ids; slot a is expert direct[a] at permuted
+  // position a.  No permutation kernel runs; the fields above are unused.
+  const int32_t* direct;
+  int direct_k;
 };
 
 // Grouped GEMM (MFMA) tiling: tokens per tile, weight rows per workgroup (four panels), K per

@@ -477,7 +477,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       // routes: it runs on the side stream while the router, top-k and permutation run here.
       URB_HIP(hipEventRecord(c->fork, s));
       URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
-      Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr};
+      Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
       const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
       {
         Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
@@ -500,12 +500,15 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       URB_HIP(hipEventRecord(c->join, c->side));
     }
     route_chunk(c, xc, n, ws.logits, idc, wc, s);
-    {
+    // One token: the GEMVs read the ranked ids directly (slot a at permuted position a).
+    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles,
+              n == 1 ? idc : nullptr, K};
+    if (n > 1) {
       Span span(c, URB_STAGE_PERMUTE, s);
       urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts,
                           ws.perm_token, ws.pos_of_slot, ws.tiles, s);
     }
-    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles};
+    const int32_t* pos = n == 1 ? nullptr : ws.pos_of_slot;
     const int max_active = std::min(E, n * K);
     const int max_tiles = urb::gemm_max_tiles(n, K, E);
     // One token: row-parallel GEMV.  Several: grouped MFMA GEMM over the row tiles.
@@ -531,11 +534,10 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     {
       Span span(c, URB_STAGE_COMBINE, s);
       if (qwen)
-        urb::launch_combine_qwen(ws.y_perm, ws.pos_of_slot, wc, ws.asc, n, K, H, yc, ws.status,
-                                 s);
+        urb::launch_combine_qwen(ws.y_perm, pos, wc, ws.asc, n, K, H, yc, ws.status, s);
       else
-        urb::launch_combine_glm(ws.y_perm, ws.pos_of_slot, wc,
-                                has_shared ? ws.shared_out : nullptr, n, K, H, yc, s);
+        urb::launch_combine_glm(ws.y_perm, pos, wc, has_shared ? ws.shared_out : nullptr, n, K,
+                                H, yc, s);
     }
     if (c->profiling) {
       urb_status st = collect_spans(c);
