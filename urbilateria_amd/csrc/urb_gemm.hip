@@ -24,67 +24,20 @@
 
 namespace urb {
 
-constexpr int kMT = kGemmMTile;   // 32 tokens: two 16-row MFMA blocks
-constexpr int kNT = kGemmNTile;   // 64 weight rows: one 16-row panel per wave
-constexpr int kKS = kGemmKStep;   // 128 k per step
-constexpr int kALd = kKS + 8;     // LDS row pitch in bf16 (16 B pad against bank conflicts)
-
-
-
-
-// A staging: thread t covers row t/8 and 16 consecutive k at 16*(t%8) of the K step.
-struct AStage { float4 v[4]; };
-
-__device__ __forceinline__ void load_a(AStage& a, const float* __restrict__ src, bool valid,
-                                       int k0) {
-  const int kc = (threadIdx.x & 7) * 16;
-  if (valid) {
-    const float4* p = reinterpret_cast<const float4*>(src + k0 + kc);
-    a.v[0] = p[0]; a.v[1] = p[1]; a.v[2] = p[2]; a.v[3] = p[3];
-  } else {
-    a.v[0] = a.v[1] = a.v[2] = a.v[3] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-}
-
-// Writes hi/lo BF16 halves of the staged values; returns whether any lo half is non-zero.
-__device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo) {
-  const int m = threadIdx.x >> 3, kc = (threadIdx.x & 7) * 16;
-  const float* v = reinterpret_cast<const float*>(a.v);
-  u16 h[16], l[16];
-  bool any = false;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    h[i] = bf16_rne_bits(v[i]);
-    float rest = v[i] - u2f((uint32_t)h[i] << 16);
-    l[i] = bf16_rne_bits(rest);
-    any |= (l[i] & 0x7fff) != 0;
-  }
-  uint4* dh = reinterpret_cast<uint4*>(hi + m * kALd + kc);
-  uint4* dl = reinterpret_cast<uint4*>(lo + m * kALd + kc);
-  dh[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
-  dh[1] = make_uint4(h[8] | (h[9] << 16), h[10] | (h[11] << 16), h[12] | (h[13] << 16), h[14] | (h[15] << 16));
-  dl[0] = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
-  dl[1] = make_uint4(l[8] | (l[9] << 16), l[10] | (l[11] << 16), l[12] | (l[13] << 16), l[14] | (l[15] << 16));
-  return any;
-}
-
-__device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + m * kALd + k));
-}
-
-template <int N>
-using Int = std::integral_constant<int, N>;
 
 // NP panels per wave (the workgroup covers 4 NP panels = 64 NP weight rows): every staged
-// activation fragment feeds NP (x2 for gate+up) MFMAs.
-template <int FMT, bool PAIR, int DEPTH, int NP>
+// activation fragment feeds NP (x2 for gate+up) MFMAs.  MT tokens per tile (32 or 64; 64 for
+// large dense batches, so each weight byte feeds twice the MFMAs before it is re-read).
+template <int FMT, bool PAIR, int DEPTH, int NP, int MT>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
                                                       Perm perm, int rows, int K,
                                                       const float* __restrict__ in,
                                                       float* __restrict__ out, int qwen,
                                                       int* status) {
-  __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
-  __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
+  constexpr int RG = MT / 32;       // staging rows per thread
+  constexpr int MBMAX = MT / 16;    // 16-token MFMA blocks per tile
+  __shared__ __attribute__((aligned(16))) u16 a_hi[2][MT * kALd];
+  __shared__ __attribute__((aligned(16))) u16 a_lo[2][MT * kALd];
 
   // ---- which tile
   const int w = blockIdx.y;
@@ -93,7 +46,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     expert = 0;
     base = 0;
     count = perm.dense_tokens;
-    m0 = w * kMT;
+    m0 = w * MT;
     if (m0 >= count) return;
   } else {
     if (w >= perm.meta[1]) return;
@@ -102,7 +55,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     base = perm.offsets[expert];
     count = perm.counts[expert];
   }
-  const int mrows = min(kMT, count - m0);
+  const int mrows = min(MT, count - m0);
   const ExpertMats m = mats[expert];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lq = lane >> 4;
@@ -115,21 +68,27 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   const uint8_t* pd1 = PAIR ? m.data[1] + panel0 * pbytes + 16 * lane : nullptr;
   const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + panel0 * pscales + lane : nullptr;
 
-  // ---- A source row of this thread's staging slot
+  // ---- A source rows of this thread's staging slots: rows am + 32 g
   const int am = threadIdx.x >> 3;
-  const bool a_valid = am < mrows;
-  const float* a_src = in;
-  if (a_valid) {
-    const int p = base + m0 + am;
-    const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
-    a_src = in + (size_t)src_row * K;
+  bool a_valid[RG];
+  const float* a_src[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const int r = am + 32 * g;
+    a_valid[g] = r < mrows;
+    a_src[g] = in;
+    if (a_valid[g]) {
+      const int p = base + m0 + r;
+      const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
+      a_src[g] = in + (size_t)src_row * K;
+    }
   }
 
-  f32x4 acc0[NP][2], acc1[NP][2];
+  f32x4 acc0[NP][MBMAX], acc1[NP][MBMAX];
 #pragma unroll
   for (int q = 0; q < NP; ++q)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < MBMAX; ++i) {
       acc0[q][i] = f32x4{0.f, 0.f, 0.f, 0.f};
       acc1[q][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -145,12 +104,19 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
         if constexpr (PAIR) load_b<FMT>(r1[d][q], pd1 + q * pbytes, ps1 + q * pscales, s);
       }
     };
+    auto stage = [&](AStage (&as)[RG], int buf) {
+      bool any = false;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) any |= store_a(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
+      return any;
+    };
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
       if (d < steps) fetch(d, d);
-    AStage as;
-    load_a(as, a_src, a_valid, 0);
-    bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
+    AStage as[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], a_valid[g], 0);
+    bool lo_any = __syncthreads_or(stage(as, 0));
     for (int s0 = 0; s0 < steps; s0 += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
@@ -158,7 +124,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
         if (s >= steps) break;
         const int buf = s & 1;
         const bool more = s + 1 < steps;
-        if (more) load_a(as, a_src, a_valid, (s + 1) * kKS);
+        if (more) {
+#pragma unroll
+          for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], a_valid[g], (s + 1) * kKS);
+        }
         BRaw<FMT> c0[NP], c1[NP];
 #pragma unroll
         for (int q = 0; q < NP; ++q) {
@@ -197,12 +166,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
             }
           }
         }
-        if (more) lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
+        if (more) lo_any = __syncthreads_or(stage(as, buf ^ 1));
       }
     }
   };
-  if (mrows > 16) body(Int<2>{});
-  else body(Int<1>{});
+  if constexpr (MT == 64) {
+    if (mrows > 32) body(Int<4>{});
+    else if (mrows > 16) body(Int<2>{});
+    else body(Int<1>{});
+  } else {
+    if (mrows > 16) body(Int<2>{});
+    else body(Int<1>{});
+  }
 
   // ---- epilogue: lane holds column `row` of panel q, rows 4*lq + i of each 16-row block
   bool bad = false;
@@ -210,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   for (int q = 0; q < NP; ++q) {
     const int row = (panel0 + q) * kPanelRows + ln;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MBMAX; ++mb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int mm = mb * 16 + 4 * lq + i;
@@ -246,129 +221,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   if (bad) flag(status, kStatusNonFinite);
 }
 
-// ------------------------------------------------------------------------------------------
-// Router logits (`router.matvec`, src/model/bf16.rs:121-216, ordered f64) for the GLM
-// composition: logits[t, e] = sum_k w[e, k] x[t, k].  BF16 weight times the hi/lo BF16 halves
-// of x are exact products; each MFMA sums 32 of them in f32 and that partial is added into an
-// f64 accumulator, so the f32 logit is the correctly rounded sum up to a few units in the last
-// place.  The router weight is in the panel layout with its rows padded to a multiple of 64
-// (zero rows).  Workgroup (x, y, z) covers experts [64 x, 64 x + 64), tokens [32 y, 32 y + 32)
-// and K steps [z * slice, (z + 1) * slice) and writes f64 partial sums part[z][t][e]; the
-// routing kernel adds the slices in order.
-// ------------------------------------------------------------------------------------------
-template <int DEPTH>
-__global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __restrict__ wp,
-                                                             int Epad, int H,
-                                                             const float* __restrict__ x,
-                                                             int T, int slice,
-                                                             double* __restrict__ part,
-                                                             int* status) {
-  __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
-  __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
-  const int m0 = blockIdx.y * kMT;
-  const int mrows = min(kMT, T - m0);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int ln = lane & 15, lq = lane >> 4;
-  const int panel = blockIdx.x * 4 + wave;
-  const int steps = H / kKS;
-  const int s_begin = blockIdx.z * slice, s_end = min(steps, s_begin + slice);
-  const uint8_t* pd = wp + (size_t)panel * (kPanelRows * panel_row_bytes<kFmtBF16>(H)) + 16 * lane;
-  const int am = threadIdx.x >> 3;
-  const bool a_valid = am < mrows;
-  const float* a_src = x + (size_t)(m0 + (a_valid ? am : 0)) * H;
-
-  double acc[2][4];
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[mb][i] = 0.0;
-
-  bool bad = false;
-  auto check = [&](const AStage& as) {
-    const float* v = reinterpret_cast<const float*>(as.v);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) bad |= !finite(v[i]);
-  };
-  auto body = [&](auto nmb) {
-    constexpr int NMB = decltype(nmb)::value;
-    BRaw<kFmtBF16> r[DEPTH];
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d)
-      if (s_begin + d < s_end) load_b<kFmtBF16>(r[d], pd, nullptr, s_begin + d);
-    AStage as;
-    load_a(as, a_src, a_valid, s_begin * kKS);
-    check(as);
-    bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = s_begin; s0 < s_end; s0 += DEPTH) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        const int s = s0 + d;
-        if (s >= s_end) break;
-        const int buf = (s - s_begin) & 1;
-        const bool more = s + 1 < s_end;
-        if (more) load_a(as, a_src, a_valid, (s + 1) * kKS);
-        const BRaw<kFmtBF16> c = r[d];
-        if (s + DEPTH < s_end) load_b<kFmtBF16>(r[d], pd, nullptr, s + DEPTH);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8 f = __builtin_bit_cast(bf16x8, c.q[j]);
-          const int kf = frag_k<kFmtBF16>(j, lq);
-#pragma unroll
-          for (int mb = 0; mb < NMB; ++mb) {
-            f32x4 pp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                lds_frag(a_hi[buf], mb * 16 + ln, kf), f, zero, 0, 0, 0);
-            if (lo_any)
-              pp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  lds_frag(a_lo[buf], mb * 16 + ln, kf), f, pp, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mb][i] += (double)pp[i];
-          }
-        }
-        if (more) {
-          check(as);
-          lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
-        }
-      }
-    }
-  };
-  if (mrows > 16) body(Int<2>{});
-  else body(Int<1>{});
-  if (bad && blockIdx.x == 0) flag(status, kStatusNonFinite);
-  const int e = panel * kPanelRows + ln;
-  double* out = part + (size_t)blockIdx.z * T * Epad;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int mm = mb * 16 + 4 * lq + i;
-      if (mm < mrows) out[(size_t)(m0 + mm) * Epad + e] = acc[mb][i];
-    }
-}
-
-int router_slices(int E, int H, int T) {
-  const int steps = H / kKS;
-  const int base = (router_rows(E) / kNT) * ((T + kMT - 1) / kMT);
-  int slices = std::min(kRouterMaxSlices, std::max(1, (512 + base - 1) / base));
-  slices = std::min(slices, std::max(1, steps / 2));
-  const int per = (steps + slices - 1) / slices;
-  return (steps + per - 1) / per;
-}
-
-void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
-                        int slices, int* status, hipStream_t s) {
-  const int steps = H / kKS;
-  const int per = (steps + slices - 1) / slices;
-  dim3 grid(router_rows(E) / kNT, (T + kMT - 1) / kMT, slices);
-  router_mfma_kernel<4><<<grid, 256, 0, s>>>(wp, router_rows(E), H, x, T, per, part, status);
-}
-
-template <int FMT, bool PAIR, int DEPTH, int NP>
+template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                          const float* in, float* out, int qwen, int* status, hipStream_t s) {
   dim3 grid(rows / (kNT * NP), max_tiles);
-  gemm_kernel<FMT, PAIR, DEPTH, NP><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, qwen,
-                                                          status);
+  gemm_kernel<FMT, PAIR, DEPTH, NP, MT><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, qwen,
+                                                              status);
 }
 
 // Weight steps in flight per wave (DEPTH) and panels per wave (NP), per format.  BF16 steps are

@@ -78,9 +78,11 @@ struct RouteParams {
   int slices;
 };
 
+
 // Router logits.
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int* status, hipStream_t s);
+
 // GLM router logits: MFMA BF16 with f64 accumulation of 32-k partials, split over K into
 // f64 partial slices.  The router weight is packed in the panel layout with router_rows(E)
 // rows (zero padding).

@@ -4,6 +4,8 @@
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
 
+#include <type_traits>
+
 namespace urb {
 
 enum { kFmtBF16 = 0, kFmtMXFP4 = 1, kFmtMXFP8 = 2 };
@@ -82,5 +84,59 @@ __device__ __forceinline__ bf16x8 decode_b(const BRaw<FMT>& r, int j) {
                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true));
   }
 }
+
+// ---- activation staging for the MFMA kernels (A operand through LDS) ----
+constexpr int kMT = kGemmMTile;   // 32 tokens: two 16-row MFMA blocks
+constexpr int kNT = kGemmNTile;   // 64 weight rows: one 16-row panel per wave
+constexpr int kKS = kGemmKStep;   // 128 k per step
+constexpr int kALd = kKS + 8;     // LDS row pitch in bf16 (16 B pad against bank conflicts)
+
+
+
+
+// A staging: thread t covers row t/8 and 16 consecutive k at 16*(t%8) of the K step.
+struct AStage { float4 v[4]; };
+
+__device__ __forceinline__ void load_a(AStage& a, const float* __restrict__ src, bool valid,
+                                       int k0) {
+  const int kc = (threadIdx.x & 7) * 16;
+  if (valid) {
+    const float4* p = reinterpret_cast<const float4*>(src + k0 + kc);
+    a.v[0] = p[0]; a.v[1] = p[1]; a.v[2] = p[2]; a.v[3] = p[3];
+  } else {
+    a.v[0] = a.v[1] = a.v[2] = a.v[3] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// Writes hi/lo BF16 halves of the staged values into LDS row m (default: this thread's staging
+// row); returns whether any lo half is non-zero.
+__device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
+                                        int m = (int)(threadIdx.x >> 3)) {
+  const int kc = (threadIdx.x & 7) * 16;
+  const float* v = reinterpret_cast<const float*>(a.v);
+  u16 h[16], l[16];
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    h[i] = bf16_rne_bits(v[i]);
+    float rest = v[i] - u2f((uint32_t)h[i] << 16);
+    l[i] = bf16_rne_bits(rest);
+    any |= (l[i] & 0x7fff) != 0;
+  }
+  uint4* dh = reinterpret_cast<uint4*>(hi + m * kALd + kc);
+  uint4* dl = reinterpret_cast<uint4*>(lo + m * kALd + kc);
+  dh[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+  dh[1] = make_uint4(h[8] | (h[9] << 16), h[10] | (h[11] << 16), h[12] | (h[13] << 16), h[14] | (h[15] << 16));
+  dl[0] = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+  dl[1] = make_uint4(l[8] | (l[9] << 16), l[10] | (l[11] << 16), l[12] | (l[13] << 16), l[14] | (l[15] << 16));
+  return any;
+}
+
+__device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + m * kALd + k));
+}
+
+template <int N>
+using Int = std::integral_constant<int, N>;
 
 }  // namespace urb

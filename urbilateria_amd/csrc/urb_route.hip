@@ -1,6 +1,9 @@
 // urb_route.hip -- router GEMV/GEMM, top-k routing and the token->expert permutation.
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
+#include "urb_panel.hpp"
+
+#include <algorithm>
 
 namespace urb {
 
@@ -181,17 +184,14 @@ __device__ __forceinline__ int argmax_round(const int32_t (&key)[EPL], const flo
   return id;
 }
 
+// Routes token t with the calling wavefront.  `sh` (kMaxExperts floats) and `grp` (64 floats)
+// are the wave's LDS scratch.
 template <int EPL, bool SOFTMAX>
-__global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, int T,
-                                                    int E, int K, RouteParams rp,
-                                                    int32_t* __restrict__ ids,
-                                                    float* __restrict__ weights,
-                                                    int32_t* __restrict__ asc, int* status) {
-  __shared__ float lds[4][kMaxExperts];
-  __shared__ float grp[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;
+__device__ void route_token(int t, float* __restrict__ logits, int T, int E, int K,
+                            const RouteParams& rp, int32_t* __restrict__ ids,
+                            float* __restrict__ weights, int32_t* __restrict__ asc, int* status,
+                            float* sh, float* grpw) {
+  const int lane = threadIdx.x & 63;
   float* lt = logits + (size_t)t * E;
   float v[EPL];
   bool open[EPL];
@@ -287,7 +287,6 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
     // route_noaux_tc (src/math/routing.rs:38-155).
     float g[EPL], sc[EPL];
     int32_t key[EPL];
-    float* sh = lds[wave];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
       const int e = lane + 64 * i;
@@ -312,13 +311,13 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
           if (k > k1) { k2 = k1; b2 = b1; k1 = k; b1 = sv; }
           else if (k > k2) { k2 = k; b2 = sv; }
         }
-        grp[wave][lane] = __fadd_rn(b1, b2);
+        grpw[lane] = __fadd_rn(b1, b2);
       }
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       // keep the top `topk_group` groups (score desc, id asc)
       const bool is_group = lane < rp.n_group;
-      const int32_t gk = is_group ? total_key(grp[wave][lane]) : INT32_MIN;
+      const int32_t gk = is_group ? total_key(grpw[lane]) : INT32_MIN;
       bool gopen = is_group, gsel = false;
       for (int r = 0; r < rp.topk_group; ++r) {
         const int32_t cand = gopen ? gk : INT32_MIN;
@@ -354,6 +353,21 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
       asc[(size_t)t * K + before] = lane;
     }
   }
+}
+
+template <int EPL, bool SOFTMAX>
+__global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, int T,
+                                                    int E, int K, RouteParams rp,
+                                                    int32_t* __restrict__ ids,
+                                                    float* __restrict__ weights,
+                                                    int32_t* __restrict__ asc, int* status) {
+  __shared__ float lds[4][kMaxExperts];
+  __shared__ float grp[4][64];
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  route_token<EPL, SOFTMAX>(t, logits, T, E, K, rp, ids, weights, asc, status, lds[wave],
+                            grp[wave]);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -449,6 +463,123 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// Router logits (`router.matvec`, src/model/bf16.rs:121-216, ordered f64) for the GLM
+// composition: logits[t, e] = sum_k w[e, k] x[t, k].  BF16 weight times the hi/lo BF16 halves
+// of x are exact products; each MFMA sums 32 of them in f32 and that partial is added into an
+// f64 accumulator, so the f32 logit is the correctly rounded sum up to a few units in the last
+// place.  The router weight is in the panel layout with its rows padded to a multiple of 64
+// (zero rows).  Workgroup (x, y, z) covers experts [64 x, 64 x + 64), tokens [32 y, 32 y + 32)
+// and K steps [z * slice, (z + 1) * slice) and writes f64 partial sums part[z][t][e]; the
+// routing kernel adds the slices in order.
+// ------------------------------------------------------------------------------------------
+template <int DEPTH>
+__global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __restrict__ wp,
+                                                             int Epad, int H,
+                                                             const float* __restrict__ x,
+                                                             int T, int slice,
+                                                             double* __restrict__ part,
+                                                             int* status) {
+  __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
+  __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
+  const int m0 = blockIdx.y * kMT;
+  const int mrows = min(kMT, T - m0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ln = lane & 15, lq = lane >> 4;
+  const int panel = blockIdx.x * 4 + wave;
+  const int steps = H / kKS;
+  const int s_begin = blockIdx.z * slice, s_end = min(steps, s_begin + slice);
+  const uint8_t* pd = wp + (size_t)panel * (kPanelRows * panel_row_bytes<kFmtBF16>(H)) + 16 * lane;
+  const int am = threadIdx.x >> 3;
+  const bool a_valid = am < mrows;
+  const float* a_src = x + (size_t)(m0 + (a_valid ? am : 0)) * H;
+
+  double acc[2][4];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[mb][i] = 0.0;
+
+  bool bad = false;
+  auto check = [&](const AStage& as) {
+    const float* v = reinterpret_cast<const float*>(as.v);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bad |= !finite(v[i]);
+  };
+  auto body = [&](auto nmb) {
+    constexpr int NMB = decltype(nmb)::value;
+    BRaw<kFmtBF16> r[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if (s_begin + d < s_end) load_b<kFmtBF16>(r[d], pd, nullptr, s_begin + d);
+    AStage as;
+    load_a(as, a_src, a_valid, s_begin * kKS);
+    check(as);
+    bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = s_begin; s0 < s_end; s0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int s = s0 + d;
+        if (s >= s_end) break;
+        const int buf = (s - s_begin) & 1;
+        const bool more = s + 1 < s_end;
+        if (more) load_a(as, a_src, a_valid, (s + 1) * kKS);
+        const BRaw<kFmtBF16> c = r[d];
+        if (s + DEPTH < s_end) load_b<kFmtBF16>(r[d], pd, nullptr, s + DEPTH);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 f = __builtin_bit_cast(bf16x8, c.q[j]);
+          const int kf = frag_k<kFmtBF16>(j, lq);
+#pragma unroll
+          for (int mb = 0; mb < NMB; ++mb) {
+            f32x4 pp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                lds_frag(a_hi[buf], mb * 16 + ln, kf), f, zero, 0, 0, 0);
+            if (lo_any)
+              pp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  lds_frag(a_lo[buf], mb * 16 + ln, kf), f, pp, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mb][i] += (double)pp[i];
+          }
+        }
+        if (more) {
+          check(as);
+          lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
+        }
+      }
+    }
+  };
+  if (mrows > 16) body(Int<2>{});
+  else body(Int<1>{});
+  if (bad && blockIdx.x == 0) flag(status, kStatusNonFinite);
+  const int e = panel * kPanelRows + ln;
+  double* out = part + (size_t)blockIdx.z * T * Epad;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int mm = mb * 16 + 4 * lq + i;
+      if (mm < mrows) out[(size_t)(m0 + mm) * Epad + e] = acc[mb][i];
+    }
+}
+
+int router_slices(int E, int H, int T) {
+  const int steps = H / kKS;
+  const int base = (router_rows(E) / kNT) * ((T + kMT - 1) / kMT);
+  int slices = std::min(kRouterMaxSlices, std::max(1, (512 + base - 1) / base));
+  slices = std::min(slices, std::max(1, steps / 2));
+  const int per = (steps + slices - 1) / slices;
+  return (steps + per - 1) / per;
+}
+
+void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
+                        int slices, int* status, hipStream_t s) {
+  const int steps = H / kKS;
+  const int per = (steps + slices - 1) / slices;
+  dim3 grid(router_rows(E) / kNT, (T + kMT - 1) / kMT, slices);
+  router_mfma_kernel<4><<<grid, 256, 0, s>>>(wp, router_rows(E), H, x, T, per, part, status);
+}
+
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s) {
   const int E8 = (E + 7) / 8 * 8;
   const size_t n = (size_t)E8 * H;
@@ -465,7 +596,8 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
   const dim3 block(64);
   const int tb_lds = (int)(65536 / per_tok);  // tokens whose staged chains fit 64 KiB of LDS
   if (T <= 512 || tb_lds < 2) {
-    router_lane8_kernel<1><<<dim3((E + 7) / 8, T), block, per_tok, s>>>(w8, E, H, x, T, logits, status);
+    router_lane8_kernel<1><<<dim3((E + 7) / 8, T), block, per_tok, s>>>(w8, E, H, x, T, logits,
+                                                                        status);
   } else if (T <= 256 || tb_lds < 4) {
     router_lane8_kernel<2><<<dim3((E + 7) / 8, (T + 1) / 2), block, 2 * per_tok, s>>>(
         w8, E, H, x, T, logits, status);
