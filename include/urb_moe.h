@@ -33,9 +33,14 @@ typedef enum {
  * MX formats use E8M0 scales per 32 consecutive columns of a row (MXFP8: ModelOpt 1x32). */
 typedef enum { URB_FMT_BF16 = 0, URB_FMT_MXFP4 = 1, URB_FMT_MXFP8 = 2 } urb_format;
 
-/* route_softmax_top_k (src/models/qwen3_8/moe.rs:91-159) or route_noaux_tc
- * (src/math/routing.rs:38-155). */
-typedef enum { URB_ROUTER_SOFTMAX_TOPK = 0, URB_ROUTER_SIGMOID_NOAUX_TC = 1 } urb_router;
+/* route_softmax_top_k (src/models/qwen3_8/moe.rs:91-159), route_noaux_tc
+ * (src/math/routing.rs:38-155) or route_sqrt_softplus without hash experts
+ * (src/models/deepseek_v4/math.rs:451-516; GLM composition only). */
+typedef enum {
+  URB_ROUTER_SOFTMAX_TOPK = 0,
+  URB_ROUTER_SIGMOID_NOAUX_TC = 1,
+  URB_ROUTER_SQRT_SOFTPLUS = 2
+} urb_router;
 
 /* Which adapter's layer call the context reproduces:
  *  QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243):
@@ -82,7 +87,7 @@ typedef struct {
   urb_composition composition;
   uint32_t n_group, topk_group;  /* noaux_tc group limiting; 1, 1 = none */
   int32_t normalize;             /* noaux_tc: divide by the selected gate sum */
-  float routed_scaling_factor;   /* noaux_tc */
+  float routed_scaling_factor;   /* noaux_tc, sqrt_softplus */
   uint32_t max_tokens;           /* largest token count one forward call may pass */
 } urb_moe_desc;
 

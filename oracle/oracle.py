@@ -20,7 +20,7 @@ _LIB_PATH = os.path.join(_HERE, "liburb_oracle.so")
 
 OK, SHAPE, INVALID_SCALE, NONFINITE, INVALID_GEOMETRY = 0, 1, 2, 3, 4
 FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
-ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC = 0, 1
+ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
 COMPOSE_QWEN36, COMPOSE_GLM = 0, 1
 
 _STATUS_NAMES = {OK: "ok", SHAPE: "shape", INVALID_SCALE: "invalid_scale",
@@ -58,6 +58,7 @@ def _load():
     lib.urbo_mxfp4_matvec_rows_fp32.argtypes = [P, P, sz, sz, sz, sz, P, P]
     lib.urbo_mxfp8_matvec_rows_f64.argtypes = [P, P, sz, sz, sz, sz, P, P]
     lib.urbo_route_softmax_top_k.argtypes = [P, sz, sz, P, P]
+    lib.urbo_route_sqrt_softplus.argtypes = [P, P, sz, sz, ctypes.c_float, P, P, P]
     lib.urbo_route_noaux_tc.argtypes = [P, P, sz, sz, sz, sz, ctypes.c_int, ctypes.c_float,
                                         P, P, P]
     lib.urbo_silu.argtypes = [ctypes.c_float]
@@ -182,6 +183,17 @@ def route_softmax_top_k(logits: np.ndarray, top_k: int):
     w = np.empty(top_k, np.float32)
     _check(_lib.urbo_route_softmax_top_k(_ptr(logits), logits.size, top_k, _ptr(ids), _ptr(w)))
     return ids, w
+
+
+def route_sqrt_softplus(logits, bias, top_k: int, scale: float):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    ids = np.empty(top_k, np.int32)
+    w = np.empty(top_k, np.float32)
+    sel = np.empty(top_k, np.float32)
+    _check(_lib.urbo_route_sqrt_softplus(_ptr(logits), _ptr(b), logits.size, top_k,
+                                         float(scale), _ptr(ids), _ptr(w), _ptr(sel)))
+    return ids, w, sel
 
 
 def route_noaux_tc(logits, bias, top_k: int, n_group: int, topk_group: int, normalize: bool,

@@ -625,6 +625,44 @@ int urbo_route_noaux_tc(const float *logits, const float *bias, size_t n, size_t
     return URBO_OK;
 }
 
+// route_sqrt_softplus (src/models/deepseek_v4/math.rs:451-516, softplus :604-610) without hash
+// experts: score = sqrt(softplus(l)); selection = score + bias ranks (desc, lower id on ties);
+// weight = score / (f32 sum of the selected scores in ranking order) * scale.
+static float softplus_f(float v) {
+    return v > 0.0f ? v + ::log1pf(::expf(-v)) : ::log1pf(::expf(v));
+}
+
+int urbo_route_sqrt_softplus(const float *logits, const float *bias, size_t n, size_t top_k,
+                             float scale, int32_t *ids, float *weights, float *selection_out) {
+    if (n == 0 || top_k == 0 || top_k > n) return URBO_SHAPE;
+    if (!std::isfinite(scale)) return URBO_NONFINITE;
+    if (scale <= 0.0f) return URBO_INVALID_GEOMETRY;  // validate_positive
+    if (!all_finite(logits, n) || (bias && !all_finite(bias, n))) return URBO_NONFINITE;
+    std::vector<float> score(n), sel(n);
+    for (size_t i = 0; i < n; ++i) {
+        score[i] = ::sqrtf(softplus_f(logits[i]));
+        sel[i] = score[i] + (bias ? bias[i] : 0.0f);
+    }
+    std::vector<size_t> ranking(n);
+    for (size_t i = 0; i < n; ++i) ranking[i] = i;
+    std::stable_sort(ranking.begin(), ranking.end(), [&](size_t l, size_t r) {
+        int32_t kl = total_key(sel[l]), kr = total_key(sel[r]);
+        if (kl != kr) return kl > kr;
+        return l < r;
+    });
+    ranking.resize(top_k);
+    float denominator = -0.0f;  // Iterator::sum identity
+    for (size_t e : ranking) denominator += score[e];
+    if (!std::isfinite(denominator) || denominator <= 0.0f) return URBO_NONFINITE;
+    for (size_t j = 0; j < top_k; ++j) {
+        size_t e = ranking[j];
+        ids[j] = (int32_t)e;
+        weights[j] = score[e] / denominator * scale;
+        if (selection_out) selection_out[j] = sel[e];
+    }
+    return URBO_OK;
+}
+
 float urbo_silu(float value) { return silu_f(value); }
 
 // ==========================================================================================
@@ -719,6 +757,9 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
         const float *lt = logits.data() + t * E;
         if (L->router == URBO_ROUTER_SOFTMAX_TOPK)
             st = urbo_route_softmax_top_k(lt, E, K, &rid[t * K], &rw8[t * K]);
+        else if (L->router == URBO_ROUTER_SQRT_SOFTPLUS)
+            st = urbo_route_sqrt_softplus(lt, L->correction_bias, E, K, L->routed_scaling_factor,
+                                          &rid[t * K], &rw8[t * K], nullptr);
         else
             st = urbo_route_noaux_tc(lt, L->correction_bias, E, K, L->n_group, L->topk_group,
                                      L->normalize, L->routed_scaling_factor, &rid[t * K],

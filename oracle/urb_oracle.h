@@ -35,7 +35,7 @@ enum {
 };
 
 enum { URBO_FMT_BF16 = 0, URBO_FMT_MXFP4 = 1, URBO_FMT_MXFP8 = 2 };
-enum { URBO_ROUTER_SOFTMAX_TOPK = 0, URBO_ROUTER_SIGMOID_NOAUX_TC = 1 };
+enum { URBO_ROUTER_SOFTMAX_TOPK = 0, URBO_ROUTER_SIGMOID_NOAUX_TC = 1, URBO_ROUTER_SQRT_SOFTPLUS = 2 };
 /* QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243).
  * GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176). */
 enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1 };
@@ -75,6 +75,9 @@ int urbo_route_softmax_top_k(const float *logits, size_t n, size_t top_k, int32_
 int urbo_route_noaux_tc(const float *logits, const float *bias, size_t n, size_t top_k,
                         size_t n_group, size_t topk_group, int normalize, float scale,
                         int32_t *ids, float *weights, float *selection);
+/* route_sqrt_softplus (src/models/deepseek_v4/math.rs:451-516), no hash experts. */
+int urbo_route_sqrt_softplus(const float *logits, const float *bias, size_t n, size_t top_k,
+                             float scale, int32_t *ids, float *weights, float *selection_out);
 float urbo_silu(float value);
 
 /* ---- one MoE layer ---- */

@@ -17,7 +17,8 @@ def ids_match(gpu_ids, ref_ids, ref_scores) -> bool:
     """Top-k ids identical except where adjacent reference scores differ by < TIE_GAP.
 
     ``ref_scores[t]`` are the per-expert values the reference ranks by (router logits for
-    softmax; sigmoid(logit) + bias for noaux_tc)."""
+    softmax; sigmoid(logit) + bias for noaux_tc; sqrt(softplus(logit)) + bias for
+    sqrt-softplus)."""
     gpu_ids = np.asarray(gpu_ids)
     ref_ids = np.asarray(ref_ids)
     for t in range(ref_ids.shape[0]):
@@ -34,4 +35,9 @@ def ids_match(gpu_ids, ref_ids, ref_scores) -> bool:
 def noaux_scores(logits, bias):
     logits = np.asarray(logits, np.float64)
     g = 1.0 / (1.0 + np.exp(-logits))
+    return g + (0.0 if bias is None else np.asarray(bias, np.float64)[None, :])
+
+
+def sqrt_softplus_scores(logits, bias):
+    g = np.sqrt(np.logaddexp(0.0, np.asarray(logits, np.float64)))
     return g + (0.0 if bias is None else np.asarray(bias, np.float64)[None, :])

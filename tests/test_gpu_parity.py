@@ -3,6 +3,7 @@ inputs.  Bars: dequantised weights bit-exact; top-k ids identical except near-ti
 layer outputs within 1e-3 relative L2."""
 
 import math
+from dataclasses import replace
 
 import numpy as np
 import pytest
@@ -12,7 +13,7 @@ from urbilateria_amd import configs as C
 from urbilateria_amd import native as N
 from urbilateria_amd import synth
 
-from .gpu_helpers import REL_L2_BAR, ids_match, noaux_scores, rel_l2
+from .gpu_helpers import REL_L2_BAR, ids_match, noaux_scores, rel_l2, sqrt_softplus_scores
 
 pytestmark = pytest.mark.gpu
 
@@ -39,6 +40,8 @@ def _oracle(host: C.HostLayer, x: np.ndarray, threads: int = 4):
 def _scores(spec, res, bias):
     if spec.router == C.ROUTER_SOFTMAX_TOPK:
         return res.logits
+    if spec.router == C.ROUTER_SQRT_SOFTPLUS:
+        return sqrt_softplus_scores(res.logits, bias)
     return noaux_scores(res.logits, bias)
 
 
@@ -200,6 +203,24 @@ def test_router_logits_match_oracle(name):
     layer.close()
 
 
+@pytest.mark.parametrize("name,T", [(n, T) for n in ("c3_mxfp4_decode", "c4_mxfp8")
+                                     for T in (1, 5, 40)])
+def test_sqrt_softplus_router_layer_matches_oracle(name, T):
+    w = C.WORKLOADS[name]
+    spec = replace(C.small_spec(w.spec, hidden=256, n_experts=64, intermediate=128, top_k=6),
+                   router=C.ROUTER_SQRT_SOFTPLUS, routed_scaling_factor=1.5, n_group=1,
+                   topk_group=1)
+    host = C.make_host_layer(spec, bias=C.zipf_bias(64, 1.1, 0.05))
+    x = synth.activations(f"x.ssp.{T}", T, spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y, ids, wt = layer.forward(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+    assert rel_l2(y.cpu().numpy(), ref.output) < REL_L2_BAR
+    assert np.allclose(wt.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    layer.close()
+
+
 def test_forward_is_deterministic_and_chunked_calls_equal_tokenwise():
     host = _small_layer("c5_mxfp4_zipf_prefill", hidden=128, n_experts=16, intermediate=128)
     T = 1100  # > one 1024-token internal chunk
@@ -329,6 +350,19 @@ def test_shape_and_geometry_errors():
         with pytest.raises(N.UrbError) as e:
             moe_mod().MoeLayer(h3, max_tokens=1)
         assert e.value.status == N.ERR_SHAPE
+    # route_sqrt_softplus: validate_positive(scale) -> invalid, non-finite bias -> NonFinite
+    # (deepseek_v4/math.rs:468-475); the router belongs to the GLM composition only.
+    ssp = dataclasses.replace(host.spec, router=C.ROUTER_SQRT_SOFTPLUS)
+    nan_bias = np.zeros(ssp.n_experts, np.float32)
+    nan_bias[3] = np.nan
+    for spec, bias, status in (
+            (dataclasses.replace(ssp, routed_scaling_factor=0.0), None, N.ERR_INVALID_GEOMETRY),
+            (ssp, nan_bias, N.ERR_NONFINITE),
+            (dataclasses.replace(ssp, composition=C.COMPOSE_QWEN36), None, N.ERR_ARGUMENT)):
+        h4 = C.HostLayer(spec, host.router_weight, host.experts, host.shared, bias)
+        with pytest.raises(N.UrbError) as e:
+            moe_mod().MoeLayer(h4, max_tokens=1)
+        assert e.value.status == status
     layer = moe_mod().MoeLayer(host, max_tokens=2)
     x = torch.zeros((3, host.spec.hidden), device="cuda")
     with pytest.raises(N.UrbError) as e:

@@ -5,6 +5,7 @@ import json
 import math
 import os
 import struct
+from dataclasses import replace
 from fractions import Fraction
 
 import numpy as np
@@ -283,6 +284,71 @@ def test_noaux_tc_matches_sorting_definition():
         order = sorted(cand, key=lambda e: (-gate[e], e))[:k]
         assert list(ids) == order
         assert np.allclose(w, gate[order] / gate[order].sum(), rtol=1e-5)
+
+
+def test_sqrt_softplus_kats():
+    k = KATS["sqrt_softplus_bias_selects_not_weights"]
+    logits = np.array(k["logits"], np.float32)
+    ids, w, _ = O.route_sqrt_softplus(logits, None, k["top_k"], k["scale"])
+    assert list(ids) == k["unbiased_experts"]
+    ids, w, sel = O.route_sqrt_softplus(logits, np.array(k["bias"], np.float32), k["top_k"],
+                                        k["scale"])
+    assert list(ids) == k["biased_experts"] and w[0] == k["biased_weight0"]
+    # softplus(0) = ln 2 (the v <= 0 branch), softplus(v) - v -> ln_1p(exp(-v)) for v > 0
+    ids, w, sel = O.route_sqrt_softplus(np.array([0.0], np.float32), None, 1, 1.0)
+    assert abs(float(sel[0]) - math.sqrt(math.log(2.0))) <= 2 * EPS32
+
+
+def _sqrt_softplus64(logits):
+    x = logits.astype(np.float64)
+    return np.sqrt(np.logaddexp(0.0, x))
+
+
+def test_sqrt_softplus_matches_sorting_definition():
+    # Ranking by sqrt(softplus(l)) + bias, weights = score / (sum of selected scores) * scale,
+    # against float64 numpy; a weight formed from the biased selection value fails it.
+    rng = np.random.default_rng(11)
+    n, k, scale = 256, 6, 1.5
+    for it in range(40):
+        logits = (rng.standard_normal(n) * (1.0 + 20.0 * (it % 4 == 3))).astype(np.float32)
+        bias = None if it % 2 == 0 else (rng.standard_normal(n) * 0.3).astype(np.float32)
+        ids, w, sel = O.route_sqrt_softplus(logits, bias, k, scale)
+        score = _sqrt_softplus64(logits)
+        key = score + (0.0 if bias is None else bias.astype(np.float64))
+        order = sorted(range(n), key=lambda e: (-key[e], e))[:k]
+        if list(ids) != order:  # only float32-level near ties may reorder
+            assert all(abs(key[a] - key[b]) < 1e-6 for a, b in zip(ids, order) if a != b)
+        got = [int(e) for e in ids]
+        assert np.allclose(w, score[got] / score[got].sum() * scale, rtol=2e-6)
+        assert np.allclose(sel, key[got], rtol=2e-6, atol=2e-6)
+        assert abs(float(w.astype(np.float64).sum()) - scale) < 1e-5
+
+
+def test_sqrt_softplus_errors():
+    ok = np.array([1.0, 2.0, 3.0], np.float32)
+    for logits, bias, top_k, scale, status in (
+            (np.array([1.0, np.nan], np.float32), None, 1, 1.0, O.NONFINITE),
+            (ok, np.array([0.0, np.inf, 0.0], np.float32), 1, 1.0, O.NONFINITE),
+            (ok, None, 4, 1.0, O.SHAPE),
+            (ok, None, 0, 1.0, O.SHAPE),
+            (ok, None, 1, 0.0, O.INVALID_GEOMETRY),
+            (ok, None, 1, float("nan"), O.NONFINITE)):
+        with pytest.raises(O.OracleError) as e:
+            O.route_sqrt_softplus(logits, bias, top_k, scale)
+        assert e.value.status == status
+
+
+def test_sqrt_softplus_layer_routes_like_the_router():
+    w = C.WORKLOADS["c3_mxfp4_decode"]
+    spec = replace(C.small_spec(w.spec, hidden=64, n_experts=8, intermediate=32, top_k=3),
+                   router=C.ROUTER_SQRT_SOFTPLUS, routed_scaling_factor=2.5)
+    bias = (np.arange(8, dtype=np.float32) - 4.0) * np.float32(0.05)
+    layer = C.make_host_layer(spec, bias=bias)
+    x = synth.activations("x", 4, spec.hidden)
+    res = O.moe_forward(spec, layer.experts, layer.router_weight, x, bias, layer.shared)
+    for t in range(4):
+        ids, wt, _ = O.route_sqrt_softplus(res.logits[t], bias, 3, 2.5)
+        assert list(res.ids[t]) == list(ids) and np.array_equal(res.weights[t], wt)
 
 
 def test_gated_mlp_formula_kat():

@@ -24,7 +24,7 @@ import numpy as np
 from . import synth
 
 FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
-ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC = 0, 1
+ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
 COMPOSE_QWEN36, COMPOSE_GLM = 0, 1
 FORMAT_NAMES = {FMT_BF16: "bf16", FMT_MXFP4: "mxfp4", FMT_MXFP8: "mxfp8"}
 

@@ -66,7 +66,7 @@ void launch_gemm_down(int fmt, const ExpertMats* mats, const Perm& perm, int max
                       int I, const float* act, float* y, int qwen, int* status, hipStream_t s);
 
 struct RouteParams {
-  int router;        // 0 softmax top-k, 1 sigmoid noaux_tc
+  int router;        // 0 softmax top-k, 1 sigmoid noaux_tc, 2 sqrt-softplus
   int qwen;          // round route weights to BF16
   int n_group, topk_group, normalize;
   float scale;

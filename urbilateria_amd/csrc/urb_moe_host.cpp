@@ -178,6 +178,11 @@ static urb_status check_desc(const urb_moe_desc* d) {
     if (per < 2) return URB_ERR_INVALID_GEOMETRY;
     if (per * d->topk_group < d->top_k) return URB_ERR_INVALID_GEOMETRY;
     if (d->n_group > 64) return URB_ERR_ARGUMENT;
+  } else if (d->router == URB_ROUTER_SQRT_SOFTPLUS) {
+    // route_sqrt_softplus: validate_positive(routed_scaling_factor) (deepseek_v4/math.rs:468)
+    if (d->composition != URB_COMPOSE_GLM) return URB_ERR_ARGUMENT;
+    if (!finite_host(d->routed_scaling_factor)) return URB_ERR_NONFINITE;
+    if (d->routed_scaling_factor <= 0.0f) return URB_ERR_INVALID_GEOMETRY;
   } else if (d->router != URB_ROUTER_SOFTMAX_TOPK) {
     return URB_ERR_ARGUMENT;
   }
@@ -383,7 +388,10 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   int host_flags[4] = {0, 0, 0, 0};
   URB_HIP(hipDeviceSynchronize());
   URB_HIP(hipMemcpy(host_flags, c->ws.status, sizeof(host_flags), hipMemcpyDeviceToHost));
-  if (host_flags[2]) return URB_ERR_INVALID_GEOMETRY;  // moe.rs:92-96: non-finite bias
+  // A non-finite bias: RuntimeMoeLayer::new's geometry error (glm/runtime/moe.rs:92-96), or
+  // route_sqrt_softplus's NonFinite (deepseek_v4/math.rs:469-475).
+  if (host_flags[2])
+    return d->router == URB_ROUTER_SQRT_SOFTPLUS ? URB_ERR_NONFINITE : URB_ERR_INVALID_GEOMETRY;
   if (host_flags[1] & 1) return URB_ERR_NONFINITE;
   if (host_flags[1] & 2) return URB_ERR_INVALID_SCALE;
   urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);

@@ -186,7 +186,8 @@ __device__ __forceinline__ int argmax_round(const int32_t (&key)[EPL], const flo
 
 // Routes token t with the calling wavefront.  `sh` (kMaxExperts floats) and `grp` (64 floats)
 // are the wave's LDS scratch.
-template <int EPL, bool SOFTMAX>
+// MODE: 0 softmax top-k, 1 sigmoid noaux_tc, 2 sqrt-softplus.
+template <int EPL, int MODE>
 __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int K,
                             const RouteParams& rp, int32_t* __restrict__ ids,
                             float* __restrict__ weights, int32_t* __restrict__ asc, int* status,
@@ -241,7 +242,7 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
   int my_id = 0;
   float my_val = 0.0f;
   float w = 0.0f;
-  if constexpr (SOFTMAX) {
+  if constexpr (MODE == 0) {
     // route_softmax_top_k (src/models/qwen3_8/moe.rs:91-159).
     int32_t mk = INT32_MIN;
 #pragma unroll
@@ -283,6 +284,36 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
         if (!rne_bf16(w, &q)) bad = true; else w = q;
       }
     }
+  } else if constexpr (MODE == 2) {
+    // route_sqrt_softplus (src/models/deepseek_v4/math.rs:451-516), no hash experts:
+    // score = sqrt(softplus(l)) with softplus(v) = v + ln_1p(exp(-v)) for v > 0, else
+    // ln_1p(exp(v)) (:604-610); selection = score + bias ranks; the weight divides by the f32
+    // sum of the selected scores in ranking order.
+    float score[EPL];
+    int32_t key[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      float sp = 0.0f;
+      if (open[i]) {
+        const float x = v[i];
+        const float ex = exp_f32(x > 0.0f ? -x : x);
+        const float l1 = (float)log1p((double)ex);
+        sp = x > 0.0f ? __fadd_rn(x, l1) : l1;
+      }
+      score[i] = open[i] ? __fsqrt_rn(sp) : 0.0f;
+      const float b = (open[i] && rp.bias) ? rp.bias[e] : 0.0f;
+      key[i] = total_key(__fadd_rn(score[i], b));
+    }
+    for (int r = 0; r < K; ++r) {
+      float val;
+      const int id = argmax_round<EPL>(key, score, open, val);
+      if (lane == r) { my_id = id; my_val = val; }
+    }
+    float den = -0.0f;  // Iterator::sum in ranking order
+    for (int r = 0; r < K; ++r) den = __fadd_rn(den, rdl(my_val, r));
+    if (!finite(den) || den <= 0.0f) bad = true;
+    w = __fmul_rn(__fdiv_rn(my_val, den), rp.scale);
   } else {
     // route_noaux_tc (src/math/routing.rs:38-155).
     float g[EPL], sc[EPL];
@@ -355,7 +386,7 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
   }
 }
 
-template <int EPL, bool SOFTMAX>
+template <int EPL, int MODE>
 __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, int T,
                                                     int E, int K, RouteParams rp,
                                                     int32_t* __restrict__ ids,
@@ -366,7 +397,7 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
-  route_token<EPL, SOFTMAX>(t, logits, T, E, K, rp, ids, weights, asc, status, lds[wave],
+  route_token<EPL, MODE>(t, logits, T, E, K, rp, ids, weights, asc, status, lds[wave],
                             grp[wave]);
 }
 
@@ -611,12 +642,13 @@ template <int EPL>
 static void launch_route_epl(float* logits, int T, int E, int K, const RouteParams& p,
                              int32_t* ids, float* weights, int32_t* asc, int* status,
                              hipStream_t s) {
+  const dim3 grid((T + 3) / 4);
   if (p.router == 0)
-    route_kernel<EPL, true><<<(T + 3) / 4, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc,
-                                                        status);
+    route_kernel<EPL, 0><<<grid, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc, status);
+  else if (p.router == 1)
+    route_kernel<EPL, 1><<<grid, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc, status);
   else
-    route_kernel<EPL, false><<<(T + 3) / 4, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc,
-                                                         status);
+    route_kernel<EPL, 2><<<grid, 256, 0, s>>>(logits, T, E, K, p, ids, weights, asc, status);
 }
 
 void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
