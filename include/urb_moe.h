@@ -47,8 +47,15 @@ typedef enum {
  *          BF16 router GEMV (FP32, 8-lane tree) + BF16 logits, BF16 route weights, BF16
  *          boundaries inside experts and in the ascending-expert-id combine.
  *  GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176): f64 router GEMV,
- *          GatedMlp experts, f64 combine in ranking order on top of the shared expert. */
-typedef enum { URB_COMPOSE_QWEN36 = 0, URB_COMPOSE_GLM = 1 } urb_composition;
+ *          GatedMlp experts, f64 combine in ranking order on top of the shared expert.
+ *  HY4:    the MX-activation mode, Hy4 MoeWeights::forward (src/models/hy4/runtime.rs:
+ *          1371-1447): f64 router GEMV; the token's activation quantized to E4M3 per 32 values
+ *          (simulate_e4m3_activation, src/math/mxfp.rs:89-115) feeds every MX projection;
+ *          routed experts Hy4Expert::forward_quantized (src/models/hy4/expert.rs:373-392,
+ *          664-680: BF16 gate/up, bounded SwiGLU with swiglu_limit, re-quantized, BF16 down);
+ *          shared expert DenseMlp::forward (runtime.rs:1311-1322); f32 combine in ascending
+ *          expert id plus the shared expert, rounded to BF16.  MX expert and shared formats. */
+typedef enum { URB_COMPOSE_QWEN36 = 0, URB_COMPOSE_GLM = 1, URB_COMPOSE_HY4 = 2 } urb_composition;
 
 /* Where urb_moe_create reads the weights from.  The context streams expert and shared-expert
  * matrices in the panel layout (see urb_pack_matrix); HOST and DEVICE_COPY sources are in the
@@ -80,15 +87,16 @@ typedef struct {
   uint32_t n_experts;            /* E */
   uint32_t top_k;                /* k */
   uint32_t intermediate;         /* I of each routed expert */
-  uint32_t shared_intermediate;  /* I of the always-on shared expert, 0 = none (GLM only) */
+  uint32_t shared_intermediate;  /* I of the always-on shared expert, 0 = none (not QWEN36) */
   urb_format expert_format;
-  urb_format shared_format;      /* BF16 */
+  urb_format shared_format;
   urb_router router;
   urb_composition composition;
   uint32_t n_group, topk_group;  /* noaux_tc group limiting; 1, 1 = none */
   int32_t normalize;             /* noaux_tc: divide by the selected gate sum */
   float routed_scaling_factor;   /* noaux_tc, sqrt_softplus */
   uint32_t max_tokens;           /* largest token count one forward call may pass */
+  float swiglu_limit;            /* HY4: bounded SwiGLU limit of the routed experts (> 0) */
 } urb_moe_desc;
 
 typedef struct {
@@ -136,6 +144,14 @@ urb_status urb_moe_sync(urb_moe_ctx *ctx, void *stream);
 urb_status urb_dequant_rows(urb_format format, const void *data, const uint8_t *scales,
                             uint32_t rows, uint32_t cols, uint32_t row0, uint32_t count,
                             float *out, void *stream);
+
+/* simulate_e4m3_activation (src/math/mxfp.rs:82-115) of a [rows, cols] f32 matrix (device,
+ * cols % 32 == 0) per 32-value block of each row, as the MX-activation mode feeds it to the
+ * scaled MFMA: E4M3 codes [rows, cols] and E8M0 scales [rows, cols / 32] (device); the
+ * simulated value is decode_e4m3fn(code) * 2^(scale - 127).  The bit-exact parity hook of the
+ * quantizer; inputs must be finite (the layer call reports non-finite ones). */
+urb_status urb_quantize_e4m3(const float *x, uint32_t rows, uint32_t cols, uint8_t *codes,
+                             uint8_t *scales, void *stream);
 
 /* Converts one row-major matrix (device, the urb_matrix layout) into the panel layout the
  * context streams (device; same byte counts: packed_data as large as data, packed_scales as

@@ -21,7 +21,7 @@ _LIB_PATH = os.path.join(_HERE, "liburb_oracle.so")
 OK, SHAPE, INVALID_SCALE, NONFINITE, INVALID_GEOMETRY = 0, 1, 2, 3, 4
 FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
 ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
-COMPOSE_QWEN36, COMPOSE_GLM = 0, 1
+COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4 = 0, 1, 2
 
 _STATUS_NAMES = {OK: "ok", SHAPE: "shape", INVALID_SCALE: "invalid_scale",
                  NONFINITE: "nonfinite", INVALID_GEOMETRY: "invalid_geometry"}
@@ -225,6 +225,7 @@ class _Layer(ctypes.Structure):
         ("normalize", ctypes.c_int32), ("routed_scaling_factor", ctypes.c_float),
         ("router_weight", ctypes.c_void_p), ("correction_bias", ctypes.c_void_p),
         ("experts", ctypes.c_void_p), ("shared", ctypes.c_void_p),
+        ("swiglu_limit", ctypes.c_float),
     ]
 
 
@@ -241,7 +242,7 @@ def moe_forward(spec, experts: Sequence, router_weight: np.ndarray, x: np.ndarra
                 threads: int = 1) -> OracleResult:
     """Runs one layer.  ``spec`` carries the layer geometry (attributes hidden, n_experts,
     top_k, intermediate, shared_intermediate, expert_format, shared_format, router, composition,
-    n_group, topk_group, normalize, routed_scaling_factor).  ``experts[e]`` is a triple of
+    n_group, topk_group, normalize, routed_scaling_factor, swiglu_limit).  ``experts[e]`` is a triple of
     (data, scales) pairs for gate, up and down; ``shared`` likewise or None."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T = x.shape[0]
@@ -268,7 +269,8 @@ def moe_forward(spec, experts: Sequence, router_weight: np.ndarray, x: np.ndarra
                    spec.shared_format, spec.router, spec.composition, spec.n_group,
                    spec.topk_group, int(spec.normalize), float(spec.routed_scaling_factor),
                    _ptr(rwt), _ptr(bias), ctypes.addressof(mats),
-                   None if sh is None else ctypes.addressof(sh))
+                   None if sh is None else ctypes.addressof(sh),
+                   float(getattr(spec, "swiglu_limit", 0.0)))
     y = np.empty((T, H), np.float32)
     ids = np.empty((T, K), np.int32)
     w = np.empty((T, K), np.float32)
@@ -299,6 +301,37 @@ def gated_mlp(fmt: int, triple, hidden: int, intermediate: int, x: np.ndarray,
                                     ctypes.c_void_p, ctypes.c_int]
     _check(_lib.urbo_gated_mlp(fmt, ctypes.addressof(mats), hidden, intermediate, _ptr(x),
                                x.shape[0], _ptr(y), threads))
+    return y
+
+
+def set_mxfp8_fma_host(fma_host: bool) -> bool:
+    """MXFP8 matvec kernel of layer calls: the AVX2+FMA host's compact kernel (True, default)
+    or the ordered-f64 kernel of other hosts.  Returns the previous setting."""
+    return bool(_lib.urbo_set_mxfp8_fma_host(int(fma_host)))
+
+
+def bounded_swiglu(gate, up, limit: float) -> np.ndarray:
+    gate = np.ascontiguousarray(gate, dtype=np.float32)
+    up = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.empty_like(gate)
+    _lib.urbo_bounded_swiglu.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                         ctypes.c_float, ctypes.c_void_p]
+    _check(_lib.urbo_bounded_swiglu(_ptr(gate), _ptr(up), gate.size, float(limit), _ptr(out)))
+    return out
+
+
+def hy4_expert(fmt: int, triple, hidden: int, intermediate: int, x: np.ndarray,
+               swiglu_limit: float, threads: int = 1) -> np.ndarray:
+    """Hy4 MX-activation expert on [n, hidden] (quantized inside): the routed expert for
+    swiglu_limit > 0, the shared DenseMlp for swiglu_limit == 0."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    mats, keep = _mats(triple)
+    y = np.empty((x.shape[0], hidden), np.float32)
+    _lib.urbo_hy4_expert.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint32,
+                                     ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32,
+                                     ctypes.c_float, ctypes.c_void_p, ctypes.c_int]
+    _check(_lib.urbo_hy4_expert(fmt, ctypes.addressof(mats), hidden, intermediate, _ptr(x),
+                                x.shape[0], float(swiglu_limit), _ptr(y), threads))
     return y
 
 

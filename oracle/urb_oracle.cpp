@@ -312,6 +312,10 @@ size_t row_bytes(int format, size_t cols) {
 // BF16 and MXFP4: ordered f64 (src/model/weight.rs:92-101 -> bf16.rs:121-216,
 // mxfp.rs:1725-1780); MXFP8 1x32: compact FMA with a non-finite output check
 // (mxfp.rs:693-783).  Output layout is token-major [batch, rows].
+// MxFp8Matrix::matvec_rows picks its kernel by host CPU (src/math/mxfp.rs:720-765): the compact
+// 8-lane FMA kernel on AVX2+FMA hosts (the default here), ordered f64 elsewhere.
+int g_mxfp8_fma_host = 1;
+
 int weight_matmul(Pool &p, int format, const uint8_t *data, const uint8_t *scales, size_t rows,
                   size_t cols, const float *x, size_t batch, float *out) {
     if (!all_finite(x, batch * cols)) return URBO_NONFINITE;
@@ -323,7 +327,9 @@ int weight_matmul(Pool &p, int format, const uint8_t *data, const uint8_t *scale
             if (format == URBO_FMT_BF16) dot_bf16_f64(row, cols, x, batch, tmp.data());
             else if (format == URBO_FMT_MXFP4)
                 dot_mxfp4_f64(row, scales + r * sb, cols, x, batch, tmp.data());
-            else dot_mxfp8_compact(row, scales + r * sb, cols, x, batch, tmp.data());
+            else if (g_mxfp8_fma_host)
+                dot_mxfp8_compact(row, scales + r * sb, cols, x, batch, tmp.data());
+            else dot_mxfp8_f64(row, scales + r * sb, cols, x, batch, tmp.data());
             for (size_t b = 0; b < batch; ++b) out[b * rows + r] = tmp[b];
         }
     });
@@ -665,6 +671,26 @@ int urbo_route_sqrt_softplus(const float *logits, const float *bias, size_t n, s
 
 float urbo_silu(float value) { return silu_f(value); }
 
+int urbo_set_mxfp8_fma_host(int fma_host) {
+    int old = g_mxfp8_fma_host;
+    g_mxfp8_fma_host = fma_host ? 1 : 0;
+    return old;
+}
+
+// bounded_swiglu_in_place (src/models/deepseek_v4/math.rs:526-548): validate_positive(limit)
+// (:669-677), non-finite inputs rejected, then gate' = min(gate, limit),
+// up' = clamp(up, -limit, limit), out = gate' / (1 + exp(-gate')) * up'.
+int urbo_bounded_swiglu(const float *gate, const float *up, size_t n, float limit, float *out) {
+    if (!(std::isfinite(limit) && limit > 0.0f)) return URBO_INVALID_GEOMETRY;
+    if (!all_finite(gate, n) || !all_finite(up, n)) return URBO_NONFINITE;
+    for (size_t i = 0; i < n; ++i) {
+        const float g = std::fmin(gate[i], limit);
+        const float u = std::fmin(std::fmax(up[i], -limit), limit);
+        out[i] = g / (1.0f + ::expf(-g)) * u;
+    }
+    return URBO_OK;
+}
+
 // ==========================================================================================
 // One MoE layer.  Tokens are routed first, then grouped by expert (the reference's
 // execute_batched_moe permutation, src/models/qwen3_6/runtime.rs:1123-1132: BTreeMap by
@@ -715,7 +741,72 @@ int gated_mlp(Pool &p, int format, const urbo_matrix *m, size_t H, size_t I, con
     return weight_matmul(p, format, m[2].data, m[2].scales, H, I, a.data(), n, y);
 }
 
+// Hy4 routed expert on quantized activations q [n, H] (src/models/hy4/expert.rs:373-392 and
+// activate_gate_up :664-680): gate/up through WeightMatrix::matvec, each rounded to BF16;
+// bounded_swiglu (deepseek_v4/math.rs:526-548): g' = min(g, limit), u' = clamp(u, +-limit),
+// a = g' / (1 + exp(-g')) * u'; a <- simulate_e4m3_activation(a, 32) per token;
+// y = bf16(down . a).
+int hy4_routed(Pool &p, int format, const urbo_matrix *m, size_t H, size_t I, const float *q,
+               size_t n, float limit, float *y) {
+    std::vector<float> g(n * I), u(n * I), a(n * I);
+    int st = weight_matmul(p, format, m[0].data, m[0].scales, I, H, q, n, g.data());
+    if (st) return st;
+    st = weight_matmul(p, format, m[1].data, m[1].scales, I, H, q, n, u.data());
+    if (st) return st;
+    if ((st = urbo_round_to_bf16_in_place(g.data(), n * I))) return st;
+    if ((st = urbo_round_to_bf16_in_place(u.data(), n * I))) return st;
+    if ((st = urbo_bounded_swiglu(g.data(), u.data(), n * I, limit, a.data()))) return st;
+    for (size_t t = 0; t < n; ++t)
+        if ((st = urbo_simulate_e4m3_activation(&a[t * I], I, 32))) return st;
+    st = weight_matmul(p, format, m[2].data, m[2].scales, H, I, a.data(), n, y);
+    if (st) return st;
+    return urbo_round_to_bf16_in_place(y, n * H);
+}
+
+// Hy4 shared DenseMlp::forward (src/models/hy4/runtime.rs:1311-1322, mx_linear :2425-2442) on
+// quantized activations q [n, H]: g = bf16(gate . q), u = bf16(up . q), a = bf16(silu(g) u),
+// y = bf16(down . simulate_e4m3_activation(a, 32)).
+int hy4_shared(Pool &p, int format, const urbo_matrix *m, size_t H, size_t I, const float *q,
+               size_t n, float *y) {
+    std::vector<float> g(n * I), u(n * I), a(n * I);
+    int st = weight_matmul(p, format, m[0].data, m[0].scales, I, H, q, n, g.data());
+    if (st) return st;
+    st = weight_matmul(p, format, m[1].data, m[1].scales, I, H, q, n, u.data());
+    if (st) return st;
+    if ((st = urbo_round_to_bf16_in_place(g.data(), n * I))) return st;
+    if ((st = urbo_round_to_bf16_in_place(u.data(), n * I))) return st;
+    for (size_t i = 0; i < n * I; ++i) a[i] = silu_f(g[i]) * u[i];
+    if ((st = urbo_round_to_bf16_in_place(a.data(), n * I))) return st;
+    for (size_t t = 0; t < n; ++t)
+        if ((st = urbo_simulate_e4m3_activation(&a[t * I], I, 32))) return st;
+    st = weight_matmul(p, format, m[2].data, m[2].scales, H, I, a.data(), n, y);
+    if (st) return st;
+    return urbo_round_to_bf16_in_place(y, n * H);
+}
+
+// mx_activation (src/models/hy4/runtime.rs:2430-2434) of n tokens [n, H].
+int hy4_quantize(const float *x, size_t n, size_t H, std::vector<float> &q) {
+    q.assign(x, x + n * H);
+    for (size_t t = 0; t < n; ++t) {
+        int st = urbo_simulate_e4m3_activation(&q[t * H], H, 32);
+        if (st) return st;
+    }
+    return URBO_OK;
+}
+
 }  // namespace
+
+int urbo_hy4_expert(int format, const urbo_matrix *m, uint32_t H, uint32_t I, const float *x,
+                    uint32_t n, float swiglu_limit, float *y, int threads) {
+    if (H == 0 || I == 0 || n == 0) return URBO_SHAPE;
+    if (format != URBO_FMT_MXFP4 && format != URBO_FMT_MXFP8) return URBO_SHAPE;
+    std::vector<float> q;
+    int st = hy4_quantize(x, n, H, q);
+    if (st) return st;
+    Pool &p = pool(threads);
+    return swiglu_limit > 0.0f ? hy4_routed(p, format, m, H, I, q.data(), n, swiglu_limit, y)
+                               : hy4_shared(p, format, m, H, I, q.data(), n, y);
+}
 
 int urbo_gated_mlp(int format, const urbo_matrix *m, uint32_t H, uint32_t I, const float *x,
                    uint32_t n, float *y, int threads) {
@@ -736,8 +827,14 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
     if (H == 0 || E == 0 || I == 0 || T == 0) return URBO_SHAPE;
     if (K == 0 || K > E) return URBO_INVALID_GEOMETRY;
     const bool qwen = L->composition == URBO_COMPOSE_QWEN36;
+    const bool hy4 = L->composition == URBO_COMPOSE_HY4;
     if (qwen && (L->expert_format != URBO_FMT_BF16 || L->shared_intermediate != 0))
         return URBO_SHAPE;
+    if (hy4 && (L->expert_format == URBO_FMT_BF16 ||
+                (L->shared_intermediate && L->shared_format == URBO_FMT_BF16)))
+        return URBO_SHAPE;
+    if (hy4 && !(L->swiglu_limit > 0.0f && std::isfinite(L->swiglu_limit)))
+        return URBO_INVALID_GEOMETRY;
     Pool &p = pool(threads);
     if (!all_finite(x, (size_t)T * H)) return URBO_NONFINITE;
 
@@ -786,17 +883,24 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
             groups.push_back(std::move(g));
         }
     }
+    // Hy4: one E4M3 activation per token shared by every routed expert and the shared expert
+    // (src/models/hy4/runtime.rs:1397, 1311-1312).
+    std::vector<float> qx;
+    if (hy4 && (st = hy4_quantize(x, T, H, qx))) return st;
+    const float *xe = hy4 ? qx.data() : x;
     // Expert outputs per route slot.
     std::vector<float> out((size_t)T * K * H);
     for (const Group &g : groups) {
         size_t n = g.tokens.size();
         std::vector<float> xin(n * H), yo(n * H);
         for (size_t i = 0; i < n; ++i)
-            std::memcpy(&xin[i * H], x + g.tokens[i] * H, H * 4);
+            std::memcpy(&xin[i * H], xe + g.tokens[i] * H, H * 4);
         const urbo_matrix *m = L->experts + g.expert * 3;
         if (!m[0].data || !m[1].data || !m[2].data) return URBO_SHAPE;  // expert not supplied
         st = qwen ? qwen_expert(p, m, H, I, xin.data(), n, yo.data())
-                  : gated_mlp(p, L->expert_format, m, H, I, xin.data(), n, yo.data());
+             : hy4 ? hy4_routed(p, L->expert_format, m, H, I, xin.data(), n, L->swiglu_limit,
+                                yo.data())
+                   : gated_mlp(p, L->expert_format, m, H, I, xin.data(), n, yo.data());
         if (st) return st;
         for (size_t i = 0; i < n; ++i)
             std::memcpy(&out[g.slots[i] * H], &yo[i * H], H * 4);
@@ -825,6 +929,35 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
             }
         }
         return URBO_OK;
+    }
+
+    if (hy4) {
+        // Hy4 MoeWeights::forward (src/models/hy4/runtime.rs:1387-1445): f32 sum of w * y over
+        // the routes in ascending expert id, plus the shared expert, rounded to BF16.
+        std::vector<float> sh;
+        if (L->shared_intermediate) {
+            sh.resize((size_t)T * H);
+            st = hy4_shared(p, L->shared_format, L->shared, H, L->shared_intermediate, qx.data(),
+                            T, sh.data());
+            if (st) return st;
+        }
+        for (size_t t = 0; t < T; ++t) {
+            std::vector<size_t> order(K);
+            for (size_t j = 0; j < K; ++j) order[j] = j;
+            std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) {
+                return rid[t * K + a] < rid[t * K + b];
+            });
+            float *yt = y + t * H;
+            for (size_t h = 0; h < H; ++h) yt[h] = 0.0f;
+            for (size_t j : order) {
+                const float w = rw8[t * K + j];
+                const float *v = &out[(t * K + j) * H];
+                for (size_t h = 0; h < H; ++h) yt[h] += w * v[h];
+            }
+            if (!sh.empty())
+                for (size_t h = 0; h < H; ++h) yt[h] += sh[t * H + h];
+        }
+        return urbo_round_to_bf16_in_place(y, (size_t)T * H);
     }
 
     // GLM: shared expert first (moe.rs:162-165), then f64 accumulation in ranking order.

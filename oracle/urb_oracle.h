@@ -38,7 +38,7 @@ enum { URBO_FMT_BF16 = 0, URBO_FMT_MXFP4 = 1, URBO_FMT_MXFP8 = 2 };
 enum { URBO_ROUTER_SOFTMAX_TOPK = 0, URBO_ROUTER_SIGMOID_NOAUX_TC = 1, URBO_ROUTER_SQRT_SOFTPLUS = 2 };
 /* QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243).
  * GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176). */
-enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1 };
+enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1, URBO_COMPOSE_HY4 = 2 };
 
 /* ---- element decoders (src/math/mxfp.rs, src/model/bf16.rs, src/models/qwen3_8/math.rs) ---- */
 int urbo_decode_e8m0(uint8_t code, float *out);
@@ -79,6 +79,12 @@ int urbo_route_noaux_tc(const float *logits, const float *bias, size_t n, size_t
 int urbo_route_sqrt_softplus(const float *logits, const float *bias, size_t n, size_t top_k,
                              float scale, int32_t *ids, float *weights, float *selection_out);
 float urbo_silu(float value);
+/* Selects MxFp8Matrix::matvec_rows's host kernel for layer calls (src/math/mxfp.rs:720-765):
+ * 1 = compact 8-lane FMA (AVX2+FMA hosts, the default), 0 = ordered f64.  Returns the previous. */
+int urbo_set_mxfp8_fma_host(int fma_host);
+/* bounded_swiglu (src/models/deepseek_v4/math.rs:526-548): out = min(g, L) / (1 + exp(-min(g, L)))
+ * * clamp(u, -L, L). */
+int urbo_bounded_swiglu(const float *gate, const float *up, size_t n, float limit, float *out);
 
 /* ---- one MoE layer ---- */
 typedef struct {
@@ -96,8 +102,15 @@ typedef struct {
     const float *correction_bias;  /* [E] or NULL (zeros) */
     const urbo_matrix *experts;    /* [E][3] = gate [I,H], up [I,H], down [H,I] */
     const urbo_matrix *shared;     /* [3] or NULL */
+    float swiglu_limit;            /* HY4: bounded SwiGLU limit of the routed experts */
 } urbo_layer;
 
+/* Hy4 MX-activation experts over n tokens [n, H] -> [n, H] (x is quantized here):
+ * routed Hy4Expert::forward_quantized (src/models/hy4/expert.rs:373-392, 664-680) when
+ * swiglu_limit > 0, else the shared DenseMlp::forward (src/models/hy4/runtime.rs:1311-1322). */
+int urbo_hy4_expert(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
+                    uint32_t intermediate, const float *x, uint32_t n, float swiglu_limit,
+                    float *y, int threads);
 /* GatedMlp::forward (src/model/mlp.rs:90-99) over n tokens [n, H] -> [n, H]. */
 int urbo_gated_mlp(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
                    uint32_t intermediate, const float *x, uint32_t n, float *y, int threads);

@@ -118,6 +118,39 @@ def test_mfma_16x16x32_bf16_lane_layout():
     assert np.array_equal(c.cpu().numpy(), A @ B)
 
 
+@pytest.mark.parametrize("fmt", [C.FMT_MXFP4, C.FMT_MXFP8])
+def test_mfma_scale_16x16x128_operands(fmt):
+    # One scaled-MFMA step of the MX-activation kernels, operands built by their own helpers:
+    # A = row-major E4M3 codes with E8M0 block scales, B = one weight panel step as the panel
+    # lanes load it.  Codes of magnitude 0.5 .. 3.75 (E2M1: 0 .. 6) and scales 2^-1 .. 2^1 make
+    # every product a multiple of 2^-10 below 2^6, so every partial sum is exact in f32 and C
+    # must equal A.B^T exactly in any summation order.
+    rng = np.random.default_rng(7)
+    fin8 = np.array([c for c in range(256) if 48 <= (c & 0x7F) <= 71], np.uint8)
+    dec8 = np.array([O.decode_e4m3fn(c) for c in range(256)], np.float64)
+    A = rng.choice(fin8, (16, 128)).astype(np.uint8)
+    sa = rng.integers(126, 129, (16, 4)).astype(np.uint8)
+    sb = rng.integers(126, 129, (16, 4)).astype(np.uint8)
+    Av = dec8[A] * np.exp2(np.repeat(sa.astype(np.float64) - 127, 32, axis=1))
+    if fmt == C.FMT_MXFP8:
+        Bc = rng.choice(fin8, (16, 128)).astype(np.uint8)
+        Bv = dec8[Bc]
+        Bbytes = Bc
+    else:
+        Bc = rng.integers(0, 16, (16, 128)).astype(np.uint8)
+        Bv = np.array([O.decode_e2m1(int(c)) for c in Bc.ravel()], np.float64).reshape(16, 128)
+        Bbytes = (Bc[:, 0::2] | (Bc[:, 1::2] << 4)).astype(np.uint8)
+    Bv = Bv * np.exp2(np.repeat(sb.astype(np.float64) - 127, 32, axis=1))
+    dev = [torch.from_numpy(np.ascontiguousarray(v)).cuda() for v in (A, sa, Bbytes, sb)]
+    c = torch.zeros((16, 16), device="cuda")
+    N.check(N.synth_lib().urb_probe_mfma_scale_16x16x128(
+        fmt, *(d.data_ptr() for d in dev), c.data_ptr(), None))
+    torch.cuda.synchronize()
+    got = c.cpu().numpy().astype(np.float64)
+    ref = Av @ Bv.T
+    assert np.array_equal(got, ref), float(np.abs(got - ref).max())
+
+
 def _probe_cvt(fmt, codes, scales):
     out = torch.empty(codes.size, dtype=torch.int16, device="cuda")
     c_dev = torch.from_numpy(codes).cuda()   # held: a dropped temporary's block can be reused
@@ -218,6 +251,94 @@ def test_sqrt_softplus_router_layer_matches_oracle(name, T):
     assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
     assert rel_l2(y.cpu().numpy(), ref.output) < REL_L2_BAR
     assert np.allclose(wt.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    layer.close()
+
+
+# ------------------------------------------------------------------------------- MX activations
+def _quantizer_cases():
+    rng = np.random.default_rng(12)
+    rows = [rng.standard_normal(256) * s for s in (1e-6, 1e-3, 0.3, 1.0, 7.0, 300.0, 1e5, 1e30)]
+    # block maxima just above / below powers of two times 448 (the power_of_two_ceiling band
+    # near exact powers, where the reference keeps its log2/ceil/powf formula)
+    edge = []
+    for e in range(-20, 20):
+        for m in (0, 1, 2, 3, 4096, 4097, 0x7FFFFF - 4097, 0x7FFFFF - 4096, 0x7FFFFF - 1, 5000):
+            v = np.float32(np.uint32(((127 + e) << 23) | m).view(np.float32)) * np.float32(448.0)
+            edge.append(v)
+    edge = np.array(edge, np.float32)
+    blocks = []
+    for v in edge:
+        b = rng.standard_normal(32).astype(np.float32) * v / 4
+        b[rng.integers(32)] = v * (1 if rng.integers(2) else -1)
+        blocks.append(b)
+    rows.append(np.concatenate(blocks)[: (len(blocks) * 32 // 256) * 256])
+    # zeros, values below the 1e-4 floor, E4M3 subnormals and ties
+    rows.append(np.concatenate([np.zeros(32), np.full(32, 3e-5), rng.standard_normal(32) * 1e-4,
+                                np.arange(-16, 16) * 2.0 ** -9 * 7, np.arange(-16, 16) * 0.5625,
+                                np.full(32, 448.0), np.full(32, -1e38), np.arange(32) - 15.5]))
+    return [np.asarray(r, np.float32) for r in rows]
+
+
+def test_quantize_e4m3_matches_simulate_e4m3_activation_bit_exact():
+    dec8 = np.array([O.decode_e4m3fn(c) for c in range(256)], np.float32)
+    for r in _quantizer_cases():
+        x = r.reshape(1, -1)
+        codes, scales = moe_mod().quantize_e4m3(torch.from_numpy(x).cuda())
+        torch.cuda.synchronize()
+        c = codes.cpu().numpy().ravel()
+        s = scales.cpu().numpy().ravel().astype(np.int64)
+        got = dec8[c] * np.exp2(np.repeat(s - 127, 32)).astype(np.float32)
+        ref = O.simulate_e4m3_activation(x.ravel(), 32)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+            np.nonzero(got.view(np.uint32) != ref.view(np.uint32))[0][:8]
+        assert not np.any((c & 0x7F) == 0x7F)  # never a NaN code
+
+
+HY4 = [(fmt, T) for fmt in (C.FMT_MXFP4, C.FMT_MXFP8) for T in (1, 5, 40)]
+
+
+def _hy4_layer(fmt, hidden=256, n_experts=32, intermediate=128, top_k=6):
+    spec = C.LayerSpec(hidden=hidden, n_experts=n_experts, top_k=top_k, intermediate=intermediate,
+                       shared_intermediate=intermediate, expert_format=fmt, shared_format=fmt,
+                       router=C.ROUTER_SIGMOID_NOAUX_TC, composition=C.COMPOSE_HY4, n_group=4,
+                       topk_group=2, normalize=True, routed_scaling_factor=2.5, swiglu_limit=7.0)
+    return C.make_host_layer(spec, bias=C.zipf_bias(n_experts, 1.1, 0.05))
+
+
+@pytest.mark.parametrize("fmt,T", HY4)
+def test_hy4_layer_matches_oracle(fmt, T):
+    host = _hy4_layer(fmt)
+    spec = host.spec
+    x = synth.activations(f"x.hy4.{T}", T, spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y, ids, w = layer.forward(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+    err = rel_l2(y.cpu().numpy(), ref.output)
+    assert err < REL_L2_BAR, err
+    assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    # BF16 outputs: every element is a BF16 value
+    assert np.all((y.cpu().numpy().view(np.uint32) & 0xFFFF) == 0)
+    layer.close()
+
+
+def test_hy4_errors():
+    host = _hy4_layer(C.FMT_MXFP8)
+    for bad, status in ((dict(swiglu_limit=0.0), N.ERR_INVALID_GEOMETRY),
+                        (dict(swiglu_limit=float("inf")), N.ERR_NONFINITE),
+                        (dict(expert_format=C.FMT_BF16), N.ERR_ARGUMENT),
+                        (dict(shared_format=C.FMT_BF16), N.ERR_ARGUMENT)):
+        h = C.HostLayer(replace(host.spec, **bad), host.router_weight, host.experts, host.shared,
+                        host.correction_bias)
+        with pytest.raises(N.UrbError) as e:
+            moe_mod().MoeLayer(h, max_tokens=1)
+        assert e.value.status == status
+    layer = moe_mod().MoeLayer(host, max_tokens=2)
+    x = torch.from_numpy(synth.activations("x.hy4.nan", 2, host.spec.hidden)).cuda()
+    x[1, 5] = float("nan")
+    with pytest.raises(N.UrbError) as e:
+        layer.forward(x)
+    assert e.value.status == N.ERR_NONFINITE
     layer.close()
 
 

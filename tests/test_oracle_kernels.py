@@ -478,3 +478,150 @@ def test_glm_layer_vs_float64_mathematics():
             acc += float(res.weights[t, j]) * mlp(spec.expert_format, layer.experts[ids[j]], I)
         rel = np.linalg.norm(res.output[t] - acc) / np.linalg.norm(acc)
         assert rel < 1e-5
+
+
+# ------------------------------------------------------------------- MX-activation mode (Hy4)
+def test_bounded_swiglu_kat():
+    k = KATS["bounded_swiglu_asymmetric_clamp"]
+    out = O.bounded_swiglu(np.array(k["gate"], np.float32), np.array(k["up"], np.float32),
+                           k["limit"])
+    assert abs(float(out[0]) - 10.0 / (1.0 + math.exp(-10.0)) * 10.0) < k["first_tolerance"]
+    lo, hi = k["second_open_interval"]
+    assert lo < float(out[1]) < hi
+    # each branch clamps on its own side: gate only from above, up on both sides
+    out = O.bounded_swiglu(np.array([-3.0, 2.0], np.float32), np.array([-20.0, 0.5], np.float32),
+                           1.0)
+    assert float(out[0]) == np.float32(np.float32(-3.0) / np.float32(1.0 + math.exp(3.0))) * -1.0
+    assert abs(float(out[1]) - 1.0 / (1.0 + math.exp(-1.0)) * 0.5) < 1e-7
+    for limit in (0.0, -1.0, float("nan"), float("inf")):
+        with pytest.raises(O.OracleError) as e:
+            O.bounded_swiglu(np.zeros(2, np.float32), np.zeros(2, np.float32), limit)
+        assert e.value.status == O.INVALID_GEOMETRY
+    with pytest.raises(O.OracleError) as e:
+        O.bounded_swiglu(np.array([np.inf], np.float32), np.zeros(1, np.float32), 7.0)
+    assert e.value.status == O.NONFINITE
+
+
+def _modelopt(rows, cols, seed, codes):
+    """modelopt_matrix of src/models/hy4/expert.rs:782-793: value i = codes[(13 i + seed) % 8],
+    scale i = 124 + (i + seed) % 7."""
+    i = np.arange(rows * cols, dtype=np.int64)
+    vals = np.asarray(codes, np.uint8)[(i * 13 + seed) % len(codes)].reshape(rows, cols)
+    j = np.arange(rows * (cols // 32), dtype=np.int64)
+    sc = (124 + (j + seed) % 7).astype(np.uint8).reshape(rows, cols // 32)
+    return vals, sc
+
+
+def _hy4_fixture_expert():
+    k = KATS["hy4_expert_batch_fixture"]
+    H, I = k["hidden"], k["intermediate"]
+    gu, gus = _modelopt(2 * I, H, k["gate_up_seed"], k["codes"])
+    dn, dns = _modelopt(H, I, k["down_seed"], k["codes"])
+    triple = [(np.ascontiguousarray(gu[:I]), np.ascontiguousarray(gus[:I])),
+              (np.ascontiguousarray(gu[I:]), np.ascontiguousarray(gus[I:])),
+              (dn, dns)]
+    return k, H, I, triple
+
+
+def test_hy4_expert_batched_equals_tokenwise_fixture():
+    # The reference's batched_expert_is_bit_exact_with_independent_tokens
+    # (src/models/hy4/expert.rs:795-828) on its own fixture matrices and inputs.
+    k, H, I, triple = _hy4_fixture_expert()
+    for batch in k["batches"]:
+        x = ((np.arange(batch * H) * 7 % 23).astype(np.float32) - 11.0) / 16.0
+        x = x.reshape(batch, H)
+        got = O.hy4_expert(O.FMT_MXFP8, triple, H, I, x, k["swiglu_limit"])
+        tok = np.stack([O.hy4_expert(O.FMT_MXFP8, triple, H, I, x[t], k["swiglu_limit"])[0]
+                        for t in range(batch)])
+        assert np.array_equal(got.view(np.uint32), tok.view(np.uint32))
+
+
+def _bf16(v):
+    return synth.bf16_to_f32(synth.bf16_rne_bits(np.asarray(v, np.float32)))
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_MXFP8, O.FMT_MXFP4])
+@pytest.mark.parametrize("shared", [False, True])
+def test_hy4_expert_vs_float64_mathematics(fmt, shared):
+    # Independent evaluation of the Hy4 expert: dequantised rows (pinned bit-exact), float64
+    # dot products, the pinned quantizer and BF16 rounding at the stated boundaries.
+    H, I, limit = 128, 64, 1.5
+    if fmt == O.FMT_MXFP8:
+        _, _, _, base = _hy4_fixture_expert()
+        rng = np.random.default_rng(4)
+        fin = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+        triple = []
+        for rows, cols in ((I, H), (I, H), (H, I)):
+            triple.append((rng.choice(fin, (rows, cols)).astype(np.uint8),
+                           rng.integers(118, 124, (rows, cols // 32)).astype(np.uint8)))
+    else:
+        triple = [synth.mxfp4_matrix(f"hy4.{n}", r, c_) for n, r, c_ in
+                  (("g", I, H), ("u", I, H), ("d", H, I))]
+    x = synth.activations("hy4.x", 6, H)
+    got = O.hy4_expert(fmt, triple, H, I, x, 0.0 if shared else limit)
+
+    def deq(d, s, rows, cols):
+        return np.stack([O.row(fmt, d, s, rows, cols, r) for r in range(rows)]).astype(np.float64)
+    G, U, D = deq(*triple[0], I, H), deq(*triple[1], I, H), deq(*triple[2], H, I)
+    same = 0
+    for t in range(x.shape[0]):
+        q = O.simulate_e4m3_activation(x[t], 32).astype(np.float64)
+        g = _bf16((G @ q).astype(np.float32)).astype(np.float64)
+        u = _bf16((U @ q).astype(np.float32)).astype(np.float64)
+        if shared:
+            a = _bf16((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
+        else:
+            gl = np.minimum(g, limit)
+            ul = np.clip(u, -limit, limit)
+            a = (gl / (1.0 + np.exp(-gl)) * ul).astype(np.float32)
+        a = O.simulate_e4m3_activation(a, 32).astype(np.float64)
+        y = _bf16((D @ a).astype(np.float32))
+        same += int(np.sum(y.view(np.uint32) == got[t].view(np.uint32)))
+        # f32 vs f64 sums may flip a BF16 rounding or an E4M3 code; the result stays close
+        assert np.linalg.norm(got[t] - y) <= 2e-2 * np.linalg.norm(y)
+    assert same >= 0.9 * got.size, same / got.size
+
+
+def _hy4_small_layer(fmt, E=8, H=128, I=64, k=3, T=7):
+    spec = C.LayerSpec(hidden=H, n_experts=E, top_k=k, intermediate=I, shared_intermediate=I,
+                       expert_format=fmt, shared_format=fmt, router=C.ROUTER_SIGMOID_NOAUX_TC,
+                       composition=C.COMPOSE_HY4, n_group=1, topk_group=1, normalize=True,
+                       routed_scaling_factor=2.5, swiglu_limit=7.0)
+    bias = (np.arange(E, dtype=np.float32) - E / 2) * np.float32(0.01)
+    return spec, C.make_host_layer(spec, bias=bias), synth.activations("hy4.layer", T, H)
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_MXFP8, O.FMT_MXFP4])
+def test_hy4_layer_composition(fmt):
+    # Hy4 MoeWeights::forward (src/models/hy4/runtime.rs:1371-1447) restated from the oracle's
+    # pinned parts: routes from the router logits, experts and shared expert on the token, then
+    # out = sum over ascending expert id of f32(w * y), + shared, BF16.  (The summation order
+    # itself is invisible after BF16 rounding at these sizes: it is pinned by review against
+    # runtime.rs:1387-1394, 1436-1441, and the GPU follows the same order.)
+    spec, layer, x = _hy4_small_layer(fmt)
+    res = O.moe_forward(spec, layer.experts, layer.router_weight, x, layer.correction_bias,
+                        layer.shared)
+    H, I, K = spec.hidden, spec.intermediate, spec.top_k
+    for t in range(x.shape[0]):
+        ids, w, _ = O.route_noaux_tc(res.logits[t], layer.correction_bias, K, 1, 1, True, 2.5)
+        assert list(ids) == list(res.ids[t]) and np.array_equal(w, res.weights[t])
+        ys = {int(e): O.hy4_expert(fmt, layer.experts[e], H, I, x[t], 7.0)[0] for e in ids}
+        sh = O.hy4_expert(fmt, layer.shared, H, I, x[t], 0.0)[0]
+
+        def combine(order):
+            acc = np.zeros(H, np.float32)
+            for j in order:
+                acc = acc + np.float32(w[j]) * ys[int(ids[j])]
+            return _bf16(acc + sh)
+        asc = sorted(range(K), key=lambda j: ids[j])
+        assert np.array_equal(combine(asc).view(np.uint32), res.output[t].view(np.uint32))
+
+
+def test_hy4_layer_rejects_bf16_and_bad_limit():
+    spec, layer, x = _hy4_small_layer(O.FMT_MXFP8)
+    for bad, status in ((replace(spec, swiglu_limit=0.0), O.INVALID_GEOMETRY),
+                        (replace(spec, expert_format=O.FMT_BF16), O.SHAPE)):
+        with pytest.raises(O.OracleError) as e:
+            O.moe_forward(bad, layer.experts, layer.router_weight, x, layer.correction_bias,
+                          layer.shared)
+        assert e.value.status == status

@@ -12,6 +12,11 @@ routed_scaling_factor) plus the projection formats of ``WeightMatrix``
 * ``COMPOSE_GLM`` -- RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176): ordered
   f64 router GEMV, softmax top-k or sigmoid noaux_tc, GatedMlp experts, f64 combine in ranking
   order on top of the shared expert.
+* ``COMPOSE_HY4`` -- the MX-activation mode, Hy4 MoeWeights::forward
+  (src/models/hy4/runtime.rs:1371-1447): ordered f64 router GEMV, every MX projection fed by
+  simulate_e4m3_activation(x, 32), routed experts with BF16 gate/up and a bounded SwiGLU
+  (``swiglu_limit``), BF16 expert outputs, f32 combine in ascending expert id plus the shared
+  expert, rounded to BF16.
 """
 
 from __future__ import annotations
@@ -25,7 +30,7 @@ from . import synth
 
 FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
 ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
-COMPOSE_QWEN36, COMPOSE_GLM = 0, 1
+COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4 = 0, 1, 2
 FORMAT_NAMES = {FMT_BF16: "bf16", FMT_MXFP4: "mxfp4", FMT_MXFP8: "mxfp8"}
 
 
@@ -44,6 +49,7 @@ class LayerSpec:
     topk_group: int = 1
     normalize: bool = True
     routed_scaling_factor: float = 1.0
+    swiglu_limit: float = 0.0   # COMPOSE_HY4 routed experts
 
 
 def matrix_bytes(fmt: int, rows: int, cols: int) -> Tuple[int, int]:

@@ -32,7 +32,7 @@ template <int FMT, bool PAIR, int DEPTH, int NP, int MT>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
                                                       Perm perm, int rows, int K,
                                                       const float* __restrict__ in,
-                                                      float* __restrict__ out, int qwen,
+                                                      float* __restrict__ out, Epi epi,
                                                       int* status) {
   constexpr int RG = MT / 32;       // staging rows per thread
   constexpr int MBMAX = MT / 16;    // 16-token MFMA blocks per tile
@@ -191,30 +191,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
         const int mm = mb * 16 + 4 * lq + i;
         if (mm >= mrows) continue;
         const size_t p = (size_t)(base + m0 + mm);
-        if constexpr (PAIR) {
-          const float g0 = acc0[q][mb][i], u0 = acc1[q][mb][i];
-          float act;
-          if (qwen) {
-            float g, u, ag;
-            bool ok = rne_bf16(g0, &g) && rne_bf16(u0, &u) && rne_bf16(silu(g), &ag);
-            float v = ag * u;
-            ok = ok && rne_bf16(v, &act);
-            if (!ok) { bad = true; act = v; }
-          } else {
-            act = silu(g0) * u0;
-            if (!finite(act)) bad = true;
-          }
-          out[p * rows + row] = act;
-        } else {
-          float y = acc0[q][mb][i];
-          if (qwen) {
-            float r;
-            if (!rne_bf16(y, &r)) bad = true; else y = r;
-          } else if (FMT == kFmtMXFP8 && !finite(y)) {
-            bad = true;
-          }
-          out[p * rows + row] = y;
-        }
+        if constexpr (PAIR)
+          out[p * rows + row] = epi_gate_up(epi, acc0[q][mb][i], acc1[q][mb][i], bad);
+        else
+          out[p * rows + row] = epi_down<FMT>(epi, acc0[q][mb][i], bad);
       }
     }
   }
@@ -223,9 +203,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
 
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
-                         const float* in, float* out, int qwen, int* status, hipStream_t s) {
+                         const float* in, float* out, Epi epi, int* status, hipStream_t s) {
   dim3 grid(rows / (kNT * NP), max_tiles);
-  gemm_kernel<FMT, PAIR, DEPTH, NP, MT><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, qwen,
+  gemm_kernel<FMT, PAIR, DEPTH, NP, MT><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, epi,
                                                               status);
 }
 
@@ -235,30 +215,30 @@ static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles
 // Rows are multiples of 128 (urb_moe_create), so NP = 2 always tiles them.
 template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
-                   const float* in, float* out, int qwen, int* status, hipStream_t s) {
+                   const float* in, float* out, Epi epi, int* status, hipStream_t s) {
   if constexpr (FMT == kFmtBF16)
-    launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+    launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
   else if constexpr (FMT == kFmtMXFP8)
-    launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+    launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
   else if (rows % (kNT * 4) == 0)
-    launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+    launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
   else
-    launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, qwen, status, s);
+    launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
 }
 
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
-                         int I, const float* x, float* act, int qwen, int* status,
+                         int I, const float* x, float* act, Epi epi, int* status,
                          hipStream_t s) {
-  if (fmt == kFmtBF16) launch<kFmtBF16, true>(mats, perm, max_tiles, I, H, x, act, qwen, status, s);
-  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, true>(mats, perm, max_tiles, I, H, x, act, qwen, status, s);
-  else launch<kFmtMXFP8, true>(mats, perm, max_tiles, I, H, x, act, qwen, status, s);
+  if (fmt == kFmtBF16) launch<kFmtBF16, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s);
+  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s);
+  else launch<kFmtMXFP8, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s);
 }
 
 void launch_gemm_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
-                      int I, const float* act, float* y, int qwen, int* status, hipStream_t s) {
-  if (fmt == kFmtBF16) launch<kFmtBF16, false>(mats, perm, max_tiles, H, I, act, y, qwen, status, s);
-  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, false>(mats, perm, max_tiles, H, I, act, y, qwen, status, s);
-  else launch<kFmtMXFP8, false>(mats, perm, max_tiles, H, I, act, y, qwen, status, s);
+                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s) {
+  if (fmt == kFmtBF16) launch<kFmtBF16, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s);
+  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s);
+  else launch<kFmtMXFP8, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s);
 }
 
 }  // namespace urb

@@ -105,7 +105,7 @@ template <int FMT, bool PAIR, int DEPTH>
 __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict__ mats,
                                                    Perm perm, int rows, int cols, int ksplit,
                                                    const float* __restrict__ in,
-                                                   float* __restrict__ out, int qwen,
+                                                   float* __restrict__ out, Epi epi,
                                                    int* status) {
   extern __shared__ float xs[];  // xs_floats(cols) staged input + [4][16][2] part sums
   int expert, base, count;
@@ -192,32 +192,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict_
   if (!valid || part != 0 || lane >= 16) return;
   const int r = panel * kPanelRows + ln;
   bool bad = false;
-  if constexpr (PAIR) {
-    // Qwen38Expert (src/models/qwen3_8/expert.rs:137-207): g, u, silu(g), g*u in BF16.
-    // GatedMlp (src/model/mlp.rs:90-99): silu(g) * u in f32; a non-finite activation is
-    // rejected by the down projection's input check.
-    float act;
-    if (qwen) {
-      float g, u, ag, v;
-      bool ok = rne_bf16(acc0, &g) && rne_bf16(acc1, &u) && rne_bf16(silu(g), &ag);
-      v = ag * u;
-      ok = ok && rne_bf16(v, &act);
-      if (!ok) { bad = true; act = v; }
-    } else {
-      act = silu(acc0) * acc1;
-      if (!finite(act)) bad = true;
-    }
-    out[(size_t)p * rows + r] = act;
-  } else {
-    float y = acc0;
-    if (qwen) {
-      float rr;
-      if (!rne_bf16(y, &rr)) bad = true; else y = rr;
-    } else if (FMT == kFmtMXFP8 && !finite(y)) {
-      bad = true;  // MxFp8Matrix::matvec_rows rejects non-finite outputs (mxfp.rs:779-781)
-    }
-    out[(size_t)p * rows + r] = y;
-  }
+  if constexpr (PAIR)
+    out[(size_t)p * rows + r] = epi_gate_up(epi, acc0, acc1, bad);
+  else
+    out[(size_t)p * rows + r] = epi_down<FMT>(epi, acc0, bad);
   if (bad) flag(status, kStatusNonFinite);
 }
 
@@ -230,7 +208,7 @@ constexpr int gemv_depth() {
 
 template <int FMT, bool PAIR>
 static void launch_gemv(const ExpertMats* mats, const Perm& perm, int max_active, int rows,
-                        int cols, const float* in, float* out, int qwen, int* status,
+                        int cols, const float* in, float* out, Epi epi, int* status,
                         hipStream_t s) {
   constexpr int D = gemv_depth<FMT, PAIR>();
   const int panels = rows / kPanelRows, steps = cols / kGemmKStep;
@@ -241,23 +219,23 @@ static void launch_gemv(const ExpertMats* mats, const Perm& perm, int max_active
   const int ppw = 4 / ksplit;
   dim3 grid((panels + ppw - 1) / ppw, max_active);
   const size_t lds = (xs_floats(cols) + 4 * 16 * 2) * sizeof(float);
-  gemv_kernel<FMT, PAIR, D><<<grid, 256, lds, s>>>(mats, perm, rows, cols, ksplit, in, out, qwen,
+  gemv_kernel<FMT, PAIR, D><<<grid, 256, lds, s>>>(mats, perm, rows, cols, ksplit, in, out, epi,
                                                    status);
 }
 
 void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
-                         int H, int I, const float* x, float* act, int qwen, int* status,
+                         int H, int I, const float* x, float* act, Epi epi, int* status,
                          hipStream_t s) {
-  if (fmt == kFmtBF16) launch_gemv<kFmtBF16, true>(mats, perm, max_active, I, H, x, act, qwen, status, s);
-  else if (fmt == kFmtMXFP4) launch_gemv<kFmtMXFP4, true>(mats, perm, max_active, I, H, x, act, qwen, status, s);
-  else launch_gemv<kFmtMXFP8, true>(mats, perm, max_active, I, H, x, act, qwen, status, s);
+  if (fmt == kFmtBF16) launch_gemv<kFmtBF16, true>(mats, perm, max_active, I, H, x, act, epi, status, s);
+  else if (fmt == kFmtMXFP4) launch_gemv<kFmtMXFP4, true>(mats, perm, max_active, I, H, x, act, epi, status, s);
+  else launch_gemv<kFmtMXFP8, true>(mats, perm, max_active, I, H, x, act, epi, status, s);
 }
 
 void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active, int H,
-                      int I, const float* act, float* y, int qwen, int* status, hipStream_t s) {
-  if (fmt == kFmtBF16) launch_gemv<kFmtBF16, false>(mats, perm, max_active, H, I, act, y, qwen, status, s);
-  else if (fmt == kFmtMXFP4) launch_gemv<kFmtMXFP4, false>(mats, perm, max_active, H, I, act, y, qwen, status, s);
-  else launch_gemv<kFmtMXFP8, false>(mats, perm, max_active, H, I, act, y, qwen, status, s);
+                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s) {
+  if (fmt == kFmtBF16) launch_gemv<kFmtBF16, false>(mats, perm, max_active, H, I, act, y, epi, status, s);
+  else if (fmt == kFmtMXFP4) launch_gemv<kFmtMXFP4, false>(mats, perm, max_active, H, I, act, y, epi, status, s);
+  else launch_gemv<kFmtMXFP8, false>(mats, perm, max_active, H, I, act, y, epi, status, s);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -1,0 +1,167 @@
+// urb_hy4.hip -- the MX-activation mode (Hy4 composition): the activation quantizer and the
+// combine.  The projections run on the BF16 MFMA kernels (urb_gemm.hip, urb_gemv.hip): a
+// simulated E4M3 activation is an E4M3 code times a power of two, exactly a BF16 value, so
+// the A operand needs no low half and every product is exact; the f32 accumulation of those
+// kernels then stays within f32 rounding of the reference's sums.
+//
+// (CDNA4's v_mfma_scale_f32_16x16x128_f8f6f4 takes the codes and E8M0 scales as they are, but
+// its sum of 128 products is not accurate to f32: measured on MI355X, its error reaches
+// ~2e-4 of the sum of |products| for full-range E4M3/E2M1 operands.  The BF16 rounding and
+// E4M3 re-quantization between Hy4's projections amplify that past the layer's parity bar, so
+// the scaled MFMA is not used here; tests/test_gpu_parity.py pins its operand layout.)
+#include "urb_device.hpp"
+#include "urb_kernels.hpp"
+#include "urb_panel.hpp"
+
+#include <algorithm>
+
+namespace urb {
+
+// ------------------------------------------------------------------------------------------
+// simulate_e4m3_activation as (code, scale) pairs.
+// ------------------------------------------------------------------------------------------
+
+// power_of_two_ceiling (src/math/mxfp.rs:300-319) for a positive finite normal value: the
+// exponent increment, except near powers of two (mantissa <= 4096 or >= 2^23 - 1 - 4096), where
+// the reference keeps 2^ceil(log2(v)) with an f32 logarithm.  log2 here is the f64 logarithm
+// rounded to f32 (correctly rounded there: no mantissa in that band puts log2(v) near an f32
+// rounding boundary).
+__device__ __forceinline__ float pow2_ceiling(float v) {
+  const uint32_t bits = f2u(v);
+  const uint32_t exponent = bits & 0x7f800000u, mantissa = bits & 0x007fffffu;
+  if (mantissa == 0) return v;
+  if (exponent == 0 || mantissa <= 4096u || mantissa >= 0x007fffffu - 4096u) {
+    const float l = (float)log2((double)v);
+    return ldexpf(1.0f, (int)ceilf(l));
+  }
+  return u2f(exponent + 0x00800000u);
+}
+
+// encode_e4m3fn_finite (src/math/mxfp.rs:246-275): clamp to +-448, round to nearest even on the
+// E4M3 grid (subnormals below 2^-6 on the 2^-9 grid), saturate at code 0x7E; -0 encodes as 0.
+__device__ __forceinline__ uint32_t encode_e4m3(float value) {
+  value = fminf(fmaxf(value, -448.0f), 448.0f);
+  const float mag = fabsf(value);
+  if (mag == 0.0f) return 0;
+  uint32_t code;
+  if (mag < 0.015625f) {
+    code = (uint32_t)rintf(mag * 512.0f);
+  } else {
+    const uint32_t b = f2u(mag);
+    const uint32_t r = (b + 0x7ffffu + ((b >> 20) & 1u)) & ~0xfffffu;
+    const uint32_t e = (r >> 23) & 0xffu;
+    const uint32_t ex = e > 120u ? e - 120u : 0u;
+    code = min((ex << 3) | ((r >> 20) & 7u), 0x7eu);
+  }
+  return (value < 0.0f && code != 0) ? (code | 0x80u) : code;
+}
+
+// One 32-lane half wavefront per 32-value block of a row-major [rows, cols] f32 matrix
+// (cols % 32 == 0).  Outputs (each optional): the simulated values decode(code) * scale
+// (`values` may alias x: every lane reads its element before any lane writes), the codes
+// [rows, cols] and the scales [rows, cols / 32] (the E8M0 byte is the biased exponent of the
+// power-of-two scale).  Non-finite input -> status (mxfp.rs:93-99).
+__global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nblocks,
+                                                       float* values,
+                                                       uint8_t* __restrict__ codes,
+                                                       uint8_t* __restrict__ scales, int* status) {
+  const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  const size_t blk = gid >> 5;
+  const bool live = blk < nblocks;
+  const float v = live ? x[gid] : 0.0f;
+  float a = fabsf(v);
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+  if (!live) return;
+  if (!finite(v) && status) flag(status, kStatusNonFinite);
+  a = fmaxf(a, 1.0e-4f);  // fold(1.0e-4, f32::max) over |x| (mxfp.rs:104-107)
+  const float scale = pow2_ceiling(a / 448.0f);
+  const uint32_t code = encode_e4m3(v / scale);
+  if (values) {
+    // E4M3 code -> value via the conversion instruction (exact), times the power of two
+    const float d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false)[0];
+    values[gid] = d * scale;
+  }
+  if (codes) codes[gid] = (uint8_t)code;
+  if (scales && (gid & 31) == 0) scales[blk] = (uint8_t)(f2u(scale) >> 23);
+}
+
+void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
+                     uint8_t* scales, int* status, hipStream_t s) {
+  const size_t nblocks = rows * cols / 32;
+  const size_t threads = nblocks * 32;
+  quantize_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(x, nblocks, values, codes,
+                                                                     scales, status);
+}
+
+// ------------------------------------------------------------------------------------------
+// Combine (Hy4 MoeWeights::forward, src/models/hy4/runtime.rs:1387-1445): out = 0; for the
+// routes in ascending expert id, out += w * y (f32 multiply, f32 add); out += shared; BF16.
+// ------------------------------------------------------------------------------------------
+template <int KMAX>
+__global__ __launch_bounds__(256) void combine_hy4_kernel(const float* __restrict__ y,
+                                                          const int32_t* __restrict__ pos,
+                                                          const float* __restrict__ w,
+                                                          const int32_t* __restrict__ asc,
+                                                          const float* __restrict__ shared,
+                                                          int T, int K, int H,
+                                                          float* __restrict__ out,
+                                                          int* status) {
+  const int h4 = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.y;
+  if (h4 * 4 >= H) return;
+  int rk[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) rk[j] = j < K ? asc[(size_t)t * K + j] : 0;
+  float wt[KMAX];
+  float4 v[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < K) {
+      wt[j] = w[(size_t)t * K + rk[j]];
+      const int p = pos ? pos[(size_t)t * K + rk[j]] : rk[j];
+      v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
+    }
+  }
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < K) {
+      acc[0] = acc[0] + wt[j] * v[j].x;
+      acc[1] = acc[1] + wt[j] * v[j].y;
+      acc[2] = acc[2] + wt[j] * v[j].z;
+      acc[3] = acc[3] + wt[j] * v[j].w;
+    }
+  }
+  if (shared) {
+    const float4 sh = reinterpret_cast<const float4*>(shared + (size_t)t * H)[h4];
+    acc[0] = acc[0] + sh.x;
+    acc[1] = acc[1] + sh.y;
+    acc[2] = acc[2] + sh.z;
+    acc[3] = acc[3] + sh.w;
+  }
+  bool bad = false;
+  float r[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (!rne_bf16(acc[u], &r[u])) {
+      bad = true;
+      r[u] = acc[u];
+    }
+  if (bad) flag(status, kStatusNonFinite);
+  reinterpret_cast<float4*>(out + (size_t)t * H)[h4] = make_float4(r[0], r[1], r[2], r[3]);
+}
+
+void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
+                        const int32_t* asc, const float* shared, int T, int K, int H,
+                        float* out, int* status, hipStream_t s) {
+  dim3 grid((H / 4 + 255) / 256, T);
+  if (K <= 8)
+    combine_hy4_kernel<8><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, shared, T, K,
+                                                H, out, status);
+  else
+    combine_hy4_kernel<32><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, shared, T,
+                                                 K, H, out, status);
+}
+
+}  // namespace urb

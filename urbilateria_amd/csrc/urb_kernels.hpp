@@ -49,6 +49,21 @@ struct Perm {
   int direct_k;
 };
 
+// Epilogue of the expert projections (gate/up pair -> activation; down -> output):
+//   kEpiGated     GatedMlp (src/model/mlp.rs:90-99): silu(g) * u in f32; f32 outputs.
+//   kEpiQwen      Qwen38Expert (src/models/qwen3_8/expert.rs:137-207): g, u, silu(g), the
+//                 product and the outputs rounded to BF16.
+//   kEpiHy4       Hy4 routed expert (src/models/hy4/expert.rs:664-680): g, u rounded to BF16,
+//                 bounded_swiglu with `limit` (src/models/deepseek_v4/math.rs:526-548); BF16
+//                 outputs.
+//   kEpiHy4Shared Hy4 shared DenseMlp (src/models/hy4/runtime.rs:1311-1321):
+//                 bf16(silu(bf16(g)) * bf16(u)); BF16 outputs.
+enum { kEpiGated = 0, kEpiQwen = 1, kEpiHy4 = 2, kEpiHy4Shared = 3 };
+struct Epi {
+  int kind;
+  float limit;
+};
+
 // Grouped GEMM (MFMA) tiling: tokens per tile, weight rows per workgroup (four panels), K per
 // step.
 constexpr int kGemmMTile = 32;
@@ -60,10 +75,10 @@ inline int gemm_max_tiles(int n, int k, int E) {
   return a + (n * k + kGemmMTile - 1) / kGemmMTile;
 }
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
-                         int I, const float* x, float* act, int qwen, int* status,
+                         int I, const float* x, float* act, Epi epi, int* status,
                          hipStream_t s);
 void launch_gemm_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
-                      int I, const float* act, float* y, int qwen, int* status, hipStream_t s);
+                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s);
 
 struct RouteParams {
   int router;        // 0 softmax top-k, 1 sigmoid noaux_tc, 2 sqrt-softplus
@@ -100,20 +115,29 @@ constexpr int kMaxChunkTokens = 1024;
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
                     int32_t* tiles, hipStream_t s);
-// Decode projections (GEMV family, one token per active expert): gate+up with the SwiGLU
-// epilogue, then down.  `qwen` selects the BF16 boundaries of Qwen38Expert; otherwise
-// GatedMlp's f32 path.
+// Decode projections (GEMV family, one token per active expert): gate+up with the activation
+// epilogue, then down.
 void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
-                         int H, int I, const float* x, float* act, int qwen, int* status,
+                         int H, int I, const float* x, float* act, Epi epi, int* status,
                          hipStream_t s);
 void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active, int H,
-                      int I, const float* act, float* y, int qwen, int* status, hipStream_t s);
+                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s);
 // Combines: Qwen BF16 ascending-id, GLM f64 ranking order.
 void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                          const int32_t* asc, int T, int K, int H, float* out, int* status,
                          hipStream_t s);
 void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                         const float* shared, int T, int K, int H, float* out, hipStream_t s);
+// MX-activation mode (Hy4 composition).  simulate_e4m3_activation (src/math/mxfp.rs:89-115)
+// of [rows, cols] f32 (cols % 32 == 0) per 32-value block of each row: the simulated f32 values
+// (`values`, may alias x) and/or the E4M3 codes [rows, cols] + E8M0 scales [rows, cols / 32]
+// they are made of; either output may be null.
+void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
+                     uint8_t* scales, int* status, hipStream_t s);
+// Hy4 combine: ascending expert id, f32, + shared, BF16.
+void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
+                        const int32_t* asc, const float* shared, int T, int K, int H,
+                        float* out, int* status, hipStream_t s);
 // Payload validation: bit 1 = non-finite BF16 / E4M3 NaN code, bit 2 = E8M0 0xFF.
 void launch_validate(int fmt, const uint8_t* data, size_t data_bytes, const uint8_t* scales,
                      size_t scale_bytes, int* flags, hipStream_t s);

@@ -44,6 +44,7 @@ struct Workspace {
   float* y_perm = nullptr;
   float* shared_act = nullptr;
   float* shared_out = nullptr;
+  float* xq = nullptr;  // HY4: the simulated E4M3 token activations [chunk, H]
   int* status = nullptr;  // [0] latched numerical failures, [1] validation flags
 };
 
@@ -164,6 +165,14 @@ static urb_status check_desc(const urb_moe_desc* d) {
     if (d->expert_format != URB_FMT_BF16 || d->shared_intermediate != 0 ||
         d->router != URB_ROUTER_SOFTMAX_TOPK)
       return URB_ERR_ARGUMENT;
+  } else if (d->composition == URB_COMPOSE_HY4) {
+    // MX projections only (the activation mode exists for MX weights), and the routed experts'
+    // SwiGLU limit must be finite and positive (Hy4Config validation, hy4/config.rs:235-236).
+    if (d->expert_format == URB_FMT_BF16 ||
+        (d->shared_intermediate && d->shared_format == URB_FMT_BF16))
+      return URB_ERR_ARGUMENT;
+    if (!finite_host(d->swiglu_limit)) return URB_ERR_NONFINITE;
+    if (d->swiglu_limit <= 0.0f) return URB_ERR_INVALID_GEOMETRY;
   } else if (d->composition != URB_COMPOSE_GLM) {
     return URB_ERR_ARGUMENT;
   }
@@ -180,7 +189,7 @@ static urb_status check_desc(const urb_moe_desc* d) {
     if (d->n_group > 64) return URB_ERR_ARGUMENT;
   } else if (d->router == URB_ROUTER_SQRT_SOFTPLUS) {
     // route_sqrt_softplus: validate_positive(routed_scaling_factor) (deepseek_v4/math.rs:468)
-    if (d->composition != URB_COMPOSE_GLM) return URB_ERR_ARGUMENT;
+    if (d->composition == URB_COMPOSE_QWEN36) return URB_ERR_ARGUMENT;
     if (!finite_host(d->routed_scaling_factor)) return URB_ERR_NONFINITE;
     if (d->routed_scaling_factor <= 0.0f) return URB_ERR_INVALID_GEOMETRY;
   } else if (d->router != URB_ROUTER_SOFTMAX_TOPK) {
@@ -208,7 +217,7 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   Workspace& w = c->ws;
   w.status = b.take<int>(4);
   w.logits = b.take<float>(C * E);
-  if (d.composition == URB_COMPOSE_GLM) {
+  if (d.composition != URB_COMPOSE_QWEN36) {
     size_t most = 0;  // largest slices x tokens any call can need
     for (size_t t = 1; t <= C; ++t)
       most = std::max(most, (size_t)urb::router_slices((int)E, (int)H, (int)t) * t);
@@ -228,6 +237,7 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   w.y_perm = b.take<float>(C * K * H);
   w.shared_act = b.take<float>(C * std::max<size_t>(d.shared_intermediate, 1));
   w.shared_out = b.take<float>(C * H);
+  if (d.composition == URB_COMPOSE_HY4) w.xq = b.take<float>(C * H);
 }
 
 static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
@@ -457,9 +467,95 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logi
   }
   {
     Span span(c, URB_STAGE_ROUTE, s);
-    urb::launch_route(logits, n, E, K, rp, ids, weights, qwen ? c->ws.asc : nullptr,
+    const bool ascending = qwen || d.composition == URB_COMPOSE_HY4;
+    urb::launch_route(logits, n, E, K, rp, ids, weights, ascending ? c->ws.asc : nullptr,
                       c->ws.status, s);
   }
+  return URB_OK;
+}
+
+// The MX-activation mode (Hy4 MoeWeights::forward, src/models/hy4/runtime.rs:1371-1447) for
+// one chunk of n tokens.  Every MX projection reads simulated E4M3 activations (BF16-exact
+// values); the BF16 MFMA / FMA kernels run them with the Hy4 epilogues.
+static urb_status forward_hy4(urb_moe_ctx* c, const float* xc, int n, float* yc, int32_t* idc,
+                              float* wc, hipStream_t s) {
+  const urb_moe_desc& d = c->desc;
+  const bool has_shared = d.shared_intermediate != 0;
+  const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
+  const int Is = (int)d.shared_intermediate;
+  Workspace& ws = c->ws;
+  const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
+  const urb::Epi dense_mlp{urb::kEpiHy4Shared, 0.0f};
+  // mx_activation(input) once per token (runtime.rs:1397); the shared expert quantizes the same
+  // input the same way (runtime.rs:1312), so both read it.
+  urb::launch_quantize(xc, (size_t)n, (size_t)H, ws.xq, nullptr, nullptr, ws.status, s);
+  if (has_shared) {
+    URB_HIP(hipEventRecord(c->fork, s));
+    URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
+    Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
+    const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
+    {
+      Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
+      if (n > 1)
+        urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                                 ws.xq, ws.shared_act, dense_mlp, ws.status, c->side);
+      else
+        urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xq,
+                                 ws.shared_act, dense_mlp, ws.status, c->side);
+      // mx_linear(down, activated) re-quantizes (runtime.rs:1321, 2425-2428)
+      urb::launch_quantize(ws.shared_act, (size_t)n, (size_t)Is, ws.shared_act, nullptr, nullptr,
+                           ws.status, c->side);
+    }
+    {
+      Span span(c, URB_STAGE_SHARED_DOWN, c->side);
+      if (n > 1)
+        urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                              ws.shared_act, ws.shared_out, dense_mlp, ws.status, c->side);
+      else
+        urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_act,
+                              ws.shared_out, dense_mlp, ws.status, c->side);
+    }
+    URB_HIP(hipEventRecord(c->join, c->side));
+  }
+  route_chunk(c, xc, n, ws.logits, idc, wc, s);
+  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles,
+            n == 1 ? idc : nullptr, K};
+  if (n > 1) {
+    Span span(c, URB_STAGE_PERMUTE, s);
+    urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token,
+                        ws.pos_of_slot, ws.tiles, s);
+  }
+  const int32_t* pos = n == 1 ? nullptr : ws.pos_of_slot;
+  const int max_active = std::min(E, n * K);
+  const int max_tiles = urb::gemm_max_tiles(n, K, E);
+  {
+    Span span(c, URB_STAGE_GATE_UP, s);
+    if (n > 1)
+      urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, ws.xq, ws.act,
+                               routed, ws.status, s);
+    else
+      urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, ws.xq, ws.act,
+                               routed, ws.status, s);
+    // activate_gate_up's simulate_e4m3_activation of the SwiGLU output (expert.rs:677)
+    urb::launch_quantize(ws.act, (size_t)n * K, (size_t)I, ws.act, nullptr, nullptr, ws.status,
+                         s);
+  }
+  {
+    Span span(c, URB_STAGE_DOWN, s);
+    if (n > 1)
+      urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act, ws.y_perm,
+                            routed, ws.status, s);
+    else
+      urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act, ws.y_perm,
+                            routed, ws.status, s);
+  }
+  if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+  {
+    Span span(c, URB_STAGE_COMBINE, s);
+    urb::launch_combine_hy4(ws.y_perm, pos, wc, ws.asc, has_shared ? ws.shared_out : nullptr, n,
+                            K, H, yc, ws.status, s);
+  }
+  if (c->profiling) return collect_spans(c);
   return URB_OK;
 }
 
@@ -474,12 +570,19 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
   const int Is = (int)d.shared_intermediate;
   hipStream_t s = static_cast<hipStream_t>(stream);
   Workspace& ws = c->ws;
+  const urb::Epi gated{urb::kEpiGated, 0.0f};
+  const urb::Epi epi{qwen ? urb::kEpiQwen : urb::kEpiGated, 0.0f};
   for (uint32_t c0 = 0; c0 < tokens; c0 += c->chunk) {
     const int n = (int)std::min<uint32_t>(c->chunk, tokens - c0);
     const float* xc = x + (size_t)c0 * H;
     float* yc = y + (size_t)c0 * H;
     int32_t* idc = ids ? ids + (size_t)c0 * K : ws.ids;
     float* wc = weights ? weights + (size_t)c0 * K : ws.weights;
+    if (d.composition == URB_COMPOSE_HY4) {
+      urb_status st = forward_hy4(c, xc, n, yc, idc, wc, s);
+      if (st) return st;
+      continue;
+    }
     if (has_shared) {
       // GatedMlp shared expert (src/models/glm/runtime/moe.rs:162) does not depend on the
       // routes: it runs on the side stream while the router, top-k and permutation run here.
@@ -491,19 +594,19 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
         Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
         if (n > 1)
           urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                   xc, ws.shared_act, 0, ws.status, c->side);
+                                   xc, ws.shared_act, gated, ws.status, c->side);
         else
           urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, xc,
-                                   ws.shared_act, 0, ws.status, c->side);
+                                   ws.shared_act, gated, ws.status, c->side);
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, c->side);
         if (n > 1)
           urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                ws.shared_act, ws.shared_out, 0, ws.status, c->side);
+                                ws.shared_act, ws.shared_out, gated, ws.status, c->side);
         else
           urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is,
-                                ws.shared_act, ws.shared_out, 0, ws.status, c->side);
+                                ws.shared_act, ws.shared_out, gated, ws.status, c->side);
       }
       URB_HIP(hipEventRecord(c->join, c->side));
     }
@@ -524,19 +627,19 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       Span span(c, URB_STAGE_GATE_UP, s);
       if (n > 1)
         urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act,
-                                 qwen ? 1 : 0, ws.status, s);
+                                 epi, ws.status, s);
       else
         urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, xc, ws.act,
-                                 qwen ? 1 : 0, ws.status, s);
+                                 epi, ws.status, s);
     }
     {
       Span span(c, URB_STAGE_DOWN, s);
       if (n > 1)
         urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act,
-                              ws.y_perm, qwen ? 1 : 0, ws.status, s);
+                              ws.y_perm, epi, ws.status, s);
       else
         urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act,
-                              ws.y_perm, qwen ? 1 : 0, ws.status, s);
+                              ws.y_perm, epi, ws.status, s);
     }
     if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {
@@ -622,6 +725,16 @@ urb_status urb_dequant_rows(urb_format format, const void* data, const uint8_t* 
   if (count == 0) return URB_OK;
   urb::launch_dequant(format, static_cast<const uint8_t*>(data), scales, (int)rows, (int)cols,
                       (int)row0, (int)count, out, static_cast<hipStream_t>(stream));
+  URB_HIP(hipGetLastError());
+  return URB_OK;
+}
+
+urb_status urb_quantize_e4m3(const float* x, uint32_t rows, uint32_t cols, uint8_t* codes,
+                             uint8_t* scales, void* stream) {
+  if (!x || !codes || !scales) return URB_ERR_ARGUMENT;
+  if (rows == 0 || cols == 0 || cols % 32) return URB_ERR_SHAPE;
+  urb::launch_quantize(x, rows, cols, nullptr, codes, scales, nullptr,
+                       static_cast<hipStream_t>(stream));
   URB_HIP(hipGetLastError());
   return URB_OK;
 }

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "urb_panel.hpp"
+
 namespace {
 
 __device__ __forceinline__ uint64_t splitmix(uint64_t seed, uint64_t n) {
@@ -108,6 +110,34 @@ __global__ void cvt_bf16_kernel(int fmt, const uint8_t* codes, const uint8_t* sc
   out[i] = __builtin_bit_cast(uint16_t, v[0]);
 }
 
+// One v_mfma_scale_f32_16x16x128_f8f6f4 step built by the MX-activation kernels' own operand
+// helpers (urb_panel.hpp): A = a row-major [16][128] E4M3 matrix with [16][4] E8M0 scales,
+// staged in LDS and read as lds_qfrag does; B = 16 weight rows as one panel's 128-column step
+// (MXFP4 packed [16][64] or MXFP8 [16][128], scales [16][4]) loaded into the panel lanes
+// (unit ln + 16 c = row ln, block c; MXFP8 as the two half-block slabs) and turned into the
+// operand by mx_operand.  C[16][16] = A . B^T in the C layout of the BF16 MFMA.
+template <int FMT>
+__global__ void mfma_scale_layout_kernel(const uint8_t* A, const uint8_t* sa, const uint8_t* B,
+                                         const uint8_t* sb, float* C) {
+  using namespace urb;
+  __shared__ __attribute__((aligned(16))) uint8_t aq[16 * kQLd];
+  const int l = threadIdx.x, r = l % 16, c = l / 16;
+  for (int i = l; i < 16 * 128; i += 64) aq[(i / 128) * kQLd + i % 128] = A[i];
+  __syncthreads();
+  const i32x8 a = lds_qfrag(aq, r, c);
+  BRaw<FMT> raw;
+  if constexpr (FMT == kFmtMXFP4) {
+    raw.q = *reinterpret_cast<const uint4*>(B + r * 64 + 16 * c);
+  } else {
+    raw.q[0] = *reinterpret_cast<const uint4*>(B + r * 128 + 32 * c);
+    raw.q[1] = *reinterpret_cast<const uint4*>(B + r * 128 + 32 * c + 16);
+  }
+  raw.s = sb[r * 4 + c];
+  const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+  const f32x4_t acc = mfma_mx<FMT>(a, sa[r * 4 + c], mx_operand(raw), (int)raw.s, z);
+  for (int i = 0; i < 4; ++i) C[(4 * c + i) * 16 + r] = acc[i];
+}
+
 int grid_for(size_t n) {
   size_t b = (n + 255) / 256;
   return (int)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
@@ -146,6 +176,21 @@ int urb_synth_e8m0(uint64_t seed, size_t n, void* out, void* stream) {
 // Diagnostics: C[16,16] = A[16,32] . B[32,16] through one MFMA (device f32 arrays).
 int urb_probe_mfma_16x16x32(const float* A, const float* B, float* C, void* stream) {
   mfma_layout_kernel<<<1, 64, 0, (hipStream_t)stream>>>(A, B, C);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+// Diagnostics: C[16,16] = (A * sa)[16,128] . (B * sb)[16,128]^T through one scaled MFMA step
+// of the MX-activation kernels.
+// fmt_b: 1 = MXFP4 weights, 2 = MXFP8 weights.
+int urb_probe_mfma_scale_16x16x128(int fmt_b, const void* A, const void* sa, const void* B,
+                                   const void* sb, float* C, void* stream) {
+  const uint8_t *a = (const uint8_t*)A, *as = (const uint8_t*)sa, *b = (const uint8_t*)B,
+                *bs = (const uint8_t*)sb;
+  if (fmt_b == 1)
+    mfma_scale_layout_kernel<urb::kFmtMXFP4><<<1, 64, 0, (hipStream_t)stream>>>(a, as, b, bs, C);
+  else if (fmt_b == 2)
+    mfma_scale_layout_kernel<urb::kFmtMXFP8><<<1, 64, 0, (hipStream_t)stream>>>(a, as, b, bs, C);
+  else
+    return 7;
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 // Diagnostics: BF16 bits of code[i] * E8M0 scale[i] via the scaled conversion instructions.

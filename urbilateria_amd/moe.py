@@ -168,7 +168,8 @@ class MoeLayer:
         desc = N.Desc(spec.hidden, E, spec.top_k, spec.intermediate, spec.shared_intermediate,
                       spec.expert_format, spec.shared_format, spec.router, spec.composition,
                       spec.n_group, spec.topk_group, int(spec.normalize),
-                      float(spec.routed_scaling_factor), max_tokens)
+                      float(spec.routed_scaling_factor), max_tokens,
+                      float(spec.swiglu_limit))
         w = N.Weights(_ptr(layer.router_weight), _ptr(layer.correction_bias),
                       ctypes.addressof(mats), None if shared is None else ctypes.addressof(shared))
         ctx = ctypes.c_void_p()
@@ -242,6 +243,17 @@ def pack_matrix(fmt: int, data, scales, rows: int, cols: int):
     N.check(N.moe_lib().urb_pack_matrix(fmt, _ptr(data), _ptr(scales), rows, cols, _ptr(pd),
                                         _ptr(ps), _stream_handle()), "urb_pack_matrix")
     return pd, ps
+
+
+def quantize_e4m3(x):
+    """simulate_e4m3_activation of a [rows, cols] f32 device tensor as (E4M3 codes, E8M0
+    scales) device tensors, blocks of 32 along each row."""
+    rows, cols = x.shape
+    codes = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((rows, cols // 32), dtype=torch.uint8, device=x.device)
+    N.check(N.moe_lib().urb_quantize_e4m3(_ptr(x), rows, cols, _ptr(codes), _ptr(scales),
+                                          _stream_handle()), "urb_quantize_e4m3")
+    return codes, scales
 
 
 def packed_layer(layer: "DeviceLayer") -> "DeviceLayer":

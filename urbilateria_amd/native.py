@@ -21,11 +21,12 @@ SOURCE_HOST, SOURCE_DEVICE_COPY, SOURCE_DEVICE_BORROW = 0, 1, 2
 # Every symbol include/urb_moe.h declares.
 EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_route",
            "urb_moe_sync", "urb_dequant_rows", "urb_moe_memory", "urb_status_string",
-           "urb_moe_profile", "urb_moe_profile_read", "urb_pack_matrix")
+           "urb_moe_profile", "urb_moe_profile_read", "urb_pack_matrix", "urb_quantize_e4m3")
 STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
-                 "urb_synth_e8m0", "urb_probe_mfma_16x16x32", "urb_probe_cvt_bf16")
+                 "urb_synth_e8m0", "urb_probe_mfma_16x16x32", "urb_probe_cvt_bf16",
+                 "urb_probe_mfma_scale_16x16x128")
 
 
 class UrbError(RuntimeError):
@@ -50,7 +51,7 @@ class Desc(ctypes.Structure):
         ("router", ctypes.c_int), ("composition", ctypes.c_int),
         ("n_group", ctypes.c_uint32), ("topk_group", ctypes.c_uint32),
         ("normalize", ctypes.c_int32), ("routed_scaling_factor", ctypes.c_float),
-        ("max_tokens", ctypes.c_uint32),
+        ("max_tokens", ctypes.c_uint32), ("swiglu_limit", ctypes.c_float),
     ]
 
 
@@ -100,6 +101,8 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_moe_profile_read.restype = ctypes.c_int
         lib.urb_pack_matrix.argtypes = [ctypes.c_int, P, P, u32, u32, P, P, P]
         lib.urb_pack_matrix.restype = ctypes.c_int
+        lib.urb_quantize_e4m3.argtypes = [P, u32, u32, P, P, P]
+        lib.urb_quantize_e4m3.restype = ctypes.c_int
         lib.urb_status_string.argtypes = [ctypes.c_int]
         lib.urb_status_string.restype = ctypes.c_char_p
         _moe = lib
@@ -120,6 +123,7 @@ def synth_lib() -> ctypes.CDLL:
         lib.urb_synth_e8m0.argtypes = [u64, sz, P, P]
         lib.urb_probe_mfma_16x16x32.argtypes = [P, P, P, P]
         lib.urb_probe_cvt_bf16.argtypes = [ctypes.c_int, P, P, ctypes.c_int, P, P]
+        lib.urb_probe_mfma_scale_16x16x128.argtypes = [ctypes.c_int, P, P, P, P, P, P]
         for f in SYNTH_EXPORTS:
             getattr(lib, f).restype = ctypes.c_int
         _synth = lib
