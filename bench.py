@@ -41,7 +41,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="all",
-                    help="comma list of name:tokens (default: all seven runs)")
+                    help="comma list of name:tokens (default: all seven runs; the "
+                         "MX-activation variants c4_mxfp8_mx_activation and "
+                         "c5_mxfp4_mx_activation run when named)")
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
                     help="CPU-baseline budget per run (the headline run gets 4x)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -139,7 +141,7 @@ def run_one(name, T, args, want_cpu, cpu_budget):
     from urbilateria_amd import configs as C
     from urbilateria_amd import moe
 
-    w = C.WORKLOADS[name]
+    w = C.workload(name)
     spec = w.spec
     bias = None
     if w.zipf_s:

@@ -498,9 +498,13 @@ FULL = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
         ("c5_mxfp4_zipf_prefill", 1024)]
 
 
-@pytest.mark.parametrize("name,T", FULL)
+FULL_MX_ACTIVATION = [("c4_mxfp8_mx_activation", 1), ("c4_mxfp8_mx_activation", 512),
+                      ("c5_mxfp4_mx_activation", 1024)]
+
+
+@pytest.mark.parametrize("name,T", FULL + FULL_MX_ACTIVATION)
 def test_full_size_workload_matches_oracle_on_sampled_tokens(name, T):
-    w = C.WORKLOADS[name]
+    w = C.workload(name)
     spec = w.spec
     bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.1) if w.zipf_s else None
     dev = moe_mod().DeviceLayer.synthesize(spec, correction_bias=bias)

@@ -130,6 +130,36 @@ WORKLOADS: Dict[str, Workload] = {
                     "prefill 1024"),
 }
 
+# The MX-activation mode on the shapes of C4 and C5: Hy4's composition (E4M3 activations per
+# 32 values into every MX projection, BF16 boundaries, bounded SwiGLU with limit 7, f32
+# ascending-id combine).  C5's shared expert is MXFP4 here: the mode feeds MX weights only.
+MX_ACTIVATION_WORKLOADS: Dict[str, Workload] = {
+    "c4_mxfp8_mx_activation": Workload(
+        "c4_mxfp8_mx_activation",
+        LayerSpec(hidden=6144, n_experts=160, top_k=8, intermediate=2048,
+                  expert_format=FMT_MXFP8, router=ROUTER_SOFTMAX_TOPK,
+                  composition=COMPOSE_HY4, swiglu_limit=7.0),
+        (1, 512), description="MXFP8 H6144 E160 softmax top-8 I2048, MX activations (Hy4 "
+                              "composition), decode 1, prefill 512"),
+    "c5_mxfp4_mx_activation": Workload(
+        "c5_mxfp4_mx_activation",
+        LayerSpec(hidden=7168, n_experts=384, top_k=8, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_MXFP4,
+                  router=ROUTER_SIGMOID_NOAUX_TC, composition=COMPOSE_HY4, n_group=1,
+                  topk_group=1, normalize=True, routed_scaling_factor=1.0, swiglu_limit=7.0),
+        (1024,), zipf_s=1.1,
+        description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias I2048 + MXFP4 shared, MX "
+                    "activations (Hy4 composition), prefill 1024"),
+}
+
+
+def workload(name: str) -> Workload:
+    """A benchmark configuration or one of its MX-activation variants, by name."""
+    if name in WORKLOADS:
+        return WORKLOADS[name]
+    return MX_ACTIVATION_WORKLOADS[name]
+
+
 
 @dataclass
 class HostLayer:
