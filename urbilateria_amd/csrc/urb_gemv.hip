@@ -239,6 +239,140 @@ void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max
 }
 
 // ------------------------------------------------------------------------------------------
+// Decode down projection fused with the combine (one token).  A workgroup owns one 16-row
+// panel of the output and computes it for every routed expert (wave w takes slots w, w + W,
+// ...), with all k SwiGLU activation rows staged in LDS.  The k partial rows meet in LDS and 16
+// threads apply the down epilogue and combine them in the composition's order, so the per-slot
+// outputs never leave the chip and no combine kernel runs.  (Splitting K over two waves per
+// slot, for twice the waves, measured slower.)  `comp` = URB composition (0 QWEN36, 1 GLM,
+// 2 HY4).
+// ------------------------------------------------------------------------------------------
+template <int FMT, int DEPTH>
+__global__ __launch_bounds__(512) void gemv_down_combine_kernel(
+    const ExpertMats* __restrict__ mats, const int32_t* __restrict__ ids,
+    const float* __restrict__ w, const int32_t* __restrict__ asc, int K, int H, int I,
+    const float* __restrict__ act, const float* __restrict__ shared, int comp, Epi epi,
+    float* __restrict__ out, int* status) {
+  extern __shared__ float xs[];  // K x xs_floats(I) staged activations, then [K][16] sums
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ln = lane & 15, lq = lane >> 4;
+  const int S = blockDim.x >> 6;
+  const int panel = blockIdx.x;
+  const int steps = I / kGemmKStep;
+  const size_t xf = xs_floats(I);
+  const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(I);
+  const size_t pscales = (size_t)kPanelRows * (I / 32);
+  float* red = xs + (size_t)K * xf;
+
+  // the first slot's first weight steps go out before the activations are staged
+  BRaw<FMT> r[DEPTH];
+  const uint8_t *pd = nullptr, *ps = nullptr;
+  auto bind = [&](int a) {
+    const ExpertMats m = mats[ids[a]];
+    pd = m.data[2] + (size_t)panel * pbytes + 16 * lane;
+    ps = FMT == kFmtBF16 ? nullptr : m.scales[2] + (size_t)panel * pscales + lane;
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if (d < steps) load_b<FMT>(r[d], pd, ps, d);
+  };
+  const int a0 = wave;
+  if (a0 < K) bind(a0);
+  for (int i = threadIdx.x; i < K * (I / 4); i += blockDim.x) {
+    const int a = i / (I / 4), c4 = i - a * (I / 4);
+    *reinterpret_cast<float4*>(xs + a * xf + xs_index(4 * c4)) =
+        reinterpret_cast<const float4*>(act + (size_t)a * I)[c4];
+  }
+  __syncthreads();
+
+  for (int a = a0; a < K; a += S) {
+    if (a != a0) bind(a);
+    const float* xa = xs + a * xf;
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < steps; s0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int st = s0 + d;
+        if (st >= steps) break;
+        BRaw<FMT> c = r[d];
+        if (st + DEPTH < steps) load_b<FMT>(r[d], pd, ps, st + DEPTH);
+        raw_dot<FMT>(c, st, lq, xa, acc);
+      }
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (lane < 16) red[a * 16 + ln] = acc;
+  }
+  __syncthreads();
+
+  if (threadIdx.x < 16) {
+    const int row = panel * kPanelRows + threadIdx.x;
+    bool bad = false;
+    auto y = [&](int a) { return epi_down<FMT>(epi, red[a * 16 + threadIdx.x], bad); };
+    float res;
+    if (comp == 1) {
+      // GLM (src/models/glm/runtime/moe.rs:162-171): f64 from the shared expert, ranking order
+      double acc = shared ? (double)shared[row] : 0.0;
+      for (int j = 0; j < K; ++j) acc += (double)w[j] * (double)y(j);
+      res = (float)acc;
+    } else {
+      float acc = 0.0f;
+      for (int j = 0; j < K; ++j) {
+        const int a = asc[j];
+        const float v = y(a);
+        if (comp == 0) {
+          // Qwen (src/models/qwen3_6/runtime.rs:1398-1415): c = bf16(w y), acc = bf16(acc + c)
+          float c;
+          if (!rne_bf16(w[a] * v, &c)) { bad = true; c = w[a] * v; }
+          const float t = acc + c;
+          if (!rne_bf16(t, &acc)) { bad = true; acc = t; }
+        } else {
+          acc = acc + w[a] * v;  // Hy4 (src/models/hy4/runtime.rs:1436-1441): f32
+        }
+      }
+      if (comp == 2) {
+        if (shared) acc = acc + shared[row];
+        float b;
+        if (!rne_bf16(acc, &b)) { bad = true; b = acc; }
+        acc = b;
+      }
+      res = acc;
+    }
+    out[row] = res;
+    if (bad) flag(status, kStatusNonFinite);
+  }
+}
+
+// Largest LDS the fused kernel stages (k activation rows); above it the down projection and the
+// combine run as separate kernels.
+constexpr size_t kFusedLdsBytes = 96 * 1024;
+
+size_t down_combine_lds(int K, int I) {
+  return ((size_t)K * xs_floats(I) + (size_t)K * 16) * sizeof(float);
+}
+
+bool down_combine_fits(int K, int I) { return K <= 32 && down_combine_lds(K, I) <= kFusedLdsBytes; }
+
+bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
+                              const float* weights, const int32_t* asc, int K, int H, int I,
+                              const float* act, const float* shared, int comp, Epi epi,
+                              float* out, int* status, hipStream_t s) {
+  if (!down_combine_fits(K, I)) return false;
+  const size_t lds = down_combine_lds(K, I);
+  const dim3 grid(H / kPanelRows), block(64 * std::min(K, 8));
+  auto go = [&](auto kernel) {
+    // dynamic LDS beyond 64 KiB must be allowed per kernel
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFusedLdsBytes);
+    kernel<<<grid, block, lds, s>>>(mats, ids, weights, asc, K, H, I, act, shared, comp, epi,
+                                    out, status);
+  };
+  if (fmt == kFmtBF16) go(gemv_down_combine_kernel<kFmtBF16, 1>);
+  else if (fmt == kFmtMXFP4) go(gemv_down_combine_kernel<kFmtMXFP4, 2>);
+  else go(gemv_down_combine_kernel<kFmtMXFP8, 2>);
+  return true;
+}
+
+// ------------------------------------------------------------------------------------------
 // Combines.
 // Qwen (src/models/qwen3_6/runtime.rs:1398-1415): routes in ascending expert id,
 //   c = bf16(w * y), acc = bf16(acc + c), acc from +0.0.

@@ -122,6 +122,16 @@ void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int 
                          hipStream_t s);
 void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active, int H,
                       int I, const float* act, float* y, Epi epi, int* status, hipStream_t s);
+// One token: the down projection of the k routed experts fused with the combine of the
+// composition (comp: 0 QWEN36, 1 GLM, 2 HY4); ids/weights/asc are the token's routes, act the
+// k SwiGLU rows [k, I] in slot order, shared the shared expert's output or null.  Only when
+// down_combine_fits (the k activation rows fit the kernel's LDS budget); returns false and
+// launches nothing otherwise.
+bool down_combine_fits(int K, int I);
+bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
+                              const float* weights, const int32_t* asc, int K, int H, int I,
+                              const float* act, const float* shared, int comp, Epi epi,
+                              float* out, int* status, hipStream_t s);
 // Combines: Qwen BF16 ascending-id, GLM f64 ranking order.
 void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                          const int32_t* asc, int T, int K, int H, float* out, int* status,

@@ -540,6 +540,17 @@ static urb_status forward_hy4(urb_moe_ctx* c, const float* xc, int n, float* yc,
     urb::launch_quantize(ws.act, (size_t)n * K, (size_t)I, ws.act, nullptr, nullptr, ws.status,
                          s);
   }
+  if (n == 1 && urb::down_combine_fits(K, I)) {
+    if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+    {
+      Span span(c, URB_STAGE_DOWN, s);
+      urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I, ws.act,
+                                    has_shared ? ws.shared_out : nullptr, 2, routed, yc,
+                                    ws.status, s);
+    }
+    if (c->profiling) return collect_spans(c);
+    return URB_OK;
+  }
   {
     Span span(c, URB_STAGE_DOWN, s);
     if (n > 1)
@@ -631,6 +642,22 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       else
         urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, xc, ws.act,
                                  epi, ws.status, s);
+    }
+    if (n == 1 && urb::down_combine_fits(K, I)) {
+      // One token: the down projection and the combine run as one kernel (it reads the shared
+      // expert's output, so it waits for the side stream first).
+      if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+      {
+        Span span(c, URB_STAGE_DOWN, s);
+        urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
+                                      ws.act, has_shared ? ws.shared_out : nullptr,
+                                      qwen ? 0 : 1, epi, yc, ws.status, s);
+      }
+      if (c->profiling) {
+        urb_status st = collect_spans(c);
+        if (st) return st;
+      }
+      continue;
     }
     {
       Span span(c, URB_STAGE_DOWN, s);
