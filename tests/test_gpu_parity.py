@@ -511,7 +511,10 @@ def test_full_size_workload_matches_oracle_on_sampled_tokens(name, T):
     x = moe_mod().synth_activations(T, spec.hidden)
     layer = moe_mod().MoeLayer(dev, max_tokens=T)
     y, ids, wts = layer.forward(x)
-    sample = sorted(set([0, T - 1] + list(range(0, T, max(1, T // 6)))))[:8]
+    # MX-activation layers: an f32-order difference occasionally flips one E4M3 code of a
+    # re-quantized activation (a 1/16 step) in some token, so those runs sample more tokens
+    n_sample = 16 if spec.composition == C.COMPOSE_HY4 else 8
+    sample = sorted(set([0, T - 1] + list(range(0, T, max(1, T // (n_sample - 2))))))[:n_sample]
     ids_np = ids.cpu().numpy()
     used = sorted(set(ids_np[sample].ravel().tolist()))
     host = dev.to_host(experts=used)
