@@ -148,7 +148,8 @@ def run_one(name, T, args, want_cpu, cpu_budget):
         from urbilateria_amd import synth
         # logit std of a BF16 N(0, 0.02) router row on N(0, 1) inputs is 0.02 * sqrt(H)
         std = np.full(spec.n_experts, 0.02 * math.sqrt(spec.hidden))
-        beta = C.calibrate_zipf_beta(spec.n_experts, spec.top_k, w.zipf_s, std)
+        beta = C.calibrate_zipf_beta(spec.n_experts, spec.top_k, w.zipf_s, std,
+                                     router=spec.router)
         bias = C.zipf_bias(spec.n_experts, w.zipf_s, beta)
     first = moe.DeviceLayer.synthesize(spec, correction_bias=bias)
     x = moe.synth_activations(T, spec.hidden)

@@ -35,7 +35,7 @@ typedef enum { URB_FMT_BF16 = 0, URB_FMT_MXFP4 = 1, URB_FMT_MXFP8 = 2 } urb_form
 
 /* route_softmax_top_k (src/models/qwen3_8/moe.rs:91-159), route_noaux_tc
  * (src/math/routing.rs:38-155) or route_sqrt_softplus without hash experts
- * (src/models/deepseek_v4/math.rs:451-516; GLM composition only). */
+ * (src/models/deepseek_v4/math.rs:451-516; not with QWEN36). */
 typedef enum {
   URB_ROUTER_SOFTMAX_TOPK = 0,
   URB_ROUTER_SIGMOID_NOAUX_TC = 1,
@@ -54,8 +54,21 @@ typedef enum {
  *          routed experts Hy4Expert::forward_quantized (src/models/hy4/expert.rs:373-392,
  *          664-680: BF16 gate/up, bounded SwiGLU with swiglu_limit, re-quantized, BF16 down);
  *          shared expert DenseMlp::forward (runtime.rs:1311-1322); f32 combine in ascending
- *          expert id plus the shared expert, rounded to BF16.  MX expert and shared formats. */
-typedef enum { URB_COMPOSE_QWEN36 = 0, URB_COMPOSE_GLM = 1, URB_COMPOSE_HY4 = 2 } urb_composition;
+ *          expert id plus the shared expert, rounded to BF16.  MX expert and shared formats.
+ *  DSV41:  the MX-activation mode of DeepSeek-V4.1 MoeWeights::forward
+ *          (src/models/deepseek_v41/runtime.rs:1963-2019): FP32 8-lane router GEMV (no BF16
+ *          step), E4M3 activations per 32 values, experts Expert::forward_with_mx_input
+ *          (runtime.rs:2243-2261: FP32-accumulated BF16 gate/up, bounded SwiGLU with
+ *          swiglu_limit, times the route weight before the BF16 step and the down projection);
+ *          the shared expert is the same without a weight; f32 sum in ascending expert id plus
+ *          the shared expert, BF16.  MX expert and shared formats; route_sqrt_softplus is its
+ *          router. */
+typedef enum {
+  URB_COMPOSE_QWEN36 = 0,
+  URB_COMPOSE_GLM = 1,
+  URB_COMPOSE_HY4 = 2,
+  URB_COMPOSE_DSV41 = 3
+} urb_composition;
 
 /* Where urb_moe_create reads the weights from.  The context streams expert and shared-expert
  * matrices in the panel layout (see urb_pack_matrix); HOST and DEVICE_COPY sources are in the
@@ -96,7 +109,7 @@ typedef struct {
   int32_t normalize;             /* noaux_tc: divide by the selected gate sum */
   float routed_scaling_factor;   /* noaux_tc, sqrt_softplus */
   uint32_t max_tokens;           /* largest token count one forward call may pass */
-  float swiglu_limit;            /* HY4: bounded SwiGLU limit of the routed experts (> 0) */
+  float swiglu_limit;            /* HY4, DSV41: bounded SwiGLU limit (> 0) */
 } urb_moe_desc;
 
 typedef struct {

@@ -21,7 +21,7 @@ _LIB_PATH = os.path.join(_HERE, "liburb_oracle.so")
 OK, SHAPE, INVALID_SCALE, NONFINITE, INVALID_GEOMETRY = 0, 1, 2, 3, 4
 FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
 ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
-COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4 = 0, 1, 2
+COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4, COMPOSE_DSV41 = 0, 1, 2, 3
 
 _STATUS_NAMES = {OK: "ok", SHAPE: "shape", INVALID_SCALE: "invalid_scale",
                  NONFINITE: "nonfinite", INVALID_GEOMETRY: "invalid_geometry"}
@@ -332,6 +332,23 @@ def hy4_expert(fmt: int, triple, hidden: int, intermediate: int, x: np.ndarray,
                                      ctypes.c_float, ctypes.c_void_p, ctypes.c_int]
     _check(_lib.urbo_hy4_expert(fmt, ctypes.addressof(mats), hidden, intermediate, _ptr(x),
                                 x.shape[0], float(swiglu_limit), _ptr(y), threads))
+    return y
+
+
+def dsv41_expert(fmt: int, triple, hidden: int, intermediate: int, x: np.ndarray,
+                 swiglu_limit: float, route_weights=None, threads: int = 1) -> np.ndarray:
+    """DeepSeek-V4.1 MX-activation expert on [n, hidden] (quantized inside); route_weights [n]
+    scale the SwiGLU output before the down projection, None for the shared expert."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    mats, keep = _mats(triple)
+    y = np.empty((x.shape[0], hidden), np.float32)
+    rw = None if route_weights is None else np.ascontiguousarray(route_weights, np.float32)
+    _lib.urbo_dsv41_expert.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint32,
+                                       ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32,
+                                       ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int]
+    _check(_lib.urbo_dsv41_expert(fmt, ctypes.addressof(mats), hidden, intermediate, _ptr(x),
+                                  x.shape[0], float(swiglu_limit), _ptr(rw), _ptr(y), threads))
     return y
 
 

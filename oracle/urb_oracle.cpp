@@ -362,6 +362,27 @@ int qwen_linear(Pool &p, const uint8_t *data, size_t rows, size_t cols, const fl
     return urbo_round_to_bf16_in_place(out, batch * rows);
 }
 
+// WeightMatrix::matvec_fp32_accum / matmul_rows_fp32_accum (src/model/weight.rs:213-260):
+// BF16 -> the 8-lane FP32 tree (bf16.rs:223-416), MXFP4 -> matvec_rows_fp32, the sequential
+// f32 dot without FMA (mxfp.rs:1660-1723), other formats -> matvec.  Per-token results are
+// identical to the batched kernels (mxfp.rs:2632-2665, bf16.rs:860-887).
+int weight_matmul_fp32_accum(Pool &p, int format, const uint8_t *data, const uint8_t *scales,
+                             size_t rows, size_t cols, const float *x, size_t batch, float *out) {
+    if (format == URBO_FMT_BF16) return bf16_matmul_fp32(p, data, rows, cols, x, batch, out);
+    if (format != URBO_FMT_MXFP4) return weight_matmul(p, format, data, scales, rows, cols, x,
+                                                      batch, out);
+    if (!all_finite(x, batch * cols)) return URBO_NONFINITE;
+    const size_t rb = (cols + 1) / 2, sb = (cols + 31) / 32;
+    for_rows(p, rows, rows * cols * batch, [&](size_t r0, size_t r1) {
+        for (size_t r = r0; r < r1; ++r)
+            for (size_t b = 0; b < batch; ++b)
+                out[b * rows + r] = dot_mxfp4_fp32(data + r * rb, scales + r * sb, cols,
+                                                   x + b * cols);
+    });
+    if (!all_finite(out, batch * rows)) return URBO_NONFINITE;
+    return URBO_OK;
+}
+
 // ------------------------------------------------------------------------------------------
 // Routers
 // ------------------------------------------------------------------------------------------
@@ -794,6 +815,36 @@ int hy4_quantize(const float *x, size_t n, size_t H, std::vector<float> &q) {
     return URBO_OK;
 }
 
+// DeepSeek-V4.1 Expert::forward_with_mx_input (src/models/deepseek_v41/runtime.rs:2243-2261)
+// on quantized activations q [n, H]: gate, up = bf16(matvec_fp32_accum(w1 / w3, q))
+// (linear_with_mx_activation, deepseek_v41/math.rs:36-52); a = bounded_swiglu(gate, up, limit)
+// times the route weight of each token when given (`w`, may be null: the shared expert);
+// a -> BF16; y = linear(w2, a) = bf16(matvec_fp32_accum(w2, simulate_e4m3_activation(a, 32)))
+// (math.rs:18-25).
+int dsv41_expert(Pool &p, int format, const urbo_matrix *m, size_t H, size_t I, const float *q,
+                 size_t n, float limit, const float *w, float *y) {
+    std::vector<float> g(n * I), u(n * I), a(n * I);
+    int st = weight_matmul_fp32_accum(p, format, m[0].data, m[0].scales, I, H, q, n, g.data());
+    if (st) return st;
+    st = weight_matmul_fp32_accum(p, format, m[1].data, m[1].scales, I, H, q, n, u.data());
+    if (st) return st;
+    if ((st = urbo_round_to_bf16_in_place(g.data(), n * I))) return st;
+    if ((st = urbo_round_to_bf16_in_place(u.data(), n * I))) return st;
+    if ((st = urbo_bounded_swiglu(g.data(), u.data(), n * I, limit, a.data()))) return st;
+    if (w)
+        for (size_t t = 0; t < n; ++t) {
+            // runtime.rs:2085-2090 rejects a non-finite or negative route weight
+            if (!std::isfinite(w[t]) || w[t] < 0.0f) return URBO_INVALID_GEOMETRY;
+            for (size_t i = 0; i < I; ++i) a[t * I + i] *= w[t];
+        }
+    if ((st = urbo_round_to_bf16_in_place(a.data(), n * I))) return st;
+    for (size_t t = 0; t < n; ++t)
+        if ((st = urbo_simulate_e4m3_activation(&a[t * I], I, 32))) return st;
+    st = weight_matmul_fp32_accum(p, format, m[2].data, m[2].scales, H, I, a.data(), n, y);
+    if (st) return st;
+    return urbo_round_to_bf16_in_place(y, n * H);
+}
+
 }  // namespace
 
 int urbo_hy4_expert(int format, const urbo_matrix *m, uint32_t H, uint32_t I, const float *x,
@@ -806,6 +857,18 @@ int urbo_hy4_expert(int format, const urbo_matrix *m, uint32_t H, uint32_t I, co
     Pool &p = pool(threads);
     return swiglu_limit > 0.0f ? hy4_routed(p, format, m, H, I, q.data(), n, swiglu_limit, y)
                                : hy4_shared(p, format, m, H, I, q.data(), n, y);
+}
+
+int urbo_dsv41_expert(int format, const urbo_matrix *m, uint32_t H, uint32_t I, const float *x,
+                      uint32_t n, float swiglu_limit, const float *route_weights, float *y,
+                      int threads) {
+    if (H == 0 || I == 0 || n == 0) return URBO_SHAPE;
+    if (format != URBO_FMT_MXFP4 && format != URBO_FMT_MXFP8) return URBO_SHAPE;
+    std::vector<float> q;
+    int st = hy4_quantize(x, n, H, q);
+    if (st) return st;
+    return dsv41_expert(pool(threads), format, m, H, I, q.data(), n, swiglu_limit, route_weights,
+                        y);
 }
 
 int urbo_gated_mlp(int format, const urbo_matrix *m, uint32_t H, uint32_t I, const float *x,
@@ -827,23 +890,27 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
     if (H == 0 || E == 0 || I == 0 || T == 0) return URBO_SHAPE;
     if (K == 0 || K > E) return URBO_INVALID_GEOMETRY;
     const bool qwen = L->composition == URBO_COMPOSE_QWEN36;
+    const bool dsv = L->composition == URBO_COMPOSE_DSV41;
     const bool hy4 = L->composition == URBO_COMPOSE_HY4;
+    const bool mxa = hy4 || dsv;  // the MX-activation compositions
     if (qwen && (L->expert_format != URBO_FMT_BF16 || L->shared_intermediate != 0))
         return URBO_SHAPE;
-    if (hy4 && (L->expert_format == URBO_FMT_BF16 ||
+    if (mxa && (L->expert_format == URBO_FMT_BF16 ||
                 (L->shared_intermediate && L->shared_format == URBO_FMT_BF16)))
         return URBO_SHAPE;
-    if (hy4 && !(L->swiglu_limit > 0.0f && std::isfinite(L->swiglu_limit)))
+    if (mxa && !(L->swiglu_limit > 0.0f && std::isfinite(L->swiglu_limit)))
         return URBO_INVALID_GEOMETRY;
     Pool &p = pool(threads);
     if (!all_finite(x, (size_t)T * H)) return URBO_NONFINITE;
 
-    // Router logits: Qwen `linear(router)` (qwen3_8/math.rs:10-26, FP32 GEMV + BF16), GLM
+    // Router logits: Qwen `linear(router)` (qwen3_8/math.rs:10-26, FP32 GEMV + BF16), DeepSeek
+    // V4.1 `router.matvec_fp32_accum` (deepseek_v41/runtime.rs:2136, FP32 GEMV), GLM and Hy4
     // `router.matvec` (ordered f64, bf16.rs:121-216).
     std::vector<float> logits((size_t)T * E);
     const uint8_t *rw = (const uint8_t *)L->router_weight;
     int st = qwen ? qwen_linear(p, rw, E, H, x, T, logits.data())
-                  : weight_matmul(p, URBO_FMT_BF16, rw, nullptr, E, H, x, T, logits.data());
+             : dsv ? bf16_matmul_fp32(p, rw, E, H, x, T, logits.data())
+                   : weight_matmul(p, URBO_FMT_BF16, rw, nullptr, E, H, x, T, logits.data());
     if (st) return st;
     if (logits_out) std::memcpy(logits_out, logits.data(), logits.size() * 4);
 
@@ -886,8 +953,8 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
     // Hy4: one E4M3 activation per token shared by every routed expert and the shared expert
     // (src/models/hy4/runtime.rs:1397, 1311-1312).
     std::vector<float> qx;
-    if (hy4 && (st = hy4_quantize(x, T, H, qx))) return st;
-    const float *xe = hy4 ? qx.data() : x;
+    if (mxa && (st = hy4_quantize(x, T, H, qx))) return st;
+    const float *xe = mxa ? qx.data() : x;
     // Expert outputs per route slot.
     std::vector<float> out((size_t)T * K * H);
     for (const Group &g : groups) {
@@ -897,9 +964,14 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
             std::memcpy(&xin[i * H], xe + g.tokens[i] * H, H * 4);
         const urbo_matrix *m = L->experts + g.expert * 3;
         if (!m[0].data || !m[1].data || !m[2].data) return URBO_SHAPE;  // expert not supplied
-        st = qwen ? qwen_expert(p, m, H, I, xin.data(), n, yo.data())
+        std::vector<float> wr;
+        if (dsv)
+            for (size_t slot : g.slots) wr.push_back(rw8[slot]);
+        st = qwen  ? qwen_expert(p, m, H, I, xin.data(), n, yo.data())
              : hy4 ? hy4_routed(p, L->expert_format, m, H, I, xin.data(), n, L->swiglu_limit,
                                 yo.data())
+             : dsv ? dsv41_expert(p, L->expert_format, m, H, I, xin.data(), n, L->swiglu_limit,
+                                  wr.data(), yo.data())
                    : gated_mlp(p, L->expert_format, m, H, I, xin.data(), n, yo.data());
         if (st) return st;
         for (size_t i = 0; i < n; ++i)
@@ -931,14 +1003,18 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
         return URBO_OK;
     }
 
-    if (hy4) {
+    if (mxa) {
         // Hy4 MoeWeights::forward (src/models/hy4/runtime.rs:1387-1445): f32 sum of w * y over
-        // the routes in ascending expert id, plus the shared expert, rounded to BF16.
+        // the routes in ascending expert id, plus the shared expert, rounded to BF16.  DeepSeek
+        // V4.1 (deepseek_v41/runtime.rs:1963-2019) the same with the route weight already
+        // applied inside each expert (the sum adds y).
         std::vector<float> sh;
         if (L->shared_intermediate) {
             sh.resize((size_t)T * H);
-            st = hy4_shared(p, L->shared_format, L->shared, H, L->shared_intermediate, qx.data(),
-                            T, sh.data());
+            st = hy4 ? hy4_shared(p, L->shared_format, L->shared, H, L->shared_intermediate,
+                                  qx.data(), T, sh.data())
+                     : dsv41_expert(p, L->shared_format, L->shared, H, L->shared_intermediate,
+                                    qx.data(), T, L->swiglu_limit, nullptr, sh.data());
             if (st) return st;
         }
         for (size_t t = 0; t < T; ++t) {
@@ -952,7 +1028,10 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
             for (size_t j : order) {
                 const float w = rw8[t * K + j];
                 const float *v = &out[(t * K + j) * H];
-                for (size_t h = 0; h < H; ++h) yt[h] += w * v[h];
+                if (dsv)
+                    for (size_t h = 0; h < H; ++h) yt[h] += v[h];
+                else
+                    for (size_t h = 0; h < H; ++h) yt[h] += w * v[h];
             }
             if (!sh.empty())
                 for (size_t h = 0; h < H; ++h) yt[h] += sh[t * H + h];

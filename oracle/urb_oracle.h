@@ -38,7 +38,7 @@ enum { URBO_FMT_BF16 = 0, URBO_FMT_MXFP4 = 1, URBO_FMT_MXFP8 = 2 };
 enum { URBO_ROUTER_SOFTMAX_TOPK = 0, URBO_ROUTER_SIGMOID_NOAUX_TC = 1, URBO_ROUTER_SQRT_SOFTPLUS = 2 };
 /* QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243).
  * GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176). */
-enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1, URBO_COMPOSE_HY4 = 2 };
+enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1, URBO_COMPOSE_HY4 = 2, URBO_COMPOSE_DSV41 = 3 };
 
 /* ---- element decoders (src/math/mxfp.rs, src/model/bf16.rs, src/models/qwen3_8/math.rs) ---- */
 int urbo_decode_e8m0(uint8_t code, float *out);
@@ -102,7 +102,7 @@ typedef struct {
     const float *correction_bias;  /* [E] or NULL (zeros) */
     const urbo_matrix *experts;    /* [E][3] = gate [I,H], up [I,H], down [H,I] */
     const urbo_matrix *shared;     /* [3] or NULL */
-    float swiglu_limit;            /* HY4: bounded SwiGLU limit of the routed experts */
+    float swiglu_limit;            /* HY4, DSV41: bounded SwiGLU limit */
 } urbo_layer;
 
 /* Hy4 MX-activation experts over n tokens [n, H] -> [n, H] (x is quantized here):
@@ -111,6 +111,11 @@ typedef struct {
 int urbo_hy4_expert(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
                     uint32_t intermediate, const float *x, uint32_t n, float swiglu_limit,
                     float *y, int threads);
+/* DeepSeek-V4.1 Expert::forward_with_mx_input (src/models/deepseek_v41/runtime.rs:2243-2261)
+ * over n tokens [n, H] (x quantized here); route_weights [n] or NULL (the shared expert). */
+int urbo_dsv41_expert(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
+                      uint32_t intermediate, const float *x, uint32_t n, float swiglu_limit,
+                      const float *route_weights, float *y, int threads);
 /* GatedMlp::forward (src/model/mlp.rs:90-99) over n tokens [n, H] -> [n, H]. */
 int urbo_gated_mlp(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
                    uint32_t intermediate, const float *x, uint32_t n, float *y, int threads);

@@ -294,20 +294,24 @@ def test_quantize_e4m3_matches_simulate_e4m3_activation_bit_exact():
         assert not np.any((c & 0x7F) == 0x7F)  # never a NaN code
 
 
-HY4 = [(fmt, T) for fmt in (C.FMT_MXFP4, C.FMT_MXFP8) for T in (1, 5, 40)]
+MX_LAYERS = [(comp, fmt, T) for comp in (C.COMPOSE_HY4, C.COMPOSE_DSV41)
+             for fmt in (C.FMT_MXFP4, C.FMT_MXFP8) for T in (1, 5, 40)]
 
 
-def _hy4_layer(fmt, hidden=256, n_experts=32, intermediate=128, top_k=6):
+def _hy4_layer(fmt, hidden=256, n_experts=32, intermediate=128, top_k=6,
+               composition=C.COMPOSE_HY4):
+    # Hy4: grouped sigmoid router; DeepSeek V4.1: its sqrt-softplus router
+    router = C.ROUTER_SIGMOID_NOAUX_TC if composition == C.COMPOSE_HY4 else C.ROUTER_SQRT_SOFTPLUS
     spec = C.LayerSpec(hidden=hidden, n_experts=n_experts, top_k=top_k, intermediate=intermediate,
                        shared_intermediate=intermediate, expert_format=fmt, shared_format=fmt,
-                       router=C.ROUTER_SIGMOID_NOAUX_TC, composition=C.COMPOSE_HY4, n_group=4,
+                       router=router, composition=composition, n_group=4,
                        topk_group=2, normalize=True, routed_scaling_factor=2.5, swiglu_limit=7.0)
     return C.make_host_layer(spec, bias=C.zipf_bias(n_experts, 1.1, 0.05))
 
 
-@pytest.mark.parametrize("fmt,T", HY4)
-def test_hy4_layer_matches_oracle(fmt, T):
-    host = _hy4_layer(fmt)
+@pytest.mark.parametrize("comp,fmt,T", MX_LAYERS)
+def test_mx_activation_layer_matches_oracle(comp, fmt, T):
+    host = _hy4_layer(fmt, composition=comp)
     spec = host.spec
     x = synth.activations(f"x.hy4.{T}", T, spec.hidden)
     layer = moe_mod().MoeLayer(host, max_tokens=T)
@@ -319,6 +323,20 @@ def test_hy4_layer_matches_oracle(fmt, T):
     assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
     # BF16 outputs: every element is a BF16 value
     assert np.all((y.cpu().numpy().view(np.uint32) & 0xFFFF) == 0)
+    layer.close()
+
+
+def test_dsv41_router_logits_are_the_fp32_tree_bit_for_bit():
+    # DeepSeek V4.1's router.matvec_fp32_accum is the 8-lane FP32 tree without a BF16 step
+    host = _hy4_layer(C.FMT_MXFP4, hidden=512, n_experts=64, composition=C.COMPOSE_DSV41)
+    x = synth.activations("x.dsv.router", 9, 512)
+    layer = moe_mod().MoeLayer(host, max_tokens=9)
+    logits, ids, w = layer.route(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    logits = logits.cpu().numpy()
+    assert np.array_equal(logits.view(np.uint32), ref.logits.view(np.uint32))
+    assert np.any((logits.view(np.uint32) & 0xFFFF) != 0)  # not BF16-rounded
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(host.spec, ref, host.correction_bias))
     layer.close()
 
 
@@ -499,7 +517,8 @@ FULL = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
 
 
 FULL_MX_ACTIVATION = [("c4_mxfp8_mx_activation", 1), ("c4_mxfp8_mx_activation", 512),
-                      ("c5_mxfp4_mx_activation", 1024)]
+                      ("c5_mxfp4_mx_activation", 1024), ("c5_mxfp4_dsv41", 1),
+                      ("c5_mxfp4_dsv41", 1024)]
 
 
 @pytest.mark.parametrize("name,T", FULL + FULL_MX_ACTIVATION)
@@ -513,7 +532,7 @@ def test_full_size_workload_matches_oracle_on_sampled_tokens(name, T):
     y, ids, wts = layer.forward(x)
     # MX-activation layers: an f32-order difference occasionally flips one E4M3 code of a
     # re-quantized activation (a 1/16 step) in some token, so those runs sample more tokens
-    n_sample = 16 if spec.composition == C.COMPOSE_HY4 else 8
+    n_sample = 16 if spec.composition in (C.COMPOSE_HY4, C.COMPOSE_DSV41) else 8
     sample = sorted(set([0, T - 1] + list(range(0, T, max(1, T // (n_sample - 2))))))[:n_sample]
     ids_np = ids.cpu().numpy()
     used = sorted(set(ids_np[sample].ravel().tolist()))

@@ -625,3 +625,103 @@ def test_hy4_layer_rejects_bf16_and_bad_limit():
             O.moe_forward(bad, layer.experts, layer.router_weight, x, layer.correction_bias,
                           layer.shared)
         assert e.value.status == status
+
+
+# ------------------------------------------------------------------- MX-activation mode (DeepSeek V4.1)
+def _identity_mxfp8(n):
+    codes = np.zeros((n, n), np.uint8)
+    np.fill_diagonal(codes, 0x38)  # E4M3 1.0
+    return codes, np.full((n, n // 32), 127, np.uint8)
+
+
+def test_dsv41_route_weight_applied_before_the_down_projection():
+    # The reference's routed_weight_is_applied_before_the_down_projection_boundary
+    # (src/models/deepseek_v4/runtime.rs:4544-4561) restated on MX weights: identity w1 = w3 =
+    # w2, input e0, weight 0.3.  The weighted expert equals bf16 -> E4M3-simulate -> bf16 of
+    # bounded_swiglu(1, 1, 10) * 0.3, and differs from weighting the unweighted output.
+    n = 32
+    eye = _identity_mxfp8(n)
+    triple = [eye, eye, eye]
+    x = np.zeros(n, np.float32)
+    x[0] = 1.0
+    weighted = O.dsv41_expert(O.FMT_MXFP8, triple, n, n, x, 10.0, [0.3])[0]
+    a = O.bounded_swiglu(np.ones(1, np.float32), np.ones(1, np.float32), 10.0)[0]
+    a = _bf16(np.float32(a) * np.float32(0.3))
+    block = np.zeros(n, np.float32)
+    block[0] = float(a)
+    expect = _bf16(O.simulate_e4m3_activation(block, 32))
+    assert np.array_equal(weighted.view(np.uint32), expect.view(np.uint32))
+    unweighted = O.dsv41_expert(O.FMT_MXFP8, triple, n, n, x, 10.0, None)[0]
+    after_w2 = _bf16(unweighted * np.float32(0.3))
+    assert not np.array_equal(weighted, after_w2)
+    with pytest.raises(O.OracleError):
+        O.dsv41_expert(O.FMT_MXFP8, triple, n, n, x, 10.0, [-0.5])
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_MXFP8, O.FMT_MXFP4])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_dsv41_expert_vs_float64_mathematics(fmt, weighted):
+    H, I, limit = 128, 64, 1.5
+    if fmt == O.FMT_MXFP8:
+        rng = np.random.default_rng(6)
+        fin = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+        triple = [(rng.choice(fin, (r, c_)).astype(np.uint8),
+                   rng.integers(118, 124, (r, c_ // 32)).astype(np.uint8))
+                  for r, c_ in ((I, H), (I, H), (H, I))]
+    else:
+        triple = [synth.mxfp4_matrix(f"dsv.{n}", r, c_) for n, r, c_ in
+                  (("g", I, H), ("u", I, H), ("d", H, I))]
+    x = synth.activations("dsv.x", 6, H)
+    rw = np.linspace(0.2, 1.7, 6).astype(np.float32) if weighted else None
+    got = O.dsv41_expert(fmt, triple, H, I, x, limit, rw)
+
+    def deq(d, s_, rows, cols):
+        return np.stack([O.row(fmt, d, s_, rows, cols, r) for r in range(rows)]).astype(np.float64)
+    G, U, D = deq(*triple[0], I, H), deq(*triple[1], I, H), deq(*triple[2], H, I)
+    same = 0
+    for t in range(x.shape[0]):
+        q = O.simulate_e4m3_activation(x[t], 32).astype(np.float64)
+        g = _bf16((G @ q).astype(np.float32)).astype(np.float64)
+        u = _bf16((U @ q).astype(np.float32)).astype(np.float64)
+        gl = np.minimum(g, limit)
+        a = (gl / (1.0 + np.exp(-gl)) * np.clip(u, -limit, limit)).astype(np.float32)
+        if weighted:
+            a = a * rw[t]
+        a = O.simulate_e4m3_activation(_bf16(a), 32).astype(np.float64)
+        y = _bf16((D @ a).astype(np.float32))
+        same += int(np.sum(y.view(np.uint32) == got[t].view(np.uint32)))
+        assert np.linalg.norm(got[t] - y) <= 2e-2 * np.linalg.norm(y)
+    assert same >= 0.9 * got.size, same / got.size
+
+
+def _dsv41_small_layer(fmt, E=8, H=128, I=64, k=3, T=7):
+    spec = C.LayerSpec(hidden=H, n_experts=E, top_k=k, intermediate=I, shared_intermediate=I,
+                       expert_format=fmt, shared_format=fmt, router=C.ROUTER_SQRT_SOFTPLUS,
+                       composition=C.COMPOSE_DSV41, routed_scaling_factor=1.5, swiglu_limit=7.0)
+    bias = (np.arange(E, dtype=np.float32) - E / 2) * np.float32(0.02)
+    return spec, C.make_host_layer(spec, bias=bias), synth.activations("dsv.layer", T, H)
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_MXFP8, O.FMT_MXFP4])
+def test_dsv41_layer_composition(fmt):
+    # DeepSeek-V4.1 MoeWeights::forward (src/models/deepseek_v41/runtime.rs:1963-2019) restated
+    # from pinned parts: FP32-tree router logits (bf16.rs:223-286), route_sqrt_softplus with the
+    # bias, each routed expert with its route weight and the shared expert without, then
+    # out = sum over ascending expert id of y (f32) + shared, BF16.
+    spec, layer, x = _dsv41_small_layer(fmt)
+    res = O.moe_forward(spec, layer.experts, layer.router_weight, x, layer.correction_bias,
+                        layer.shared)
+    H, I, E, K = spec.hidden, spec.intermediate, spec.n_experts, spec.top_k
+    for t in range(x.shape[0]):
+        logits = O.bf16_matvec_rows_fp32(layer.router_weight, E, H, x[t])
+        assert np.array_equal(logits.view(np.uint32), res.logits[t].view(np.uint32))
+        ids, w, _ = O.route_sqrt_softplus(logits, layer.correction_bias, K, 1.5)
+        assert list(ids) == list(res.ids[t]) and np.array_equal(w, res.weights[t])
+        ys = {int(e): O.dsv41_expert(fmt, layer.experts[e], H, I, x[t], 7.0, [w[j]])[0]
+              for j, e in enumerate(ids)}
+        sh = O.dsv41_expert(fmt, layer.shared, H, I, x[t], 7.0, None)[0]
+        acc = np.zeros(H, np.float32)
+        for e in sorted(ys):
+            acc = acc + ys[e]
+        out = _bf16(acc + sh)
+        assert np.array_equal(out.view(np.uint32), res.output[t].view(np.uint32))

@@ -12,6 +12,10 @@ routed_scaling_factor) plus the projection formats of ``WeightMatrix``
 * ``COMPOSE_GLM`` -- RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176): ordered
   f64 router GEMV, softmax top-k or sigmoid noaux_tc, GatedMlp experts, f64 combine in ranking
   order on top of the shared expert.
+* ``COMPOSE_DSV41`` -- the MX-activation mode of DeepSeek-V4.1 MoeWeights::forward
+  (src/models/deepseek_v41/runtime.rs:1963-2019): FP32 router GEMV, sqrt-softplus routing,
+  experts with FP32-accumulated projections whose SwiGLU output is scaled by the route weight
+  before the BF16 step and the down projection, f32 ascending-id sum plus the shared expert.
 * ``COMPOSE_HY4`` -- the MX-activation mode, Hy4 MoeWeights::forward
   (src/models/hy4/runtime.rs:1371-1447): ordered f64 router GEMV, every MX projection fed by
   simulate_e4m3_activation(x, 32), routed experts with BF16 gate/up and a bounded SwiGLU
@@ -30,7 +34,7 @@ from . import synth
 
 FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
 ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
-COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4 = 0, 1, 2
+COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4, COMPOSE_DSV41 = 0, 1, 2, 3
 FORMAT_NAMES = {FMT_BF16: "bf16", FMT_MXFP4: "mxfp4", FMT_MXFP8: "mxfp8"}
 
 
@@ -132,7 +136,9 @@ WORKLOADS: Dict[str, Workload] = {
 
 # The MX-activation mode on the shapes of C4 and C5: Hy4's composition (E4M3 activations per
 # 32 values into every MX projection, BF16 boundaries, bounded SwiGLU with limit 7, f32
-# ascending-id combine).  C5's shared expert is MXFP4 here: the mode feeds MX weights only.
+# ascending-id combine) and DeepSeek-V4.1's (the same activations, FP32-accumulated
+# projections, route weight applied before the down projection, sqrt-softplus router).  C5's
+# shared expert is MXFP4 here: the mode feeds MX weights only.
 MX_ACTIVATION_WORKLOADS: Dict[str, Workload] = {
     "c4_mxfp8_mx_activation": Workload(
         "c4_mxfp8_mx_activation",
@@ -150,6 +156,15 @@ MX_ACTIVATION_WORKLOADS: Dict[str, Workload] = {
         (1024,), zipf_s=1.1,
         description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias I2048 + MXFP4 shared, MX "
                     "activations (Hy4 composition), prefill 1024"),
+    "c5_mxfp4_dsv41": Workload(
+        "c5_mxfp4_dsv41",
+        LayerSpec(hidden=7168, n_experts=384, top_k=8, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_MXFP4,
+                  router=ROUTER_SQRT_SOFTPLUS, composition=COMPOSE_DSV41,
+                  routed_scaling_factor=1.5, swiglu_limit=7.0),
+        (1, 1024), zipf_s=1.1,
+        description="MXFP4 H7168 E384 sqrt-softplus top-8 + Zipf(1.1) bias I2048 + MXFP4 shared, "
+                    "MX activations (DeepSeek-V4.1 composition), decode 1, prefill 1024"),
 }
 
 
@@ -215,13 +230,18 @@ def zipf_bias(n_experts: int, s: float, beta: float, base_seed: int = synth.BASE
 
 
 def calibrate_zipf_beta(n_experts: int, top_k: int, s: float, logit_std: np.ndarray,
-                        tokens: int = 4096, base_seed: int = synth.BASE_SEED) -> float:
+                        tokens: int = 4096, base_seed: int = synth.BASE_SEED,
+                        router: int = ROUTER_SIGMOID_NOAUX_TC) -> float:
     """Bisection on beta so the log-log slope of expert selection frequency against popularity
     rank is -s.  Router logits are drawn as independent N(0, logit_std[e]^2), the distribution
-    a BF16 N(0, 0.02) router produces on N(0, 1) activations (logit_std[e] = ||w_e||)."""
+    a BF16 N(0, 0.02) router produces on N(0, 1) activations (logit_std[e] = ||w_e||); the
+    selection score is the router's: sigmoid, or sqrt(softplus) for ROUTER_SQRT_SOFTPLUS."""
     z = synth.normals(synth.stream_seed("zipf.calibration", base_seed), tokens * n_experts)
     logits = z.reshape(tokens, n_experts).astype(np.float64) * logit_std[None, :]
-    gates = 1.0 / (1.0 + np.exp(-logits))
+    if router == ROUTER_SQRT_SOFTPLUS:
+        gates = np.sqrt(np.logaddexp(0.0, logits))
+    else:
+        gates = 1.0 / (1.0 + np.exp(-logits))
     keys = synth.splitmix64(synth.stream_seed("zipf.rank", base_seed), 0, n_experts)
     rank = np.empty(n_experts, np.int64)
     rank[np.argsort(keys, kind="stable")] = np.arange(1, n_experts + 1)

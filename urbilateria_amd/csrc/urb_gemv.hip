@@ -245,7 +245,7 @@ void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max
 // threads apply the down epilogue and combine them in the composition's order, so the per-slot
 // outputs never leave the chip and no combine kernel runs.  (Splitting K over two waves per
 // slot, for twice the waves, measured slower.)  `comp` = URB composition (0 QWEN36, 1 GLM,
-// 2 HY4).
+// 2 HY4, 3 DSV41).
 // ------------------------------------------------------------------------------------------
 template <int FMT, int DEPTH>
 __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
@@ -325,11 +325,13 @@ __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
           if (!rne_bf16(w[a] * v, &c)) { bad = true; c = w[a] * v; }
           const float t = acc + c;
           if (!rne_bf16(t, &acc)) { bad = true; acc = t; }
-        } else {
+        } else if (comp == 2) {
           acc = acc + w[a] * v;  // Hy4 (src/models/hy4/runtime.rs:1436-1441): f32
+        } else {
+          acc = acc + v;  // DeepSeek V4.1 (deepseek_v41/runtime.rs:1995-1998): weight applied
         }
       }
-      if (comp == 2) {
+      if (comp >= 2) {
         if (shared) acc = acc + shared[row];
         float b;
         if (!rne_bf16(acc, &b)) { bad = true; b = acc; }

@@ -61,14 +61,26 @@ __device__ __forceinline__ uint32_t encode_e4m3(float value) {
 // (`values` may alias x: every lane reads its element before any lane writes), the codes
 // [rows, cols] and the scales [rows, cols / 32] (the E8M0 byte is the biased exponent of the
 // power-of-two scale).  Non-finite input -> status (mxfp.rs:93-99).
-__global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nblocks,
+__global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nblocks, int cols,
                                                        float* values,
                                                        uint8_t* __restrict__ codes,
-                                                       uint8_t* __restrict__ scales, int* status) {
+                                                       uint8_t* __restrict__ scales, int* status,
+                                                       int round_first,
+                                                       const float* __restrict__ row_w,
+                                                       const int32_t* __restrict__ row_slot) {
   const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   const size_t blk = gid >> 5;
   const bool live = blk < nblocks;
-  const float v = live ? x[gid] : 0.0f;
+  float v = live ? x[gid] : 0.0f;
+  if (round_first && live) {
+    if (row_w) {
+      const size_t row = gid / (size_t)cols;
+      v = v * row_w[row_slot ? row_slot[row] : row];
+    }
+    float r;
+    if (!rne_bf16(v, &r) && status) flag(status, kStatusNonFinite);
+    else v = r;
+  }
   float a = fabsf(v);
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
@@ -87,16 +99,18 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nb
 }
 
 void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
-                     uint8_t* scales, int* status, hipStream_t s) {
+                     uint8_t* scales, int* status, hipStream_t s, int round_first,
+                     const float* row_w, const int32_t* row_slot) {
   const size_t nblocks = rows * cols / 32;
   const size_t threads = nblocks * 32;
-  quantize_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(x, nblocks, values, codes,
-                                                                     scales, status);
+  quantize_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(
+      x, nblocks, (int)cols, values, codes, scales, status, round_first, row_w, row_slot);
 }
 
 // ------------------------------------------------------------------------------------------
 // Combine (Hy4 MoeWeights::forward, src/models/hy4/runtime.rs:1387-1445): out = 0; for the
 // routes in ascending expert id, out += w * y (f32 multiply, f32 add); out += shared; BF16.
+// Without weights (DeepSeek V4.1, deepseek_v41/runtime.rs:1995-2017) out += y (1 * y is y).
 // ------------------------------------------------------------------------------------------
 template <int KMAX>
 __global__ __launch_bounds__(256) void combine_hy4_kernel(const float* __restrict__ y,
@@ -118,7 +132,7 @@ __global__ __launch_bounds__(256) void combine_hy4_kernel(const float* __restric
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) {
     if (j < K) {
-      wt[j] = w[(size_t)t * K + rk[j]];
+      wt[j] = w ? w[(size_t)t * K + rk[j]] : 1.0f;
       const int p = pos ? pos[(size_t)t * K + rk[j]] : rk[j];
       v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
     }

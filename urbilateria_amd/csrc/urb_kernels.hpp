@@ -95,8 +95,9 @@ struct RouteParams {
 
 
 // Router logits.
+// Router logits, the reference's 8-lane FP32 tree (BF16-rounded when round_bf16).
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
-                         int* status, hipStream_t s);
+                         int round_bf16, int* status, hipStream_t s);
 
 // GLM router logits: MFMA BF16 with f64 accumulation of 32-k partials, split over K into
 // f64 partial slices.  The router weight is packed in the panel layout with router_rows(E)
@@ -112,9 +113,10 @@ void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int3
                   float* weights, int32_t* asc, int* status, hipStream_t s);
 // Permutation for T <= kMaxChunkTokens tokens.
 constexpr int kMaxChunkTokens = 1024;
+// slot_of_pos (may be null) receives the route slot t k + j of each permuted position.
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
-                    int32_t* tiles, hipStream_t s);
+                    int32_t* tiles, int32_t* slot_of_pos, hipStream_t s);
 // Decode projections (GEMV family, one token per active expert): gate+up with the activation
 // epilogue, then down.
 void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
@@ -123,7 +125,7 @@ void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int 
 void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active, int H,
                       int I, const float* act, float* y, Epi epi, int* status, hipStream_t s);
 // One token: the down projection of the k routed experts fused with the combine of the
-// composition (comp: 0 QWEN36, 1 GLM, 2 HY4); ids/weights/asc are the token's routes, act the
+// composition (comp: 0 QWEN36, 1 GLM, 2 HY4, 3 DSV41); ids/weights/asc are the token's routes, act the
 // k SwiGLU rows [k, I] in slot order, shared the shared expert's output or null.  Only when
 // down_combine_fits (the k activation rows fit the kernel's LDS budget); returns false and
 // launches nothing otherwise.
@@ -142,9 +144,14 @@ void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const f
 // of [rows, cols] f32 (cols % 32 == 0) per 32-value block of each row: the simulated f32 values
 // (`values`, may alias x) and/or the E4M3 codes [rows, cols] + E8M0 scales [rows, cols / 32]
 // they are made of; either output may be null.
+// With `round_first`, each value is first multiplied by its row's weight (row_w[row_slot[row]],
+// row_w[row] when row_slot is null, none when row_w is null) and rounded to BF16 (DeepSeek
+// V4.1's weighted, BF16-materialised SwiGLU output).
 void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
-                     uint8_t* scales, int* status, hipStream_t s);
-// Hy4 combine: ascending expert id, f32, + shared, BF16.
+                     uint8_t* scales, int* status, hipStream_t s, int round_first = 0,
+                     const float* row_w = nullptr, const int32_t* row_slot = nullptr);
+// Hy4 combine: ascending expert id, f32, + shared, BF16 (weights null: the plain sum of DeepSeek
+// V4.1, whose experts already applied their route weight).
 void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                         const int32_t* asc, const float* shared, int T, int K, int H,
                         float* out, int* status, hipStream_t s);

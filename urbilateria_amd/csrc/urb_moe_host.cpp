@@ -39,6 +39,7 @@ struct Workspace {
   int32_t* counts = nullptr;
   int32_t* perm_token = nullptr;
   int32_t* pos_of_slot = nullptr;
+  int32_t* slot_of_pos = nullptr;  // DSV41: route slot of each permuted position
   int32_t* tiles = nullptr;
   float* act = nullptr;
   float* y_perm = nullptr;
@@ -71,7 +72,7 @@ struct urb_moe_ctx {
   void* work = nullptr;
   size_t work_bytes = 0;
   const uint16_t* router = nullptr;    // [E, H] BF16 (rows zero-padded to router_rows(E))
-  uint16_t* router_lane8 = nullptr;    // per-lane chain layout (QWEN36)
+  uint16_t* router_lane8 = nullptr;    // per-lane chain layout (QWEN36, DSV41)
   uint8_t* router_panel = nullptr;     // panel layout of the padded router (GLM)
   const float* bias = nullptr;         // [E] or nullptr
   ExpertMats* table = nullptr;         // device [E]
@@ -165,7 +166,7 @@ static urb_status check_desc(const urb_moe_desc* d) {
     if (d->expert_format != URB_FMT_BF16 || d->shared_intermediate != 0 ||
         d->router != URB_ROUTER_SOFTMAX_TOPK)
       return URB_ERR_ARGUMENT;
-  } else if (d->composition == URB_COMPOSE_HY4) {
+  } else if (d->composition == URB_COMPOSE_HY4 || d->composition == URB_COMPOSE_DSV41) {
     // MX projections only (the activation mode exists for MX weights), and the routed experts'
     // SwiGLU limit must be finite and positive (Hy4Config validation, hy4/config.rs:235-236).
     if (d->expert_format == URB_FMT_BF16 ||
@@ -232,12 +233,14 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   w.counts = b.take<int32_t>(E);
   w.perm_token = b.take<int32_t>(C * K);
   w.pos_of_slot = b.take<int32_t>(C * K);
+  if (d.composition == URB_COMPOSE_DSV41) w.slot_of_pos = b.take<int32_t>(C * K);
   w.tiles = b.take<int32_t>(2 * (size_t)urb::gemm_max_tiles((int)C, (int)K, (int)E));
   w.act = b.take<float>(C * K * I);
   w.y_perm = b.take<float>(C * K * H);
   w.shared_act = b.take<float>(C * std::max<size_t>(d.shared_intermediate, 1));
   w.shared_out = b.take<float>(C * H);
-  if (d.composition == URB_COMPOSE_HY4) w.xq = b.take<float>(C * H);
+  if (d.composition == URB_COMPOSE_HY4 || d.composition == URB_COMPOSE_DSV41)
+    w.xq = b.take<float>(C * H);
 }
 
 static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
@@ -245,6 +248,8 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   const size_t H = d->hidden, E = d->n_experts, I = d->intermediate, Is = d->shared_intermediate;
   const bool has_shared = Is != 0;
   const bool qwen = d->composition == URB_COMPOSE_QWEN36;
+  // the 8-lane FP32 router tree reads a lane-chain copy; the f64 MFMA router a panel copy
+  const bool lane8 = qwen || d->composition == URB_COMPOSE_DSV41;
   if (!w->router_weight || !w->experts || (has_shared && !w->shared)) return URB_ERR_ARGUMENT;
   if (src != URB_SOURCE_HOST && src != URB_SOURCE_DEVICE_COPY && src != URB_SOURCE_DEVICE_BORROW)
     return URB_ERR_ARGUMENT;
@@ -272,7 +277,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
 
   // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
   const size_t Ep = urb::router_rows((int)E);
-  size_t arena = align_up(Ep * H * 2) + (qwen ? align_up((E + 7) / 8 * 8 * H * 2) : align_up(Ep * H * 2)) +
+  size_t arena = align_up(Ep * H * 2) + (lane8 ? align_up((E + 7) / 8 * 8 * H * 2) : align_up(Ep * H * 2)) +
                  align_up(E * 4);
   size_t wbytes = 0;
   if (!borrow) {
@@ -291,8 +296,8 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   c->weight_bytes = wbytes;
   Bump ab{static_cast<char*>(c->arena)};
   uint16_t* router = ab.take<uint16_t>(Ep * H);
-  c->router_lane8 = qwen ? ab.take<uint16_t>((E + 7) / 8 * 8 * H) : nullptr;
-  c->router_panel = qwen ? nullptr : ab.take<uint8_t>(Ep * H * 2);
+  c->router_lane8 = lane8 ? ab.take<uint16_t>((E + 7) / 8 * 8 * H) : nullptr;
+  c->router_panel = lane8 ? nullptr : ab.take<uint8_t>(Ep * H * 2);
   float* bias = ab.take<float>(E);
   c->table = ab.take<ExpertMats>(E);
   c->shared_table = ab.take<ExpertMats>(1);
@@ -406,7 +411,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   if (host_flags[1] & 2) return URB_ERR_INVALID_SCALE;
   urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
 
-  if (qwen)
+  if (lane8)
     urb::launch_relayout_lane8(router, (int)E, (int)H, c->router_lane8, nullptr);
   else
     urb::launch_pack(URB_FMT_BF16, reinterpret_cast<const uint8_t*>(router), nullptr, (int)Ep,
@@ -456,8 +461,9 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logi
                       d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias, nullptr, 0};
   {
     Span span(c, URB_STAGE_ROUTER, s);
-    if (qwen) {
-      urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, c->ws.status, s);
+    if (c->router_lane8) {
+      urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status,
+                               s);
     } else {
       rp.slices = urb::router_slices(E, H, n);
       rp.part = c->ws.router_part;
@@ -467,25 +473,29 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logi
   }
   {
     Span span(c, URB_STAGE_ROUTE, s);
-    const bool ascending = qwen || d.composition == URB_COMPOSE_HY4;
+    const bool ascending = d.composition != URB_COMPOSE_GLM;
     urb::launch_route(logits, n, E, K, rp, ids, weights, ascending ? c->ws.asc : nullptr,
                       c->ws.status, s);
   }
   return URB_OK;
 }
 
-// The MX-activation mode (Hy4 MoeWeights::forward, src/models/hy4/runtime.rs:1371-1447) for
-// one chunk of n tokens.  Every MX projection reads simulated E4M3 activations (BF16-exact
-// values); the BF16 MFMA / FMA kernels run them with the Hy4 epilogues.
-static urb_status forward_hy4(urb_moe_ctx* c, const float* xc, int n, float* yc, int32_t* idc,
+// The MX-activation compositions for one chunk of n tokens: Hy4 MoeWeights::forward
+// (src/models/hy4/runtime.rs:1371-1447) and DeepSeek-V4.1 MoeWeights::forward
+// (src/models/deepseek_v41/runtime.rs:1963-2019).  Every MX projection reads simulated E4M3
+// activations (BF16-exact values); the BF16 MFMA / FMA kernels run them with the Hy4 epilogues.
+static urb_status forward_mx(urb_moe_ctx* c, const float* xc, int n, float* yc, int32_t* idc,
                               float* wc, hipStream_t s) {
   const urb_moe_desc& d = c->desc;
   const bool has_shared = d.shared_intermediate != 0;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
+  const bool dsv = d.composition == URB_COMPOSE_DSV41;
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
-  const urb::Epi dense_mlp{urb::kEpiHy4Shared, 0.0f};
+  // Hy4's shared DenseMlp is a plain BF16 SwiGLU; DeepSeek's shared expert is a routed expert
+  // without a weight
+  const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
   // mx_activation(input) once per token (runtime.rs:1397); the shared expert quantizes the same
   // input the same way (runtime.rs:1312), so both read it.
   urb::launch_quantize(xc, (size_t)n, (size_t)H, ws.xq, nullptr, nullptr, ws.status, s);
@@ -502,9 +512,10 @@ static urb_status forward_hy4(urb_moe_ctx* c, const float* xc, int n, float* yc,
       else
         urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xq,
                                  ws.shared_act, dense_mlp, ws.status, c->side);
-      // mx_linear(down, activated) re-quantizes (runtime.rs:1321, 2425-2428)
+      // the down projection re-quantizes its input (Hy4 mx_linear, runtime.rs:1321, 2425-2428;
+      // DeepSeek `linear` after the BF16 step, deepseek_v41/runtime.rs:2258-2260)
       urb::launch_quantize(ws.shared_act, (size_t)n, (size_t)Is, ws.shared_act, nullptr, nullptr,
-                           ws.status, c->side);
+                           ws.status, c->side, dsv ? 1 : 0);
     }
     {
       Span span(c, URB_STAGE_SHARED_DOWN, c->side);
@@ -523,9 +534,10 @@ static urb_status forward_hy4(urb_moe_ctx* c, const float* xc, int n, float* yc,
   if (n > 1) {
     Span span(c, URB_STAGE_PERMUTE, s);
     urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token,
-                        ws.pos_of_slot, ws.tiles, s);
+                        ws.pos_of_slot, ws.tiles, ws.slot_of_pos, s);
   }
   const int32_t* pos = n == 1 ? nullptr : ws.pos_of_slot;
+  const int32_t* slot = n == 1 ? nullptr : ws.slot_of_pos;  // one token: position = slot
   const int max_active = std::min(E, n * K);
   const int max_tiles = urb::gemm_max_tiles(n, K, E);
   {
@@ -536,16 +548,18 @@ static urb_status forward_hy4(urb_moe_ctx* c, const float* xc, int n, float* yc,
     else
       urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, ws.xq, ws.act,
                                routed, ws.status, s);
-    // activate_gate_up's simulate_e4m3_activation of the SwiGLU output (expert.rs:677)
+    // the SwiGLU output re-quantized for the down projection (Hy4 activate_gate_up,
+    // expert.rs:677); DeepSeek first scales each row by its route weight and rounds to BF16
+    // (runtime.rs:2254-2258)
     urb::launch_quantize(ws.act, (size_t)n * K, (size_t)I, ws.act, nullptr, nullptr, ws.status,
-                         s);
+                         s, dsv ? 1 : 0, dsv ? wc : nullptr, dsv ? slot : nullptr);
   }
   if (n == 1 && urb::down_combine_fits(K, I)) {
     if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {
       Span span(c, URB_STAGE_DOWN, s);
       urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I, ws.act,
-                                    has_shared ? ws.shared_out : nullptr, 2, routed, yc,
+                                    has_shared ? ws.shared_out : nullptr, dsv ? 3 : 2, routed, yc,
                                     ws.status, s);
     }
     if (c->profiling) return collect_spans(c);
@@ -563,8 +577,8 @@ static urb_status forward_hy4(urb_moe_ctx* c, const float* xc, int n, float* yc,
   if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
   {
     Span span(c, URB_STAGE_COMBINE, s);
-    urb::launch_combine_hy4(ws.y_perm, pos, wc, ws.asc, has_shared ? ws.shared_out : nullptr, n,
-                            K, H, yc, ws.status, s);
+    urb::launch_combine_hy4(ws.y_perm, pos, dsv ? nullptr : wc, ws.asc,
+                            has_shared ? ws.shared_out : nullptr, n, K, H, yc, ws.status, s);
   }
   if (c->profiling) return collect_spans(c);
   return URB_OK;
@@ -589,8 +603,8 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     float* yc = y + (size_t)c0 * H;
     int32_t* idc = ids ? ids + (size_t)c0 * K : ws.ids;
     float* wc = weights ? weights + (size_t)c0 * K : ws.weights;
-    if (d.composition == URB_COMPOSE_HY4) {
-      urb_status st = forward_hy4(c, xc, n, yc, idc, wc, s);
+    if (d.composition == URB_COMPOSE_HY4 || d.composition == URB_COMPOSE_DSV41) {
+      urb_status st = forward_mx(c, xc, n, yc, idc, wc, s);
       if (st) return st;
       continue;
     }
@@ -628,7 +642,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     if (n > 1) {
       Span span(c, URB_STAGE_PERMUTE, s);
       urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts,
-                          ws.perm_token, ws.pos_of_slot, ws.tiles, s);
+                          ws.perm_token, ws.pos_of_slot, ws.tiles, nullptr, s);
     }
     const int32_t* pos = n == 1 ? nullptr : ws.pos_of_slot;
     const int max_active = std::min(E, n * K);

@@ -9,7 +9,8 @@ namespace urb {
 
 // ------------------------------------------------------------------------------------------
 // Qwen router: `linear(router)` = Bf16Matrix::matvec_fp32 + BF16 (src/models/qwen3_8/math.rs:
-// 10-26).  The reference GEMV is the 8-lane FP32 FMA tree (src/model/bf16.rs:589-610): lane j
+// 10-26); DeepSeek-V4.1's `router.matvec_fp32_accum` is the same GEMV without the BF16 step
+// (src/models/deepseek_v41/runtime.rs:2136).  The reference GEMV is the 8-lane FP32 FMA tree (src/model/bf16.rs:589-610): lane j
 // accumulates columns == j (mod 8) in order, lanes are summed 0..7 (H is a multiple of 128
 // here, so there is no tail).  One thread per (expert, lane) runs that exact chain, so the
 // BF16 logits -- and hence their exact ties -- are bit-identical to the reference.  The
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
                                                           int E, int H,
                                                           const float* __restrict__ x, int T,
                                                           float* __restrict__ logits,
-                                                          int* status) {
+                                                          int round_bf16, int* status) {
   // [tok][8][H8 + 4] transposed chains: the pad of 4 floats puts the 8 chains of a column in
   // different LDS banks and keeps 16-byte alignment.  H is a multiple of 128.
   extern __shared__ float xs[];
@@ -122,8 +123,9 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
 #pragma unroll
     for (int u = 1; u < 8; ++u) sum = __fadd_rn(sum, __shfl(acc[tt], base + u, 64));
     if (e < E && j == 0 && tt < nt) {
-      float r;
-      if (!rne_bf16(sum, &r)) {
+      // Qwen's linear() rounds the logits to BF16; the plain FP32 GEMV rejects non-finite ones
+      float r = sum;
+      if (round_bf16 ? !rne_bf16(sum, &r) : !finite(sum)) {
         flag(status, kStatusNonFinite);
         r = sum;
       }
@@ -440,7 +442,8 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
                                                        int E, int K, int32_t* meta,
                                                        int32_t* active, int32_t* offsets,
                                                        int32_t* counts, int32_t* perm_token,
-                                                       int32_t* pos_of_slot, int32_t* tiles) {
+                                                       int32_t* pos_of_slot, int32_t* tiles,
+                                                       int32_t* slot_of_pos) {
   // LDS: bm[E][W] token bitmaps (64 tokens per word), then pre[E][W] = tokens routed to the
   // expert in the words before (u16), so a token's rank inside its expert is O(1).
   extern __shared__ uint64_t bm[];
@@ -491,6 +494,7 @@ __global__ __launch_bounds__(1024) void permute_kernel(const int32_t* __restrict
     const int p = off_s[ex] + pre[ex * W + w] + __popcll(below);
     pos_of_slot[i] = p;
     perm_token[p] = t;
+    if (slot_of_pos) slot_of_pos[p] = i;
   }
 }
 
@@ -619,7 +623,7 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 }
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
-                         int* status, hipStream_t s) {
+                         int round_bf16, int* status, hipStream_t s) {
   // One token per block gives the most independent waves; beyond 512 tokens, 2 or 4 tokens
   // share each weight chain (independent FMA chains interleave in the lane).
   const int H8 = H / 8;
@@ -628,13 +632,13 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
   const int tb_lds = (int)(65536 / per_tok);  // tokens whose staged chains fit 64 KiB of LDS
   if (T <= 512 || tb_lds < 2) {
     router_lane8_kernel<1><<<dim3((E + 7) / 8, T), block, per_tok, s>>>(w8, E, H, x, T, logits,
-                                                                        status);
-  } else if (T <= 256 || tb_lds < 4) {
+                                                                        round_bf16, status);
+  } else if (tb_lds < 4) {
     router_lane8_kernel<2><<<dim3((E + 7) / 8, (T + 1) / 2), block, 2 * per_tok, s>>>(
-        w8, E, H, x, T, logits, status);
+        w8, E, H, x, T, logits, round_bf16, status);
   } else {
     router_lane8_kernel<4><<<dim3((E + 7) / 8, (T + 3) / 4), block, 4 * per_tok, s>>>(
-        w8, E, H, x, T, logits, status);
+        w8, E, H, x, T, logits, round_bf16, status);
   }
 }
 
@@ -662,10 +666,10 @@ void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int3
 
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
-                    int32_t* tiles, hipStream_t s) {
+                    int32_t* tiles, int32_t* slot_of_pos, hipStream_t s) {
   size_t lds = (size_t)E * ((T + 63) / 64) * (sizeof(uint64_t) + sizeof(uint16_t));
   permute_kernel<<<1, 1024, lds, s>>>(ids, T, E, K, meta, active, offsets, counts, perm_token,
-                                      pos_of_slot, tiles);
+                                      pos_of_slot, tiles, slot_of_pos);
 }
 
 }  // namespace urb
