@@ -360,6 +360,27 @@ def test_hy4_errors():
     layer.close()
 
 
+@pytest.mark.parametrize("comp,T,E", [(C.COMPOSE_QWEN36, 40, 40), (C.COMPOSE_QWEN36, 600, 40),
+                                      (C.COMPOSE_QWEN36, 600, 248), (C.COMPOSE_DSV41, 777, 40)])
+def test_batched_lane8_router_is_bit_identical(comp, T, E):
+    # Batches of more than 512 tokens take the tiled 8-lane router (16 or 8 tokens per
+    # workgroup); its logits must equal the reference tree bit for bit, for partial token tiles
+    # and expert counts that are not multiples of 32 as well.
+    if comp == C.COMPOSE_QWEN36:
+        spec = C.small_spec(C.WORKLOADS["c1_bf16_decode"].spec, hidden=640, n_experts=E,
+                            intermediate=128)
+        host = C.make_host_layer(spec)
+    else:
+        host = _hy4_layer(C.FMT_MXFP4, hidden=640, n_experts=E, composition=C.COMPOSE_DSV41)
+    x = synth.activations(f"x.tiled.{T}", T, host.spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    logits, ids, w = layer.route(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert np.array_equal(logits.cpu().numpy().view(np.uint32), ref.logits.view(np.uint32))
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(host.spec, ref, host.correction_bias))
+    layer.close()
+
+
 def test_forward_is_deterministic_and_chunked_calls_equal_tokenwise():
     host = _small_layer("c5_mxfp4_zipf_prefill", hidden=128, n_experts=16, intermediate=128)
     T = 1100  # > one 1024-token internal chunk
