@@ -24,6 +24,13 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
   const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)p;
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// Non-temporal form for data read once (streamed expert weights): the load does not keep its
+// lines in the caches, so they do not evict what is reused.
+__device__ __forceinline__ uint4 ldg16_stream(const void* p) {
+  const u32x4_t v =
+      __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ uint32_t ldg_u8(const void* p) {
   return *(const __attribute__((address_space(1))) uint8_t*)p;
 }

@@ -56,6 +56,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     count = perm.counts[expert];
   }
   const int mrows = min(MT, count - m0);
+  // An expert whose tokens fit one tile has its weights read by this tile only: stream them
+  // (non-temporal loads).  A hot expert's tiles instead share its lines through the caches.
+  const bool stream = count <= MT;
   const ExpertMats m = mats[expert];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lq = lane >> 4;
@@ -94,14 +97,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     }
 
   const int steps = K / kKS;
-  auto body = [&](auto nmb) {
+  auto body = [&](auto nmb, auto streamed) {
     constexpr int NMB = decltype(nmb)::value;  // 16-token MFMA blocks this tile needs
+    constexpr bool STREAM = decltype(streamed)::value;
     BRaw<FMT> r0[DEPTH][NP], r1[DEPTH][NP];
     auto fetch = [&](int d, int s) {
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
-        load_b<FMT>(r0[d][q], pd0 + q * pbytes, ps0 + q * pscales, s);
-        if constexpr (PAIR) load_b<FMT>(r1[d][q], pd1 + q * pbytes, ps1 + q * pscales, s);
+        load_b<FMT, STREAM>(r0[d][q], pd0 + q * pbytes, ps0 + q * pscales, s);
+        if constexpr (PAIR) load_b<FMT, STREAM>(r1[d][q], pd1 + q * pbytes, ps1 + q * pscales, s);
       }
     };
     auto stage = [&](AStage (&as)[RG], int buf) {
@@ -170,13 +174,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
       }
     }
   };
+  using Stream = std::true_type;
+  using Cached = std::false_type;
   if constexpr (MT == 64) {
-    if (mrows > 32) body(Int<4>{});
-    else if (mrows > 16) body(Int<2>{});
-    else body(Int<1>{});
+    if (mrows > 32) body(Int<4>{}, Cached{});
+    else if (mrows > 16) body(Int<2>{}, Cached{});
+    else body(Int<1>{}, Cached{});
+  } else if (stream) {
+    if (mrows > 16) body(Int<2>{}, Stream{});
+    else body(Int<1>{}, Stream{});
   } else {
-    if (mrows > 16) body(Int<2>{});
-    else body(Int<1>{});
+    if (mrows > 16) body(Int<2>{}, Cached{});
+    else body(Int<1>{}, Cached{});
   }
 
   // ---- epilogue: lane holds column `row` of panel q, rows 4*lq + i of each 16-row block

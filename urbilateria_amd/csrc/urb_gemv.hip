@@ -9,6 +9,7 @@
 // multiplication by 2^k of the block partial), against the input vector staged in LDS.  The
 // four lq lanes are summed by shuffles and the K parts through LDS, in a fixed order.  (FMA
 // lanes beat the matrix cores here: with one token, 15 of an MFMA's 16 rows would be zero.)
+// Each weight is read once per call, so the weight loads are non-temporal.
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
 #include "urb_panel.hpp"
@@ -134,8 +135,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict_
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
       if (s_begin + d < s_end) {
-        load_b<FMT>(r0[d], pd0, ps0, s_begin + d);
-        if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, s_begin + d);
+        load_b<FMT, true>(r0[d], pd0, ps0, s_begin + d);
+        if constexpr (PAIR) load_b<FMT, true>(r1[d], pd1, ps1, s_begin + d);
       }
   }
   const int p = base;  // the expert's one permuted position
@@ -159,8 +160,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const ExpertMats* __restrict_
         BRaw<FMT> c0 = r0[d], c1;
         if constexpr (PAIR) c1 = r1[d];
         if (s + DEPTH < s_end) {
-          load_b<FMT>(r0[d], pd0, ps0, s + DEPTH);
-          if constexpr (PAIR) load_b<FMT>(r1[d], pd1, ps1, s + DEPTH);
+          load_b<FMT, true>(r0[d], pd0, ps0, s + DEPTH);
+          if constexpr (PAIR) load_b<FMT, true>(r1[d], pd1, ps1, s + DEPTH);
         }
         raw_dot<FMT>(c0, s, lq, xs, acc0);
         if constexpr (PAIR) raw_dot<FMT>(c1, s, lq, xs, acc1);
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
     ps = FMT == kFmtBF16 ? nullptr : m.scales[2] + (size_t)panel * pscales + lane;
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
-      if (d < steps) load_b<FMT>(r[d], pd, ps, d);
+      if (d < steps) load_b<FMT, true>(r[d], pd, ps, d);
   };
   const int a0 = wave;
   if (a0 < K) bind(a0);
@@ -294,7 +295,7 @@ __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
         const int st = s0 + d;
         if (st >= steps) break;
         BRaw<FMT> c = r[d];
-        if (st + DEPTH < steps) load_b<FMT>(r[d], pd, ps, st + DEPTH);
+        if (st + DEPTH < steps) load_b<FMT, true>(r[d], pd, ps, st + DEPTH);
         raw_dot<FMT>(c, st, lq, xa, acc);
       }
     }

@@ -26,18 +26,21 @@ template <>
 struct BRaw<kFmtMXFP8> { uint4 q[2]; uint32_t s; };
 
 // pd = panel data + 16 * lane, ps = panel scales + lane (see the layout in urb_kernels.hpp).
-template <int FMT>
+// STREAM: non-temporal weight loads, for weights this launch reads only once.  (A compile-time
+// choice: with a runtime one the compiler merges both loads into one and drops the hint.)
+template <int FMT, bool STREAM = false>
 __device__ __forceinline__ void load_b(BRaw<FMT>& r, const uint8_t* __restrict__ pd,
                                        const uint8_t* __restrict__ ps, int step) {
+  auto ld = [](const void* p) { return STREAM ? ldg16_stream(p) : ldg16(p); };
   if constexpr (FMT == kFmtBF16) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.q[j] = ldg16(pd + (size_t)(4 * step + j) * 1024);
+    for (int j = 0; j < 4; ++j) r.q[j] = ld(pd + (size_t)(4 * step + j) * 1024);
   } else if constexpr (FMT == kFmtMXFP4) {
-    r.q = ldg16(pd + (size_t)step * 1024);
+    r.q = ld(pd + (size_t)step * 1024);
     r.s = ldg_u8(ps + (size_t)step * 64);
   } else {
-    r.q[0] = ldg16(pd + (size_t)(2 * step) * 1024);
-    r.q[1] = ldg16(pd + (size_t)(2 * step + 1) * 1024);
+    r.q[0] = ld(pd + (size_t)(2 * step) * 1024);
+    r.q[1] = ld(pd + (size_t)(2 * step + 1) * 1024);
     r.s = ldg_u8(ps + (size_t)step * 64);
   }
 }
