@@ -151,6 +151,43 @@ def test_mfma_scale_16x16x128_operands(fmt):
     assert np.array_equal(got, ref), float(np.abs(got - ref).max())
 
 
+def _bf16_rne_bits(x):
+    """Round-to-nearest-even BF16 bits of finite float32 values (the textbook bit formula)."""
+    b = x.view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_activation_split_is_round_to_nearest_even_hi_and_lo():
+    # The grouped GEMM stages f32 activations as hi = bf16(x), lo = bf16(x - hi) through the
+    # hardware pack conversion.  Exact against the RNE bit formula for normal values of every
+    # magnitude, halfway ties, f32 denormals, signed zeros and the overflow to infinity.
+    rng = np.random.default_rng(7)
+    parts = [
+        (rng.standard_normal(20000) * np.exp2(rng.integers(-126, 127, 20000))).astype(np.float32),
+        # ties: bf16 value plus exactly half an ulp (even and odd lower neighbours)
+        ((rng.integers(0, 1 << 16, 4000, dtype=np.uint32) << 16) | 0x8000).view(np.float32),
+        rng.integers(1, 1 << 23, 4000, dtype=np.uint32).view(np.float32),       # denormals
+        (rng.integers(1, 1 << 23, 4000, dtype=np.uint32) | (1 << 31)).view(np.float32),
+        np.array([0.0, -0.0, 1.0, -1.0, np.finfo(np.float32).max, -np.finfo(np.float32).max,
+                  np.finfo(np.float32).tiny, 3.0e38, 1e-45, -1e-45], np.float32),
+    ]
+    x = np.concatenate(parts)
+    x = x[np.isfinite(x)]
+    x = x[: x.size // 2 * 2]
+    hi_ref = _bf16_rne_bits(x)
+    with np.errstate(invalid="ignore", over="ignore"):
+        rest = (x - (hi_ref.astype(np.uint32) << 16).view(np.float32)).astype(np.float32)
+    lo_ref = _bf16_rne_bits(rest)
+    xd = torch.from_numpy(x).cuda()
+    hi = torch.empty(x.size, dtype=torch.int16, device="cuda")
+    lo = torch.empty(x.size, dtype=torch.int16, device="cuda")
+    N.check(N.synth_lib().urb_probe_split_bf16(xd.data_ptr(), x.size, hi.data_ptr(),
+                                               lo.data_ptr(), None))
+    torch.cuda.synchronize()
+    assert np.array_equal(hi.cpu().numpy().view(np.uint16), hi_ref)
+    assert np.array_equal(lo.cpu().numpy().view(np.uint16), lo_ref)
+
+
 def _probe_cvt(fmt, codes, scales):
     out = torch.empty(codes.size, dtype=torch.int16, device="cuda")
     c_dev = torch.from_numpy(codes).cuda()   # held: a dropped temporary's block can be reused

@@ -28,9 +28,17 @@ namespace urb {
 // NP panels per wave (the workgroup covers 4 NP panels = 64 NP weight rows): every staged
 // activation fragment feeds NP (x2 for gate+up) MFMAs.  MT tokens per tile (32 or 64; 64 for
 // large dense batches, so each weight byte feeds twice the MFMAs before it is re-read).
+//
+// Placement: workgroups go to the eight XCDs round robin (blockIdx.x % 8), and each XCD has its
+// own L2.  XCD c = cx + xsplit cy takes the contiguous run cy (of 8 / xsplit) of the tile list
+// and the run cx (of xsplit) of the panel groups, tile by tile.  Tiles are in expert order, so
+// the tiles of an expert, which read the same weight panels, share one L2, and so do the
+// workgroups of a tile, which read the same activation rows.  xsplit > 1 (a dense batch, one
+// expert) trades weight re-reads across XCDs for activation re-reads.
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
-                                                      Perm perm, int rows, int K,
+                                                      Perm perm, int max_tiles, int xsplit,
+                                                      int rows, int K,
                                                       const float* __restrict__ in,
                                                       float* __restrict__ out, Epi epi,
                                                       int* status) {
@@ -39,17 +47,24 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   __shared__ __attribute__((aligned(16))) u16 a_hi[2][MT * kALd];
   __shared__ __attribute__((aligned(16))) u16 a_lo[2][MT * kALd];
 
-  // ---- which tile
-  const int w = blockIdx.y;
+  // ---- which tile and panel group
+  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
+  const int cx = xcd % xsplit, cy = xcd / xsplit, ysplit = 8 / xsplit;
+  const int groups = rows / (kNT * NP);
+  const int g0 = cx * groups / xsplit, width = (cx + 1) * groups / xsplit - g0;
+  const int ntiles = min(perm.dense_tokens > 0 ? (perm.dense_tokens + MT - 1) / MT : perm.meta[1],
+                         max_tiles);
+  const int t1 = (cy + 1) * ntiles / ysplit;
+  const int w = cy * ntiles / ysplit + local / width;
+  if (w >= t1) return;
+  const int group = g0 + local % width;
   int expert, base, count, m0;
   if (perm.dense_tokens > 0) {
     expert = 0;
     base = 0;
     count = perm.dense_tokens;
     m0 = w * MT;
-    if (m0 >= count) return;
   } else {
-    if (w >= perm.meta[1]) return;
     expert = perm.tiles[2 * w];
     m0 = perm.tiles[2 * w + 1];
     base = perm.offsets[expert];
@@ -60,31 +75,31 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   // (non-temporal loads).  A hot expert's tiles instead share its lines through the caches.
   const bool stream = count <= MT;
   const ExpertMats m = mats[expert];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, lq = lane >> 4;
-  const int panel0 = (blockIdx.x * 4 + wave) * NP;
+  const int panel0 = (group * 4 + wave) * NP;
   const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(K);
   const size_t pscales = (size_t)kPanelRows * (K / 32);
 
-  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + panel0 * pbytes + 16 * lane;
-  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + panel0 * pscales + lane;
-  const uint8_t* pd1 = PAIR ? m.data[1] + panel0 * pbytes + 16 * lane : nullptr;
-  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + panel0 * pscales + lane : nullptr;
+  // wavefront-uniform panel bases; the lane's unit is at 16 lane (data), lane (scales)
+  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + panel0 * pbytes;
+  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + panel0 * pscales;
+  const uint8_t* pd1 = PAIR ? m.data[1] + panel0 * pbytes : nullptr;
+  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + panel0 * pscales : nullptr;
+  const uint32_t doff = 16u * lane, soff = lane;
 
-  // ---- A source rows of this thread's staging slots: rows am + 32 g
+  // ---- A source rows of this thread's staging slots: rows am + 32 g.  A slot past the tile's
+  // last row stages the tile's first row instead: its products land in accumulator rows the
+  // epilogue never stores, and the loads need no mask.
   const int am = threadIdx.x >> 3;
-  bool a_valid[RG];
   const float* a_src[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
-    const int r = am + 32 * g;
-    a_valid[g] = r < mrows;
-    a_src[g] = in;
-    if (a_valid[g]) {
-      const int p = base + m0 + r;
-      const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
-      a_src[g] = in + (size_t)src_row * K;
-    }
+    const int r = am + 32 * g < mrows ? am + 32 * g : 0;
+    const int p = base + m0 + r;
+    const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
+    a_src[g] = in + (size_t)src_row * K;
   }
 
   f32x4 acc0[NP][MBMAX], acc1[NP][MBMAX];
@@ -97,15 +112,19 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     }
 
   const int steps = K / kKS;
+  // B registers: a ring of R = DEPTH + 1 step slots, the step loop unrolled R times so that
+  // step s computes from slot s % R while slot (s + DEPTH) % R fills (no register copies).
+  constexpr int R = DEPTH + 1;
   auto body = [&](auto nmb, auto streamed) {
     constexpr int NMB = decltype(nmb)::value;  // 16-token MFMA blocks this tile needs
     constexpr bool STREAM = decltype(streamed)::value;
-    BRaw<FMT> r0[DEPTH][NP], r1[DEPTH][NP];
-    auto fetch = [&](int d, int s) {
+    BRaw<FMT> r0[R][NP], r1[R][NP];
+    auto fetch = [&](int slot, int s) {
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
-        load_b<FMT, STREAM>(r0[d][q], pd0 + q * pbytes, ps0 + q * pscales, s);
-        if constexpr (PAIR) load_b<FMT, STREAM>(r1[d][q], pd1 + q * pbytes, ps1 + q * pscales, s);
+        load_b<FMT, STREAM>(r0[slot][q], pd0 + q * pbytes, doff, ps0 + q * pscales, soff, s);
+        if constexpr (PAIR)
+          load_b<FMT, STREAM>(r1[slot][q], pd1 + q * pbytes, doff, ps1 + q * pscales, soff, s);
       }
     };
     auto stage = [&](AStage (&as)[RG], int buf) {
@@ -114,62 +133,63 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
       for (int g = 0; g < RG; ++g) any |= store_a(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
       return any;
     };
+    // One K step from ring slot `slot`; the lo-half MFMAs only when some lo half is non-zero.
+    // (A uniform runtime branch: compiling both variants straight-line spills the MXFP4
+    // four-panel kernel.)
+    auto mma = [&](int slot, const u16* hi, const u16* lo, bool with_lo) {
+      const bool LO = with_lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bf16x8 f0[NP], f1[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          f0[q] = decode_b<FMT>(r0[slot][q], j);
+          if constexpr (PAIR) f1[q] = decode_b<FMT>(r1[slot][q], j);
+        }
+        const int kf = frag_k<FMT>(j, lq);
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb) {
+          const bf16x8 ah = lds_frag(hi, mb * 16 + ln, kf);
+          bf16x8 al;
+          if (LO) al = lds_frag(lo, mb * 16 + ln, kf);
+#pragma unroll
+          for (int q = 0; q < NP; ++q) {
+            acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0[q], acc0[q][mb], 0, 0, 0);
+            if constexpr (PAIR)
+              acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1[q], acc1[q][mb], 0, 0, 0);
+          }
+          if (LO) {
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0[q], acc0[q][mb], 0, 0, 0);
+              if constexpr (PAIR)
+                acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1[q], acc1[q][mb], 0, 0, 0);
+            }
+          }
+        }
+      }
+    };
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
       if (d < steps) fetch(d, d);
     AStage as[RG];
 #pragma unroll
-    for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], a_valid[g], 0);
+    for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], true, 0);
     bool lo_any = __syncthreads_or(stage(as, 0));
-    for (int s0 = 0; s0 < steps; s0 += DEPTH) {
+    for (int s0 = 0; s0 < steps; s0 += R) {
 #pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
+      for (int d = 0; d < R; ++d) {
         const int s = s0 + d;
         if (s >= steps) break;
         const int buf = s & 1;
         const bool more = s + 1 < steps;
         if (more) {
 #pragma unroll
-          for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], a_valid[g], (s + 1) * kKS);
+          for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], true, (s + 1) * kKS);
         }
-        BRaw<FMT> c0[NP], c1[NP];
-#pragma unroll
-        for (int q = 0; q < NP; ++q) {
-          c0[q] = r0[d][q];
-          if constexpr (PAIR) c1[q] = r1[d][q];
-        }
-        if (s + DEPTH < steps) fetch(d, s + DEPTH);  // refill this ring slot DEPTH steps ahead
-        const u16* hi = a_hi[buf];
-        const u16* lo = a_lo[buf];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          bf16x8 f0[NP], f1[NP];
-#pragma unroll
-          for (int q = 0; q < NP; ++q) {
-            f0[q] = decode_b<FMT>(c0[q], j);
-            if constexpr (PAIR) f1[q] = decode_b<FMT>(c1[q], j);
-          }
-          const int kf = frag_k<FMT>(j, lq);
-#pragma unroll
-          for (int mb = 0; mb < NMB; ++mb) {
-            const bf16x8 ah = lds_frag(hi, mb * 16 + ln, kf);
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0[q], acc0[q][mb], 0, 0, 0);
-              if constexpr (PAIR)
-                acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1[q], acc1[q][mb], 0, 0, 0);
-            }
-            if (lo_any) {
-              const bf16x8 al = lds_frag(lo, mb * 16 + ln, kf);
-#pragma unroll
-              for (int q = 0; q < NP; ++q) {
-                acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0[q], acc0[q][mb], 0, 0, 0);
-                if constexpr (PAIR)
-                  acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1[q], acc1[q][mb], 0, 0, 0);
-              }
-            }
-          }
-        }
+        // refill the slot step s - 1 used, DEPTH steps ahead
+        if (s + DEPTH < steps) fetch((d + DEPTH) % R, s + DEPTH);
+        mma(d, a_hi[buf], a_lo[buf], lo_any);
         if (more) lo_any = __syncthreads_or(stage(as, buf ^ 1));
       }
     }
@@ -210,12 +230,33 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   if (bad) flag(status, kStatusNonFinite);
 }
 
+// Panel-group split across XCDs: 1 for routed experts (each expert's weights once, from the
+// XCD holding its tiles); for one dense expert the split that minimises weight re-reads
+// (8 / xsplit times) plus activation re-reads (xsplit times).
+template <int FMT, bool PAIR, int NP>
+static int xcd_split(const Perm& perm, int max_tiles, int rows, int K) {
+  const int groups = rows / (kNT * NP);
+  if (perm.dense_tokens <= 0 || max_tiles < 8) return 1;
+  const double wbytes = (PAIR ? 2.0 : 1.0) * rows * (double)panel_row_bytes<FMT>(K);
+  const double abytes = (double)perm.dense_tokens * K * 4;
+  int best = 1;
+  double best_cost = 8 * wbytes + abytes;
+  for (int x = 2; x <= 8 && x <= groups; x *= 2) {
+    const double cost = 8.0 / x * wbytes + x * abytes;
+    if (cost < best_cost) best = x, best_cost = cost;
+  }
+  return best;
+}
+
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                          const float* in, float* out, Epi epi, int* status, hipStream_t s) {
-  dim3 grid(rows / (kNT * NP), max_tiles);
-  gemm_kernel<FMT, PAIR, DEPTH, NP, MT><<<grid, 256, 0, s>>>(mats, perm, rows, K, in, out, epi,
-                                                              status);
+  const int xsplit = xcd_split<FMT, PAIR, NP>(perm, max_tiles, rows, K);
+  const int groups = rows / (kNT * NP), ysplit = 8 / xsplit;
+  // per XCD: at most ceil(tiles / ysplit) tiles times ceil(groups / xsplit) panel groups
+  const int per_xcd = (max_tiles + ysplit - 1) / ysplit * ((groups + xsplit - 1) / xsplit);
+  gemm_kernel<FMT, PAIR, DEPTH, NP, MT><<<dim3(8 * per_xcd), 256, 0, s>>>(
+      mats, perm, max_tiles, xsplit, rows, K, in, out, epi, status);
 }
 
 // Weight steps in flight per wave (DEPTH) and panels per wave (NP), per format.  BF16 steps are

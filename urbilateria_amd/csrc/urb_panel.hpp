@@ -45,12 +45,32 @@ __device__ __forceinline__ void load_b(BRaw<FMT>& r, const uint8_t* __restrict__
   }
 }
 
-typedef unsigned short u16;
-
-__device__ __forceinline__ u16 bf16_rne_bits(float v) {
-  uint32_t b = f2u(v);
-  return (u16)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+// The same from a wavefront-uniform panel base (held in SGPRs) plus 32-bit per-lane offsets
+// (doff = 16 * lane, soff = lane): the loads take the scalar-base form of global_load, with no
+// 64-bit address arithmetic per lane.
+template <int FMT, bool STREAM = false>
+__device__ __forceinline__ void load_b(BRaw<FMT>& r, const uint8_t* __restrict__ pbase,
+                                       uint32_t doff, const uint8_t* __restrict__ sbase,
+                                       uint32_t soff, int step) {
+  auto ld = [&](uint32_t o) {
+    const uint8_t* p = pbase + o;
+    return STREAM ? ldg16_stream(p) : ldg16(p);
+  };
+  const uint32_t st = (uint32_t)step;
+  if constexpr (FMT == kFmtBF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.q[j] = ld(doff + (4 * st + j) * 1024u);
+  } else if constexpr (FMT == kFmtMXFP4) {
+    r.q = ld(doff + st * 1024u);
+    r.s = ldg_u8(sbase + (soff + st * 64u));
+  } else {
+    r.q[0] = ld(doff + 2 * st * 1024u);
+    r.q[1] = ld(doff + (2 * st + 1) * 1024u);
+    r.s = ldg_u8(sbase + (soff + st * 64u));
+  }
 }
+
+typedef unsigned short u16;
 
 // k offset (within the K step) of MFMA j's operands for lane group lq.
 template <int FMT>
@@ -154,28 +174,39 @@ __device__ __forceinline__ void load_a(AStage& a, const float* __restrict__ src,
   }
 }
 
+// Two floats to packed BF16, round to nearest even (v_cvt_pk_bf16_f32; denormals kept).
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{a, b}, bf16x2v));
+}
+
+// hi/lo BF16 split of two floats: hi = bf16(v), lo = bf16(v - hi) (v - hi is exact), packed
+// (element 0 in the low half).
+__device__ __forceinline__ void split_bf16(float v0, float v1, uint32_t& hi, uint32_t& lo) {
+  hi = pk_bf16(v0, v1);
+  lo = pk_bf16(v0 - u2f(hi << 16), v1 - u2f(hi & 0xffff0000u));
+}
+
 // Writes hi/lo BF16 halves of the staged values into LDS row m (default: this thread's staging
 // row); returns whether any lo half is non-zero.
 __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
                                         int m = (int)(threadIdx.x >> 3)) {
   const int kc = (threadIdx.x & 7) * 16;
   const float* v = reinterpret_cast<const float*>(a.v);
-  u16 h[16], l[16];
-  bool any = false;
+  uint32_t h[8], l[8], lor = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    h[i] = bf16_rne_bits(v[i]);
-    float rest = v[i] - u2f((uint32_t)h[i] << 16);
-    l[i] = bf16_rne_bits(rest);
-    any |= (l[i] & 0x7fff) != 0;
+  for (int i = 0; i < 8; ++i) {
+    split_bf16(v[2 * i], v[2 * i + 1], h[i], l[i]);
+    lor |= l[i];
   }
   uint4* dh = reinterpret_cast<uint4*>(hi + m * kALd + kc);
   uint4* dl = reinterpret_cast<uint4*>(lo + m * kALd + kc);
-  dh[0] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
-  dh[1] = make_uint4(h[8] | (h[9] << 16), h[10] | (h[11] << 16), h[12] | (h[13] << 16), h[14] | (h[15] << 16));
-  dl[0] = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
-  dl[1] = make_uint4(l[8] | (l[9] << 16), l[10] | (l[11] << 16), l[12] | (l[13] << 16), l[14] | (l[15] << 16));
-  return any;
+  dh[0] = make_uint4(h[0], h[1], h[2], h[3]);
+  dh[1] = make_uint4(h[4], h[5], h[6], h[7]);
+  dl[0] = make_uint4(l[0], l[1], l[2], l[3]);
+  dl[1] = make_uint4(l[4], l[5], l[6], l[7]);
+  return (lor & 0x7fff7fffu) != 0;
 }
 
 __device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {

@@ -110,6 +110,16 @@ __global__ void cvt_bf16_kernel(int fmt, const uint8_t* codes, const uint8_t* sc
   out[i] = __builtin_bit_cast(uint16_t, v[0]);
 }
 
+// hi/lo BF16 split of the GEMM activation staging, for n / 2 float pairs.
+__global__ void split_bf16_kernel(const float* x, int pairs, uint32_t* hi, uint32_t* lo) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pairs) return;
+  uint32_t h, l;
+  urb::split_bf16(x[2 * i], x[2 * i + 1], h, l);
+  hi[i] = h;
+  lo[i] = l;
+}
+
 // One v_mfma_scale_f32_16x16x128_f8f6f4 step built by the MX-activation kernels' own operand
 // helpers (urb_panel.hpp): A = a row-major [16][128] E4M3 matrix with [16][4] E8M0 scales,
 // staged in LDS and read as lds_qfrag does; B = 16 weight rows as one panel's 128-column step
@@ -198,6 +208,16 @@ int urb_probe_cvt_bf16(int fmt, const void* codes, const void* scales, int n, vo
                        void* stream) {
   cvt_bf16_kernel<<<(n + 255) / 256, 256, 0, (hipStream_t)stream>>>(
       fmt, (const uint8_t*)codes, (const uint8_t*)scales, n, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? 0 : 5;
+}
+
+// Diagnostics: the activation hi/lo BF16 split (hi = bf16(x), lo = bf16(x - hi)) of n floats
+// (n even); hi and lo receive n BF16 values each.
+int urb_probe_split_bf16(const float* x, int n, void* hi, void* lo, void* stream) {
+  if (n <= 0 || n % 2) return 7;
+  const int pairs = n / 2;
+  split_bf16_kernel<<<(pairs + 255) / 256, 256, 0, (hipStream_t)stream>>>(
+      x, pairs, (uint32_t*)hi, (uint32_t*)lo);
   return hipGetLastError() == hipSuccess ? 0 : 5;
 }
 

@@ -26,7 +26,7 @@ STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "sh
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
                  "urb_synth_e8m0", "urb_probe_mfma_16x16x32", "urb_probe_cvt_bf16",
-                 "urb_probe_mfma_scale_16x16x128")
+                 "urb_probe_mfma_scale_16x16x128", "urb_probe_split_bf16")
 
 
 class UrbError(RuntimeError):
@@ -105,6 +105,9 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_quantize_e4m3.restype = ctypes.c_int
         lib.urb_status_string.argtypes = [ctypes.c_int]
         lib.urb_status_string.restype = ctypes.c_char_p
+        for f in EXPORTS:
+            if getattr(lib, f).argtypes is None:
+                raise RuntimeError(f"{f}: no ctypes signature")
         _moe = lib
     return _moe
 
@@ -124,7 +127,11 @@ def synth_lib() -> ctypes.CDLL:
         lib.urb_probe_mfma_16x16x32.argtypes = [P, P, P, P]
         lib.urb_probe_cvt_bf16.argtypes = [ctypes.c_int, P, P, ctypes.c_int, P, P]
         lib.urb_probe_mfma_scale_16x16x128.argtypes = [ctypes.c_int, P, P, P, P, P, P]
+        lib.urb_probe_split_bf16.argtypes = [P, ctypes.c_int, P, P, P]
         for f in SYNTH_EXPORTS:
+            # without argtypes ctypes would pass a device pointer as a 32-bit int
+            if getattr(lib, f).argtypes is None:
+                raise RuntimeError(f"{f}: no ctypes signature")
             getattr(lib, f).restype = ctypes.c_int
         _synth = lib
     return _synth
