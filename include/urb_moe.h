@@ -179,6 +179,20 @@ urb_status urb_pack_matrix(urb_format format, const void *data, const uint8_t *s
                            uint32_t rows, uint32_t cols, void *packed_data,
                            uint8_t *packed_scales, void *stream);
 
+/* Per-expert views of consolidated checkpoint tensors, for urb_moe_weights.experts: fills
+ * out[E * 3] with pointers into the tensors (no copy, no device work).  gate_up is [E, 2I, H]
+ * with each expert's gate rows 0..I-1 followed by its up rows I..2I-1, down is [E, H, I], both
+ * in the urb_matrix layout per expert; the scale tensors are [E, 2I, H/32] and [E, H, I/32]
+ * for the MX formats and NULL for BF16 (URB_ERR_ARGUMENT otherwise); H and I multiples of 32.
+ * Replaces the per-expert slicing of the Qwen3.6 packed BF16 gate_up_proj / down_proj
+ * (src/models/qwen3_6/expert_store.rs:125-158) and of the Hy4 consolidated E4M3 + U8-scale
+ * tensors (src/models/hy4/expert.rs:436-625, gate/up split at I as activate_gate_up,
+ * src/models/hy4/expert.rs:664-680). */
+urb_status urb_expert_views(urb_format format, uint32_t n_experts, uint32_t hidden,
+                            uint32_t intermediate, const void *gate_up,
+                            const uint8_t *gate_up_scales, const void *down,
+                            const uint8_t *down_scales, urb_matrix *out);
+
 /* Device-time spans per stage of a layer call: the counterpart of the reference's profiling
  * spans (ProfileStage, src/profiling.rs:75-136; span_with_work, src/profiling.rs:581-600).
  * While enabled, every forward call brackets each stage with HIP events on the stream the

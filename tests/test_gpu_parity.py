@@ -230,7 +230,7 @@ SMALL = [(name, T) for name in C.WORKLOADS for T in (1, 3, 40)]
 
 
 def _small_layer(name, hidden=256, n_experts=16, intermediate=128):
-    w = C.WORKLOADS[name]
+    w = C.workload(name)
     spec = C.small_spec(w.spec, hidden=hidden, n_experts=n_experts, intermediate=intermediate)
     bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.05) if w.zipf_s else None
     return C.make_host_layer(spec, bias=bias)
@@ -493,6 +493,43 @@ def test_borrowed_panel_layer_equals_copied_layer():
         assert borrowed.memory()[0] == 0
         copied.close()
         borrowed.close()
+
+
+def _consolidate(dev):
+    """Stacks a layer's per-expert matrices into the consolidated checkpoint tensors:
+    gate_up [E, 2I, ...] (gate rows, then up rows), down [E, H, ...], scale sidecars alike."""
+    spec = dev.spec
+    E, H, I = spec.n_experts, spec.hidden, spec.intermediate
+    rows = lambda t, r: t.contiguous().view(torch.uint8).reshape(r, -1)
+    gu = torch.stack([torch.cat([rows(dev.experts[e][0][0], I), rows(dev.experts[e][1][0], I)])
+                      for e in range(E)]).contiguous()
+    dn = torch.stack([rows(dev.experts[e][2][0], H) for e in range(E)]).contiguous()
+    gus = dns = None
+    if dev.experts[0][0][1] is not None:
+        gus = torch.stack([torch.cat([rows(dev.experts[e][0][1], I), rows(dev.experts[e][1][1], I)])
+                           for e in range(E)]).contiguous()
+        dns = torch.stack([rows(dev.experts[e][2][1], H) for e in range(E)]).contiguous()
+    return gu, gus, dn, dns
+
+
+def test_consolidated_checkpoint_layer_equals_per_expert_layer():
+    # Qwen3.6 packed BF16 gate_up_proj / down_proj and Hy4 consolidated E4M3 + U8 scales,
+    # used through per-expert views, give the per-expert layer's results bit for bit.
+    for name in ("c2_bf16_prefill", "c3_mxfp4_decode", "c4_mxfp8_mx_activation"):
+        host = _small_layer(name)
+        dev = moe_mod().DeviceLayer.from_host(host)
+        gu, gus, dn, dns = _consolidate(dev)
+        cons = moe_mod().DeviceLayer.from_consolidated(dev.spec, dev.router_weight, gu, gus, dn,
+                                                       dns, dev.shared, dev.correction_bias)
+        x = torch.from_numpy(synth.activations("x.consolidated", 5, host.spec.hidden)).cuda()
+        a = moe_mod().MoeLayer(dev, max_tokens=5)
+        b = moe_mod().MoeLayer(cons, max_tokens=5)
+        for T in (1, 5):
+            y1, i1, w1 = a.forward(x[:T].contiguous())
+            y2, i2, w2 = b.forward(x[:T].contiguous())
+            assert torch.equal(y1, y2) and torch.equal(i1, i2) and torch.equal(w1, w2)
+        a.close()
+        b.close()
 
 
 # ------------------------------------------------------------------------------- errors

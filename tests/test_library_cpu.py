@@ -96,3 +96,45 @@ def test_zipf_bias_is_monotone_in_rank():
     b = C.zipf_bias(384, 1.1, 0.1)
     assert b.shape == (384,) and np.all(np.isfinite(b))
     assert len(np.unique(b)) == 384
+
+
+@pytest.mark.parametrize("fmt", [C.FMT_BF16, C.FMT_MXFP4, C.FMT_MXFP8])
+def test_expert_views_slice_consolidated_tensors(fmt):
+    # urb_expert_views only computes addresses, so host tensors stand in for device ones.  The
+    # views must be the per-expert slices the reference takes: gate = rows 0..I-1 and up = rows
+    # I..2I-1 of each expert's [2I, H] block, down = the expert's [H, I] block, with the scale
+    # sidecars sliced the same way (qwen3_6/expert_store.rs:146-158, hy4/expert.rs:664-680).
+    torch = pytest.importorskip("torch")
+    from urbilateria_amd import moe
+    E, H, I = 3, 256, 128
+    spec = C.LayerSpec(hidden=H, n_experts=E, top_k=2, intermediate=I, expert_format=fmt)
+    width = {C.FMT_BF16: 2 * H, C.FMT_MXFP4: H // 2, C.FMT_MXFP8: H}[fmt]
+    dwidth = {C.FMT_BF16: 2 * I, C.FMT_MXFP4: I // 2, C.FMT_MXFP8: I}[fmt]
+    gu = torch.zeros((E, 2 * I, width), dtype=torch.uint8)
+    dn = torch.zeros((E, H, dwidth), dtype=torch.uint8)
+    mx = fmt != C.FMT_BF16
+    gus = torch.zeros((E, 2 * I, H // 32), dtype=torch.uint8) if mx else None
+    dns = torch.zeros((E, H, I // 32), dtype=torch.uint8) if mx else None
+    layer = moe.DeviceLayer.from_consolidated(spec, None, gu, gus, dn, dns)
+    views = moe.expert_views(fmt, E, H, I, gu, gus, dn, dns)
+    for e in range(E):
+        for m in range(3):
+            d, s = layer.experts[e][m]
+            assert d.is_contiguous() and (s is None or s.is_contiguous())
+            assert views[3 * e + m] == (d.data_ptr(), None if s is None else s.data_ptr())
+    # the up view starts one [I, H] matrix after the gate view
+    row = C.matrix_bytes(fmt, I, H)[0]
+    assert views[1][0] - views[0][0] == row
+    assert views[3][0] - views[0][0] == 2 * row
+
+
+def test_expert_views_rejects_bad_arguments():
+    lib = N.moe_lib()
+    out = (N.Matrix * 3)()
+    a = ctypes.addressof(out)
+    # BF16 takes no scales; MX formats need both scale tensors
+    assert lib.urb_expert_views(C.FMT_BF16, 1, 256, 128, 16, 16, 16, None, a) == N.ERR_ARGUMENT
+    assert lib.urb_expert_views(C.FMT_MXFP4, 1, 256, 128, 16, 16, 16, None, a) == N.ERR_ARGUMENT
+    assert lib.urb_expert_views(C.FMT_MXFP8, 1, 250, 128, 16, 16, 16, 16, a) == N.ERR_SHAPE
+    assert lib.urb_expert_views(C.FMT_BF16, 0, 256, 128, 16, None, 16, None, a) == N.ERR_ARGUMENT
+    assert lib.urb_expert_views(C.FMT_BF16, 1, 256, 128, 16, None, 16, None, a) == N.OK

@@ -795,6 +795,29 @@ urb_status urb_pack_matrix(urb_format format, const void* data, const uint8_t* s
   return URB_OK;
 }
 
+urb_status urb_expert_views(urb_format format, uint32_t n_experts, uint32_t hidden,
+                            uint32_t intermediate, const void* gate_up,
+                            const uint8_t* gate_up_scales, const void* down,
+                            const uint8_t* down_scales, urb_matrix* out) {
+  if (format != URB_FMT_BF16 && format != URB_FMT_MXFP4 && format != URB_FMT_MXFP8)
+    return URB_ERR_ARGUMENT;
+  const bool mx = format != URB_FMT_BF16;
+  if (!gate_up || !down || !out || n_experts == 0) return URB_ERR_ARGUMENT;
+  if (mx != (gate_up_scales != nullptr) || mx != (down_scales != nullptr)) return URB_ERR_ARGUMENT;
+  if (hidden == 0 || intermediate == 0 || hidden % 32 || intermediate % 32) return URB_ERR_SHAPE;
+  const size_t H = hidden, I = intermediate;
+  size_t gs, gd = matrix_bytes(format, I, H, &gs);  // one [I, H] half of an expert's [2I, H]
+  size_t ds, dd = matrix_bytes(format, H, I, &ds);
+  const uint8_t* gu = static_cast<const uint8_t*>(gate_up);
+  const uint8_t* dn = static_cast<const uint8_t*>(down);
+  for (size_t e = 0; e < n_experts; ++e) {
+    out[3 * e + 0] = urb_matrix{gu + e * 2 * gd, mx ? gate_up_scales + e * 2 * gs : nullptr};
+    out[3 * e + 1] = urb_matrix{gu + e * 2 * gd + gd, mx ? gate_up_scales + e * 2 * gs + gs : nullptr};
+    out[3 * e + 2] = urb_matrix{dn + e * dd, mx ? down_scales + e * ds : nullptr};
+  }
+  return URB_OK;
+}
+
 urb_status urb_moe_memory(const urb_moe_ctx* c, size_t* weight_bytes, size_t* workspace_bytes) {
   if (!c) return URB_ERR_ARGUMENT;
   if (weight_bytes) *weight_bytes = c->weight_bytes;

@@ -124,6 +124,26 @@ class DeviceLayer:
             bias = torch.from_numpy(np.ascontiguousarray(correction_bias, np.float32)).to(device)
         return DeviceLayer(spec, rw.view(torch.int16).view(E, H), ex, sh, bias, arena)
 
+    @staticmethod
+    def from_consolidated(spec: C.LayerSpec, router_weight, gate_up, gate_up_scales, down,
+                          down_scales, shared: Optional[List[Pair]] = None,
+                          correction_bias=None) -> "DeviceLayer":
+        """A layer over consolidated expert tensors, used in place: gate_up [E, 2I, H] (each
+        expert's gate rows, then its up rows) and down [E, H, I] in the on-disk layouts, scales
+        [E, 2I, H/32] and [E, H, I/32] for the MX formats (None for BF16) -- the Qwen3.6 packed
+        BF16 and Hy4 consolidated E4M3 + U8 checkpoints.  The per-expert views are the ones
+        ``urb_expert_views`` computes for C callers."""
+        E, I = spec.n_experts, spec.intermediate
+        if gate_up.shape[0] != E or gate_up.shape[1] != 2 * I or down.shape[0] != E:
+            raise ValueError("consolidated tensors do not match the layer geometry")
+        ex = []
+        for e in range(E):
+            gs = None if gate_up_scales is None else gate_up_scales[e, :I]
+            us = None if gate_up_scales is None else gate_up_scales[e, I:]
+            ds = None if down_scales is None else down_scales[e]
+            ex.append([(gate_up[e, :I], gs), (gate_up[e, I:], us), (down[e], ds)])
+        return DeviceLayer(spec, router_weight, ex, shared, correction_bias)
+
     def to_host(self, experts: Optional[List[int]] = None) -> C.HostLayer:
         """Copies (a subset of) the layer back to host memory for the CPU oracle."""
         def down(t):
@@ -234,6 +254,17 @@ class MoeLayer:
             self.close()
         except Exception:
             pass
+
+
+def expert_views(fmt: int, n_experts: int, hidden: int, intermediate: int, gate_up,
+                 gate_up_scales, down, down_scales) -> List[Tuple[int, Optional[int]]]:
+    """``urb_expert_views``: (data, scales) addresses of every expert's gate, up and down
+    inside consolidated tensors, in urb_moe_weights.experts order."""
+    out = (N.Matrix * (3 * n_experts))()
+    N.check(N.moe_lib().urb_expert_views(fmt, n_experts, hidden, intermediate, _ptr(gate_up),
+                                         _ptr(gate_up_scales), _ptr(down), _ptr(down_scales),
+                                         ctypes.addressof(out)), "urb_expert_views")
+    return [(m.data, m.scales) for m in out]
 
 
 def pack_matrix(fmt: int, data, scales, rows: int, cols: int):
