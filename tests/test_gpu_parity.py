@@ -398,11 +398,13 @@ def test_hy4_errors():
 
 
 @pytest.mark.parametrize("comp,T,E", [(C.COMPOSE_QWEN36, 40, 40), (C.COMPOSE_QWEN36, 600, 40),
-                                      (C.COMPOSE_QWEN36, 600, 248), (C.COMPOSE_DSV41, 777, 40)])
+                                      (C.COMPOSE_QWEN36, 600, 248), (C.COMPOSE_DSV41, 777, 40),
+                                      (C.COMPOSE_QWEN36, 64, 40), (C.COMPOSE_QWEN36, 300, 248),
+                                      (C.COMPOSE_DSV41, 512, 72)])
 def test_batched_lane8_router_is_bit_identical(comp, T, E):
-    # Batches of more than 512 tokens take the tiled 8-lane router (16 or 8 tokens per
-    # workgroup); its logits must equal the reference tree bit for bit, for partial token tiles
-    # and expert counts that are not multiples of 32 as well.
+    # From 64 tokens the tiled 8-lane router runs (one token per workgroup up to 512 tokens,
+    # then 16 or 8 tokens per workgroup); its logits must equal the reference tree bit for bit,
+    # for partial token tiles and expert counts that are not multiples of 32 as well.
     if comp == C.COMPOSE_QWEN36:
         spec = C.small_spec(C.WORKLOADS["c1_bf16_decode"].spec, hidden=640, n_experts=E,
                             intermediate=128)

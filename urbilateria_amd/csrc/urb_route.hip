@@ -728,7 +728,7 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int round_bf16, int* status, hipStream_t s) {
-  if (T <= 512) {
+  if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
     const size_t per_tok = (size_t)8 * (H / 8 + 4) * sizeof(float);
@@ -736,12 +736,16 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
                                                                      round_bf16, status);
     return;
   }
-  // ... which the tiled kernel divides by 8 or 16 tokens per streamed chain batch (it is bound
-  // by LDS reads of the staged activations instead: measured faster only for large batches,
-  // e.g. 1024 tokens x 384 experts x 7168 from 1.74 ms to 0.29 ms, while 128 x 128 x 2048 went
-  // from 14 to 28 us).
+  // ... and the tiled kernel shares each staged activation chunk between 32 experts' chains
+  // (one token per workgroup up to 512 tokens: measured on MI355X at 128 x 128 x 2048, 13.8 ->
+  // 11.8 us; 256 tokens 17.7 -> 14.2 us; slower below 64 tokens), and beyond 512 tokens divides
+  // the weight traffic by streaming each chain batch for 8 or 16 tokens (bound by LDS reads of
+  // the staged activations instead: 1024 tokens x 384 experts x 7168 from 1.74 ms to 0.29 ms).
   const int eg = (E + 31) / 32;
-  if ((long)eg * ((T + 15) / 16) >= 256)
+  if (T <= 512)
+    router_lane8_tiled_kernel<1><<<dim3(eg, T), 256, 0, s>>>(w8, E, H, x, T, logits, round_bf16,
+                                                             status);
+  else if ((long)eg * ((T + 15) / 16) >= 256)
     router_lane8_tiled_kernel<16><<<dim3(eg, (T + 15) / 16), 256, 0, s>>>(w8, E, H, x, T, logits,
                                                                         round_bf16, status);
   else
