@@ -158,6 +158,27 @@ urb_status urb_dequant_rows(urb_format format, const void *data, const uint8_t *
                             uint32_t rows, uint32_t cols, uint32_t row0, uint32_t count,
                             float *out, void *stream);
 
+/* The decoder layer's FFN block around the MoE call, for the QWEN36 composition
+ * (src/models/qwen3_6/runtime.rs:1053-1060 tokenwise, :1001-1019 batched):
+ *   n = bf16(zero_centered_rms_norm(h, norm_weight, eps)),  out = bf16(h + moe(n))
+ * h, out [tokens, H] (device, f32; out may alias h), norm_weight [H] (device, f32: the
+ * checkpoint's post_attention_layernorm offset, the scale being 1 + weight); ids / weights as
+ * urb_moe_forward.  The mean square is the reference's sequential f32 sum
+ * (src/models/qwen3_8/norm.rs:176-186), so the MoE sees the reference's inputs bit for bit.
+ * eps not finite or <= 0 -> URB_ERR_INVALID_GEOMETRY (NormError::InvalidEpsilon); non-finite
+ * h, norm_weight or results -> URB_ERR_NONFINITE at urb_moe_sync (NormError::NonFinite, the
+ * residual's "produced NaN or infinity"); other compositions -> URB_ERR_ARGUMENT. */
+urb_status urb_moe_forward_block(urb_moe_ctx *ctx, const float *h, const float *norm_weight,
+                                 float eps, uint32_t tokens, float *out, int32_t *ids,
+                                 float *weights, void *stream);
+
+/* zero_centered_rms_norm + round_runtime_bf16 of [rows, hidden] f32 rows (device; hidden % 4
+ * == 0 and <= 16384): the bit-exact parity hook of urb_moe_forward_block's first step
+ * (src/models/qwen3_8/norm.rs:38-52; src/models/qwen3_6/runtime.rs:1053-1057).  Inputs must be
+ * finite (the block call reports non-finite ones). */
+urb_status urb_zc_rms_norm_bf16(const float *x, const float *weight, uint32_t rows,
+                                uint32_t hidden, float eps, float *out, void *stream);
+
 /* simulate_e4m3_activation (src/math/mxfp.rs:82-115) of a [rows, cols] f32 matrix (device,
  * cols % 32 == 0) per 32-value block of each row, as the MX-activation mode feeds it to the
  * scaled MFMA: E4M3 codes [rows, cols] and E8M0 scales [rows, cols / 32] (device); the

@@ -363,3 +363,26 @@ def qwen_expert(triple, hidden: int, intermediate: int, x: np.ndarray,
     _check(_lib.urbo_qwen_expert(ctypes.addressof(mats), hidden, intermediate, _ptr(x),
                                  x.shape[0], _ptr(y), threads))
     return y
+
+
+def zc_rms_norm(x: np.ndarray, weight: np.ndarray, eps: float, round_bf16: bool = True) -> np.ndarray:
+    """zero_centered_rms_norm of every row of x [n, H], then (round_bf16) the Qwen3.6 runtime's
+    BF16 cast (src/models/qwen3_8/norm.rs:38-52; src/models/qwen3_6/runtime.rs:1053-1057)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    weight = np.ascontiguousarray(weight, dtype=np.float32)
+    out = np.empty_like(x)
+    _lib.urbo_zc_rms_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_size_t, ctypes.c_float, ctypes.c_int,
+                                      ctypes.c_void_p]
+    _check(_lib.urbo_zc_rms_norm(_ptr(x), _ptr(weight), x.shape[0], x.shape[1], float(eps),
+                                 int(round_bf16), _ptr(out)))
+    return out
+
+
+def add_residual_bf16(residual: np.ndarray, update: np.ndarray) -> np.ndarray:
+    """add_residual with BF16 activations (src/models/qwen3_6/runtime.rs:1470-1494)."""
+    out = np.array(residual, dtype=np.float32, copy=True, order="C")
+    update = np.ascontiguousarray(update, dtype=np.float32)
+    _lib.urbo_add_residual_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    _check(_lib.urbo_add_residual_bf16(_ptr(out), _ptr(update), out.size))
+    return out

@@ -713,6 +713,45 @@ int urbo_bounded_swiglu(const float *gate, const float *up, size_t n, float limi
 }
 
 // ==========================================================================================
+// The steps either side of the MoE call in the Qwen3.6 decoder layer.
+// ==========================================================================================
+// zero_centered_rms_norm (src/models/qwen3_8/norm.rs:38-52): validate (norm.rs:142-174),
+// inverse_rms (norm.rs:176-186: f32 fold of value * value from 0.0, divided by the length,
+// (mean_square + eps).sqrt().recip()), out = value * inverse * (1.0 + offset), finite check
+// (norm.rs:188-193); then the runtime's BF16 cast (qwen3_6/runtime.rs:1053-1057).
+int urbo_zc_rms_norm(const float *x, const float *weight, size_t n, size_t hidden, float eps,
+                     int round_bf16, float *out) {
+    if (hidden == 0) return URBO_SHAPE;
+    if (!(std::isfinite(eps) && eps > 0.0f)) return URBO_INVALID_GEOMETRY;
+    if (!all_finite(weight, hidden)) return URBO_NONFINITE;
+    for (size_t t = 0; t < n; ++t) {
+        const float *v = x + t * hidden;
+        float *o = out + t * hidden;
+        if (!all_finite(v, hidden)) return URBO_NONFINITE;
+        float sum = 0.0f;
+        for (size_t i = 0; i < hidden; ++i) sum = sum + v[i] * v[i];
+        const float mean_square = sum / (float)hidden;
+        const float inverse = 1.0f / std::sqrt(mean_square + eps);
+        if (!std::isfinite(inverse)) return URBO_NONFINITE;
+        for (size_t i = 0; i < hidden; ++i) o[i] = v[i] * inverse * (1.0f + weight[i]);
+        if (!all_finite(o, hidden)) return URBO_NONFINITE;
+        if (round_bf16) {
+            const int st = urbo_round_to_bf16_in_place(o, hidden);
+            if (st) return st;
+        }
+    }
+    return URBO_OK;
+}
+
+// add_residual (src/models/qwen3_6/runtime.rs:1470-1494) with bf16_activations.
+int urbo_add_residual_bf16(float *residual, const float *update, size_t n) {
+    for (size_t i = 0; i < n; ++i) residual[i] += update[i];
+    const int st = urbo_round_to_bf16_in_place(residual, n);
+    if (st) return st;
+    return all_finite(residual, n) ? URBO_OK : URBO_NONFINITE;
+}
+
+// ==========================================================================================
 // One MoE layer.  Tokens are routed first, then grouped by expert (the reference's
 // execute_batched_moe permutation, src/models/qwen3_6/runtime.rs:1123-1132: BTreeMap by
 // expert id, tokens in order); each group runs the batched projections, whose per-token

@@ -86,6 +86,18 @@ int urbo_set_mxfp8_fma_host(int fma_host);
  * * clamp(u, -L, L). */
 int urbo_bounded_swiglu(const float *gate, const float *up, size_t n, float limit, float *out);
 
+/* ---- the decoder layer's steps either side of the MoE call (Qwen3.6) ---- */
+/* zero_centered_rms_norm (src/models/qwen3_8/norm.rs:38-52, 142-193) of each of n rows [n, H],
+ * followed (round_bf16 != 0) by round_runtime_bf16 (src/models/qwen3_6/runtime.rs:1053-1057):
+ * mean square as the sequential f32 sum of x*x divided by H, inverse = 1 / sqrt(mean_square +
+ * eps), out = x * inverse * (1 + weight).  eps must be finite and > 0 (URBO_INVALID_GEOMETRY
+ * otherwise); non-finite input, weight, factor or output -> URBO_NONFINITE. */
+int urbo_zc_rms_norm(const float *x, const float *weight, size_t n, size_t hidden, float eps,
+                     int round_bf16, float *out);
+/* add_residual with BF16 activations (src/models/qwen3_6/runtime.rs:1470-1494): residual +=
+ * update in f32, rounded to BF16; non-finite -> URBO_NONFINITE. */
+int urbo_add_residual_bf16(float *residual, const float *update, size_t n);
+
 /* ---- one MoE layer ---- */
 typedef struct {
     const uint8_t *data;   /* BF16 LE bytes, packed E2M1 nibbles, or E4M3 bytes */

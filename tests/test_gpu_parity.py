@@ -534,6 +534,87 @@ def test_consolidated_checkpoint_layer_equals_per_expert_layer():
         b.close()
 
 
+# ------------------------------------------------- the Qwen3.6 FFN block around the MoE call
+def _block_inputs(T, H, seed):
+    rng = np.random.default_rng(seed)
+    h = (rng.standard_normal((T, H)) * np.exp2(rng.integers(-3, 4, (T, 1)))).astype(np.float32)
+    h = np.array([O.round_to_bf16(v) for v in h.ravel()], np.float32).reshape(T, H)
+    w = (rng.standard_normal(H) * 0.1).astype(np.float32)
+    return h, w
+
+
+@pytest.mark.parametrize("T,H", [(1, 128), (37, 2048), (3, 7168)])
+def test_zc_rms_norm_hook_is_bit_exact(T, H):
+    # the sequential f32 mean square of the reference, the 1 + weight scale and the BF16 cast
+    h, w = _block_inputs(T, H, 11 + H)
+    if T > 2:
+        h[1] = 1.0
+        h[1, 0] = 4096.0  # x0^2 absorbs every later square in a left-to-right f32 sum
+    got = moe_mod().zc_rms_norm_bf16(torch.from_numpy(h).cuda(), torch.from_numpy(w).cuda(),
+                                     1e-6).cpu().numpy()
+    ref = O.zc_rms_norm(h, w, 1e-6)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_forward_block_matches_oracle(T):
+    # out = bf16(h + moe(bf16(zero_centered_rms_norm(h)))): the normalized input is exact, so
+    # the router sees the reference's inputs and the routes agree exactly
+    host = _small_layer("c2_bf16_prefill")
+    spec = host.spec
+    h, w = _block_inputs(T, spec.hidden, 5 + T)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    hd, wd = torch.from_numpy(h).cuda(), torch.from_numpy(w).cuda()
+    out, ids, rw = layer.forward_block(hd, wd, 1e-6)
+    n = O.zc_rms_norm(h, w, 1e-6)
+    ref = _oracle(host, n)
+    want = O.add_residual_bf16(h, ref.output)
+    assert np.array_equal(ids.cpu().numpy(), ref.ids)
+    assert np.allclose(rw.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    err = rel_l2(out.cpu().numpy() - h, want - h)
+    assert err < REL_L2_BAR, err
+    # the block equals the plain call on the normalized input plus the BF16 residual step
+    y, _, _ = layer.forward(torch.from_numpy(n).cuda())
+    resid = O.add_residual_bf16(h, y.cpu().numpy())
+    assert np.array_equal(out.cpu().numpy(), resid)
+    # out may alias h
+    lib = N.moe_lib()
+    N.check(lib.urb_moe_forward_block(layer._ctx, hd.data_ptr(), wd.data_ptr(), 1e-6, T,
+                                      hd.data_ptr(), None, None, None))
+    layer.sync()
+    assert torch.equal(hd, out)
+    layer.close()
+
+
+def test_forward_block_errors():
+    host = _small_layer("c2_bf16_prefill")
+    layer = moe_mod().MoeLayer(host, max_tokens=4)
+    h, w = _block_inputs(4, host.spec.hidden, 9)
+    hd, wd = torch.from_numpy(h).cuda(), torch.from_numpy(w).cuda()
+    for eps in (0.0, -1.0, float("nan")):
+        with pytest.raises(N.UrbError) as e:
+            layer.forward_block(hd, wd, eps)
+        assert e.value.status == N.ERR_INVALID_GEOMETRY
+    bad = hd.clone()
+    bad[2, 3] = float("inf")
+    with pytest.raises(N.UrbError) as e:
+        layer.forward_block(bad, wd, 1e-6)
+    assert e.value.status == N.ERR_NONFINITE
+    wbad = wd.clone()
+    wbad[0] = float("nan")
+    with pytest.raises(N.UrbError) as e:
+        layer.forward_block(hd, wbad, 1e-6)
+    assert e.value.status == N.ERR_NONFINITE
+    out, _, _ = layer.forward_block(hd, wd, 1e-6)  # the latched error was cleared
+    assert torch.isfinite(out).all()
+    layer.close()
+    glm = moe_mod().MoeLayer(_small_layer("c3_mxfp4_decode"), max_tokens=4)
+    with pytest.raises(N.UrbError) as e:
+        glm.forward_block(hd, wd, 1e-6)
+    assert e.value.status == N.ERR_ARGUMENT
+    glm.close()
+
+
 # ------------------------------------------------------------------------------- errors
 def test_nonfinite_input_is_reported():
     for name in ("c1_bf16_decode", "c3_mxfp4_decode"):

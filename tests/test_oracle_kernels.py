@@ -725,3 +725,73 @@ def test_dsv41_layer_composition(fmt):
             acc = acc + ys[e]
         out = _bf16(acc + sh)
         assert np.array_equal(out.view(np.uint32), res.output[t].view(np.uint32))
+
+
+# ------------------------------------------------------- Qwen3.6 FFN-block steps around the MoE
+def test_zc_rms_norm_reference_kat():
+    # src/models/qwen3_8/norm.rs:205-211 (zero_centered_weight_is_an_offset_from_one)
+    out = O.zc_rms_norm(np.array([[3.0, 4.0]], np.float32), np.array([0.0, 1.0], np.float32),
+                        1e-6, round_bf16=False)[0]
+    inverse = np.float32(1.0) / np.sqrt(np.float32(12.5) + np.float32(1e-6))
+    assert abs(out[0] - 3.0 * inverse) < 1e-6
+    assert abs(out[1] - 8.0 * inverse) < 1e-6
+
+
+def test_zc_rms_norm_sums_squares_sequentially_in_f32():
+    # x0^2 = 2^24 absorbs every later 1.0 in a left-to-right f32 sum; a pairwise, f64 or
+    # reordered sum would see 2^24 + 127.  The mean is over all H values.
+    H = 128
+    x = np.ones((1, H), np.float32)
+    x[0, 0] = 4096.0
+    w = np.zeros(H, np.float32)
+    out = O.zc_rms_norm(x, w, 1e-6, round_bf16=False)[0]
+    seq_inv = np.float32(1.0) / np.sqrt(np.float32(2.0 ** 24 / H) + np.float32(1e-6))
+    wide_inv = np.float32(1.0) / np.sqrt(np.float32((2.0 ** 24 + H - 1) / H) + np.float32(1e-6))
+    assert seq_inv != wide_inv
+    assert out[1] == np.float32(seq_inv)
+    assert out[0] == np.float32(np.float32(4096.0) * seq_inv)
+
+
+def test_zc_rms_norm_unit_rows_closed_form():
+    # all-ones rows: mean square exactly 1, so out = (1 / sqrt(1 + eps)) * (1 + w), with the
+    # weight an offset from one (not the scale itself)
+    H = 256
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal(H) * 0.1).astype(np.float32)
+    out = O.zc_rms_norm(np.ones((3, H), np.float32), w, 1e-5, round_bf16=False)
+    inv = np.float32(1.0) / np.sqrt(np.float32(1.0) + np.float32(1e-5))
+    assert np.array_equal(out, np.broadcast_to(np.float32(inv) * (np.float32(1.0) + w), out.shape))
+
+
+def test_zc_rms_norm_bf16_cast_and_errors():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((5, 384)).astype(np.float32)
+    w = (rng.standard_normal(384) * 0.05).astype(np.float32)
+    plain = O.zc_rms_norm(x, w, 1e-6, round_bf16=False)
+    cast = O.zc_rms_norm(x, w, 1e-6)
+    assert np.array_equal(cast, np.array([O.round_to_bf16(v) for v in plain.ravel()],
+                                         np.float32).reshape(cast.shape))
+    for eps in (0.0, -1e-6, float("nan"), float("inf")):
+        with pytest.raises(O.OracleError) as e:
+            O.zc_rms_norm(x, w, eps)
+        assert e.value.status == 4  # InvalidEpsilon -> invalid geometry
+    bad = x.copy()
+    bad[2, 7] = np.nan
+    with pytest.raises(O.OracleError) as e:
+        O.zc_rms_norm(bad, w, 1e-6)
+    assert e.value.status == 3
+    wbad = w.copy()
+    wbad[0] = np.inf
+    with pytest.raises(O.OracleError) as e:
+        O.zc_rms_norm(x, wbad, 1e-6)
+    assert e.value.status == 3
+
+
+def test_add_residual_bf16():
+    # f32 add, then RNE to BF16: 1 + 2^-9 rounds to 1, 1 + 3 * 2^-9 to 1 + 2^-7
+    out = O.add_residual_bf16(np.array([1.0, 1.0, -2.0], np.float32),
+                              np.array([2.0 ** -9, 3 * 2.0 ** -9, 0.5], np.float32))
+    assert np.array_equal(out, np.array([1.0, 1.0 + 2.0 ** -7, -1.5], np.float32))
+    with pytest.raises(O.OracleError) as e:
+        O.add_residual_bf16(np.array([3.0e38], np.float32), np.array([3.0e38], np.float32))
+    assert e.value.status == 3

@@ -253,7 +253,7 @@ __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
     const ExpertMats* __restrict__ mats, const int32_t* __restrict__ ids,
     const float* __restrict__ w, const int32_t* __restrict__ asc, int K, int H, int I,
     const float* __restrict__ act, const float* __restrict__ shared, int comp, Epi epi,
-    float* __restrict__ out, int* status) {
+    const float* __restrict__ residual, float* __restrict__ out, int* status) {
   extern __shared__ float xs[];  // K x xs_floats(I) staged activations, then [K][16] sums
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lq = lane >> 4;
@@ -340,6 +340,11 @@ __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
       }
       res = acc;
     }
+    if (residual) {
+      // add_residual with BF16 activations (src/models/qwen3_6/runtime.rs:1470-1494)
+      const float t = residual[row] + res;
+      if (!rne_bf16(t, &res)) { bad = true; res = t; }
+    }
     out[row] = res;
     if (bad) flag(status, kStatusNonFinite);
   }
@@ -358,7 +363,7 @@ bool down_combine_fits(int K, int I) { return K <= 32 && down_combine_lds(K, I) 
 bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                               const float* weights, const int32_t* asc, int K, int H, int I,
                               const float* act, const float* shared, int comp, Epi epi,
-                              float* out, int* status, hipStream_t s) {
+                              float* out, int* status, hipStream_t s, const float* residual) {
   if (!down_combine_fits(K, I)) return false;
   const size_t lds = down_combine_lds(K, I);
   const dim3 grid(H / kPanelRows), block(64 * std::min(K, 8));
@@ -367,7 +372,7 @@ bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* id
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFusedLdsBytes);
     kernel<<<grid, block, lds, s>>>(mats, ids, weights, asc, K, H, I, act, shared, comp, epi,
-                                    out, status);
+                                    residual, out, status);
   };
   if (fmt == kFmtBF16) go(gemv_down_combine_kernel<kFmtBF16, 1>);
   else if (fmt == kFmtMXFP4) go(gemv_down_combine_kernel<kFmtMXFP4, 2>);
@@ -388,6 +393,7 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
                                                            const float* __restrict__ w,
                                                            const int32_t* __restrict__ asc,
                                                            int T, int K, int H,
+                                                           const float* __restrict__ res,
                                                            float* __restrict__ out,
                                                            int* status) {
   const int h4 = blockIdx.x * blockDim.x + threadIdx.x;
@@ -420,6 +426,16 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
         const float s = acc[u] + c;
         if (!rne_bf16(s, &acc[u])) { bad = true; acc[u] = s; }
       }
+    }
+  }
+  if (res) {
+    // add_residual with BF16 activations (src/models/qwen3_6/runtime.rs:1470-1494)
+    const float4 r4 = reinterpret_cast<const float4*>(res + (size_t)t * H)[h4];
+    const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float s = rr[u] + acc[u];
+      if (!rne_bf16(s, &acc[u])) { bad = true; acc[u] = s; }
     }
   }
   if (bad) flag(status, kStatusNonFinite);
@@ -467,14 +483,14 @@ __global__ __launch_bounds__(256) void combine_glm_kernel(const float* __restric
 
 void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                          const int32_t* asc, int T, int K, int H, float* out, int* status,
-                         hipStream_t s) {
+                         hipStream_t s, const float* residual) {
   dim3 grid((H / 4 + 255) / 256, T);
   if (K <= 8)
-    combine_qwen_kernel<8><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H, out,
-                                                status);
+    combine_qwen_kernel<8><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H,
+                                                residual, out, status);
   else
-    combine_qwen_kernel<32><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H, out,
-                                                 status);
+    combine_qwen_kernel<32><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H,
+                                                 residual, out, status);
 }
 
 void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,

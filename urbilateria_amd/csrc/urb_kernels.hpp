@@ -130,14 +130,18 @@ void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max
 // down_combine_fits (the k activation rows fit the kernel's LDS budget); returns false and
 // launches nothing otherwise.
 bool down_combine_fits(int K, int I);
+// With `residual` [H] (not null), out = bf16(residual + combined) (the decoder layer's
+// residual add with BF16 activations).
 bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                               const float* weights, const int32_t* asc, int K, int H, int I,
                               const float* act, const float* shared, int comp, Epi epi,
-                              float* out, int* status, hipStream_t s);
-// Combines: Qwen BF16 ascending-id, GLM f64 ranking order.
+                              float* out, int* status, hipStream_t s,
+                              const float* residual = nullptr);
+// Combines: Qwen BF16 ascending-id, GLM f64 ranking order.  Qwen with `residual` [T, H] (not
+// null): out = bf16(residual + combined).
 void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                          const int32_t* asc, int T, int K, int H, float* out, int* status,
-                         hipStream_t s);
+                         hipStream_t s, const float* residual = nullptr);
 void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                         const float* shared, int T, int K, int H, float* out, hipStream_t s);
 // MX-activation mode (Hy4 composition).  simulate_e4m3_activation (src/math/mxfp.rs:89-115)
@@ -155,6 +159,11 @@ void launch_quantize(const float* x, size_t rows, size_t cols, float* values, ui
 void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                         const int32_t* asc, const float* shared, int T, int K, int H,
                         float* out, int* status, hipStream_t s);
+// zero_centered_rms_norm + BF16 cast of T rows [T, H] (H % 4 == 0, H <= 16384), exact to the
+// reference's sequential f32 mean square; non-finite input, weight, factor or output set
+// kStatusNonFinite in `status` (may be null).
+void launch_rms_norm(const float* h, const float* weight, int T, int H, float eps, float* out,
+                     int* status, hipStream_t s);
 // Payload validation: bit 1 = non-finite BF16 / E4M3 NaN code, bit 2 = E8M0 0xFF.
 void launch_validate(int fmt, const uint8_t* data, size_t data_bytes, const uint8_t* scales,
                      size_t scale_bytes, int* flags, hipStream_t s);

@@ -46,6 +46,7 @@ struct Workspace {
   float* shared_act = nullptr;
   float* shared_out = nullptr;
   float* xq = nullptr;  // HY4: the simulated E4M3 token activations [chunk, H]
+  float* xn = nullptr;  // QWEN36 block calls: the normalized BF16 token activations [chunk, H]
   int* status = nullptr;  // [0] latched numerical failures, [1] validation flags
 };
 
@@ -241,6 +242,7 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   w.shared_out = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_HY4 || d.composition == URB_COMPOSE_DSV41)
     w.xq = b.take<float>(C * H);
+  if (d.composition == URB_COMPOSE_QWEN36) w.xn = b.take<float>(C * H);
 }
 
 static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
@@ -584,9 +586,15 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, int n, float* yc, 
   return URB_OK;
 }
 
-urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, float* y,
-                           int32_t* ids, float* weights, void* stream) {
-  if (!c || !x || !y) return URB_ERR_ARGUMENT;
+// The decoder layer's steps either side of the MoE call (urb_moe_forward_block).
+struct BlockArgs {
+  const float* norm_weight;
+  float eps;
+};
+
+static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, float* y,
+                               int32_t* ids, float* weights, void* stream,
+                               const BlockArgs* blk) {
   if (tokens == 0 || tokens > c->desc.max_tokens) return URB_ERR_SHAPE;
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
@@ -601,6 +609,14 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     const int n = (int)std::min<uint32_t>(c->chunk, tokens - c0);
     const float* xc = x + (size_t)c0 * H;
     float* yc = y + (size_t)c0 * H;
+    // block calls: x is the residual stream; the MoE reads its normalized BF16 form and the
+    // combine adds the residual back
+    const float* resid = nullptr;
+    if (blk) {
+      resid = xc;
+      urb::launch_rms_norm(xc, blk->norm_weight, n, H, blk->eps, ws.xn, ws.status, s);
+      xc = ws.xn;
+    }
     int32_t* idc = ids ? ids + (size_t)c0 * K : ws.ids;
     float* wc = weights ? weights + (size_t)c0 * K : ws.weights;
     if (d.composition == URB_COMPOSE_HY4 || d.composition == URB_COMPOSE_DSV41) {
@@ -665,7 +681,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
         Span span(c, URB_STAGE_DOWN, s);
         urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
                                       ws.act, has_shared ? ws.shared_out : nullptr,
-                                      qwen ? 0 : 1, epi, yc, ws.status, s);
+                                      qwen ? 0 : 1, epi, yc, ws.status, s, resid);
       }
       if (c->profiling) {
         urb_status st = collect_spans(c);
@@ -686,7 +702,7 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
     {
       Span span(c, URB_STAGE_COMBINE, s);
       if (qwen)
-        urb::launch_combine_qwen(ws.y_perm, pos, wc, ws.asc, n, K, H, yc, ws.status, s);
+        urb::launch_combine_qwen(ws.y_perm, pos, wc, ws.asc, n, K, H, yc, ws.status, s, resid);
       else
         urb::launch_combine_glm(ws.y_perm, pos, wc, has_shared ? ws.shared_out : nullptr, n, K,
                                 H, yc, s);
@@ -696,6 +712,33 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
       if (st) return st;
     }
   }
+  URB_HIP(hipGetLastError());
+  return URB_OK;
+}
+
+urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, float* y,
+                           int32_t* ids, float* weights, void* stream) {
+  if (!c || !x || !y) return URB_ERR_ARGUMENT;
+  return forward_impl(c, x, tokens, y, ids, weights, stream, nullptr);
+}
+
+urb_status urb_moe_forward_block(urb_moe_ctx* c, const float* h, const float* norm_weight,
+                                 float eps, uint32_t tokens, float* out, int32_t* ids,
+                                 float* weights, void* stream) {
+  if (!c || !h || !norm_weight || !out) return URB_ERR_ARGUMENT;
+  if (c->desc.composition != URB_COMPOSE_QWEN36) return URB_ERR_ARGUMENT;
+  if (!finite_host(eps) || !(eps > 0.0f)) return URB_ERR_INVALID_GEOMETRY;
+  const BlockArgs blk{norm_weight, eps};
+  return forward_impl(c, h, tokens, out, ids, weights, stream, &blk);
+}
+
+urb_status urb_zc_rms_norm_bf16(const float* x, const float* weight, uint32_t rows,
+                                uint32_t hidden, float eps, float* out, void* stream) {
+  if (!x || !weight || !out) return URB_ERR_ARGUMENT;
+  if (rows == 0 || hidden == 0 || hidden % 4 || hidden > 16384) return URB_ERR_SHAPE;
+  if (!finite_host(eps) || !(eps > 0.0f)) return URB_ERR_INVALID_GEOMETRY;
+  urb::launch_rms_norm(x, weight, (int)rows, (int)hidden, eps, out, nullptr,
+                       static_cast<hipStream_t>(stream));
   URB_HIP(hipGetLastError());
   return URB_OK;
 }

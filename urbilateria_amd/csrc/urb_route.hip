@@ -407,7 +407,7 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
         const float l1 = (float)log1p((double)ex);
         sp = x > 0.0f ? __fadd_rn(x, l1) : l1;
       }
-      score[i] = open[i] ? __fsqrt_rn(sp) : 0.0f;
+      score[i] = open[i] ? sqrtf(sp) : 0.0f;  // correctly rounded (not the native root)
       const float b = (open[i] && rp.bias) ? rp.bias[e] : 0.0f;
       key[i] = total_key(__fadd_rn(score[i], b));
     }

@@ -219,6 +219,19 @@ class MoeLayer:
         self.sync()
         return y, ids, w
 
+    def forward_block(self, h: "torch.Tensor", norm_weight: "torch.Tensor", eps: float):
+        """The Qwen3.6 decoder layer's FFN block around this MoE layer (``urb_moe_forward_block``):
+        h [T, H] residual stream -> (bf16(h + moe(bf16(rmsnorm(h)))), ids, weights)."""
+        T = h.shape[0]
+        out = torch.empty((T, self.spec.hidden), dtype=torch.float32, device=h.device)
+        ids = torch.empty((T, self.spec.top_k), dtype=torch.int32, device=h.device)
+        w = torch.empty((T, self.spec.top_k), dtype=torch.float32, device=h.device)
+        N.check(N.moe_lib().urb_moe_forward_block(self._ctx, _ptr(h), _ptr(norm_weight),
+                                                  float(eps), T, _ptr(out), _ptr(ids), _ptr(w),
+                                                  _stream_handle()), "urb_moe_forward_block")
+        self.sync()
+        return out, ids, w
+
     def route(self, x: "torch.Tensor"):
         T = x.shape[0]
         logits = torch.empty((T, self.spec.n_experts), dtype=torch.float32, device=x.device)
@@ -274,6 +287,16 @@ def pack_matrix(fmt: int, data, scales, rows: int, cols: int):
     N.check(N.moe_lib().urb_pack_matrix(fmt, _ptr(data), _ptr(scales), rows, cols, _ptr(pd),
                                         _ptr(ps), _stream_handle()), "urb_pack_matrix")
     return pd, ps
+
+
+def zc_rms_norm_bf16(x, weight, eps: float):
+    """``urb_zc_rms_norm_bf16``: bf16(zero_centered_rms_norm(x, weight, eps)) of x [rows, H]."""
+    out = torch.empty_like(x)
+    N.check(N.moe_lib().urb_zc_rms_norm_bf16(_ptr(x), _ptr(weight), x.shape[0], x.shape[1],
+                                             float(eps), _ptr(out), _stream_handle()),
+            "urb_zc_rms_norm_bf16")
+    torch.cuda.synchronize()
+    return out
 
 
 def quantize_e4m3(x):
