@@ -112,11 +112,12 @@ def cpu_baseline(name, spec, C, dev, x, budget_s, threads):
     T = x.shape[0]
     host = dev.to_host()
     xs = x.cpu().numpy()
+    # warm pool and page cache
     O.moe_forward(spec, host.experts, host.router_weight, xs[:1], host.correction_bias,
-                  host.shared, threads=threads)  # warm pool and page cache
+                  host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate)
     t0 = time.perf_counter()
     O.moe_forward(spec, host.experts, host.router_weight, xs[:1], host.correction_bias,
-                  host.shared, threads=threads)
+                  host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate)
     one = time.perf_counter() - t0
     # tokens per call: the whole batch when a call fits the budget, else a prefix that does;
     # whole calls repeat until the budget is spent
@@ -125,7 +126,7 @@ def cpu_baseline(name, spec, C, dev, x, budget_s, threads):
     t0 = time.perf_counter()
     while True:
         O.moe_forward(spec, host.experts, host.router_weight, xs[:n], host.correction_bias,
-                      host.shared, threads=threads)
+                      host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate)
         reps += 1
         if time.perf_counter() - t0 >= budget_s or reps >= 5000:
             break

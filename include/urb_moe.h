@@ -45,7 +45,10 @@ typedef enum {
 /* Which adapter's layer call the context reproduces:
  *  QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243):
  *          BF16 router GEMV (FP32, 8-lane tree) + BF16 logits, BF16 route weights, BF16
- *          boundaries inside experts and in the ascending-expert-id combine.
+ *          boundaries inside experts and in the ascending-expert-id combine; with a shared
+ *          expert (BF16, shared_intermediate > 0) finish_ordered_moe (:1417-1468): the shared
+ *          expert's output scaled by bf16(sigmoid(shared_expert_gate . x)) and added last, in
+ *          BF16.
  *  GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176): f64 router GEMV,
  *          GatedMlp experts, f64 combine in ranking order on top of the shared expert.
  *  HY4:    the MX-activation mode, Hy4 MoeWeights::forward (src/models/hy4/runtime.rs:
@@ -100,7 +103,7 @@ typedef struct {
   uint32_t n_experts;            /* E */
   uint32_t top_k;                /* k */
   uint32_t intermediate;         /* I of each routed expert */
-  uint32_t shared_intermediate;  /* I of the always-on shared expert, 0 = none (not QWEN36) */
+  uint32_t shared_intermediate;  /* I of the always-on shared expert, 0 = none */
   urb_format expert_format;
   urb_format shared_format;
   urb_router router;
@@ -117,6 +120,10 @@ typedef struct {
   const float *correction_bias;    /* [E] f32 selection bias (noaux_tc), NULL = zeros */
   const urb_matrix *experts;       /* [E * 3]: gate [I, H], up [I, H], down [H, I] */
   const urb_matrix *shared;        /* [3] or NULL */
+  /* QWEN36 with a shared expert: mlp.shared_expert_gate [1, H] BF16, the sigmoid gate of the
+   * shared expert's contribution (finish_ordered_moe, src/models/qwen3_6/runtime.rs:1417-1468);
+   * NULL otherwise. */
+  const uint16_t *shared_expert_gate;
 } urb_moe_weights;
 
 typedef struct urb_moe_ctx urb_moe_ctx;

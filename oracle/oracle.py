@@ -226,6 +226,7 @@ class _Layer(ctypes.Structure):
         ("router_weight", ctypes.c_void_p), ("correction_bias", ctypes.c_void_p),
         ("experts", ctypes.c_void_p), ("shared", ctypes.c_void_p),
         ("swiglu_limit", ctypes.c_float),
+        ("shared_expert_gate", ctypes.c_void_p),
     ]
 
 
@@ -239,7 +240,7 @@ class OracleResult:
 
 def moe_forward(spec, experts: Sequence, router_weight: np.ndarray, x: np.ndarray,
                 correction_bias: Optional[np.ndarray] = None, shared: Optional[Sequence] = None,
-                threads: int = 1) -> OracleResult:
+                threads: int = 1, shared_expert_gate: Optional[np.ndarray] = None) -> OracleResult:
     """Runs one layer.  ``spec`` carries the layer geometry (attributes hidden, n_experts,
     top_k, intermediate, shared_intermediate, expert_format, shared_format, router, composition,
     n_group, topk_group, normalize, routed_scaling_factor, swiglu_limit).  ``experts[e]`` is a triple of
@@ -265,12 +266,13 @@ def moe_forward(spec, experts: Sequence, router_weight: np.ndarray, x: np.ndarra
             sh[m] = _Matrix(_ptr(d), _ptr(s))
     rwt = np.ascontiguousarray(router_weight)
     bias = None if correction_bias is None else np.ascontiguousarray(correction_bias, np.float32)
+    sgate = None if shared_expert_gate is None else np.ascontiguousarray(shared_expert_gate)
     layer = _Layer(H, E, K, spec.intermediate, spec.shared_intermediate, spec.expert_format,
                    spec.shared_format, spec.router, spec.composition, spec.n_group,
                    spec.topk_group, int(spec.normalize), float(spec.routed_scaling_factor),
                    _ptr(rwt), _ptr(bias), ctypes.addressof(mats),
                    None if sh is None else ctypes.addressof(sh),
-                   float(getattr(spec, "swiglu_limit", 0.0)))
+                   float(getattr(spec, "swiglu_limit", 0.0)), _ptr(sgate))
     y = np.empty((T, H), np.float32)
     ids = np.empty((T, K), np.int32)
     w = np.empty((T, K), np.float32)

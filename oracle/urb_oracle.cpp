@@ -932,7 +932,9 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
     const bool dsv = L->composition == URBO_COMPOSE_DSV41;
     const bool hy4 = L->composition == URBO_COMPOSE_HY4;
     const bool mxa = hy4 || dsv;  // the MX-activation compositions
-    if (qwen && (L->expert_format != URBO_FMT_BF16 || L->shared_intermediate != 0))
+    if (qwen && (L->expert_format != URBO_FMT_BF16 ||
+                 (L->shared_intermediate &&
+                  (L->shared_format != URBO_FMT_BF16 || !L->shared_expert_gate || !L->shared))))
         return URBO_SHAPE;
     if (mxa && (L->expert_format == URBO_FMT_BF16 ||
                 (L->shared_intermediate && L->shared_format == URBO_FMT_BF16)))
@@ -1036,6 +1038,36 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
                     if (!rne_bf16(w * v[h], &c)) return URBO_NONFINITE;
                     float acc = yt[h] + c;
                     if (!rne_bf16(acc, &yt[h])) return URBO_NONFINITE;
+                }
+            }
+        }
+        if (L->shared_intermediate) {
+            // finish_ordered_moe (qwen3_6/runtime.rs:1417-1468; batched :1169-1211): the shared
+            // Qwen38Expert, its gate linear(shared_expert_gate) (FP32 GEMV + BF16), scale =
+            // bf16(sigmoid(gate)) in the two-branch form, acc = bf16(acc + bf16(scale * s)).
+            const size_t Is = L->shared_intermediate;
+            std::vector<float> sh((size_t)T * H), gate(T);
+            st = qwen_expert(p, L->shared, H, Is, x, T, sh.data());
+            if (st) return st;
+            st = qwen_linear(p, (const uint8_t *)L->shared_expert_gate, 1, H, x, T, gate.data());
+            if (st) return st;
+            for (size_t t = 0; t < T; ++t) {
+                const float g = gate[t];
+                if (!std::isfinite(g)) return URBO_NONFINITE;
+                float scale;
+                if (g >= 0.0f) {
+                    scale = 1.0f / (1.0f + ::expf(-g));
+                } else {
+                    const float e = ::expf(g);
+                    scale = e / (1.0f + e);
+                }
+                if (!rne_bf16(scale, &scale)) return URBO_NONFINITE;
+                float *yt = y + t * H;
+                const float *s = &sh[t * H];
+                for (size_t h = 0; h < H; ++h) {
+                    float c;
+                    if (!rne_bf16(scale * s[h], &c)) return URBO_NONFINITE;
+                    if (!rne_bf16(yt[h] + c, &yt[h])) return URBO_NONFINITE;
                 }
             }
         }

@@ -115,6 +115,7 @@ typedef struct {
     const urbo_matrix *experts;    /* [E][3] = gate [I,H], up [I,H], down [H,I] */
     const urbo_matrix *shared;     /* [3] or NULL */
     float swiglu_limit;            /* HY4, DSV41: bounded SwiGLU limit */
+    const uint16_t *shared_expert_gate; /* QWEN36 with a shared expert: [H] BF16 gate row */
 } urbo_layer;
 
 /* Hy4 MX-activation experts over n tokens [n, H] -> [n, H] (x is quantized here):

@@ -34,7 +34,8 @@ def moe_mod():
 
 def _oracle(host: C.HostLayer, x: np.ndarray, threads: int = 4):
     return O.moe_forward(host.spec, host.experts, host.router_weight, x, host.correction_bias,
-                         host.shared, threads=threads)
+                         host.shared, threads=threads,
+                         shared_expert_gate=host.shared_expert_gate)
 
 
 def _scores(spec, res, bias):
@@ -532,6 +533,54 @@ def test_consolidated_checkpoint_layer_equals_per_expert_layer():
             assert torch.equal(y1, y2) and torch.equal(i1, i2) and torch.equal(w1, w2)
         a.close()
         b.close()
+
+
+# ------------------------------------------------ Qwen3.6 with its sigmoid-gated shared expert
+def _qwen_shared_layer(hidden=256, n_experts=16, intermediate=128):
+    spec = replace(C.small_spec(C.WORKLOADS["c2_bf16_prefill"].spec, hidden=hidden,
+                                n_experts=n_experts, intermediate=intermediate),
+                   shared_intermediate=intermediate, shared_format=C.FMT_BF16)
+    return C.make_host_layer(spec)
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_qwen_gated_shared_expert_matches_oracle(T):
+    # T = 1 takes the fused down+combine kernel, T > 1 the grouped GEMMs and combine kernel;
+    # the gate logit is the router's 8-lane tree, so routes and gates agree exactly
+    host = _qwen_shared_layer()
+    x = synth.activations(f"x.qsh.{T}", T, host.spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y, ids, w = layer.forward(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert np.array_equal(ids.cpu().numpy(), ref.ids)
+    assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    err = rel_l2(y.cpu().numpy(), ref.output)
+    assert err < REL_L2_BAR, err
+    # the FFN block over the same layer
+    h, nw = _block_inputs(T, host.spec.hidden, 21 + T)
+    out, bids, _ = layer.forward_block(torch.from_numpy(h).cuda(), torch.from_numpy(nw).cuda(),
+                                       1e-6)
+    bref = _oracle(host, O.zc_rms_norm(h, nw, 1e-6))
+    assert np.array_equal(bids.cpu().numpy(), bref.ids)
+    want = O.add_residual_bf16(h, bref.output)
+    assert rel_l2(out.cpu().numpy() - h, want - h) < REL_L2_BAR
+    layer.close()
+
+
+def test_qwen_shared_expert_needs_its_gate_and_bf16():
+    host = _qwen_shared_layer()
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(replace(host, shared_expert_gate=None), max_tokens=2)
+    assert e.value.status == N.ERR_ARGUMENT
+    spec = replace(host.spec, shared_format=C.FMT_MXFP4)
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(C.make_host_layer(spec), max_tokens=2)
+    assert e.value.status == N.ERR_ARGUMENT
+    bad = host.shared_expert_gate.copy()
+    bad[3] = 0x7F80  # +inf
+    with pytest.raises(N.UrbError) as e:
+        moe_mod().MoeLayer(replace(host, shared_expert_gate=bad), max_tokens=2)
+    assert e.value.status == N.ERR_NONFINITE
 
 
 # ------------------------------------------------- the Qwen3.6 FFN block around the MoE call

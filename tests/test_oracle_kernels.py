@@ -795,3 +795,54 @@ def test_add_residual_bf16():
     with pytest.raises(O.OracleError) as e:
         O.add_residual_bf16(np.array([3.0e38], np.float32), np.array([3.0e38], np.float32))
     assert e.value.status == 3
+
+
+# --------------------------------------------- Qwen3.6 / Qwen3.8 sigmoid-gated shared expert
+def _qwen_shared_layer(H=128, E=8, I=128, k=3):
+    spec = replace(C.small_spec(C.WORKLOADS["c1_bf16_decode"].spec, hidden=H, n_experts=E,
+                                intermediate=I, top_k=k),
+                   shared_intermediate=I, shared_format=C.FMT_BF16)
+    return C.make_host_layer(spec)
+
+
+def _sigmoid_two_branch(g: np.float32) -> np.float32:
+    # qwen3_8/moe.rs:409-417, in f32 with a correctly rounded exp
+    if g >= 0:
+        return np.float32(np.float32(1.0) / (np.float32(1.0) + np.float32(np.exp(-np.float64(g)))))
+    e = np.float32(np.exp(np.float64(g)))
+    return np.float32(e / (np.float32(1.0) + e))
+
+
+def test_qwen_shared_expert_is_added_last_with_a_bf16_sigmoid_scale():
+    # finish_ordered_moe (qwen3_6/runtime.rs:1417-1468), the same steps as Qwen38Moe::forward
+    # (qwen3_8/moe.rs:330-395, KAT :467-490 on unrounded weights): the routed BF16 sum first,
+    # then c = bf16(bf16(sigmoid(bf16(gate . x))) * shared(x)), acc = bf16(acc + c).  Built
+    # from the separately pinned routed layer, Qwen expert and 8-lane FP32 linear.
+    layer = _qwen_shared_layer()
+    spec = layer.spec
+    x = synth.activations("x.qshared", 6, spec.hidden)
+    with_shared = O.moe_forward(spec, layer.experts, layer.router_weight, x, None, layer.shared,
+                                shared_expert_gate=layer.shared_expert_gate)
+    routed = O.moe_forward(replace(spec, shared_intermediate=0), layer.experts,
+                           layer.router_weight, x)
+    assert np.array_equal(with_shared.ids, routed.ids)
+    s = O.qwen_expert(layer.shared, spec.hidden, spec.shared_intermediate, x)
+    gates = []
+    for t in range(x.shape[0]):
+        g = O.bf16_matvec_rows_fp32(layer.shared_expert_gate, 1, spec.hidden, x[t])[0]
+        g = O.round_to_bf16(g)
+        gates.append(g)
+        scale = O.round_to_bf16(_sigmoid_two_branch(np.float32(g)))
+        want = np.array([O.round_to_bf16(routed.output[t, h] +
+                                         O.round_to_bf16(np.float32(scale * s[t, h])))
+                         for h in range(spec.hidden)], np.float32)
+        assert np.array_equal(with_shared.output[t], want)
+    assert min(gates) < 0 < max(gates)  # both sigmoid branches
+
+
+def test_qwen_shared_expert_requires_bf16_and_its_gate():
+    layer = _qwen_shared_layer()
+    x = synth.activations("x.qshared.err", 2, layer.spec.hidden)
+    with pytest.raises(O.OracleError) as e:
+        O.moe_forward(layer.spec, layer.experts, layer.router_weight, x, None, layer.shared)
+    assert e.value.status == 1

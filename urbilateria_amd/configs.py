@@ -184,6 +184,7 @@ class HostLayer:
     experts: List[List[Tuple[np.ndarray, Optional[np.ndarray]]]]  # [E][gate, up, down]
     shared: Optional[List[Tuple[np.ndarray, Optional[np.ndarray]]]] = None
     correction_bias: Optional[np.ndarray] = None     # [E] f32
+    shared_expert_gate: Optional[np.ndarray] = None  # [H] uint16 BF16 (QWEN36 shared expert)
 
 
 def _matrix(fmt: int, name: str, rows: int, cols: int, base_seed: int):
@@ -215,7 +216,10 @@ def make_host_layer(spec: LayerSpec, base_seed: int = synth.BASE_SEED,
             _matrix(spec.shared_format, "shared.up", Is, H, base_seed),
             _matrix(spec.shared_format, "shared.down", H, Is, base_seed),
         ]
-    return HostLayer(spec, router, experts, shared, bias)
+    gate = None
+    if spec.shared_intermediate and spec.composition == COMPOSE_QWEN36:
+        gate = synth.bf16_matrix("shared.expert_gate", 1, H, 0.02, base_seed).reshape(H)
+    return HostLayer(spec, router, experts, shared, bias, gate)
 
 
 def zipf_bias(n_experts: int, s: float, beta: float, base_seed: int = synth.BASE_SEED) -> np.ndarray:

@@ -76,6 +76,29 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + exp_f32(-v))
 
 __device__ __forceinline__ void flag(int* status, int bits) { atomicOr(status, bits); }
 
+// Qwen3.6's shared-expert scale (finish_ordered_moe, src/models/qwen3_6/runtime.rs:1436-1448):
+// sigmoid of the gate logit in the two-branch form, rounded to BF16; `bad` on a non-finite gate
+// or scale.
+__device__ __forceinline__ float qwen_shared_scale(float g, bool& bad) {
+  if (!finite(g)) {
+    bad = true;
+    return 0.0f;
+  }
+  float s;
+  if (g >= 0.0f) {
+    s = 1.0f / (1.0f + exp_f32(-g));
+  } else {
+    const float e = exp_f32(g);
+    s = e / (1.0f + e);
+  }
+  float r;
+  if (!rne_bf16(s, &r)) {
+    bad = true;
+    return s;
+  }
+  return r;
+}
+
 // Wave64 reductions through cross-lane shuffles.
 __device__ __forceinline__ float wave_sum_f32(float v, int width = kWave) {
   for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, width);

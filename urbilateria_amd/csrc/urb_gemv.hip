@@ -253,7 +253,8 @@ __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
     const ExpertMats* __restrict__ mats, const int32_t* __restrict__ ids,
     const float* __restrict__ w, const int32_t* __restrict__ asc, int K, int H, int I,
     const float* __restrict__ act, const float* __restrict__ shared, int comp, Epi epi,
-    const float* __restrict__ residual, float* __restrict__ out, int* status) {
+    const float* __restrict__ residual, const float* __restrict__ gate, float* __restrict__ out,
+    int* status) {
   extern __shared__ float xs[];  // K x xs_floats(I) staged activations, then [K][16] sums
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int ln = lane & 15, lq = lane >> 4;
@@ -332,6 +333,14 @@ __global__ __launch_bounds__(512) void gemv_down_combine_kernel(
           acc = acc + v;  // DeepSeek V4.1 (deepseek_v41/runtime.rs:1995-1998): weight applied
         }
       }
+      if (comp == 0 && shared) {
+        // the gated shared expert (src/models/qwen3_6/runtime.rs:1436-1461)
+        const float sc = qwen_shared_scale(gate[0], bad);
+        float c;
+        if (!rne_bf16(sc * shared[row], &c)) { bad = true; c = sc * shared[row]; }
+        const float t = acc + c;
+        if (!rne_bf16(t, &acc)) { bad = true; acc = t; }
+      }
       if (comp >= 2) {
         if (shared) acc = acc + shared[row];
         float b;
@@ -363,7 +372,8 @@ bool down_combine_fits(int K, int I) { return K <= 32 && down_combine_lds(K, I) 
 bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                               const float* weights, const int32_t* asc, int K, int H, int I,
                               const float* act, const float* shared, int comp, Epi epi,
-                              float* out, int* status, hipStream_t s, const float* residual) {
+                              float* out, int* status, hipStream_t s, const float* residual,
+                              const float* gate) {
   if (!down_combine_fits(K, I)) return false;
   const size_t lds = down_combine_lds(K, I);
   const dim3 grid(H / kPanelRows), block(64 * std::min(K, 8));
@@ -372,7 +382,7 @@ bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* id
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFusedLdsBytes);
     kernel<<<grid, block, lds, s>>>(mats, ids, weights, asc, K, H, I, act, shared, comp, epi,
-                                    residual, out, status);
+                                    residual, gate, out, status);
   };
   if (fmt == kFmtBF16) go(gemv_down_combine_kernel<kFmtBF16, 1>);
   else if (fmt == kFmtMXFP4) go(gemv_down_combine_kernel<kFmtMXFP4, 2>);
@@ -394,6 +404,8 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
                                                            const int32_t* __restrict__ asc,
                                                            int T, int K, int H,
                                                            const float* __restrict__ res,
+                                                           const float* __restrict__ shared,
+                                                           const float* __restrict__ gate,
                                                            float* __restrict__ out,
                                                            int* status) {
   const int h4 = blockIdx.x * blockDim.x + threadIdx.x;
@@ -426,6 +438,20 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
         const float s = acc[u] + c;
         if (!rne_bf16(s, &acc[u])) { bad = true; acc[u] = s; }
       }
+    }
+  }
+  if (shared) {
+    // the gated shared expert, added last (src/models/qwen3_6/runtime.rs:1449-1461):
+    // c = bf16(scale * s), acc = bf16(acc + c)
+    const float sc = qwen_shared_scale(gate[t], bad);
+    const float4 s4 = reinterpret_cast<const float4*>(shared + (size_t)t * H)[h4];
+    const float ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float c;
+      if (!rne_bf16(sc * ss[u], &c)) { bad = true; c = sc * ss[u]; }
+      const float a = acc[u] + c;
+      if (!rne_bf16(a, &acc[u])) { bad = true; acc[u] = a; }
     }
   }
   if (res) {
@@ -483,14 +509,15 @@ __global__ __launch_bounds__(256) void combine_glm_kernel(const float* __restric
 
 void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                          const int32_t* asc, int T, int K, int H, float* out, int* status,
-                         hipStream_t s, const float* residual) {
+                         hipStream_t s, const float* residual, const float* shared,
+                         const float* gate) {
   dim3 grid((H / 4 + 255) / 256, T);
   if (K <= 8)
     combine_qwen_kernel<8><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H,
-                                                residual, out, status);
+                                                residual, shared, gate, out, status);
   else
     combine_qwen_kernel<32><<<grid, 256, 0, s>>>(y_perm, pos_of_slot, weights, asc, T, K, H,
-                                                 residual, out, status);
+                                                 residual, shared, gate, out, status);
 }
 
 void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,

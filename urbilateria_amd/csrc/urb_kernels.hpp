@@ -130,18 +130,21 @@ void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max
 // down_combine_fits (the k activation rows fit the kernel's LDS budget); returns false and
 // launches nothing otherwise.
 bool down_combine_fits(int K, int I);
-// With `residual` [H] (not null), out = bf16(residual + combined) (the decoder layer's
-// residual add with BF16 activations).
+// QWEN36 (comp 0) with `shared`: the shared expert's output enters with scale
+// bf16(sigmoid(gate[0])) after the routes.  With `residual` [H] (not null), out =
+// bf16(residual + combined) (the decoder layer's residual add with BF16 activations).
 bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                               const float* weights, const int32_t* asc, int K, int H, int I,
                               const float* act, const float* shared, int comp, Epi epi,
                               float* out, int* status, hipStream_t s,
-                              const float* residual = nullptr);
-// Combines: Qwen BF16 ascending-id, GLM f64 ranking order.  Qwen with `residual` [T, H] (not
-// null): out = bf16(residual + combined).
+                              const float* residual = nullptr, const float* gate = nullptr);
+// Combines: Qwen BF16 ascending-id, GLM f64 ranking order.  Qwen with `shared` [T, H]: the
+// gated shared expert (scale bf16(sigmoid(gate[t]))) added last; with `residual` [T, H]:
+// out = bf16(residual + combined).
 void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                          const int32_t* asc, int T, int K, int H, float* out, int* status,
-                         hipStream_t s, const float* residual = nullptr);
+                         hipStream_t s, const float* residual = nullptr,
+                         const float* shared = nullptr, const float* gate = nullptr);
 void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                         const float* shared, int T, int K, int H, float* out, hipStream_t s);
 // MX-activation mode (Hy4 composition).  simulate_e4m3_activation (src/math/mxfp.rs:89-115)

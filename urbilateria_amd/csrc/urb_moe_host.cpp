@@ -47,6 +47,7 @@ struct Workspace {
   float* shared_out = nullptr;
   float* xq = nullptr;  // HY4: the simulated E4M3 token activations [chunk, H]
   float* xn = nullptr;  // QWEN36 block calls: the normalized BF16 token activations [chunk, H]
+  float* gate_logit = nullptr;  // QWEN36 shared expert: bf16(shared_expert_gate . x) [chunk]
   int* status = nullptr;  // [0] latched numerical failures, [1] validation flags
 };
 
@@ -74,6 +75,7 @@ struct urb_moe_ctx {
   size_t work_bytes = 0;
   const uint16_t* router = nullptr;    // [E, H] BF16 (rows zero-padded to router_rows(E))
   uint16_t* router_lane8 = nullptr;    // per-lane chain layout (QWEN36, DSV41)
+  uint16_t* shared_gate8 = nullptr;    // QWEN36 shared expert gate row, per-lane chain layout
   uint8_t* router_panel = nullptr;     // panel layout of the padded router (GLM)
   const float* bias = nullptr;         // [E] or nullptr
   ExpertMats* table = nullptr;         // device [E]
@@ -163,9 +165,9 @@ static urb_status check_desc(const urb_moe_desc* d) {
   for (uint32_t dim : {d->hidden, d->intermediate, d->shared_intermediate})
     if (dim % urb::kPanelCols || dim > kMaxDim) return URB_ERR_SHAPE;
   if (d->composition == URB_COMPOSE_QWEN36) {
-    // The Qwen3.6 composition reproduced here: BF16 experts, softmax router, no shared expert.
-    if (d->expert_format != URB_FMT_BF16 || d->shared_intermediate != 0 ||
-        d->router != URB_ROUTER_SOFTMAX_TOPK)
+    // The Qwen3.6 composition: BF16 experts, softmax router, an optional BF16 shared expert.
+    if (d->expert_format != URB_FMT_BF16 || d->router != URB_ROUTER_SOFTMAX_TOPK ||
+        (d->shared_intermediate && d->shared_format != URB_FMT_BF16))
       return URB_ERR_ARGUMENT;
   } else if (d->composition == URB_COMPOSE_HY4 || d->composition == URB_COMPOSE_DSV41) {
     // MX projections only (the activation mode exists for MX weights), and the routed experts'
@@ -243,6 +245,7 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   if (d.composition == URB_COMPOSE_HY4 || d.composition == URB_COMPOSE_DSV41)
     w.xq = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36) w.xn = b.take<float>(C * H);
+  if (d.composition == URB_COMPOSE_QWEN36 && d.shared_intermediate) w.gate_logit = b.take<float>(C);
 }
 
 static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
@@ -253,6 +256,8 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   // the 8-lane FP32 router tree reads a lane-chain copy; the f64 MFMA router a panel copy
   const bool lane8 = qwen || d->composition == URB_COMPOSE_DSV41;
   if (!w->router_weight || !w->experts || (has_shared && !w->shared)) return URB_ERR_ARGUMENT;
+  const bool qwen_gate = qwen && has_shared;
+  if (qwen_gate && !w->shared_expert_gate) return URB_ERR_ARGUMENT;
   if (src != URB_SOURCE_HOST && src != URB_SOURCE_DEVICE_COPY && src != URB_SOURCE_DEVICE_BORROW)
     return URB_ERR_ARGUMENT;
   const bool mx = d->expert_format != URB_FMT_BF16;
@@ -280,7 +285,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
   const size_t Ep = urb::router_rows((int)E);
   size_t arena = align_up(Ep * H * 2) + (lane8 ? align_up((E + 7) / 8 * 8 * H * 2) : align_up(Ep * H * 2)) +
-                 align_up(E * 4);
+                 align_up(E * 4) + (qwen_gate ? 2 * align_up(8 * H * 2) : 0);
   size_t wbytes = 0;
   if (!borrow) {
     for (int m = 0; m < 3; ++m) {
@@ -303,6 +308,13 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   float* bias = ab.take<float>(E);
   c->table = ab.take<ExpertMats>(E);
   c->shared_table = ab.take<ExpertMats>(1);
+  // the shared expert's gate row as an 8-row lane-chain block (rows 1..7 zero)
+  uint16_t* gate_rows = qwen_gate ? ab.take<uint16_t>(8 * H) : nullptr;
+  c->shared_gate8 = qwen_gate ? ab.take<uint16_t>(8 * H) : nullptr;
+  if (qwen_gate) {
+    urb::launch_fill_i32(reinterpret_cast<int32_t*>(gate_rows), 0, 8 * H / 2, nullptr);
+    URB_HIP(hipMemcpy(gate_rows, w->shared_expert_gate, H * 2, kind));
+  }
   URB_HIP(hipMemcpy(router, w->router_weight, E * H * 2, kind));
   if (Ep > E) urb::launch_fill_i32(reinterpret_cast<int32_t*>(router + E * H), 0, (Ep - E) * H / 2,
                                    nullptr);
@@ -401,6 +413,9 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
                            nullptr);
     }
   if (c->bias) urb::launch_check_finite(c->bias, E, c->ws.status + 2, nullptr);
+  if (qwen_gate)
+    urb::launch_validate(URB_FMT_BF16, reinterpret_cast<const uint8_t*>(gate_rows), H * 2,
+                         nullptr, 0, flags, nullptr);
   URB_HIP(hipGetLastError());
   int host_flags[4] = {0, 0, 0, 0};
   URB_HIP(hipDeviceSynchronize());
@@ -413,6 +428,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   if (host_flags[1] & 2) return URB_ERR_INVALID_SCALE;
   urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
 
+  if (qwen_gate) urb::launch_relayout_lane8(gate_rows, 1, (int)H, c->shared_gate8, nullptr);
   if (lane8)
     urb::launch_relayout_lane8(router, (int)E, (int)H, c->router_lane8, nullptr);
   else
@@ -625,29 +641,35 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, 
       continue;
     }
     if (has_shared) {
-      // GatedMlp shared expert (src/models/glm/runtime/moe.rs:162) does not depend on the
-      // routes: it runs on the side stream while the router, top-k and permutation run here.
+      // The shared expert does not depend on the routes: it runs on the side stream while the
+      // router, top-k and permutation run here.  GLM: GatedMlp (src/models/glm/runtime/moe.rs:
+      // 162).  QWEN36: a Qwen38Expert and its gate logit linear(shared_expert_gate) -- the
+      // router's 8-lane FP32 tree with BF16 output, one row (qwen3_6/runtime.rs:1417-1435).
       URB_HIP(hipEventRecord(c->fork, s));
       URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
+      const urb::Epi sepi = qwen ? epi : gated;
       Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
       const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
       {
         Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
+        if (qwen)
+          urb::launch_router_lane8(c->shared_gate8, 1, H, xc, n, ws.gate_logit, 1, ws.status,
+                                   c->side);
         if (n > 1)
           urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                   xc, ws.shared_act, gated, ws.status, c->side);
+                                   xc, ws.shared_act, sepi, ws.status, c->side);
         else
           urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, xc,
-                                   ws.shared_act, gated, ws.status, c->side);
+                                   ws.shared_act, sepi, ws.status, c->side);
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, c->side);
         if (n > 1)
           urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                ws.shared_act, ws.shared_out, gated, ws.status, c->side);
+                                ws.shared_act, ws.shared_out, sepi, ws.status, c->side);
         else
           urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is,
-                                ws.shared_act, ws.shared_out, gated, ws.status, c->side);
+                                ws.shared_act, ws.shared_out, sepi, ws.status, c->side);
       }
       URB_HIP(hipEventRecord(c->join, c->side));
     }
@@ -681,7 +703,8 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, 
         Span span(c, URB_STAGE_DOWN, s);
         urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
                                       ws.act, has_shared ? ws.shared_out : nullptr,
-                                      qwen ? 0 : 1, epi, yc, ws.status, s, resid);
+                                      qwen ? 0 : 1, epi, yc, ws.status, s, resid,
+                                      ws.gate_logit);
       }
       if (c->profiling) {
         urb_status st = collect_spans(c);
@@ -702,7 +725,8 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, 
     {
       Span span(c, URB_STAGE_COMBINE, s);
       if (qwen)
-        urb::launch_combine_qwen(ws.y_perm, pos, wc, ws.asc, n, K, H, yc, ws.status, s, resid);
+        urb::launch_combine_qwen(ws.y_perm, pos, wc, ws.asc, n, K, H, yc, ws.status, s, resid,
+                                 has_shared ? ws.shared_out : nullptr, ws.gate_logit);
       else
         urb::launch_combine_glm(ws.y_perm, pos, wc, has_shared ? ws.shared_out : nullptr, n, K,
                                 H, yc, s);

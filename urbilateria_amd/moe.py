@@ -55,6 +55,7 @@ class DeviceLayer:
     shared: Optional[List[Pair]]
     correction_bias: Optional["torch.Tensor"]     # [E] f32
     arena: Optional["torch.Tensor"] = None
+    shared_expert_gate: Optional["torch.Tensor"] = None  # [H] int16 BF16 (QWEN36 shared expert)
 
     @staticmethod
     def from_host(host: C.HostLayer, device="cuda") -> "DeviceLayer":
@@ -64,7 +65,10 @@ class DeviceLayer:
         sh = None if host.shared is None else [(up(d), up(s)) for d, s in host.shared]
         rw = torch.from_numpy(host.router_weight.view(np.int16)).to(device)
         bias = up(host.correction_bias)
-        return DeviceLayer(host.spec, rw, ex, sh, bias)
+        gate = None
+        if host.shared_expert_gate is not None:
+            gate = torch.from_numpy(host.shared_expert_gate.view(np.int16)).to(device)
+        return DeviceLayer(host.spec, rw, ex, sh, bias, shared_expert_gate=gate)
 
     @staticmethod
     def synthesize(spec: C.LayerSpec, base_seed: int = synth.BASE_SEED,
@@ -84,7 +88,8 @@ class DeviceLayer:
                      ("shared.up", spec.shared_format, Is, H),
                      ("shared.down", spec.shared_format, H, Is)]
         al = lambda n: (n + 255) // 256 * 256
-        total = al(E * H * 2)
+        qwen_gate = bool(Is) and spec.composition == C.COMPOSE_QWEN36
+        total = al(E * H * 2) + (al(H * 2) if qwen_gate else 0)
         for _, fmt, r, c in mats:
             db, sb = C.matrix_bytes(fmt, r, c)
             total += al(db) + al(sb)
@@ -119,15 +124,21 @@ class DeviceLayer:
             out.append((d, sc))
         ex = [out[3 * e:3 * e + 3] for e in range(E)]
         sh = out[3 * E:3 * E + 3] if Is else None
+        gate = None
+        if qwen_gate:
+            gate = take(H * 2)
+            N.check(lib.urb_synth_bf16(synth.stream_seed("shared.expert_gate", base_seed), H, 0.0,
+                                       0.02, gate.data_ptr(), s), "synth shared expert gate")
+            gate = gate.view(torch.int16)
         bias = None
         if correction_bias is not None:
             bias = torch.from_numpy(np.ascontiguousarray(correction_bias, np.float32)).to(device)
-        return DeviceLayer(spec, rw.view(torch.int16).view(E, H), ex, sh, bias, arena)
+        return DeviceLayer(spec, rw.view(torch.int16).view(E, H), ex, sh, bias, arena, gate)
 
     @staticmethod
     def from_consolidated(spec: C.LayerSpec, router_weight, gate_up, gate_up_scales, down,
                           down_scales, shared: Optional[List[Pair]] = None,
-                          correction_bias=None) -> "DeviceLayer":
+                          correction_bias=None, shared_expert_gate=None) -> "DeviceLayer":
         """A layer over consolidated expert tensors, used in place: gate_up [E, 2I, H] (each
         expert's gate rows, then its up rows) and down [E, H, I] in the on-disk layouts, scales
         [E, 2I, H/32] and [E, H, I/32] for the MX formats (None for BF16) -- the Qwen3.6 packed
@@ -142,7 +153,8 @@ class DeviceLayer:
             us = None if gate_up_scales is None else gate_up_scales[e, I:]
             ds = None if down_scales is None else down_scales[e]
             ex.append([(gate_up[e, :I], gs), (gate_up[e, I:], us), (down[e], ds)])
-        return DeviceLayer(spec, router_weight, ex, shared, correction_bias)
+        return DeviceLayer(spec, router_weight, ex, shared, correction_bias,
+                           shared_expert_gate=shared_expert_gate)
 
     def to_host(self, experts: Optional[List[int]] = None) -> C.HostLayer:
         """Copies (a subset of) the layer back to host memory for the CPU oracle."""
@@ -156,7 +168,10 @@ class DeviceLayer:
         rw = self.router_weight.contiguous().cpu().numpy().view(np.uint16).reshape(
             self.spec.n_experts, self.spec.hidden)
         bias = None if self.correction_bias is None else self.correction_bias.cpu().numpy()
-        return C.HostLayer(self.spec, rw, ex, sh, bias)
+        gate = None
+        if self.shared_expert_gate is not None:
+            gate = self.shared_expert_gate.cpu().numpy().view(np.uint16).reshape(-1)
+        return C.HostLayer(self.spec, rw, ex, sh, bias, gate)
 
 
 class MoeLayer:
@@ -191,7 +206,8 @@ class MoeLayer:
                       float(spec.routed_scaling_factor), max_tokens,
                       float(spec.swiglu_limit))
         w = N.Weights(_ptr(layer.router_weight), _ptr(layer.correction_bias),
-                      ctypes.addressof(mats), None if shared is None else ctypes.addressof(shared))
+                      ctypes.addressof(mats), None if shared is None else ctypes.addressof(shared),
+                      _ptr(getattr(layer, "shared_expert_gate", None)))
         ctx = ctypes.c_void_p()
         st = lib.urb_moe_create(ctypes.byref(desc), ctypes.byref(w), source, ctypes.byref(ctx))
         N.check(st, "urb_moe_create")
@@ -324,7 +340,8 @@ def packed_layer(layer: "DeviceLayer") -> "DeviceLayer":
         sh = [pack_matrix(spec.shared_format, d, sc, *sdims[m])
               for m, (d, sc) in enumerate(layer.shared)]
     torch.cuda.current_stream().synchronize()
-    return DeviceLayer(spec, layer.router_weight, ex, sh, layer.correction_bias, None)
+    return DeviceLayer(spec, layer.router_weight, ex, sh, layer.correction_bias, None,
+                       layer.shared_expert_gate)
 
 
 def dequant_rows(fmt: int, data, scales, rows: int, cols: int, row0: int = 0,

@@ -58,7 +58,8 @@ class Desc(ctypes.Structure):
 
 class Weights(ctypes.Structure):
     _fields_ = [("router_weight", ctypes.c_void_p), ("correction_bias", ctypes.c_void_p),
-                ("experts", ctypes.c_void_p), ("shared", ctypes.c_void_p)]
+                ("experts", ctypes.c_void_p), ("shared", ctypes.c_void_p),
+                ("shared_expert_gate", ctypes.c_void_p)]
 
 
 _moe = None
