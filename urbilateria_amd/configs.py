@@ -168,10 +168,26 @@ MX_ACTIVATION_WORKLOADS: Dict[str, Workload] = {
 }
 
 
+# The Qwen3.6 release MoE geometry (src/models/qwen3_6/expert_store.rs:180-190: H 2048, 256
+# experts of I 512, BF16) with its sigmoid-gated BF16 shared expert (I 512), top-8: the full
+# QWEN36 composition the C1/C2 shapes leave the shared expert out of.
+QWEN36_RELEASE_WORKLOADS: Dict[str, Workload] = {
+    "qwen36_release": Workload(
+        "qwen36_release",
+        LayerSpec(hidden=2048, n_experts=256, top_k=8, intermediate=512,
+                  shared_intermediate=512, expert_format=FMT_BF16, shared_format=FMT_BF16,
+                  router=ROUTER_SOFTMAX_TOPK, composition=COMPOSE_QWEN36),
+        (1, 128), description="Qwen3.6 release MoE: BF16 H2048 E256 softmax top-8 I512 + gated "
+                              "BF16 shared expert I512, decode 1, prefill 128"),
+}
+
+
 def workload(name: str) -> Workload:
-    """A benchmark configuration or one of its MX-activation variants, by name."""
+    """A benchmark configuration or one of its variants, by name."""
     if name in WORKLOADS:
         return WORKLOADS[name]
+    if name in QWEN36_RELEASE_WORKLOADS:
+        return QWEN36_RELEASE_WORKLOADS[name]
     return MX_ACTIVATION_WORKLOADS[name]
 
 
