@@ -207,6 +207,18 @@ urb_status urb_pack_matrix(urb_format format, const void *data, const uint8_t *s
                            uint32_t rows, uint32_t cols, void *packed_data,
                            uint8_t *packed_scales, void *stream);
 
+/* Points expert `expert` of a URB_SOURCE_DEVICE_BORROW context at other panel-layout matrices
+ * (mats[3]: gate, up, down, device, as urb_pack_matrix writes them): with
+ * include/urb_residency.h this is how a caller keeps a subset of a layer's experts resident in
+ * HBM slots of its own and swaps them between calls.  The payload is validated first, as
+ * urb_moe_create does (E8M0 0xFF -> URB_ERR_INVALID_SCALE; E4M3 NaN codes or non-finite BF16
+ * -> URB_ERR_NONFINITE, the entry unchanged); the change is ordered on `stream` and the call
+ * returns once it is in place.  Other contexts -> URB_ERR_ARGUMENT.  No reference counterpart:
+ * the reference's expert stores hand the layer owned matrices per access
+ * (Qwen36ExpertStore::acquire / acquire_grouped, src/models/qwen3_6/expert_store.rs:291-317). */
+urb_status urb_moe_set_expert(urb_moe_ctx *ctx, uint32_t expert, const urb_matrix *mats,
+                              void *stream);
+
 /* Per-expert views of consolidated checkpoint tensors, for urb_moe_weights.experts: fills
  * out[E * 3] with pointers into the tensors (no copy, no device work).  gate_up is [E, 2I, H]
  * with each expert's gate rows 0..I-1 followed by its up rows I..2I-1, down is [E, H, I], both

@@ -583,6 +583,57 @@ def test_qwen_shared_expert_needs_its_gate_and_bf16():
     assert e.value.status == N.ERR_NONFINITE
 
 
+# ------------------------------------------------------ experts streamed through HBM slots
+@pytest.mark.parametrize("name", ["c2_bf16_prefill", "c3_mxfp4_decode", "c4_mxfp8"])
+def test_streamed_residency_layer_equals_resident_layer(name):
+    # 16 experts in host memory, 10 HBM slots placed by the residency policy: every call gives
+    # the fully resident layer's results on the same token runs, bit for bit, and the policy's
+    # telemetry is the serial LRU replay of the calls' access sequences
+    from urbilateria_amd import residency as R
+    host = _small_layer(name)
+    spec = host.spec
+    streamed = R.StreamedMoeLayer(host, slots=10, max_tokens=6)
+    resident = moe_mod().MoeLayer(host, max_tokens=6)
+    replay, rt = R.LayerLruCache(1, 10), R.Telemetry()
+    for call, T in enumerate((1, 3, 6, 2, 6)):
+        x = torch.from_numpy(synth.activations(f"x.stream.{call}", T, spec.hidden)).cuda()
+        y, ids, w = streamed.forward(x)
+        parts = [resident.forward(x[a:b].contiguous()) for a, b in streamed.last_runs]
+        assert torch.equal(y, torch.cat([p[0] for p in parts]))
+        assert torch.equal(ids, torch.cat([p[1] for p in parts]))
+        assert torch.equal(w, torch.cat([p[2] for p in parts]))
+        for t in range(T):
+            for key in sorted(ids[t].tolist()):
+                replay.access(rt, 0, key, lambda key=key: (key, 1, 1))
+    got, want = streamed.telemetry, rt
+    assert (got.hits, got.misses, got.evictions) == (want.hits, want.misses, want.evictions)
+    assert got.misses > 10 and got.evictions > 0  # the slots did turn over
+    streamed.close()
+    resident.close()
+
+
+def test_set_expert_validates_and_needs_a_borrowed_context():
+    host = _small_layer("c3_mxfp4_decode")
+    dev = moe_mod().DeviceLayer.from_host(host)
+    layer = moe_mod().MoeLayer(dev, max_tokens=2)  # a copied context
+    lib = N.moe_lib()
+    mats = (N.Matrix * 3)(*[N.Matrix(d.data_ptr(), s.data_ptr()) for d, s in dev.experts[0]])
+    import ctypes
+    assert lib.urb_moe_set_expert(layer._ctx, 0, ctypes.addressof(mats), None) == N.ERR_ARGUMENT
+    layer.close()
+    packed = moe_mod().packed_layer(dev)
+    borrowed = moe_mod().MoeLayer(packed, max_tokens=2, source=N.SOURCE_DEVICE_BORROW)
+    bad_scales = packed.experts[1][0][1].clone()
+    bad_scales[5] = 0xFF  # an E8M0 NaN scale
+    mats = (N.Matrix * 3)(N.Matrix(packed.experts[1][0][0].data_ptr(), bad_scales.data_ptr()),
+                          *[N.Matrix(d.data_ptr(), s.data_ptr()) for d, s in packed.experts[1][1:]])
+    assert lib.urb_moe_set_expert(borrowed._ctx, 1, ctypes.addressof(mats), None) == \
+        N.ERR_INVALID_SCALE
+    assert lib.urb_moe_set_expert(borrowed._ctx, 16, ctypes.addressof(mats), None) == \
+        N.ERR_ARGUMENT
+    borrowed.close()
+
+
 # ------------------------------------------------- the Qwen3.6 FFN block around the MoE call
 def _block_inputs(T, H, seed):
     rng = np.random.default_rng(seed)

@@ -76,6 +76,7 @@ struct urb_moe_ctx {
   const uint16_t* router = nullptr;    // [E, H] BF16 (rows zero-padded to router_rows(E))
   uint16_t* router_lane8 = nullptr;    // per-lane chain layout (QWEN36, DSV41)
   uint16_t* shared_gate8 = nullptr;    // QWEN36 shared expert gate row, per-lane chain layout
+  bool borrowed = false;               // experts borrowed in the panel layout (repointable)
   uint8_t* router_panel = nullptr;     // panel layout of the padded router (GLM)
   const float* bias = nullptr;         // [E] or nullptr
   ExpertMats* table = nullptr;         // device [E]
@@ -275,6 +276,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   c->chunk = std::min<uint32_t>({d->max_tokens, (uint32_t)urb::kMaxChunkTokens, bitmap_chunk});
 
   const bool borrow = src == URB_SOURCE_DEVICE_BORROW;
+  c->borrowed = borrow;
   const hipMemcpyKind kind = src == URB_SOURCE_HOST ? hipMemcpyHostToDevice
                                                     : hipMemcpyDeviceToDevice;
   if (!borrow) URB_HIP(hipDeviceSynchronize());  // device sources may come from any stream
@@ -882,6 +884,40 @@ urb_status urb_expert_views(urb_format format, uint32_t n_experts, uint32_t hidd
     out[3 * e + 1] = urb_matrix{gu + e * 2 * gd + gd, mx ? gate_up_scales + e * 2 * gs + gs : nullptr};
     out[3 * e + 2] = urb_matrix{dn + e * dd, mx ? down_scales + e * ds : nullptr};
   }
+  return URB_OK;
+}
+
+urb_status urb_moe_set_expert(urb_moe_ctx* c, uint32_t expert, const urb_matrix* mats,
+                              void* stream) {
+  if (!c || !mats || !c->borrowed) return URB_ERR_ARGUMENT;
+  const urb_moe_desc& d = c->desc;
+  if (expert >= d.n_experts) return URB_ERR_ARGUMENT;
+  const bool mx = d.expert_format != URB_FMT_BF16;
+  for (int m = 0; m < 3; ++m)
+    if (!mats[m].data || (mx && !mats[m].scales)) return URB_ERR_ARGUMENT;
+  const size_t H = d.hidden, I = d.intermediate;
+  const size_t dims[3][2] = {{I, H}, {I, H}, {H, I}};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // validate the payload as urb_moe_create does (codes and scales are layout-independent), on
+  // the caller's stream, after anything already queued there
+  int* flags = c->ws.status + 3;
+  urb::launch_fill_i32(flags, 0, 1, s);
+  ExpertMats e{};
+  for (int m = 0; m < 3; ++m) {
+    size_t sb, db = matrix_bytes(d.expert_format, dims[m][0], dims[m][1], &sb);
+    e.data[m] = static_cast<const uint8_t*>(mats[m].data);
+    e.scales[m] = sb ? mats[m].scales : nullptr;
+    urb::launch_validate(d.expert_format, e.data[m], db, e.scales[m], sb, flags, s);
+  }
+  URB_HIP(hipGetLastError());
+  int host_flags = 0;
+  URB_HIP(hipMemcpyAsync(&host_flags, flags, sizeof(int), hipMemcpyDeviceToHost, s));
+  URB_HIP(hipStreamSynchronize(s));
+  if (host_flags & 1) return URB_ERR_NONFINITE;
+  if (host_flags & 2) return URB_ERR_INVALID_SCALE;
+  // the table entry changes in stream order: calls queued before keep the previous matrices
+  URB_HIP(hipMemcpyAsync(c->table + expert, &e, sizeof(ExpertMats), hipMemcpyHostToDevice, s));
+  URB_HIP(hipStreamSynchronize(s));
   return URB_OK;
 }
 

@@ -22,7 +22,8 @@ SOURCE_HOST, SOURCE_DEVICE_COPY, SOURCE_DEVICE_BORROW = 0, 1, 2
 EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_route",
            "urb_moe_sync", "urb_dequant_rows", "urb_moe_memory", "urb_status_string",
            "urb_moe_profile", "urb_moe_profile_read", "urb_pack_matrix", "urb_quantize_e4m3",
-           "urb_expert_views", "urb_moe_forward_block", "urb_zc_rms_norm_bf16")
+           "urb_expert_views", "urb_moe_forward_block", "urb_zc_rms_norm_bf16",
+           "urb_moe_set_expert")
 STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
@@ -105,6 +106,8 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_pack_matrix.restype = ctypes.c_int
         lib.urb_quantize_e4m3.argtypes = [P, u32, u32, P, P, P]
         lib.urb_quantize_e4m3.restype = ctypes.c_int
+        lib.urb_moe_set_expert.argtypes = [P, u32, P, P]
+        lib.urb_moe_set_expert.restype = ctypes.c_int
         lib.urb_moe_forward_block.argtypes = [P, P, P, ctypes.c_float, u32, P, P, P, P]
         lib.urb_moe_forward_block.restype = ctypes.c_int
         lib.urb_zc_rms_norm_bf16.argtypes = [P, P, u32, u32, ctypes.c_float, P, P]

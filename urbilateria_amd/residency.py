@@ -292,3 +292,138 @@ class LayerLruCache:
         m = self._lib.urb_lru_restore_layer_capacity(self._h, ctypes.byref(telemetry), layer,
                                                      capacity, out)
         return [out[i] for i in range(m)]
+
+
+def _to_device(a):
+    """Device copy of a host array or CPU tensor (bytes preserved); device tensors pass."""
+    import numpy as np
+    import torch
+    if a is None or (isinstance(a, torch.Tensor) and a.is_cuda):
+        return a
+    if isinstance(a, torch.Tensor):
+        a = a.numpy()
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+class StreamedMoeLayer:
+    """A layer whose experts stay in caller memory (the reference's expert store), with at most
+    ``slots`` of them resident in HBM at a time, placed by the residency policy.
+
+    A call routes first (``urb_moe_route``), replays the batch's expert accesses in the
+    reference's order -- each token's experts in ascending id, tokens in order, as
+    execute_batched_moe builds them (src/models/qwen3_6/runtime.rs:1086-1104) -- through the
+    LRU, packing each miss into the slot its victim frees (``urb_pack_matrix``) and repointing
+    the context's table (``urb_moe_set_expert``), then runs the layer.  A batch needing more
+    distinct experts than slots is cut into token runs that fit."""
+
+    def __init__(self, layer, slots: int, max_tokens: int, layer_index: int = 0,
+                 cache: Optional[LayerLruCache] = None):
+        import torch
+        from . import configs as C
+        from . import moe
+        spec = layer.spec
+        if slots < spec.top_k:
+            raise ValueError("a token's experts must fit the slots at once")
+        self.spec, self.slots, self.layer_index = spec, slots, layer_index
+        self._src = layer
+        H, I = spec.hidden, spec.intermediate
+        self._dims = ((I, H), (I, H), (H, I))
+        sizes = [C.matrix_bytes(spec.expert_format, r, c) for r, c in self._dims]
+        al = lambda n: (n + 255) // 256 * 256
+        self._slot_bytes = sum(al(d) + al(s) for d, s in sizes)
+        self._arena = torch.empty(slots * self._slot_bytes, dtype=torch.uint8, device="cuda")
+        self._slot_mats = []
+        for k in range(slots):
+            off, mats = k * self._slot_bytes, []
+            for d, s in sizes:
+                data = self._arena[off:off + d]
+                off += al(d)
+                sc = self._arena[off:off + s] if s else None
+                off += al(s)
+                mats.append((data, sc))
+            self._slot_mats.append(mats)
+        self._pack(0, 0)  # every table entry starts at slot 0, which holds valid matrices
+        shared = None
+        if layer.shared is not None:  # always resident, in the panel layout too
+            Is = spec.shared_intermediate
+            sdims = ((Is, H), (Is, H), (H, Is))
+            shared = [moe.pack_matrix(spec.shared_format, _to_device(d), _to_device(sc),
+                                      *sdims[m])
+                      for m, (d, sc) in enumerate(layer.shared)]
+        torch.cuda.synchronize()
+        placeholder = moe.DeviceLayer(spec, _to_device(layer.router_weight),
+                                      [self._slot_mats[0]] * spec.n_experts, shared,
+                                      _to_device(layer.correction_bias), None,
+                                      _to_device(getattr(layer, "shared_expert_gate", None)))
+        self.layer = moe.MoeLayer(placeholder, max_tokens, source=N.SOURCE_DEVICE_BORROW)
+        self.cache = cache if cache is not None else LayerLruCache(layer_index + 1, slots)
+        self.telemetry = Telemetry()
+        self._free = list(range(slots))
+
+    def _pack(self, expert: int, slot: int) -> None:
+        from . import moe
+
+        for m, (r, c) in enumerate(self._dims):
+            # host sources (numpy, CPU tensors) are staged on the device first
+            d, s = (_to_device(a) for a in self._src.experts[expert][m])
+            pd, ps = self._slot_mats[slot][m]
+            N.check(N.moe_lib().urb_pack_matrix(self.spec.expert_format, moe._ptr(d), moe._ptr(s),
+                                                r, c, moe._ptr(pd), moe._ptr(ps),
+                                                moe._stream_handle()), "urb_pack_matrix")
+
+    def _point(self, expert: int, slot: int) -> None:
+        from . import moe
+        mats = (N.Matrix * 3)(*[N.Matrix(moe._ptr(d), moe._ptr(s))
+                                for d, s in self._slot_mats[slot]])
+        N.check(N.moe_lib().urb_moe_set_expert(self.layer._ctx, expert, ctypes.addressof(mats),
+                                               moe._stream_handle()), "urb_moe_set_expert")
+
+    def _access(self, key: int) -> None:
+        layer = self.layer_index
+        if not self.cache.contains(layer, key):
+            if self._free:
+                slot = self._free.pop()
+            else:  # the victim the access is about to evict frees its slot
+                ents = self.cache.entries(layer)
+                slot = min(ents, key=lambda e: (e.last_used, e.key)).value
+
+            def load(key=key, slot=slot):
+                self._pack(key, slot)
+                self._point(key, slot)
+                return slot, self._slot_bytes, self._slot_bytes
+        else:
+            def load():  # never called on a hit
+                raise RuntimeError("unexpected load")
+        self.cache.access_with_evicted(self.telemetry, layer, key, load)
+
+    def forward(self, x):
+        """x [T, H] f32 (device) -> (y, ids, weights) of the resident layer."""
+        import torch
+        T, k = x.shape[0], self.spec.top_k
+        _, ids, _ = self.layer.route(x)
+        ids = ids.cpu().tolist()
+        runs, start, seen = [], 0, set()
+        for t in range(T):
+            nxt = seen | set(ids[t])
+            if len(nxt) > self.slots:
+                runs.append((start, t))
+                start, nxt = t, set(ids[t])
+            seen = nxt
+        runs.append((start, T))
+        self.last_runs = runs
+        ys, idl, wl = [], [], []
+        for a, b in runs:
+            for t in range(a, b):
+                for key in sorted(ids[t]):
+                    self._access(key)
+            y, i, w = self.layer.forward(x[a:b].contiguous())
+            ys.append(y)
+            idl.append(i)
+            wl.append(w)
+        return torch.cat(ys), torch.cat(idl), torch.cat(wl)
+
+    def close(self) -> None:
+        self.layer.close()
