@@ -360,12 +360,23 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
     float p[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) p[i] = open[i] ? exp_f32(v[i] - m) : 0.0f;
-    float den = 0.0f;  // sequential in expert order e = 64 i + lane
+    // the denominator sums in expert order: every lane adds all E values from LDS in order
+    // (broadcast reads), so each holds the sequential sum
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      const int n_here = min(64, E - 64 * i);
-      for (int l = 0; l < n_here; ++l) den = __fadd_rn(den, rdl(p[i], l));
+    for (int i = 0; i < EPL; ++i)
+      if (open[i]) sh[64 * i + lane] = p[i];
+    __builtin_amdgcn_wave_barrier();
+    float den = 0.0f;
+    const float4* sh4 = reinterpret_cast<const float4*>(sh);
+    int e = 0;
+    for (; e + 4 <= E; e += 4) {
+      const float4 q = sh4[e >> 2];
+      den = __fadd_rn(den, q.x);
+      den = __fadd_rn(den, q.y);
+      den = __fadd_rn(den, q.z);
+      den = __fadd_rn(den, q.w);
     }
+    for (; e < E; ++e) den = __fadd_rn(den, sh[e]);
     if (!finite(den) || den <= 0.0f) bad = true;
     int32_t key[EPL];
 #pragma unroll
@@ -498,7 +509,7 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
                                                     int32_t* __restrict__ ids,
                                                     float* __restrict__ weights,
                                                     int32_t* __restrict__ asc, int* status) {
-  __shared__ float lds[4][kMaxExperts];
+  __shared__ __attribute__((aligned(16))) float lds[4][kMaxExperts];
   __shared__ float grp[4][64];
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
