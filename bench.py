@@ -104,7 +104,7 @@ def measured_traffic(workload, tokens, stage):
     return None
 
 
-def cpu_baseline(name, spec, C, dev, x, budget_s, threads):
+def cpu_baseline(name, spec, C, dev, x, budget_s, threads, tok=None):
     """The CPU oracle (a C++ restatement of the reference's CPU path) timed on a bounded
     sample of the same workload's tokens, one worker per core."""
     import numpy as np
@@ -112,12 +112,15 @@ def cpu_baseline(name, spec, C, dev, x, budget_s, threads):
     T = x.shape[0]
     host = dev.to_host()
     xs = x.cpu().numpy()
-    # warm pool and page cache
-    O.moe_forward(spec, host.experts, host.router_weight, xs[:1], host.correction_bias,
-                  host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate)
+    ts = None if tok is None else tok.cpu().numpy().astype(np.uint32)
+
+    def call(n):
+        O.moe_forward(spec, host.experts, host.router_weight, xs[:n], host.correction_bias,
+                      host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate,
+                      token_ids=None if ts is None else ts[:n], hash_experts=host.hash_experts)
+    call(1)  # warm pool and page cache
     t0 = time.perf_counter()
-    O.moe_forward(spec, host.experts, host.router_weight, xs[:1], host.correction_bias,
-                  host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate)
+    call(1)
     one = time.perf_counter() - t0
     # tokens per call: the whole batch when a call fits the budget, else a prefix that does;
     # whole calls repeat until the budget is spent
@@ -125,8 +128,7 @@ def cpu_baseline(name, spec, C, dev, x, budget_s, threads):
     reps = 0
     t0 = time.perf_counter()
     while True:
-        O.moe_forward(spec, host.experts, host.router_weight, xs[:n], host.correction_bias,
-                      host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate)
+        call(n)
         reps += 1
         if time.perf_counter() - t0 >= budget_s or reps >= 5000:
             break
@@ -152,10 +154,23 @@ def run_one(name, T, args, want_cpu, cpu_budget):
         beta = C.calibrate_zipf_beta(spec.n_experts, spec.top_k, w.zipf_s, std,
                                      router=spec.router)
         bias = C.zipf_bias(spec.n_experts, w.zipf_s, beta)
-    first = moe.DeviceLayer.synthesize(spec, correction_bias=bias)
+    table = tok = None
+    if w.hash_vocab:
+        from urbilateria_amd import synth
+        # a synthetic tid2eid table and uniform token ids
+        table = torch.from_numpy(C.hash_table(w.hash_vocab, spec.n_experts, spec.top_k)).cuda()
+        ids_tok = synth.splitmix64(synth.stream_seed("bench.tokens"), 0, T) % np.uint64(
+            w.hash_vocab)
+        tok = torch.from_numpy(ids_tok.astype(np.int32)).cuda()
+
+    def synthesize():
+        d = moe.DeviceLayer.synthesize(spec, correction_bias=bias)
+        d.hash_experts = table
+        return d
+    first = synthesize()
     x = moe.synth_activations(T, spec.hidden)
     probe = moe.MoeLayer(first, max_tokens=T)
-    _, ids, _ = probe.forward(x)
+    _, ids, _ = probe.forward(x, token_ids=tok)
     ids_np = ids.cpu().numpy()
     distinct = len(np.unique(ids_np))
     counts = np.bincount(ids_np.ravel(), minlength=spec.n_experts)
@@ -164,19 +179,19 @@ def run_one(name, T, args, want_cpu, cpu_budget):
     full = C.expert_bytes(spec) * spec.n_experts + C.shared_bytes(spec)
     layers, devs = [probe], [first]
     for _ in range(copies - 1):
-        d = moe.DeviceLayer.synthesize(spec, correction_bias=bias)
+        d = synthesize()
         devs.append(d)
         layers.append(moe.MoeLayer(d, max_tokens=T))
     y = torch.empty((T, spec.hidden), dtype=torch.float32, device="cuda")
     idb = torch.empty((T, spec.top_k), dtype=torch.int32, device="cuda")
     wb = torch.empty((T, spec.top_k), dtype=torch.float32, device="cuda")
     for i in range(args.warmup):
-        layers[i % copies].forward_into(x, y, idb, wb)
+        layers[i % copies].forward_into(x, y, idb, wb, token_ids=tok)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(args.steps):
-        layers[i % copies].forward_into(x, y, idb, wb)
+        layers[i % copies].forward_into(x, y, idb, wb, token_ids=tok)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
@@ -186,7 +201,7 @@ def run_one(name, T, args, want_cpu, cpu_budget):
     for l in layers:
         l.profile(True)
     for i in range(args.profile_steps * copies):
-        layers[i % copies].forward_into(x, y, idb, wb)
+        layers[i % copies].forward_into(x, y, idb, wb, token_ids=tok)
     torch.cuda.synchronize()
     stages = {}
     for l in layers:
@@ -221,7 +236,7 @@ def run_one(name, T, args, want_cpu, cpu_budget):
         rec["zipf_bias_beta"] = float(beta)
     if want_cpu:
         threads = min(16, os.cpu_count() or 1)
-        rec["cpu_baseline"] = cpu_baseline(name, spec, C, first, x, cpu_budget, threads)
+        rec["cpu_baseline"] = cpu_baseline(name, spec, C, first, x, cpu_budget, threads, tok)
     for l in layers:
         l.close()
     del layers, devs, first, x, y

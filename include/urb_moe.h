@@ -34,8 +34,8 @@ typedef enum {
 typedef enum { URB_FMT_BF16 = 0, URB_FMT_MXFP4 = 1, URB_FMT_MXFP8 = 2 } urb_format;
 
 /* route_softmax_top_k (src/models/qwen3_8/moe.rs:91-159), route_noaux_tc
- * (src/math/routing.rs:38-155) or route_sqrt_softplus without hash experts
- * (src/models/deepseek_v4/math.rs:451-516; not with QWEN36). */
+ * (src/math/routing.rs:38-155) or route_sqrt_softplus (src/models/deepseek_v4/math.rs:451-516;
+ * not with QWEN36), with hash experts when the weights carry a tid2eid table. */
 typedef enum {
   URB_ROUTER_SOFTMAX_TOPK = 0,
   URB_ROUTER_SIGMOID_NOAUX_TC = 1,
@@ -65,12 +65,19 @@ typedef enum {
  *          swiglu_limit, times the route weight before the BF16 step and the down projection);
  *          the shared expert is the same without a weight; f32 sum in ascending expert id plus
  *          the shared expert, BF16.  MX expert and shared formats; route_sqrt_softplus is its
- *          router. */
+ *          router.
+ *  DSV4:   DeepSeek-V4 MoeWeights::forward{,_batch} (src/models/deepseek_v4/runtime.rs:
+ *          2484-2828): as DSV41 but the router GEMV is the ordered f64 `linear(router)`
+ *          (deepseek_v4/math.rs:106-115) and the activations are quantized per 128 values
+ *          (prepare_mx_activation, math.rs:120-126) before the MX projections
+ *          (DeepExpert::forward_with_mx_input, runtime.rs:3081-3155).  The first
+ *          num_hash_layers layers route by a tid2eid table (urb_moe_weights.hash_experts). */
 typedef enum {
   URB_COMPOSE_QWEN36 = 0,
   URB_COMPOSE_GLM = 1,
   URB_COMPOSE_HY4 = 2,
-  URB_COMPOSE_DSV41 = 3
+  URB_COMPOSE_DSV41 = 3,
+  URB_COMPOSE_DSV4 = 4
 } urb_composition;
 
 /* Where urb_moe_create reads the weights from.  The context streams expert and shared-expert
@@ -112,7 +119,7 @@ typedef struct {
   int32_t normalize;             /* noaux_tc: divide by the selected gate sum */
   float routed_scaling_factor;   /* noaux_tc, sqrt_softplus */
   uint32_t max_tokens;           /* largest token count one forward call may pass */
-  float swiglu_limit;            /* HY4, DSV41: bounded SwiGLU limit (> 0) */
+  float swiglu_limit;            /* HY4, DSV41, DSV4: bounded SwiGLU limit (> 0) */
 } urb_moe_desc;
 
 typedef struct {
@@ -124,6 +131,15 @@ typedef struct {
    * shared expert's contribution (finish_ordered_moe, src/models/qwen3_6/runtime.rs:1417-1468);
    * NULL otherwise. */
   const uint16_t *shared_expert_gate;
+  /* route_sqrt_softplus hash experts: layers.N.ffn.gate.tid2eid [hash_vocab, top_k] i64, the
+   * experts of each token id in table order (src/models/deepseek_v4/runtime.rs:2664-2681), in
+   * the memory the source names; NULL = routing by score.  Checked at creation: every id in
+   * [0, E) (URB_ERR_INVALID_GEOMETRY, the reference's "hash expert IDs must be in range",
+   * math.rs:483-489) and distinct within a row (URB_ERR_ARGUMENT: the reference would run a
+   * repeated expert twice; the permutation here needs distinct ids).  Layer calls then take
+   * token ids (urb_moe_forward_tokens / urb_moe_route_tokens). */
+  const int64_t *hash_experts;
+  uint32_t hash_vocab;
 } urb_moe_weights;
 
 typedef struct urb_moe_ctx urb_moe_ctx;
@@ -147,12 +163,26 @@ void urb_moe_destroy(urb_moe_ctx *ctx);
 urb_status urb_moe_forward(urb_moe_ctx *ctx, const float *x, uint32_t tokens, float *y,
                            int32_t *ids, float *weights, void *stream);
 
+/* urb_moe_forward with the tokens' ids [tokens] (device, u32), which hash routing needs
+ * (MoeWeights::forward's `token`, src/models/deepseek_v4/runtime.rs:2484-2495, 2664-2681); an
+ * id >= hash_vocab is reported by urb_moe_sync as URB_ERR_SHAPE (load_i64_matrix_row's bounds
+ * check).  Without a hash table the ids are not read.  urb_moe_forward on a context with a hash
+ * table returns URB_ERR_ARGUMENT. */
+urb_status urb_moe_forward_tokens(urb_moe_ctx *ctx, const float *x, const uint32_t *token_ids,
+                                  uint32_t tokens, float *y, int32_t *ids, float *weights,
+                                  void *stream);
+
 /* Router only: logits [tokens, E] (device, may be NULL), ids/weights as above.  Replaces
  * `linear(router)` + route_softmax_top_k (src/models/qwen3_8/math.rs:10-26,
  * src/models/qwen3_8/moe.rs:91-159) and router.matvec + route_noaux_tc
  * (src/models/glm/runtime/moe.rs:152-161). */
 urb_status urb_moe_route(urb_moe_ctx *ctx, const float *x, uint32_t tokens, float *logits,
                          int32_t *ids, float *weights, void *stream);
+/* urb_moe_route with token ids, as urb_moe_forward_tokens (DeepSeek-V4 prepare_routes,
+ * src/models/deepseek_v4/runtime.rs:2656-2703). */
+urb_status urb_moe_route_tokens(urb_moe_ctx *ctx, const float *x, const uint32_t *token_ids,
+                                uint32_t tokens, float *logits, int32_t *ids, float *weights,
+                                void *stream);
 
 /* Waits for `stream` and returns the first numerical failure latched since the previous
  * urb_moe_sync (URB_OK if none), then clears it.  The Result of the reference's layer calls. */
@@ -193,6 +223,11 @@ urb_status urb_zc_rms_norm_bf16(const float *x, const float *weight, uint32_t ro
  * quantizer; inputs must be finite (the layer call reports non-finite ones). */
 urb_status urb_quantize_e4m3(const float *x, uint32_t rows, uint32_t cols, uint8_t *codes,
                              uint8_t *scales, void *stream);
+/* urb_quantize_e4m3 per `block` values (32, or 128: DeepSeek-V4 prepare_mx_activation,
+ * src/models/deepseek_v4/math.rs:120-126); cols % block == 0; scales [rows, cols / block].
+ * Other block widths -> URB_ERR_ARGUMENT. */
+urb_status urb_quantize_e4m3_blocks(const float *x, uint32_t rows, uint32_t cols, uint32_t block,
+                                    uint8_t *codes, uint8_t *scales, void *stream);
 
 /* Converts one row-major matrix (device, the urb_matrix layout) into the panel layout the
  * context streams (device; same byte counts: packed_data as large as data, packed_scales as

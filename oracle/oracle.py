@@ -19,9 +19,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liburb_oracle.so")
 
 OK, SHAPE, INVALID_SCALE, NONFINITE, INVALID_GEOMETRY = 0, 1, 2, 3, 4
-FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
+FMT_BF16, FMT_MXFP4, FMT_MXFP8, FMT_F32 = 0, 1, 2, 3
 ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
-COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4, COMPOSE_DSV41 = 0, 1, 2, 3
+COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4, COMPOSE_DSV41, COMPOSE_DSV4 = 0, 1, 2, 3, 4
 
 _STATUS_NAMES = {OK: "ok", SHAPE: "shape", INVALID_SCALE: "invalid_scale",
                  NONFINITE: "nonfinite", INVALID_GEOMETRY: "invalid_geometry"}
@@ -59,11 +59,15 @@ def _load():
     lib.urbo_mxfp8_matvec_rows_f64.argtypes = [P, P, sz, sz, sz, sz, P, P]
     lib.urbo_route_softmax_top_k.argtypes = [P, sz, sz, P, P]
     lib.urbo_route_sqrt_softplus.argtypes = [P, P, sz, sz, ctypes.c_float, P, P, P]
+    lib.urbo_route_sqrt_softplus_hashed.argtypes = [P, P, P, sz, sz, ctypes.c_float, P, P, P]
     lib.urbo_route_noaux_tc.argtypes = [P, P, sz, sz, sz, sz, ctypes.c_int, ctypes.c_float,
                                         P, P, P]
     lib.urbo_silu.argtypes = [ctypes.c_float]
     lib.urbo_silu.restype = ctypes.c_float
     lib.urbo_moe_forward.argtypes = [P, P, ctypes.c_uint32, P, P, P, P, ctypes.c_int]
+    lib.urbo_moe_forward_tokens.argtypes = [P, P, P, ctypes.c_uint32, P, P, P, P, ctypes.c_int]
+    lib.urbo_dsv4_expert.argtypes = [ctypes.c_int, P, ctypes.c_uint32, ctypes.c_uint32, P,
+                                     ctypes.c_uint32, ctypes.c_float, P, P, ctypes.c_int]
     return lib
 
 
@@ -185,14 +189,19 @@ def route_softmax_top_k(logits: np.ndarray, top_k: int):
     return ids, w
 
 
-def route_sqrt_softplus(logits, bias, top_k: int, scale: float):
+def route_sqrt_softplus(logits, bias, top_k: int, scale: float, hash_experts=None):
+    """route_sqrt_softplus; ``hash_experts`` (top_k ids, table order) replaces the ranking."""
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    h = None if hash_experts is None else np.ascontiguousarray(hash_experts, dtype=np.int64)
+    if h is not None and h.size != top_k:
+        raise OracleError(SHAPE)
     ids = np.empty(top_k, np.int32)
     w = np.empty(top_k, np.float32)
     sel = np.empty(top_k, np.float32)
-    _check(_lib.urbo_route_sqrt_softplus(_ptr(logits), _ptr(b), logits.size, top_k,
-                                         float(scale), _ptr(ids), _ptr(w), _ptr(sel)))
+    _check(_lib.urbo_route_sqrt_softplus_hashed(_ptr(logits), _ptr(b), _ptr(h), logits.size,
+                                                top_k, float(scale), _ptr(ids), _ptr(w),
+                                                _ptr(sel)))
     return ids, w, sel
 
 
@@ -227,6 +236,8 @@ class _Layer(ctypes.Structure):
         ("experts", ctypes.c_void_p), ("shared", ctypes.c_void_p),
         ("swiglu_limit", ctypes.c_float),
         ("shared_expert_gate", ctypes.c_void_p),
+        ("hash_experts", ctypes.c_void_p), ("hash_vocab", ctypes.c_uint32),
+        ("router_weight_f32", ctypes.c_void_p),
     ]
 
 
@@ -240,11 +251,15 @@ class OracleResult:
 
 def moe_forward(spec, experts: Sequence, router_weight: np.ndarray, x: np.ndarray,
                 correction_bias: Optional[np.ndarray] = None, shared: Optional[Sequence] = None,
-                threads: int = 1, shared_expert_gate: Optional[np.ndarray] = None) -> OracleResult:
+                threads: int = 1, shared_expert_gate: Optional[np.ndarray] = None,
+                token_ids: Optional[np.ndarray] = None, hash_experts: Optional[np.ndarray] = None,
+                router_weight_f32: Optional[np.ndarray] = None) -> OracleResult:
     """Runs one layer.  ``spec`` carries the layer geometry (attributes hidden, n_experts,
     top_k, intermediate, shared_intermediate, expert_format, shared_format, router, composition,
     n_group, topk_group, normalize, routed_scaling_factor, swiglu_limit).  ``experts[e]`` is a triple of
-    (data, scales) pairs for gate, up and down; ``shared`` likewise or None."""
+    (data, scales) pairs for gate, up and down; ``shared`` likewise or None.  ``hash_experts``
+    [vocab, k] routes token t by row ``token_ids[t]``; ``router_weight_f32`` [E, H] replaces the
+    BF16 router of a DeepSeek-V4 layer."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T = x.shape[0]
     H, E, K = spec.hidden, spec.n_experts, spec.top_k
@@ -267,18 +282,25 @@ def moe_forward(spec, experts: Sequence, router_weight: np.ndarray, x: np.ndarra
     rwt = np.ascontiguousarray(router_weight)
     bias = None if correction_bias is None else np.ascontiguousarray(correction_bias, np.float32)
     sgate = None if shared_expert_gate is None else np.ascontiguousarray(shared_expert_gate)
+    hx = None if hash_experts is None else np.ascontiguousarray(hash_experts, np.int64)
+    tok = None if token_ids is None else np.ascontiguousarray(token_ids, np.uint32)
+    rf32 = None if router_weight_f32 is None else np.ascontiguousarray(router_weight_f32,
+                                                                       np.float32)
+    if tok is not None and tok.size != T:
+        raise OracleError(SHAPE)
     layer = _Layer(H, E, K, spec.intermediate, spec.shared_intermediate, spec.expert_format,
                    spec.shared_format, spec.router, spec.composition, spec.n_group,
                    spec.topk_group, int(spec.normalize), float(spec.routed_scaling_factor),
                    _ptr(rwt), _ptr(bias), ctypes.addressof(mats),
                    None if sh is None else ctypes.addressof(sh),
-                   float(getattr(spec, "swiglu_limit", 0.0)), _ptr(sgate))
+                   float(getattr(spec, "swiglu_limit", 0.0)), _ptr(sgate), _ptr(hx),
+                   0 if hx is None else hx.shape[0], _ptr(rf32))
     y = np.empty((T, H), np.float32)
     ids = np.empty((T, K), np.int32)
     w = np.empty((T, K), np.float32)
     logits = np.empty((T, E), np.float32)
-    status = _lib.urbo_moe_forward(ctypes.byref(layer), _ptr(x), T, _ptr(y), _ptr(ids), _ptr(w),
-                                   _ptr(logits), threads)
+    status = _lib.urbo_moe_forward_tokens(ctypes.byref(layer), _ptr(x), _ptr(tok), T, _ptr(y),
+                                          _ptr(ids), _ptr(w), _ptr(logits), threads)
     _check(status)
     return OracleResult(y, ids, w, logits)
 
@@ -351,6 +373,19 @@ def dsv41_expert(fmt: int, triple, hidden: int, intermediate: int, x: np.ndarray
                                        ctypes.c_int]
     _check(_lib.urbo_dsv41_expert(fmt, ctypes.addressof(mats), hidden, intermediate, _ptr(x),
                                   x.shape[0], float(swiglu_limit), _ptr(rw), _ptr(y), threads))
+    return y
+
+
+def dsv4_expert(fmt: int, triple, hidden: int, intermediate: int, x: np.ndarray,
+                swiglu_limit: float, route_weights=None, threads: int = 1) -> np.ndarray:
+    """DeepSeek-V4 expert on [n, hidden]: MX weights read x quantized per 128 values (inside)
+    and round to BF16; BF16 and F32 weights read x as it is."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    mats, keep = _mats(triple)
+    y = np.empty((x.shape[0], hidden), np.float32)
+    rw = None if route_weights is None else np.ascontiguousarray(route_weights, np.float32)
+    _check(_lib.urbo_dsv4_expert(fmt, ctypes.addressof(mats), hidden, intermediate, _ptr(x),
+                                 x.shape[0], float(swiglu_limit), _ptr(rw), _ptr(y), threads))
     return y
 
 

@@ -203,6 +203,19 @@ void dot_bf16_f64(const uint8_t *row, size_t cols, const float *x, size_t batch,
     for (size_t b = 0; b < batch; ++b) out[b] = (float)sum[b];
 }
 
+// src/model/matrix.rs:236-259 Matrix::matvec_rows (F32 weights): ordered f64 additions of
+// f64(w) * f64(x) from -0.0, rounded to f32 once.
+void dot_f32_f64(const uint8_t *row, size_t cols, const float *x, size_t batch, float *out) {
+    std::vector<double> sum(batch, -0.0);
+    for (size_t c = 0; c < cols; ++c) {
+        float wf;
+        std::memcpy(&wf, row + 4 * c, 4);
+        const double w = (double)wf;
+        for (size_t b = 0; b < batch; ++b) sum[b] += w * (double)x[b * cols + c];
+    }
+    for (size_t b = 0; b < batch; ++b) out[b] = (float)sum[b];
+}
+
 // src/model/bf16.rs:589-610 dot_bf16_fp32_avx2_fma (also :693-741 four-row and :612-687
 // batched forms, which keep this tree): lane j FMA-accumulates columns == j (mod 8) over the
 // complete 8-column prefix from +0.0; lanes are summed 0..7 in order; the tail is added with a
@@ -304,6 +317,7 @@ size_t row_bytes(int format, size_t cols) {
     switch (format) {
     case URBO_FMT_BF16: return cols * 2;
     case URBO_FMT_MXFP4: return (cols + 1) / 2;
+    case URBO_FMT_F32: return cols * 4;
     default: return cols;
     }
 }
@@ -325,6 +339,7 @@ int weight_matmul(Pool &p, int format, const uint8_t *data, const uint8_t *scale
         for (size_t r = r0; r < r1; ++r) {
             const uint8_t *row = data + r * rb;
             if (format == URBO_FMT_BF16) dot_bf16_f64(row, cols, x, batch, tmp.data());
+            else if (format == URBO_FMT_F32) dot_f32_f64(row, cols, x, batch, tmp.data());
             else if (format == URBO_FMT_MXFP4)
                 dot_mxfp4_f64(row, scales + r * sb, cols, x, batch, tmp.data());
             else if (g_mxfp8_fma_host)
@@ -474,7 +489,9 @@ int urbo_round_to_bf16_in_place(float *values, size_t n) {
 }
 
 size_t urbo_matrix_bytes(int format, size_t rows, size_t cols, size_t *scale_bytes) {
-    if (scale_bytes) *scale_bytes = format == URBO_FMT_BF16 ? 0 : rows * ((cols + 31) / 32);
+    if (scale_bytes)
+        *scale_bytes = format == URBO_FMT_BF16 || format == URBO_FMT_F32 ? 0
+                                                                         : rows * ((cols + 31) / 32);
     return rows * row_bytes(format, cols);
 }
 
@@ -486,6 +503,14 @@ int urbo_validate(int format, const uint8_t *data, const uint8_t *scales, size_t
                   size_t cols) {
     if (rows == 0 || cols == 0) return URBO_SHAPE;
     size_t sb = 0, nb = urbo_matrix_bytes(format, rows, cols, &sb);
+    if (format == URBO_FMT_F32) {  // DenseMatrix::new (src/model/matrix.rs:45-63): finite data
+        for (size_t i = 0; i < nb; i += 4) {
+            float v;
+            std::memcpy(&v, data + i, 4);
+            if (!std::isfinite(v)) return URBO_NONFINITE;
+        }
+        return URBO_OK;
+    }
     if (format == URBO_FMT_BF16) {
         for (size_t i = 0; i < nb; i += 2)
             if ((data[i + 1] & 0x7f) == 0x7f && (data[i] & 0x80)) return URBO_NONFINITE;
@@ -508,6 +533,7 @@ int urbo_row(int format, const uint8_t *data, const uint8_t *scales, size_t rows
     const uint8_t *r = data + row * rb;
     for (size_t c = 0; c < cols; ++c) {
         if (format == URBO_FMT_BF16) out[c] = bf16_at(r, c);
+        else if (format == URBO_FMT_F32) std::memcpy(&out[c], r + 4 * c, 4);
         else if (format == URBO_FMT_MXFP4) out[c] = kE2M1[nibble(r, c)] * e8m0(scales[row * sb + c / 32]);
         else out[c] = e4m3_table().v[r[c]] * e8m0(scales[row * sb + c / 32]);
     }
@@ -661,6 +687,18 @@ static float softplus_f(float v) {
 
 int urbo_route_sqrt_softplus(const float *logits, const float *bias, size_t n, size_t top_k,
                              float scale, int32_t *ids, float *weights, float *selection_out) {
+    return urbo_route_sqrt_softplus_hashed(logits, bias, nullptr, n, top_k, scale, ids, weights,
+                                           selection_out);
+}
+
+// route_sqrt_softplus with `hash_experts` (deepseek_v4/math.rs:451-516): the checks in the
+// reference's order (geometry, scale, finite logits and bias, hash ids in range), scores
+// s = sqrt(softplus(l)), selection s + bias; the experts are the hash row as given (table order)
+// or the top_k of the selection (value descending, lower id on ties); the denominator sums the
+// chosen scores in that order from -0.0; weight = s / denominator * scale.
+int urbo_route_sqrt_softplus_hashed(const float *logits, const float *bias, const int64_t *hash,
+                                    size_t n, size_t top_k, float scale, int32_t *ids,
+                                    float *weights, float *selection_out) {
     if (n == 0 || top_k == 0 || top_k > n) return URBO_SHAPE;
     if (!std::isfinite(scale)) return URBO_NONFINITE;
     if (scale <= 0.0f) return URBO_INVALID_GEOMETRY;  // validate_positive
@@ -670,14 +708,21 @@ int urbo_route_sqrt_softplus(const float *logits, const float *bias, size_t n, s
         score[i] = ::sqrtf(softplus_f(logits[i]));
         sel[i] = score[i] + (bias ? bias[i] : 0.0f);
     }
-    std::vector<size_t> ranking(n);
-    for (size_t i = 0; i < n; ++i) ranking[i] = i;
-    std::stable_sort(ranking.begin(), ranking.end(), [&](size_t l, size_t r) {
-        int32_t kl = total_key(sel[l]), kr = total_key(sel[r]);
-        if (kl != kr) return kl > kr;
-        return l < r;
-    });
-    ranking.resize(top_k);
+    std::vector<size_t> ranking;
+    if (hash) {
+        for (size_t j = 0; j < top_k; ++j)  // "hash expert IDs must be in range"
+            if (hash[j] < 0 || (uint64_t)hash[j] >= n) return URBO_INVALID_GEOMETRY;
+        for (size_t j = 0; j < top_k; ++j) ranking.push_back((size_t)hash[j]);
+    } else {
+        ranking.resize(n);
+        for (size_t i = 0; i < n; ++i) ranking[i] = i;
+        std::stable_sort(ranking.begin(), ranking.end(), [&](size_t l, size_t r) {
+            int32_t kl = total_key(sel[l]), kr = total_key(sel[r]);
+            if (kl != kr) return kl > kr;
+            return l < r;
+        });
+        ranking.resize(top_k);
+    }
     float denominator = -0.0f;  // Iterator::sum identity
     for (size_t e : ranking) denominator += score[e];
     if (!std::isfinite(denominator) || denominator <= 0.0f) return URBO_NONFINITE;
@@ -854,34 +899,56 @@ int hy4_quantize(const float *x, size_t n, size_t H, std::vector<float> &q) {
     return URBO_OK;
 }
 
-// DeepSeek-V4.1 Expert::forward_with_mx_input (src/models/deepseek_v41/runtime.rs:2243-2261)
-// on quantized activations q [n, H]: gate, up = bf16(matvec_fp32_accum(w1 / w3, q))
-// (linear_with_mx_activation, deepseek_v41/math.rs:36-52); a = bounded_swiglu(gate, up, limit)
-// times the route weight of each token when given (`w`, may be null: the shared expert);
-// a -> BF16; y = linear(w2, a) = bf16(matvec_fp32_accum(w2, simulate_e4m3_activation(a, 32)))
-// (math.rs:18-25).
-int dsv41_expert(Pool &p, int format, const urbo_matrix *m, size_t H, size_t I, const float *q,
-                 size_t n, float limit, const float *w, float *y) {
+// The DeepSeek routed expert on its input rows xin [n, H] (the simulated E4M3 activation for MX
+// weights, the plain input otherwise):
+//   V4.1 Expert::forward_with_mx_input (src/models/deepseek_v41/runtime.rs:2243-2261):
+//     projections through matvec_fp32_accum (deepseek_v41/math.rs:36-52), 32-wide blocks;
+//   V4 DeepExpert::forward_with_mx_input{,_batch} (src/models/deepseek_v4/runtime.rs:3081-3155):
+//     projections through WeightMatrix::matvec / matmul_rows (deepseek_v4/math.rs:130-158),
+//     128-wide blocks.
+// gate, up = linear_with_mx_activation(w1 / w3) (BF16-rounded for MX weights only);
+// a = bounded_swiglu(gate, up, limit) times the route weight of each token when given (`w`,
+// may be null: the shared expert); a -> BF16; y = linear(w2, a): MX weights read
+// simulate_e4m3_activation(a, block) and round y to BF16, other weights read a as it is.
+int dsv_expert(Pool &p, bool v41, int format, const urbo_matrix *m, size_t H, size_t I,
+               const float *xin, size_t n, float limit, const float *w, float *y) {
+    const bool mx = format == URBO_FMT_MXFP4 || format == URBO_FMT_MXFP8;
+    const size_t block = v41 ? 32 : 128;
+    auto mm = [&](const urbo_matrix &mat, size_t rows, size_t cols, const float *x, float *out) {
+        return v41 ? weight_matmul_fp32_accum(p, format, mat.data, mat.scales, rows, cols, x, n,
+                                              out)
+                   : weight_matmul(p, format, mat.data, mat.scales, rows, cols, x, n, out);
+    };
     std::vector<float> g(n * I), u(n * I), a(n * I);
-    int st = weight_matmul_fp32_accum(p, format, m[0].data, m[0].scales, I, H, q, n, g.data());
+    int st = mm(m[0], I, H, xin, g.data());
     if (st) return st;
-    st = weight_matmul_fp32_accum(p, format, m[1].data, m[1].scales, I, H, q, n, u.data());
-    if (st) return st;
-    if ((st = urbo_round_to_bf16_in_place(g.data(), n * I))) return st;
-    if ((st = urbo_round_to_bf16_in_place(u.data(), n * I))) return st;
+    if ((st = mm(m[1], I, H, xin, u.data()))) return st;
+    if (mx && (st = urbo_round_to_bf16_in_place(g.data(), n * I))) return st;
+    if (mx && (st = urbo_round_to_bf16_in_place(u.data(), n * I))) return st;
     if ((st = urbo_bounded_swiglu(g.data(), u.data(), n * I, limit, a.data()))) return st;
     if (w)
         for (size_t t = 0; t < n; ++t) {
-            // runtime.rs:2085-2090 rejects a non-finite or negative route weight
+            // v4 runtime.rs:3089-3094, v4.1 runtime.rs:2085-2090: a non-finite or negative
+            // route weight is rejected
             if (!std::isfinite(w[t]) || w[t] < 0.0f) return URBO_INVALID_GEOMETRY;
             for (size_t i = 0; i < I; ++i) a[t * I + i] *= w[t];
         }
     if ((st = urbo_round_to_bf16_in_place(a.data(), n * I))) return st;
-    for (size_t t = 0; t < n; ++t)
-        if ((st = urbo_simulate_e4m3_activation(&a[t * I], I, 32))) return st;
-    st = weight_matmul_fp32_accum(p, format, m[2].data, m[2].scales, H, I, a.data(), n, y);
-    if (st) return st;
-    return urbo_round_to_bf16_in_place(y, n * H);
+    if (mx)
+        for (size_t t = 0; t < n; ++t)
+            if ((st = urbo_simulate_e4m3_activation(&a[t * I], I, block))) return st;
+    if ((st = mm(m[2], H, I, a.data(), y))) return st;
+    return mx ? urbo_round_to_bf16_in_place(y, n * H) : URBO_OK;
+}
+
+// mx_activation / prepare_mx_activation of n tokens [n, H] per `block` values.
+int quantize_rows(const float *x, size_t n, size_t H, size_t block, std::vector<float> &q) {
+    q.assign(x, x + n * H);
+    for (size_t t = 0; t < n; ++t) {
+        int st = urbo_simulate_e4m3_activation(&q[t * H], H, block);
+        if (st) return st;
+    }
+    return URBO_OK;
 }
 
 }  // namespace
@@ -906,8 +973,24 @@ int urbo_dsv41_expert(int format, const urbo_matrix *m, uint32_t H, uint32_t I, 
     std::vector<float> q;
     int st = hy4_quantize(x, n, H, q);
     if (st) return st;
-    return dsv41_expert(pool(threads), format, m, H, I, q.data(), n, swiglu_limit, route_weights,
-                        y);
+    return dsv_expert(pool(threads), true, format, m, H, I, q.data(), n, swiglu_limit,
+                      route_weights, y);
+}
+
+int urbo_dsv4_expert(int format, const urbo_matrix *m, uint32_t H, uint32_t I, const float *x,
+                     uint32_t n, float swiglu_limit, const float *route_weights, float *y,
+                     int threads) {
+    if (H == 0 || I == 0 || n == 0) return URBO_SHAPE;
+    if (format < URBO_FMT_BF16 || format > URBO_FMT_F32) return URBO_SHAPE;
+    if (!all_finite(x, (size_t)n * H)) return URBO_NONFINITE;
+    std::vector<float> q;
+    const bool mx = format == URBO_FMT_MXFP4 || format == URBO_FMT_MXFP8;
+    if (mx) {
+        int st = quantize_rows(x, n, H, 128, q);
+        if (st) return st;
+    }
+    return dsv_expert(pool(threads), false, format, m, H, I, mx ? q.data() : x, n, swiglu_limit,
+                      route_weights, y);
 }
 
 int urbo_gated_mlp(int format, const urbo_matrix *m, uint32_t H, uint32_t I, const float *x,
@@ -925,13 +1008,27 @@ int urbo_qwen_expert(const urbo_matrix *m, uint32_t H, uint32_t I, const float *
 
 int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, int32_t *ids,
                      float *weights, float *logits_out, int threads) {
+    return urbo_moe_forward_tokens(L, x, nullptr, T, y, ids, weights, logits_out, threads);
+}
+
+int urbo_moe_forward_tokens(const urbo_layer *L, const float *x, const uint32_t *tokens,
+                            uint32_t T, float *y, int32_t *ids, float *weights,
+                            float *logits_out, int threads) {
     const size_t H = L->hidden, E = L->n_experts, K = L->top_k, I = L->intermediate;
     if (H == 0 || E == 0 || I == 0 || T == 0) return URBO_SHAPE;
     if (K == 0 || K > E) return URBO_INVALID_GEOMETRY;
     const bool qwen = L->composition == URBO_COMPOSE_QWEN36;
-    const bool dsv = L->composition == URBO_COMPOSE_DSV41;
+    const bool v4 = L->composition == URBO_COMPOSE_DSV4;
+    const bool v41 = L->composition == URBO_COMPOSE_DSV41;
+    const bool dsv = v41 || v4;
     const bool hy4 = L->composition == URBO_COMPOSE_HY4;
-    const bool mxa = hy4 || dsv;  // the MX-activation compositions
+    const bool mxa = hy4 || v41;  // MX projections only
+    auto is_mx = [](int f) { return f == URBO_FMT_MXFP4 || f == URBO_FMT_MXFP8; };
+    // hash experts (the first num_hash_layers layers of DeepSeek V4, runtime.rs:2664-2681): a
+    // [hash_vocab, K] table row per token id; only with route_sqrt_softplus
+    if (L->hash_experts && (L->router != URBO_ROUTER_SQRT_SOFTPLUS || !tokens)) return URBO_SHAPE;
+    if (v4 && !(L->swiglu_limit > 0.0f && std::isfinite(L->swiglu_limit)))
+        return URBO_INVALID_GEOMETRY;
     if (qwen && (L->expert_format != URBO_FMT_BF16 ||
                  (L->shared_intermediate &&
                   (L->shared_format != URBO_FMT_BF16 || !L->shared_expert_gate || !L->shared))))
@@ -947,11 +1044,16 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
     // Router logits: Qwen `linear(router)` (qwen3_8/math.rs:10-26, FP32 GEMV + BF16), DeepSeek
     // V4.1 `router.matvec_fp32_accum` (deepseek_v41/runtime.rs:2136, FP32 GEMV), GLM and Hy4
     // `router.matvec` (ordered f64, bf16.rs:121-216).
+    // DeepSeek V4 `linear(router)` on its BF16 or F32 router is the ordered-f64 matvec too
+    // (deepseek_v4/math.rs:106-115; bf16.rs:121-216, matrix.rs:236-259).
     std::vector<float> logits((size_t)T * E);
     const uint8_t *rw = (const uint8_t *)L->router_weight;
-    int st = qwen ? qwen_linear(p, rw, E, H, x, T, logits.data())
-             : dsv ? bf16_matmul_fp32(p, rw, E, H, x, T, logits.data())
-                   : weight_matmul(p, URBO_FMT_BF16, rw, nullptr, E, H, x, T, logits.data());
+    int st = qwen  ? qwen_linear(p, rw, E, H, x, T, logits.data())
+             : v41 ? bf16_matmul_fp32(p, rw, E, H, x, T, logits.data())
+             : (v4 && L->router_weight_f32)
+                 ? weight_matmul(p, URBO_FMT_F32, (const uint8_t *)L->router_weight_f32, nullptr,
+                                 E, H, x, T, logits.data())
+                 : weight_matmul(p, URBO_FMT_BF16, rw, nullptr, E, H, x, T, logits.data());
     if (st) return st;
     if (logits_out) std::memcpy(logits_out, logits.data(), logits.size() * 4);
 
@@ -962,9 +1064,17 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
         const float *lt = logits.data() + t * E;
         if (L->router == URBO_ROUTER_SOFTMAX_TOPK)
             st = urbo_route_softmax_top_k(lt, E, K, &rid[t * K], &rw8[t * K]);
-        else if (L->router == URBO_ROUTER_SQRT_SOFTPLUS)
-            st = urbo_route_sqrt_softplus(lt, L->correction_bias, E, K, L->routed_scaling_factor,
-                                          &rid[t * K], &rw8[t * K], nullptr);
+        else if (L->router == URBO_ROUTER_SQRT_SOFTPLUS) {
+            const int64_t *row = nullptr;
+            if (L->hash_experts) {
+                // load_i64_matrix_row(tid2eid, token, vocab, K) (runtime.rs:2665-2671)
+                if (tokens[t] >= L->hash_vocab) return URBO_SHAPE;
+                row = L->hash_experts + (size_t)tokens[t] * K;
+            }
+            st = urbo_route_sqrt_softplus_hashed(lt, L->correction_bias, row, E, K,
+                                                 L->routed_scaling_factor, &rid[t * K],
+                                                 &rw8[t * K], nullptr);
+        }
         else
             st = urbo_route_noaux_tc(lt, L->correction_bias, E, K, L->n_group, L->topk_group,
                                      L->normalize, L->routed_scaling_factor, &rid[t * K],
@@ -993,9 +1103,15 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
     }
     // Hy4: one E4M3 activation per token shared by every routed expert and the shared expert
     // (src/models/hy4/runtime.rs:1397, 1311-1312).
+    // DeepSeek V4 prepare_mx_activation (runtime.rs:2691-2693): 128-wide blocks, read by the
+    // MX matrices only.
     std::vector<float> qx;
     if (mxa && (st = hy4_quantize(x, T, H, qx))) return st;
-    const float *xe = mxa ? qx.data() : x;
+    if (v4 && (is_mx(L->expert_format) || (L->shared_intermediate && is_mx(L->shared_format))) &&
+        (st = quantize_rows(x, T, H, 128, qx)))
+        return st;
+    const float *xe = mxa || (v4 && is_mx(L->expert_format)) ? qx.data() : x;
+    const float *xs = mxa || (v4 && is_mx(L->shared_format)) ? qx.data() : x;
     // Expert outputs per route slot.
     std::vector<float> out((size_t)T * K * H);
     for (const Group &g : groups) {
@@ -1011,8 +1127,8 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
         st = qwen  ? qwen_expert(p, m, H, I, xin.data(), n, yo.data())
              : hy4 ? hy4_routed(p, L->expert_format, m, H, I, xin.data(), n, L->swiglu_limit,
                                 yo.data())
-             : dsv ? dsv41_expert(p, L->expert_format, m, H, I, xin.data(), n, L->swiglu_limit,
-                                  wr.data(), yo.data())
+             : dsv ? dsv_expert(p, v41, L->expert_format, m, H, I, xin.data(), n,
+                                L->swiglu_limit, wr.data(), yo.data())
                    : gated_mlp(p, L->expert_format, m, H, I, xin.data(), n, yo.data());
         if (st) return st;
         for (size_t i = 0; i < n; ++i)
@@ -1074,18 +1190,18 @@ int urbo_moe_forward(const urbo_layer *L, const float *x, uint32_t T, float *y, 
         return URBO_OK;
     }
 
-    if (mxa) {
+    if (mxa || v4) {
         // Hy4 MoeWeights::forward (src/models/hy4/runtime.rs:1387-1445): f32 sum of w * y over
         // the routes in ascending expert id, plus the shared expert, rounded to BF16.  DeepSeek
-        // V4.1 (deepseek_v41/runtime.rs:1963-2019) the same with the route weight already
-        // applied inside each expert (the sum adds y).
+        // V4.1 (deepseek_v41/runtime.rs:1963-2019) and V4 (deepseek_v4/runtime.rs:2498-2653) the
+        // same with the route weight already applied inside each expert (the sum adds y).
         std::vector<float> sh;
         if (L->shared_intermediate) {
             sh.resize((size_t)T * H);
             st = hy4 ? hy4_shared(p, L->shared_format, L->shared, H, L->shared_intermediate,
                                   qx.data(), T, sh.data())
-                     : dsv41_expert(p, L->shared_format, L->shared, H, L->shared_intermediate,
-                                    qx.data(), T, L->swiglu_limit, nullptr, sh.data());
+                     : dsv_expert(p, v41, L->shared_format, L->shared, H, L->shared_intermediate,
+                                  xs, T, L->swiglu_limit, nullptr, sh.data());
             if (st) return st;
         }
         for (size_t t = 0; t < T; ++t) {

@@ -34,11 +34,17 @@ enum {
     URBO_INVALID_GEOMETRY = 4, /* RouteError::InvalidGeometry, Qwen38MoeError::InvalidGeometry */
 };
 
-enum { URBO_FMT_BF16 = 0, URBO_FMT_MXFP4 = 1, URBO_FMT_MXFP8 = 2 };
+/* F32: little-endian f32 [rows, cols], WeightMatrix::F32 (src/model/matrix.rs), the format of
+ * DeepSeek V4's reference fixtures. */
+enum { URBO_FMT_BF16 = 0, URBO_FMT_MXFP4 = 1, URBO_FMT_MXFP8 = 2, URBO_FMT_F32 = 3 };
 enum { URBO_ROUTER_SOFTMAX_TOPK = 0, URBO_ROUTER_SIGMOID_NOAUX_TC = 1, URBO_ROUTER_SQRT_SOFTPLUS = 2 };
 /* QWEN36: execute_streamed_moe / execute_batched_moe (src/models/qwen3_6/runtime.rs:1067-1243).
- * GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176). */
-enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1, URBO_COMPOSE_HY4 = 2, URBO_COMPOSE_DSV41 = 3 };
+ * GLM:    RuntimeMoeLayer::forward (src/models/glm/runtime/moe.rs:138-176).
+ * HY4:    Hy4 MoeWeights::forward (src/models/hy4/runtime.rs:1371-1447).
+ * DSV41:  DeepSeek-V4.1 MoeWeights::forward (src/models/deepseek_v41/runtime.rs:1963-2019).
+ * DSV4:   DeepSeek-V4 MoeWeights::forward{,_batch} (src/models/deepseek_v4/runtime.rs:2484-2828). */
+enum { URBO_COMPOSE_QWEN36 = 0, URBO_COMPOSE_GLM = 1, URBO_COMPOSE_HY4 = 2, URBO_COMPOSE_DSV41 = 3,
+       URBO_COMPOSE_DSV4 = 4 };
 
 /* ---- element decoders (src/math/mxfp.rs, src/model/bf16.rs, src/models/qwen3_8/math.rs) ---- */
 int urbo_decode_e8m0(uint8_t code, float *out);
@@ -78,6 +84,11 @@ int urbo_route_noaux_tc(const float *logits, const float *bias, size_t n, size_t
 /* route_sqrt_softplus (src/models/deepseek_v4/math.rs:451-516), no hash experts. */
 int urbo_route_sqrt_softplus(const float *logits, const float *bias, size_t n, size_t top_k,
                              float scale, int32_t *ids, float *weights, float *selection_out);
+/* The same with hash_experts = hash[0..top_k) (NULL: none); ids out of range ->
+ * URBO_INVALID_GEOMETRY (DeepseekMathError::Invalid). */
+int urbo_route_sqrt_softplus_hashed(const float *logits, const float *bias, const int64_t *hash,
+                                    size_t n, size_t top_k, float scale, int32_t *ids,
+                                    float *weights, float *selection_out);
 float urbo_silu(float value);
 /* Selects MxFp8Matrix::matvec_rows's host kernel for layer calls (src/math/mxfp.rs:720-765):
  * 1 = compact 8-lane FMA (AVX2+FMA hosts, the default), 0 = ordered f64.  Returns the previous. */
@@ -114,8 +125,13 @@ typedef struct {
     const float *correction_bias;  /* [E] or NULL (zeros) */
     const urbo_matrix *experts;    /* [E][3] = gate [I,H], up [I,H], down [H,I] */
     const urbo_matrix *shared;     /* [3] or NULL */
-    float swiglu_limit;            /* HY4, DSV41: bounded SwiGLU limit */
+    float swiglu_limit;            /* HY4, DSV41, DSV4: bounded SwiGLU limit */
     const uint16_t *shared_expert_gate; /* QWEN36 with a shared expert: [H] BF16 gate row */
+    /* DeepSeek hash routing: layers.N.ffn.gate.tid2eid [hash_vocab, top_k] (NULL = none); the
+     * layer call then needs token ids (urbo_moe_forward_tokens). */
+    const int64_t *hash_experts;
+    uint32_t hash_vocab;
+    const float *router_weight_f32; /* DSV4: an F32 [E, H] router instead of router_weight */
 } urbo_layer;
 
 /* Hy4 MX-activation experts over n tokens [n, H] -> [n, H] (x is quantized here):
@@ -129,6 +145,12 @@ int urbo_hy4_expert(int format, const urbo_matrix *gate_up_down, uint32_t hidden
 int urbo_dsv41_expert(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
                       uint32_t intermediate, const float *x, uint32_t n, float swiglu_limit,
                       const float *route_weights, float *y, int threads);
+/* DeepSeek-V4 DeepExpert::forward_with_mx_input{,_batch} (src/models/deepseek_v4/runtime.rs:
+ * 3081-3155) over n tokens [n, H]: MX weights read x quantized per 128 values (here) and round
+ * their outputs to BF16; BF16 and F32 weights read x as it is. */
+int urbo_dsv4_expert(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
+                     uint32_t intermediate, const float *x, uint32_t n, float swiglu_limit,
+                     const float *route_weights, float *y, int threads);
 /* GatedMlp::forward (src/model/mlp.rs:90-99) over n tokens [n, H] -> [n, H]. */
 int urbo_gated_mlp(int format, const urbo_matrix *gate_up_down, uint32_t hidden,
                    uint32_t intermediate, const float *x, uint32_t n, float *y, int threads);
@@ -142,6 +164,11 @@ int urbo_qwen_expert(const urbo_matrix *gate_up_down, uint32_t hidden, uint32_t 
  * Returns the first error in token order. */
 int urbo_moe_forward(const urbo_layer *layer, const float *x, uint32_t tokens, float *y,
                      int32_t *ids, float *weights, float *logits, int threads);
+/* The same with the tokens' ids [tokens] (hash routing reads the layer's tid2eid row of each;
+ * an id >= hash_vocab -> URBO_SHAPE). */
+int urbo_moe_forward_tokens(const urbo_layer *layer, const float *x, const uint32_t *token_ids,
+                            uint32_t tokens, float *y, int32_t *ids, float *weights,
+                            float *logits, int threads);
 
 /* Bytes of one expert matrix for a format. */
 size_t urbo_matrix_bytes(int format, size_t rows, size_t cols, size_t *scale_bytes);

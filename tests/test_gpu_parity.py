@@ -32,10 +32,11 @@ def moe_mod():
     return moe
 
 
-def _oracle(host: C.HostLayer, x: np.ndarray, threads: int = 4):
+def _oracle(host: C.HostLayer, x: np.ndarray, threads: int = 4, token_ids=None):
     return O.moe_forward(host.spec, host.experts, host.router_weight, x, host.correction_bias,
                          host.shared, threads=threads,
-                         shared_expert_gate=host.shared_expert_gate)
+                         shared_expert_gate=host.shared_expert_gate, token_ids=token_ids,
+                         hash_experts=host.hash_experts)
 
 
 def _scores(spec, res, bias):
@@ -332,7 +333,35 @@ def test_quantize_e4m3_matches_simulate_e4m3_activation_bit_exact():
         assert not np.any((c & 0x7F) == 0x7F)  # never a NaN code
 
 
-MX_LAYERS = [(comp, fmt, T) for comp in (C.COMPOSE_HY4, C.COMPOSE_DSV41)
+def test_quantize_e4m3_128_value_blocks_bit_exact():
+    # DeepSeek V4's prepare_mx_activation: simulate_e4m3_activation(x, 128)
+    dec8 = np.array([O.decode_e4m3fn(c) for c in range(256)], np.float32)
+    for r in _quantizer_cases():
+        x = np.ascontiguousarray(r[: r.size // 128 * 128].reshape(1, -1))
+        if x.size == 0:
+            continue
+        codes, scales = moe_mod().quantize_e4m3(torch.from_numpy(x).cuda(), block=128)
+        torch.cuda.synchronize()
+        c = codes.cpu().numpy().ravel()
+        s = scales.cpu().numpy().ravel().astype(np.int64)
+        got = dec8[c] * np.exp2(np.repeat(s - 127, 128)).astype(np.float32)
+        ref = O.simulate_e4m3_activation(x.ravel(), 128)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # blocks of 32 whose magnitudes alternate by 2^16: the 128-value scale differs from the
+    # 32-value one and puts the small blocks on E4M3's subnormal grid
+    x = synth.activations("x.q128", 2, 512)
+    x = np.ascontiguousarray(x * np.repeat(np.exp2(16.0 * (np.arange(16) % 2)), 32),
+                             dtype=np.float32)
+    c128, s128 = moe_mod().quantize_e4m3(torch.from_numpy(x).cuda(), block=128)
+    torch.cuda.synchronize()
+    got = dec8[c128.cpu().numpy()] * np.exp2(
+        np.repeat(s128.cpu().numpy().astype(np.int64) - 127, 128, axis=1)).astype(np.float32)
+    ref = np.stack([O.simulate_e4m3_activation(row, 128) for row in x])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert not np.array_equal(ref, np.stack([O.simulate_e4m3_activation(row, 32) for row in x]))
+
+
+MX_LAYERS = [(comp, fmt, T) for comp in (C.COMPOSE_HY4, C.COMPOSE_DSV41, C.COMPOSE_DSV4)
              for fmt in (C.FMT_MXFP4, C.FMT_MXFP8) for T in (1, 5, 40)]
 
 
@@ -376,6 +405,68 @@ def test_dsv41_router_logits_are_the_fp32_tree_bit_for_bit():
     assert np.any((logits.view(np.uint32) & 0xFFFF) != 0)  # not BF16-rounded
     assert ids_match(ids.cpu().numpy(), ref.ids, _scores(host.spec, ref, host.correction_bias))
     layer.close()
+
+
+def _dsv4_hash_layer(fmt=C.FMT_MXFP4, vocab=50, n_experts=32, top_k=6):
+    spec = C.LayerSpec(hidden=256, n_experts=n_experts, top_k=top_k, intermediate=128,
+                       shared_intermediate=128, expert_format=fmt, shared_format=fmt,
+                       router=C.ROUTER_SQRT_SOFTPLUS, composition=C.COMPOSE_DSV4,
+                       routed_scaling_factor=1.5, swiglu_limit=10.0)
+    return C.make_host_layer(spec, hash_vocab=vocab)
+
+
+@pytest.mark.parametrize("fmt,T", [(C.FMT_MXFP4, 1), (C.FMT_MXFP4, 7), (C.FMT_MXFP8, 40),
+                                   (C.FMT_MXFP4, 300)])
+def test_dsv4_hash_layer_matches_oracle(fmt, T):
+    # DeepSeek V4's hash layers: the token's tid2eid row gives the experts in table order, the
+    # weights s / sum(s) * 1.5 over that row (deepseek_v4/math.rs:451-516, runtime.rs:2664-2681)
+    host = _dsv4_hash_layer(fmt)
+    x = synth.activations(f"x.dsv4.hash.{T}", T, host.spec.hidden)
+    tokens = (synth.splitmix64(synth.stream_seed(f"tok.{T}"), 0, T) % 50).astype(np.uint32)
+    tokens[T // 2:] = tokens[: T - T // 2]  # repeated tokens
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    tok = torch.from_numpy(tokens.view(np.int32)).cuda()
+    y, ids, w = layer.forward(torch.from_numpy(x).cuda(), token_ids=tok)
+    ref = _oracle(host, x, token_ids=tokens)
+    ids = ids.cpu().numpy()
+    assert np.array_equal(ids, ref.ids)
+    assert np.array_equal(ids, host.hash_experts[tokens].astype(np.int32))
+    assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    err = rel_l2(y.cpu().numpy(), ref.output)
+    assert err < REL_L2_BAR, err
+    logits, rids, rw = layer.route(torch.from_numpy(x).cuda(), token_ids=tok)
+    assert np.array_equal(rids.cpu().numpy(), ref.ids)
+    assert np.allclose(logits.cpu().numpy(), ref.logits, rtol=2e-6, atol=1e-7)
+    layer.close()
+
+
+def test_dsv4_hash_errors():
+    host = _dsv4_hash_layer()
+    x = torch.from_numpy(synth.activations("x.dsv4.err", 3, host.spec.hidden)).cuda()
+    layer = moe_mod().MoeLayer(host, max_tokens=3)
+    with pytest.raises(N.UrbError) as e:  # hash routing needs the token ids
+        layer.forward(x)
+    assert e.value.status == N.ERR_ARGUMENT
+    with pytest.raises(N.UrbError) as e:  # token id outside the table (load_i64_matrix_row)
+        layer.forward(x, token_ids=torch.tensor([3, 50, 1], dtype=torch.int32, device="cuda"))
+    assert e.value.status == N.ERR_SHAPE
+    y, ids, _ = layer.forward(x, token_ids=torch.tensor([3, 49, 1], dtype=torch.int32,
+                                                        device="cuda"))
+    assert np.array_equal(ids.cpu().numpy(), host.hash_experts[[3, 49, 1]])
+    layer.close()
+    bad = host.hash_experts.copy()
+    bad[7, 2] = host.spec.n_experts  # "hash expert IDs must be in range"
+    dup = host.hash_experts.copy()
+    dup[9, 1] = dup[9, 0]
+    for table, spec, status in ((bad, host.spec, N.ERR_INVALID_GEOMETRY),
+                                (dup, host.spec, N.ERR_ARGUMENT),
+                                (host.hash_experts,
+                                 replace(host.spec, router=C.ROUTER_SIGMOID_NOAUX_TC),
+                                 N.ERR_ARGUMENT)):
+        h = replace(host, spec=spec, hash_experts=table)
+        with pytest.raises(N.UrbError) as e:
+            moe_mod().MoeLayer(h, max_tokens=1)
+        assert e.value.status == status
 
 
 def test_hy4_errors():

@@ -30,6 +30,39 @@ def test_moe_library_exports_every_declared_symbol():
     assert set(N.EXPORTS) == set(declared)
 
 
+def _prototypes(header):
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", header)).read(),
+                  flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(urb_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        ps = [p.strip() for p in params.replace("\n", " ").split(",")]
+        out[name] = [p for p in ps if p and p != "void"]
+    return out
+
+
+_SCALARS = {"uint32_t": ctypes.c_uint32, "int": ctypes.c_int, "float": ctypes.c_float,
+            "urb_format": ctypes.c_int, "urb_weight_source": ctypes.c_int,
+            "urb_status": ctypes.c_int}
+
+
+def test_moe_bindings_match_the_header_prototypes():
+    # Every ctypes binding passes each parameter as the header declares it: pointers as
+    # pointer-sized values, scalars as their C type (a pointer bound as an int would be cut to
+    # 32 bits).
+    lib = N.moe_lib()
+    protos = _prototypes("urb_moe.h")
+    assert set(protos) == set(N.EXPORTS)
+    for name, params in protos.items():
+        at = getattr(lib, name).argtypes
+        assert at is not None and len(at) == len(params), name
+        for p, t in zip(params, at):
+            if "*" in p:
+                assert t is ctypes.c_void_p or issubclass(t, ctypes._Pointer), (name, p, t)
+            else:
+                ctype = p.replace("const ", "").rsplit(" ", 1)[0].strip()
+                assert t is _SCALARS[ctype], (name, p, t)
+
+
 def test_synth_library_exports():
     lib = ctypes.CDLL(N.SYNTH_LIB)
     for name in N.SYNTH_EXPORTS:

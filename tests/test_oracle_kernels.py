@@ -7,6 +7,7 @@ import os
 import struct
 from dataclasses import replace
 from fractions import Fraction
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -720,6 +721,185 @@ def test_dsv41_layer_composition(fmt):
         ys = {int(e): O.dsv41_expert(fmt, layer.experts[e], H, I, x[t], 7.0, [w[j]])[0]
               for j, e in enumerate(ids)}
         sh = O.dsv41_expert(fmt, layer.shared, H, I, x[t], 7.0, None)[0]
+        acc = np.zeros(H, np.float32)
+        for e in sorted(ys):
+            acc = acc + ys[e]
+        out = _bf16(acc + sh)
+        assert np.array_equal(out.view(np.uint32), res.output[t].view(np.uint32))
+
+
+# ------------------------------------------------------------ DeepSeek V4 (hash routing, 128)
+TINY_V4 = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                      "deepseek_v4_tiny_moe.json")))
+
+
+def _v4_tensor(name):
+    t = TINY_V4["weights"][name]
+    dtype = {"F32": np.float32, "I64": np.int64}[t["dtype"]]
+    return np.array(t["values"], dtype).reshape(t["shape"])
+
+
+def _v4_tiny_layer():
+    g = TINY_V4["geometry"]
+    E, H, I, K = (g["n_routed_experts"], g["hidden_size"], g["moe_intermediate_size"],
+                  g["num_experts_per_tok"])
+    spec = SimpleNamespace(hidden=H, n_experts=E, top_k=K, intermediate=I, shared_intermediate=I,
+                           expert_format=O.FMT_F32, shared_format=O.FMT_F32,
+                           router=O.ROUTER_SQRT_SOFTPLUS, composition=O.COMPOSE_DSV4, n_group=1,
+                           topk_group=1, normalize=1,
+                           routed_scaling_factor=g["routed_scaling_factor"],
+                           swiglu_limit=g["swiglu_limit"])
+
+    def triple(prefix):
+        return [(_v4_tensor(f"{prefix}.{w}.weight"), None) for w in ("w1", "w3", "w2")]
+    experts = [triple(f"layers.0.ffn.experts.{e}") for e in range(E)]
+    shared = triple("layers.0.ffn.shared_experts")
+    return spec, experts, shared
+
+
+def test_dsv4_tiny_fixture_hash_moe_layer():
+    # The reference's independent tiny oracle (tests/fixtures/deepseek_v4_tiny_oracle.json,
+    # consumed by independent_tiny_oracle_matches_one_hash_moe_layer, deepseek_v4/runtime.rs:
+    # 4604-4645): F32 router and experts, token 2's tid2eid row [2, 0] as the routes, route
+    # weight s / sum(s) * 1.5 in table order, the weight applied before w2, an f32 sum in
+    # ascending expert id plus the shared expert, BF16.
+    spec, experts, shared = _v4_tiny_layer()
+    ex = TINY_V4["expected"]
+    x = np.array([ex["ffn_input"]], np.float32)
+    router = _v4_tensor("layers.0.ffn.gate.weight")
+    table = _v4_tensor("layers.0.ffn.gate.tid2eid")
+    E, H, I = spec.n_experts, spec.hidden, spec.intermediate
+    res = O.moe_forward(spec, experts, np.zeros((E, H), np.uint16), x, shared=shared,
+                        token_ids=np.array([TINY_V4["token"]]), hash_experts=table,
+                        router_weight_f32=router)
+    np.testing.assert_allclose(res.logits[0], ex["router_logits"], rtol=1e-6)
+    routes = ex["routes"]
+    assert list(res.ids[0]) == [r["expert"] for r in routes] == [2, 0]
+    np.testing.assert_allclose(res.weights[0], [r["weight"] for r in routes], rtol=1e-6)
+    ids, w, sel = O.route_sqrt_softplus(res.logits[0], None, 2, 1.5,
+                                        hash_experts=table[TINY_V4["token"]])
+    np.testing.assert_allclose(sel, [r["selection_score"] for r in routes], rtol=1e-6)
+    for j, e in enumerate(ids):
+        y = O.dsv4_expert(O.FMT_F32, experts[e], H, I, x, spec.swiglu_limit, [w[j]])[0]
+        np.testing.assert_allclose(y, ex["routed_experts"][j], rtol=1e-6)
+    sh = O.dsv4_expert(O.FMT_F32, shared, H, I, x, spec.swiglu_limit, None)[0]
+    np.testing.assert_allclose(sh, ex["shared_expert"], rtol=1e-6)
+    assert list(res.output[0]) == ex["moe_branch"]
+
+
+def test_dsv4_hash_routing_errors():
+    spec, experts, shared = _v4_tiny_layer()
+    x = np.array([TINY_V4["expected"]["ffn_input"]], np.float32)
+    router = _v4_tensor("layers.0.ffn.gate.weight")
+    table = _v4_tensor("layers.0.ffn.gate.tid2eid")
+    rw = np.zeros((spec.n_experts, spec.hidden), np.uint16)
+
+    def run(tokens, tab):
+        return O.moe_forward(spec, experts, rw, x, shared=shared, token_ids=tokens,
+                             hash_experts=tab, router_weight_f32=router)
+    with pytest.raises(O.OracleError) as e:  # load_i64_matrix_row: token outside the vocab
+        run(np.array([4]), table)
+    assert e.value.status == O.SHAPE
+    with pytest.raises(O.OracleError) as e:  # a hash table needs the token ids
+        run(None, table)
+    assert e.value.status == O.SHAPE
+    bad = table.copy()
+    bad[2, 1] = 3  # "hash expert IDs must be in range" (math.rs:483-489)
+    with pytest.raises(O.OracleError) as e:
+        run(np.array([2]), bad)
+    assert e.value.status == O.INVALID_GEOMETRY
+    with pytest.raises(O.OracleError) as e:
+        O.route_sqrt_softplus(np.zeros(3, np.float32), None, 2, 1.5, hash_experts=[0])
+    assert e.value.status == O.SHAPE
+    # the hash row replaces the ranking but the checks on logits still run (math.rs:469-476)
+    with pytest.raises(O.OracleError) as e:
+        O.route_sqrt_softplus(np.array([0.0, np.inf, 0.0], np.float32), None, 2, 1.5,
+                              hash_experts=[0, 2])
+    assert e.value.status == O.NONFINITE
+    # table order, not ranking order: the weights follow the ids given
+    ids, w, _ = O.route_sqrt_softplus(np.array([3.0, -1.0, 0.5], np.float32), None, 2, 1.0,
+                                      hash_experts=[1, 0])
+    assert list(ids) == [1, 0] and w[0] < w[1]
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_MXFP8, O.FMT_MXFP4])
+def test_dsv4_expert_reads_128_wide_activation_blocks(fmt):
+    # DeepExpert::forward_with_mx_input{,_batch} (deepseek_v4/runtime.rs:3081-3155) with MX
+    # weights: gate/up = bf16(matvec(w, simulate_e4m3_activation(x, 128))), bounded SwiGLU, route
+    # weight, BF16, 128-wide re-quantization, bf16(matvec(w2, .)).  Evaluated from the pinned
+    # matvec and quantizer.  The input's 32-value blocks alternate in magnitude by 2^16: a
+    # power-of-two scale leaves E4M3 rounding unchanged in the normal range, but 128-wide blocks
+    # push the small blocks into E4M3's subnormals, so 32-wide blocks (V4.1's) differ.
+    H, I, limit = 256, 128, 2.0
+    if fmt == O.FMT_MXFP8:
+        rng = np.random.default_rng(8)
+        fin = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+        triple = [(rng.choice(fin, (r, c_)).astype(np.uint8),
+                   rng.integers(116, 121, (r, c_ // 32)).astype(np.uint8))
+                  for r, c_ in ((I, H), (I, H), (H, I))]
+    else:
+        triple = [synth.mxfp4_matrix(f"dsv4.{n}", r, c_) for n, r, c_ in
+                  (("g", I, H), ("u", I, H), ("d", H, I))]
+    x = synth.activations("dsv4.x", 3, H)
+    x = (x * np.repeat(np.exp2(16.0 * (np.arange(H // 32) % 2)), 32)[None, :]).astype(np.float32)
+    rw = np.array([0.25, 1.0, 0.7], np.float32)
+    got = O.dsv4_expert(fmt, triple, H, I, x, limit, rw)
+    for t in range(x.shape[0]):
+        q = O.simulate_e4m3_activation(x[t], 128)
+        g = _bf16(O.matvec_rows(fmt, *triple[0], I, H, q))
+        u = _bf16(O.matvec_rows(fmt, *triple[1], I, H, q))
+        a = _bf16(O.bounded_swiglu(g, u, limit) * rw[t])
+        a = O.simulate_e4m3_activation(a, 128)
+        y = _bf16(O.matvec_rows(fmt, *triple[2], H, I, a))
+        assert np.array_equal(y.view(np.uint32), got[t].view(np.uint32))
+    # identity weights make every output read one input column: the small blocks keep E4M3's
+    # normal precision in 32-wide blocks and fall onto its coarser subnormal grid in 128-wide
+    # ones
+    n = 256
+    if fmt == O.FMT_MXFP8:
+        eye = _identity_mxfp8(n)
+    else:
+        codes = np.zeros((n, n // 2), np.uint8)
+        codes[np.arange(n), np.arange(n) // 2] = np.where(np.arange(n) % 2 == 0, 0x02, 0x20)
+        eye = (codes, np.full((n, n // 32), 127, np.uint8))  # E2M1 0x2 = 1.0, low nibble first
+    eyes = [eye, eye, eye]
+    xs = np.abs(x[:1]) + np.float32(1.0)
+    v4 = O.dsv4_expert(fmt, eyes, n, n, xs, 20.0, None)[0]
+    v41 = O.dsv41_expert(fmt, eyes, n, n, xs, 20.0, None)[0]
+    small = np.repeat(np.arange(n // 32) % 2 == 0, 32)
+    assert len(np.unique(v4[small])) < len(np.unique(v41[small]))
+    assert not np.array_equal(v4[small], v41[small])
+
+
+@pytest.mark.parametrize("fmt", [O.FMT_MXFP8, O.FMT_MXFP4])
+@pytest.mark.parametrize("hashed", [False, True])
+def test_dsv4_layer_composition(fmt, hashed):
+    # DeepSeek-V4 MoeWeights::forward (deepseek_v4/runtime.rs:2484-2653) from pinned parts: the
+    # ordered-f64 BF16 router (bf16.rs:121-216), route_sqrt_softplus with the bias (or the token's
+    # tid2eid row), each routed expert with its weight, the shared expert without, then
+    # out = sum over ascending expert id of y (f32) + shared, BF16.
+    E, H, I, K, T = 8, 256, 128, 3, 6
+    spec = C.LayerSpec(hidden=H, n_experts=E, top_k=K, intermediate=I, shared_intermediate=I,
+                       expert_format=fmt, shared_format=fmt, router=C.ROUTER_SQRT_SOFTPLUS,
+                       composition=O.COMPOSE_DSV4, routed_scaling_factor=1.5, swiglu_limit=7.0)
+    bias = (np.arange(E, dtype=np.float32) - E / 2) * np.float32(0.02)
+    layer = C.make_host_layer(replace(spec, composition=C.COMPOSE_DSV41), bias=bias)
+    x = synth.activations("dsv4.layer", T, H)
+    vocab = 11
+    table = np.array([np.roll(np.arange(E), v)[:K] for v in range(vocab)], np.int64)
+    tokens = np.array([3, 0, 10, 3, 7, 5], np.uint32)
+    res = O.moe_forward(spec, layer.experts, layer.router_weight, x, layer.correction_bias,
+                        layer.shared, token_ids=tokens if hashed else None,
+                        hash_experts=table if hashed else None)
+    for t in range(T):
+        logits = O.matvec_rows(O.FMT_BF16, layer.router_weight, None, E, H, x[t])
+        assert np.array_equal(logits.view(np.uint32), res.logits[t].view(np.uint32))
+        ids, w, _ = O.route_sqrt_softplus(logits, layer.correction_bias, K, 1.5,
+                                          hash_experts=table[tokens[t]] if hashed else None)
+        assert list(ids) == list(res.ids[t]) and np.array_equal(w, res.weights[t])
+        ys = {int(e): O.dsv4_expert(fmt, layer.experts[e], H, I, x[t], 7.0, [w[j]])[0]
+              for j, e in enumerate(ids)}
+        sh = O.dsv4_expert(fmt, layer.shared, H, I, x[t], 7.0, None)[0]
         acc = np.zeros(H, np.float32)
         for e in sorted(ys):
             acc = acc + ys[e]

@@ -16,6 +16,10 @@ routed_scaling_factor) plus the projection formats of ``WeightMatrix``
   (src/models/deepseek_v41/runtime.rs:1963-2019): FP32 router GEMV, sqrt-softplus routing,
   experts with FP32-accumulated projections whose SwiGLU output is scaled by the route weight
   before the BF16 step and the down projection, f32 ascending-id sum plus the shared expert.
+* ``COMPOSE_DSV4`` -- DeepSeek-V4 MoeWeights::forward{,_batch}
+  (src/models/deepseek_v4/runtime.rs:2484-2828): as ``COMPOSE_DSV41`` with the ordered f64
+  router GEMV and 128-value activation blocks; its first layers route by a tid2eid table
+  (``HostLayer.hash_experts``) instead of the scores.
 * ``COMPOSE_HY4`` -- the MX-activation mode, Hy4 MoeWeights::forward
   (src/models/hy4/runtime.rs:1371-1447): ordered f64 router GEMV, every MX projection fed by
   simulate_e4m3_activation(x, 32), routed experts with BF16 gate/up and a bounded SwiGLU
@@ -34,7 +38,7 @@ from . import synth
 
 FMT_BF16, FMT_MXFP4, FMT_MXFP8 = 0, 1, 2
 ROUTER_SOFTMAX_TOPK, ROUTER_SIGMOID_NOAUX_TC, ROUTER_SQRT_SOFTPLUS = 0, 1, 2
-COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4, COMPOSE_DSV41 = 0, 1, 2, 3
+COMPOSE_QWEN36, COMPOSE_GLM, COMPOSE_HY4, COMPOSE_DSV41, COMPOSE_DSV4 = 0, 1, 2, 3, 4
 FORMAT_NAMES = {FMT_BF16: "bf16", FMT_MXFP4: "mxfp4", FMT_MXFP8: "mxfp8"}
 
 
@@ -93,6 +97,7 @@ class Workload:
     tokens: Tuple[int, ...]
     zipf_s: Optional[float] = None
     description: str = ""
+    hash_vocab: int = 0   # > 0: routed by a synthetic tid2eid table of this many token ids
 
 
 # The five benchmark configurations (shapes, routers, formats and value distributions).
@@ -182,12 +187,39 @@ QWEN36_RELEASE_WORKLOADS: Dict[str, Workload] = {
 }
 
 
+# The DeepSeek-V4 Flash MoE geometry (the reference's tests/fixtures/
+# deepseek_v4_flash_0731_config.json: hidden 4096, 256 routed experts of I 2048, top-6, one
+# shared expert, routed_scaling_factor 1.5, swiglu_limit 10, FP4 experts, sqrt-softplus scores,
+# 3 hash layers over a 129280-token vocabulary) in the DSV4 composition; the shared expert is
+# synthesized in MXFP4 like the routed ones.
+DSV4_WORKLOADS: Dict[str, Workload] = {
+    "dsv4_flash": Workload(
+        "dsv4_flash",
+        LayerSpec(hidden=4096, n_experts=256, top_k=6, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_MXFP4,
+                  router=ROUTER_SQRT_SOFTPLUS, composition=COMPOSE_DSV4,
+                  routed_scaling_factor=1.5, swiglu_limit=10.0),
+        (1, 1024), zipf_s=1.1,
+        description="DeepSeek-V4 Flash MoE: MXFP4 H4096 E256 sqrt-softplus top-6 + Zipf(1.1) "
+                    "bias I2048 + MXFP4 shared, 128-value MX activations, decode 1, prefill "
+                    "1024"),
+    "dsv4_flash_hash": Workload(
+        "dsv4_flash_hash",
+        LayerSpec(hidden=4096, n_experts=256, top_k=6, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_MXFP4,
+                  router=ROUTER_SQRT_SOFTPLUS, composition=COMPOSE_DSV4,
+                  routed_scaling_factor=1.5, swiglu_limit=10.0),
+        (1, 1024), hash_vocab=129280,
+        description="DeepSeek-V4 Flash hash layer: as dsv4_flash, experts from a synthetic "
+                    "129280 x 6 tid2eid table indexed by uniform token ids"),
+}
+
+
 def workload(name: str) -> Workload:
     """A benchmark configuration or one of its variants, by name."""
-    if name in WORKLOADS:
-        return WORKLOADS[name]
-    if name in QWEN36_RELEASE_WORKLOADS:
-        return QWEN36_RELEASE_WORKLOADS[name]
+    for table in (WORKLOADS, QWEN36_RELEASE_WORKLOADS, DSV4_WORKLOADS):
+        if name in table:
+            return table[name]
     return MX_ACTIVATION_WORKLOADS[name]
 
 
@@ -201,6 +233,24 @@ class HostLayer:
     shared: Optional[List[Tuple[np.ndarray, Optional[np.ndarray]]]] = None
     correction_bias: Optional[np.ndarray] = None     # [E] f32
     shared_expert_gate: Optional[np.ndarray] = None  # [H] uint16 BF16 (QWEN36 shared expert)
+    hash_experts: Optional[np.ndarray] = None        # [vocab, k] int64 tid2eid (sqrt-softplus)
+
+
+def hash_table(vocab: int, n_experts: int, top_k: int,
+               base_seed: int = synth.BASE_SEED) -> np.ndarray:
+    """A synthetic tid2eid table [vocab, top_k] (int64): row v holds the distinct expert ids
+    (a_v + j * b_v) mod E, j < top_k, with seeded a_v and a seeded stride b_v coprime to E."""
+    E = n_experts
+    keys = synth.splitmix64(synth.stream_seed("tid2eid", base_seed), 0, 2 * vocab)
+    start = (keys[0::2] % np.uint64(E)).astype(np.int64)
+    stride = (keys[1::2] % np.uint64(E)).astype(np.int64) | 1
+    while True:  # step each stride until coprime with E (E = 1: any stride)
+        bad = np.gcd(stride, E) != 1
+        if E == 1 or not bad.any():
+            break
+        stride[bad] += 1
+    j = np.arange(top_k, dtype=np.int64)
+    return np.ascontiguousarray((start[:, None] + j[None, :] * stride[:, None]) % E)
 
 
 def _matrix(fmt: int, name: str, rows: int, cols: int, base_seed: int):
@@ -212,7 +262,7 @@ def _matrix(fmt: int, name: str, rows: int, cols: int, base_seed: int):
 
 
 def make_host_layer(spec: LayerSpec, base_seed: int = synth.BASE_SEED,
-                    bias: Optional[np.ndarray] = None) -> HostLayer:
+                    bias: Optional[np.ndarray] = None, hash_vocab: int = 0) -> HostLayer:
     """Generates a layer on the host (numpy).  Practical for small shapes only; full-size
     layers are generated on the device by ``urbilateria_amd.device.make_device_layer``."""
     H, I, E = spec.hidden, spec.intermediate, spec.n_experts
@@ -235,7 +285,8 @@ def make_host_layer(spec: LayerSpec, base_seed: int = synth.BASE_SEED,
     gate = None
     if spec.shared_intermediate and spec.composition == COMPOSE_QWEN36:
         gate = synth.bf16_matrix("shared.expert_gate", 1, H, 0.02, base_seed).reshape(H)
-    return HostLayer(spec, router, experts, shared, bias, gate)
+    table = hash_table(hash_vocab, E, spec.top_k, base_seed) if hash_vocab else None
+    return HostLayer(spec, router, experts, shared, bias, gate, table)
 
 
 def zipf_bias(n_experts: int, s: float, beta: float, base_seed: int = synth.BASE_SEED) -> np.ndarray:

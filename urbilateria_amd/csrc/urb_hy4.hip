@@ -56,11 +56,14 @@ __device__ __forceinline__ uint32_t encode_e4m3(float value) {
   return (value < 0.0f && code != 0) ? (code | 0x80u) : code;
 }
 
-// One 32-lane half wavefront per 32-value block of a row-major [rows, cols] f32 matrix
-// (cols % 32 == 0).  Outputs (each optional): the simulated values decode(code) * scale
-// (`values` may alias x: every lane reads its element before any lane writes), the codes
-// [rows, cols] and the scales [rows, cols / 32] (the E8M0 byte is the biased exponent of the
-// power-of-two scale).  Non-finite input -> status (mxfp.rs:93-99).
+// One 32-lane half wavefront per block of 32 * VPT values of a row-major [rows, cols] f32
+// matrix (cols % (32 * VPT) == 0), VPT consecutive values per lane: 32-value blocks (Hy4,
+// DeepSeek V4.1) with VPT 1, DeepSeek V4's 128-value blocks with VPT 4.  Outputs (each
+// optional): the simulated values decode(code) * scale (`values` may alias x: every lane reads
+// its elements before any lane writes), the codes [rows, cols] and the scales
+// [rows, cols / (32 * VPT)] (the E8M0 byte is the biased exponent of the power-of-two scale).
+// Non-finite input -> status (mxfp.rs:93-99).
+template <int VPT>
 __global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nblocks, int cols,
                                                        float* values,
                                                        uint8_t* __restrict__ codes,
@@ -70,41 +73,72 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nb
                                                        const int32_t* __restrict__ row_slot) {
   const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   const size_t blk = gid >> 5;
+  const size_t e0 = gid * VPT;  // first element of this lane
   const bool live = blk < nblocks;
-  float v = live ? x[gid] : 0.0f;
-  if (round_first && live) {
-    if (row_w) {
-      const size_t row = gid / (size_t)cols;
-      v = v * row_w[row_slot ? row_slot[row] : row];
-    }
-    float r;
-    if (!rne_bf16(v, &r) && status) flag(status, kStatusNonFinite);
-    else v = r;
+  float v[VPT];
+  if constexpr (VPT == 4) {
+    const float4 q = live ? *reinterpret_cast<const float4*>(x + e0)
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else {
+    v[0] = live ? x[e0] : 0.0f;
   }
-  float a = fabsf(v);
+  if (round_first && live) {
+    // the lane's values lie in one row (cols is a multiple of the block)
+    const float rw = row_w ? row_w[row_slot ? row_slot[e0 / (size_t)cols] : e0 / (size_t)cols]
+                           : 1.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      float r;
+      const float p = row_w ? v[j] * rw : v[j];
+      if (!rne_bf16(p, &r) && status) flag(status, kStatusNonFinite);
+      else v[j] = r;
+    }
+  }
+  float a = fabsf(v[0]);
+#pragma unroll
+  for (int j = 1; j < VPT; ++j) a = fmaxf(a, fabsf(v[j]));
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
   if (!live) return;
-  if (!finite(v) && status) flag(status, kStatusNonFinite);
+  bool fin = true;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) fin = fin && finite(v[j]);
+  if (!fin && status) flag(status, kStatusNonFinite);
   a = fmaxf(a, 1.0e-4f);  // fold(1.0e-4, f32::max) over |x| (mxfp.rs:104-107)
   const float scale = pow2_ceiling(a / 448.0f);
-  const uint32_t code = encode_e4m3(v / scale);
+  uint32_t code[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) code[j] = encode_e4m3(v[j] / scale);
   if (values) {
     // E4M3 code -> value via the conversion instruction (exact), times the power of two
-    const float d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code, 1.0f, false)[0];
-    values[gid] = d * scale;
+    float d[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      d[j] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code[j], 1.0f, false)[0] * scale;
+    if constexpr (VPT == 4)
+      *reinterpret_cast<float4*>(values + e0) = make_float4(d[0], d[1], d[2], d[3]);
+    else
+      values[e0] = d[0];
   }
-  if (codes) codes[gid] = (uint8_t)code;
+  if (codes)
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) codes[e0 + j] = (uint8_t)code[j];
   if (scales && (gid & 31) == 0) scales[blk] = (uint8_t)(f2u(scale) >> 23);
 }
 
 void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
                      uint8_t* scales, int* status, hipStream_t s, int round_first,
-                     const float* row_w, const int32_t* row_slot) {
-  const size_t nblocks = rows * cols / 32;
+                     const float* row_w, const int32_t* row_slot, int block) {
+  const size_t nblocks = rows * cols / block;
   const size_t threads = nblocks * 32;
-  quantize_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(
-      x, nblocks, (int)cols, values, codes, scales, status, round_first, row_w, row_slot);
+  const unsigned grid = (unsigned)((threads + 255) / 256);
+  if (block == 128)
+    quantize_kernel<4><<<grid, 256, 0, s>>>(x, nblocks, (int)cols, values, codes, scales, status,
+                                            round_first, row_w, row_slot);
+  else
+    quantize_kernel<1><<<grid, 256, 0, s>>>(x, nblocks, (int)cols, values, codes, scales, status,
+                                            round_first, row_w, row_slot);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -8,6 +8,7 @@ namespace urb {
 
 // Error bits written to the per-context status word (the host maps them to urb_status).
 constexpr int kStatusNonFinite = 1;
+constexpr int kStatusBadToken = 2;  // a token id outside the hash table
 
 // Panel layout of a [rows, cols] weight matrix in HBM (rows % 16 == 0, cols % 128 == 0).
 // The matrix is a sequence of 16-row panels, each holding exactly the bytes of its 16 rows.
@@ -91,6 +92,12 @@ struct RouteParams {
   // `logits` as f32.
   const double* part;
   int slices;
+  // sqrt-softplus hash experts (DeepSeek V4's first layers): the token's row of the [vocab, K]
+  // table `hash` (ids validated in range and distinct per row) replaces the ranking; a token id
+  // >= vocab sets kStatusBadToken and reads row 0.
+  const int32_t* hash;
+  const uint32_t* tokens;
+  uint32_t vocab;
 };
 
 
@@ -147,16 +154,17 @@ void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const 
                          const float* shared = nullptr, const float* gate = nullptr);
 void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
                         const float* shared, int T, int K, int H, float* out, hipStream_t s);
-// MX-activation mode (Hy4 composition).  simulate_e4m3_activation (src/math/mxfp.rs:89-115)
-// of [rows, cols] f32 (cols % 32 == 0) per 32-value block of each row: the simulated f32 values
-// (`values`, may alias x) and/or the E4M3 codes [rows, cols] + E8M0 scales [rows, cols / 32]
-// they are made of; either output may be null.
+// MX-activation mode.  simulate_e4m3_activation (src/math/mxfp.rs:89-115) of [rows, cols] f32
+// (cols % block == 0) per `block`-value block of each row (32, or DeepSeek V4's 128): the
+// simulated f32 values (`values`, may alias x) and/or the E4M3 codes [rows, cols] + E8M0 scales
+// [rows, cols / block] they are made of; either output may be null.
 // With `round_first`, each value is first multiplied by its row's weight (row_w[row_slot[row]],
 // row_w[row] when row_slot is null, none when row_w is null) and rounded to BF16 (DeepSeek
 // V4.1's weighted, BF16-materialised SwiGLU output).
 void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
                      uint8_t* scales, int* status, hipStream_t s, int round_first = 0,
-                     const float* row_w = nullptr, const int32_t* row_slot = nullptr);
+                     const float* row_w = nullptr, const int32_t* row_slot = nullptr,
+                     int block = 32);
 // Hy4 combine: ascending expert id, f32, + shared, BF16 (weights null: the plain sum of DeepSeek
 // V4.1, whose experts already applied their route weight).
 void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const float* weights,

@@ -39,13 +39,13 @@ struct Workspace {
   int32_t* counts = nullptr;
   int32_t* perm_token = nullptr;
   int32_t* pos_of_slot = nullptr;
-  int32_t* slot_of_pos = nullptr;  // DSV41: route slot of each permuted position
+  int32_t* slot_of_pos = nullptr;  // DSV41, DSV4: route slot of each permuted position
   int32_t* tiles = nullptr;
   float* act = nullptr;
   float* y_perm = nullptr;
   float* shared_act = nullptr;
   float* shared_out = nullptr;
-  float* xq = nullptr;  // HY4: the simulated E4M3 token activations [chunk, H]
+  float* xq = nullptr;  // HY4, DSV41, DSV4: the simulated E4M3 token activations [chunk, H]
   float* xn = nullptr;  // QWEN36 block calls: the normalized BF16 token activations [chunk, H]
   float* gate_logit = nullptr;  // QWEN36 shared expert: bf16(shared_expert_gate . x) [chunk]
   int* status = nullptr;  // [0] latched numerical failures, [1] validation flags
@@ -79,6 +79,8 @@ struct urb_moe_ctx {
   bool borrowed = false;               // experts borrowed in the panel layout (repointable)
   uint8_t* router_panel = nullptr;     // panel layout of the padded router (GLM)
   const float* bias = nullptr;         // [E] or nullptr
+  const int32_t* hash = nullptr;       // [hash_vocab, K] tid2eid rows (sqrt-softplus) or nullptr
+  uint32_t hash_vocab = 0;
   ExpertMats* table = nullptr;         // device [E]
   ExpertMats* shared_table = nullptr;  // device [1]
   Workspace ws;
@@ -152,6 +154,11 @@ const char* urb_status_string(urb_status s) {
 
 constexpr uint32_t kMaxDim = 12288;
 
+// The MX-activation compositions (Hy4, DeepSeek V4.1, DeepSeek V4).
+static bool mx_activation(urb_composition c) {
+  return c == URB_COMPOSE_HY4 || c == URB_COMPOSE_DSV41 || c == URB_COMPOSE_DSV4;
+}
+
 static bool finite_host(float v) { return v == v && v <= 3.4028235e38f && v >= -3.4028235e38f; }
 
 static urb_status check_desc(const urb_moe_desc* d) {
@@ -170,7 +177,7 @@ static urb_status check_desc(const urb_moe_desc* d) {
     if (d->expert_format != URB_FMT_BF16 || d->router != URB_ROUTER_SOFTMAX_TOPK ||
         (d->shared_intermediate && d->shared_format != URB_FMT_BF16))
       return URB_ERR_ARGUMENT;
-  } else if (d->composition == URB_COMPOSE_HY4 || d->composition == URB_COMPOSE_DSV41) {
+  } else if (mx_activation(d->composition)) {
     // MX projections only (the activation mode exists for MX weights), and the routed experts'
     // SwiGLU limit must be finite and positive (Hy4Config validation, hy4/config.rs:235-236).
     if (d->expert_format == URB_FMT_BF16 ||
@@ -237,14 +244,14 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   w.counts = b.take<int32_t>(E);
   w.perm_token = b.take<int32_t>(C * K);
   w.pos_of_slot = b.take<int32_t>(C * K);
-  if (d.composition == URB_COMPOSE_DSV41) w.slot_of_pos = b.take<int32_t>(C * K);
+  if (d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4)
+    w.slot_of_pos = b.take<int32_t>(C * K);
   w.tiles = b.take<int32_t>(2 * (size_t)urb::gemm_max_tiles((int)C, (int)K, (int)E));
   w.act = b.take<float>(C * K * I);
   w.y_perm = b.take<float>(C * K * H);
   w.shared_act = b.take<float>(C * std::max<size_t>(d.shared_intermediate, 1));
   w.shared_out = b.take<float>(C * H);
-  if (d.composition == URB_COMPOSE_HY4 || d.composition == URB_COMPOSE_DSV41)
-    w.xq = b.take<float>(C * H);
+  if (mx_activation(d.composition)) w.xq = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36) w.xn = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36 && d.shared_intermediate) w.gate_logit = b.take<float>(C);
 }
@@ -259,6 +266,11 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   if (!w->router_weight || !w->experts || (has_shared && !w->shared)) return URB_ERR_ARGUMENT;
   const bool qwen_gate = qwen && has_shared;
   if (qwen_gate && !w->shared_expert_gate) return URB_ERR_ARGUMENT;
+  // hash experts: route_sqrt_softplus only, ids in range (deepseek_v4/math.rs:483-489) and,
+  // for the permutation, distinct within a row
+  const bool hashed = w->hash_experts != nullptr;
+  if (hashed && d->router != URB_ROUTER_SQRT_SOFTPLUS) return URB_ERR_ARGUMENT;
+  if (hashed && w->hash_vocab == 0) return URB_ERR_SHAPE;
   if (src != URB_SOURCE_HOST && src != URB_SOURCE_DEVICE_COPY && src != URB_SOURCE_DEVICE_BORROW)
     return URB_ERR_ARGUMENT;
   const bool mx = d->expert_format != URB_FMT_BF16;
@@ -287,7 +299,8 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
   const size_t Ep = urb::router_rows((int)E);
   size_t arena = align_up(Ep * H * 2) + (lane8 ? align_up((E + 7) / 8 * 8 * H * 2) : align_up(Ep * H * 2)) +
-                 align_up(E * 4) + (qwen_gate ? 2 * align_up(8 * H * 2) : 0);
+                 align_up(E * 4) + (qwen_gate ? 2 * align_up(8 * H * 2) : 0) +
+                 (hashed ? align_up((size_t)w->hash_vocab * d->top_k * 4) : 0);
   size_t wbytes = 0;
   if (!borrow) {
     for (int m = 0; m < 3; ++m) {
@@ -316,6 +329,26 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   if (qwen_gate) {
     urb::launch_fill_i32(reinterpret_cast<int32_t*>(gate_rows), 0, 8 * H / 2, nullptr);
     URB_HIP(hipMemcpy(gate_rows, w->shared_expert_gate, H * 2, kind));
+  }
+  if (hashed) {
+    // tid2eid as stored (i64), checked and narrowed on the host
+    const size_t n = (size_t)w->hash_vocab * d->top_k, K = d->top_k;
+    std::vector<int64_t> tab(n);
+    URB_HIP(hipMemcpy(tab.data(), w->hash_experts, n * 8,
+                      src == URB_SOURCE_HOST ? hipMemcpyHostToHost : hipMemcpyDeviceToHost));
+    std::vector<int32_t> narrow(n);
+    for (size_t i = 0; i < n; ++i) {
+      if (tab[i] < 0 || tab[i] >= (int64_t)E) return URB_ERR_INVALID_GEOMETRY;
+      narrow[i] = (int32_t)tab[i];
+    }
+    for (size_t r = 0; r < w->hash_vocab; ++r)
+      for (size_t i = 0; i < K; ++i)
+        for (size_t j = i + 1; j < K; ++j)
+          if (narrow[r * K + i] == narrow[r * K + j]) return URB_ERR_ARGUMENT;
+    int32_t* hash = ab.take<int32_t>(n);
+    URB_HIP(hipMemcpy(hash, narrow.data(), n * 4, hipMemcpyHostToDevice));
+    c->hash = hash;
+    c->hash_vocab = w->hash_vocab;
   }
   URB_HIP(hipMemcpy(router, w->router_weight, E * H * 2, kind));
   if (Ep > E) urb::launch_fill_i32(reinterpret_cast<int32_t*>(router + E * H), 0, (Ep - E) * H / 2,
@@ -472,13 +505,14 @@ void urb_moe_destroy(urb_moe_ctx* ctx) {
   destroy_ctx(ctx);
 }
 
-static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logits,
-                              int32_t* ids, float* weights, hipStream_t s) {
+static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* tokens, int n,
+                              float* logits, int32_t* ids, float* weights, hipStream_t s) {
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
   urb::RouteParams rp{(int)d.router, qwen ? 1 : 0, (int)d.n_group, (int)d.topk_group,
-                      d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias, nullptr, 0};
+                      d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias, nullptr, 0,
+                      c->hash, tokens, c->hash_vocab};
   {
     Span span(c, URB_STAGE_ROUTER, s);
     if (c->router_lane8) {
@@ -501,24 +535,28 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, int n, float* logi
 }
 
 // The MX-activation compositions for one chunk of n tokens: Hy4 MoeWeights::forward
-// (src/models/hy4/runtime.rs:1371-1447) and DeepSeek-V4.1 MoeWeights::forward
-// (src/models/deepseek_v41/runtime.rs:1963-2019).  Every MX projection reads simulated E4M3
-// activations (BF16-exact values); the BF16 MFMA / FMA kernels run them with the Hy4 epilogues.
-static urb_status forward_mx(urb_moe_ctx* c, const float* xc, int n, float* yc, int32_t* idc,
-                              float* wc, hipStream_t s) {
+// (src/models/hy4/runtime.rs:1371-1447), DeepSeek-V4.1 MoeWeights::forward
+// (src/models/deepseek_v41/runtime.rs:1963-2019) and DeepSeek-V4 MoeWeights::forward{,_batch}
+// (src/models/deepseek_v4/runtime.rs:2484-2828: 128-value activation blocks).  Every MX
+// projection reads simulated E4M3 activations (BF16-exact values); the BF16 MFMA / FMA kernels
+// run them with the Hy4 epilogues.
+static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* tokens, int n,
+                              float* yc, int32_t* idc, float* wc, hipStream_t s) {
   const urb_moe_desc& d = c->desc;
   const bool has_shared = d.shared_intermediate != 0;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
-  const bool dsv = d.composition == URB_COMPOSE_DSV41;
+  const bool dsv = d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4;
+  const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;  // activation block width
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
   // Hy4's shared DenseMlp is a plain BF16 SwiGLU; DeepSeek's shared expert is a routed expert
   // without a weight
   const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
   // mx_activation(input) once per token (runtime.rs:1397); the shared expert quantizes the same
   // input the same way (runtime.rs:1312), so both read it.
-  urb::launch_quantize(xc, (size_t)n, (size_t)H, ws.xq, nullptr, nullptr, ws.status, s);
+  urb::launch_quantize(xc, (size_t)n, (size_t)H, ws.xq, nullptr, nullptr, ws.status, s, 0,
+                       nullptr, nullptr, block);
   if (has_shared) {
     URB_HIP(hipEventRecord(c->fork, s));
     URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
@@ -535,7 +573,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, int n, float* yc, 
       // the down projection re-quantizes its input (Hy4 mx_linear, runtime.rs:1321, 2425-2428;
       // DeepSeek `linear` after the BF16 step, deepseek_v41/runtime.rs:2258-2260)
       urb::launch_quantize(ws.shared_act, (size_t)n, (size_t)Is, ws.shared_act, nullptr, nullptr,
-                           ws.status, c->side, dsv ? 1 : 0);
+                           ws.status, c->side, dsv ? 1 : 0, nullptr, nullptr, block);
     }
     {
       Span span(c, URB_STAGE_SHARED_DOWN, c->side);
@@ -548,7 +586,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, int n, float* yc, 
     }
     URB_HIP(hipEventRecord(c->join, c->side));
   }
-  route_chunk(c, xc, n, ws.logits, idc, wc, s);
+  route_chunk(c, xc, tokens, n, ws.logits, idc, wc, s);
   Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles,
             n == 1 ? idc : nullptr, K};
   if (n > 1) {
@@ -572,7 +610,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, int n, float* yc, 
     // expert.rs:677); DeepSeek first scales each row by its route weight and rounds to BF16
     // (runtime.rs:2254-2258)
     urb::launch_quantize(ws.act, (size_t)n * K, (size_t)I, ws.act, nullptr, nullptr, ws.status,
-                         s, dsv ? 1 : 0, dsv ? wc : nullptr, dsv ? slot : nullptr);
+                         s, dsv ? 1 : 0, dsv ? wc : nullptr, dsv ? slot : nullptr, block);
   }
   if (n == 1 && urb::down_combine_fits(K, I)) {
     if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
@@ -610,10 +648,11 @@ struct BlockArgs {
   float eps;
 };
 
-static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, float* y,
-                               int32_t* ids, float* weights, void* stream,
-                               const BlockArgs* blk) {
+static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* token_ids,
+                               uint32_t tokens, float* y, int32_t* ids, float* weights,
+                               void* stream, const BlockArgs* blk) {
   if (tokens == 0 || tokens > c->desc.max_tokens) return URB_ERR_SHAPE;
+  if (c->hash && !token_ids) return URB_ERR_ARGUMENT;  // hash routing reads the token ids
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
   const bool has_shared = d.shared_intermediate != 0;
@@ -637,8 +676,9 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, 
     }
     int32_t* idc = ids ? ids + (size_t)c0 * K : ws.ids;
     float* wc = weights ? weights + (size_t)c0 * K : ws.weights;
-    if (d.composition == URB_COMPOSE_HY4 || d.composition == URB_COMPOSE_DSV41) {
-      urb_status st = forward_mx(c, xc, n, yc, idc, wc, s);
+    const uint32_t* tc = token_ids ? token_ids + c0 : nullptr;
+    if (mx_activation(d.composition)) {
+      urb_status st = forward_mx(c, xc, tc, n, yc, idc, wc, s);
       if (st) return st;
       continue;
     }
@@ -675,7 +715,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, 
       }
       URB_HIP(hipEventRecord(c->join, c->side));
     }
-    route_chunk(c, xc, n, ws.logits, idc, wc, s);
+    route_chunk(c, xc, tc, n, ws.logits, idc, wc, s);
     // One token: the GEMVs read the ranked ids directly (slot a at permuted position a).
     Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles,
               n == 1 ? idc : nullptr, K};
@@ -745,7 +785,14 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, uint32_t tokens, 
 urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, float* y,
                            int32_t* ids, float* weights, void* stream) {
   if (!c || !x || !y) return URB_ERR_ARGUMENT;
-  return forward_impl(c, x, tokens, y, ids, weights, stream, nullptr);
+  return forward_impl(c, x, nullptr, tokens, y, ids, weights, stream, nullptr);
+}
+
+urb_status urb_moe_forward_tokens(urb_moe_ctx* c, const float* x, const uint32_t* token_ids,
+                                  uint32_t tokens, float* y, int32_t* ids, float* weights,
+                                  void* stream) {
+  if (!c || !x || !y || !token_ids) return URB_ERR_ARGUMENT;
+  return forward_impl(c, x, token_ids, tokens, y, ids, weights, stream, nullptr);
 }
 
 urb_status urb_moe_forward_block(urb_moe_ctx* c, const float* h, const float* norm_weight,
@@ -755,7 +802,7 @@ urb_status urb_moe_forward_block(urb_moe_ctx* c, const float* h, const float* no
   if (c->desc.composition != URB_COMPOSE_QWEN36) return URB_ERR_ARGUMENT;
   if (!finite_host(eps) || !(eps > 0.0f)) return URB_ERR_INVALID_GEOMETRY;
   const BlockArgs blk{norm_weight, eps};
-  return forward_impl(c, h, tokens, out, ids, weights, stream, &blk);
+  return forward_impl(c, h, nullptr, tokens, out, ids, weights, stream, &blk);
 }
 
 urb_status urb_zc_rms_norm_bf16(const float* x, const float* weight, uint32_t rows,
@@ -792,10 +839,11 @@ urb_status urb_moe_profile_read(const urb_moe_ctx* c, double* ms, uint64_t* laun
   return URB_OK;
 }
 
-urb_status urb_moe_route(urb_moe_ctx* c, const float* x, uint32_t tokens, float* logits,
-                         int32_t* ids, float* weights, void* stream) {
-  if (!c || !x) return URB_ERR_ARGUMENT;
+static urb_status route_impl(urb_moe_ctx* c, const float* x, const uint32_t* token_ids,
+                             uint32_t tokens, float* logits, int32_t* ids, float* weights,
+                             void* stream) {
   if (tokens == 0 || tokens > c->desc.max_tokens) return URB_ERR_SHAPE;
+  if (c->hash && !token_ids) return URB_ERR_ARGUMENT;  // hash routing reads the token ids
   const urb_moe_desc& d = c->desc;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -804,10 +852,23 @@ urb_status urb_moe_route(urb_moe_ctx* c, const float* x, uint32_t tokens, float*
     float* lc = logits ? logits + (size_t)c0 * E : c->ws.logits;
     int32_t* idc = ids ? ids + (size_t)c0 * K : c->ws.ids;
     float* wc = weights ? weights + (size_t)c0 * K : c->ws.weights;
-    route_chunk(c, x + (size_t)c0 * H, n, lc, idc, wc, s);
+    route_chunk(c, x + (size_t)c0 * H, token_ids ? token_ids + c0 : nullptr, n, lc, idc, wc, s);
   }
   URB_HIP(hipGetLastError());
   return URB_OK;
+}
+
+urb_status urb_moe_route(urb_moe_ctx* c, const float* x, uint32_t tokens, float* logits,
+                         int32_t* ids, float* weights, void* stream) {
+  if (!c || !x) return URB_ERR_ARGUMENT;
+  return route_impl(c, x, nullptr, tokens, logits, ids, weights, stream);
+}
+
+urb_status urb_moe_route_tokens(urb_moe_ctx* c, const float* x, const uint32_t* token_ids,
+                                uint32_t tokens, float* logits, int32_t* ids, float* weights,
+                                void* stream) {
+  if (!c || !x || !token_ids) return URB_ERR_ARGUMENT;
+  return route_impl(c, x, token_ids, tokens, logits, ids, weights, stream);
 }
 
 urb_status urb_moe_sync(urb_moe_ctx* c, void* stream) {
@@ -821,6 +882,7 @@ urb_status urb_moe_sync(urb_moe_ctx* c, void* stream) {
   URB_HIP(hipGetLastError());
   URB_HIP(hipStreamSynchronize(s));
   if (st & urb::kStatusNonFinite) return URB_ERR_NONFINITE;
+  if (st & urb::kStatusBadToken) return URB_ERR_SHAPE;  // load_i64_matrix_row's bounds check
   return URB_OK;
 }
 
@@ -839,14 +901,21 @@ urb_status urb_dequant_rows(urb_format format, const void* data, const uint8_t* 
   return URB_OK;
 }
 
-urb_status urb_quantize_e4m3(const float* x, uint32_t rows, uint32_t cols, uint8_t* codes,
-                             uint8_t* scales, void* stream) {
+urb_status urb_quantize_e4m3_blocks(const float* x, uint32_t rows, uint32_t cols,
+                                    uint32_t block, uint8_t* codes, uint8_t* scales,
+                                    void* stream) {
   if (!x || !codes || !scales) return URB_ERR_ARGUMENT;
-  if (rows == 0 || cols == 0 || cols % 32) return URB_ERR_SHAPE;
+  if (block != 32 && block != 128) return URB_ERR_ARGUMENT;
+  if (rows == 0 || cols == 0 || cols % block) return URB_ERR_SHAPE;
   urb::launch_quantize(x, rows, cols, nullptr, codes, scales, nullptr,
-                       static_cast<hipStream_t>(stream));
+                       static_cast<hipStream_t>(stream), 0, nullptr, nullptr, (int)block);
   URB_HIP(hipGetLastError());
   return URB_OK;
+}
+
+urb_status urb_quantize_e4m3(const float* x, uint32_t rows, uint32_t cols, uint8_t* codes,
+                             uint8_t* scales, void* stream) {
+  return urb_quantize_e4m3_blocks(x, rows, cols, 32, codes, scales, stream);
 }
 
 urb_status urb_pack_matrix(urb_format format, const void* data, const uint8_t* scales,

@@ -402,10 +402,11 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
       }
     }
   } else if constexpr (MODE == 2) {
-    // route_sqrt_softplus (src/models/deepseek_v4/math.rs:451-516), no hash experts:
+    // route_sqrt_softplus (src/models/deepseek_v4/math.rs:451-516):
     // score = sqrt(softplus(l)) with softplus(v) = v + ln_1p(exp(-v)) for v > 0, else
-    // ln_1p(exp(v)) (:604-610); selection = score + bias ranks; the weight divides by the f32
-    // sum of the selected scores in ranking order.
+    // ln_1p(exp(v)) (:604-610); selection = score + bias ranks, or the token's hash row gives
+    // the experts in table order; the weight divides by the f32 sum of the chosen scores in
+    // that order.
     float score[EPL];
     int32_t key[EPL];
 #pragma unroll
@@ -422,12 +423,31 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
       const float b = (open[i] && rp.bias) ? rp.bias[e] : 0.0f;
       key[i] = total_key(__fadd_rn(score[i], b));
     }
-    for (int r = 0; r < K; ++r) {
-      float val;
-      const int id = argmax_round<EPL>(key, score, open, val);
-      if (lane == r) { my_id = id; my_val = val; }
+    if (rp.hash) {
+      // the tid2eid row of the token (deepseek_v4/runtime.rs:2664-2681); lane r < K reads the
+      // score of its expert from LDS
+      uint32_t tok = rp.tokens[t];
+      if (tok >= rp.vocab) {
+        if (lane == 0) flag(status, kStatusBadToken);
+        tok = 0;
+      }
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (open[i]) sh[lane + 64 * i] = score[i];
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      if (lane < K) {
+        my_id = rp.hash[(size_t)tok * K + lane];
+        my_val = sh[my_id];
+      }
+    } else {
+      for (int r = 0; r < K; ++r) {
+        float val;
+        const int id = argmax_round<EPL>(key, score, open, val);
+        if (lane == r) { my_id = id; my_val = val; }
+      }
     }
-    float den = -0.0f;  // Iterator::sum in ranking order
+    float den = -0.0f;  // Iterator::sum in ranking (or table) order
     for (int r = 0; r < K; ++r) den = __fadd_rn(den, rdl(my_val, r));
     if (!finite(den) || den <= 0.0f) bad = true;
     w = __fmul_rn(__fdiv_rn(my_val, den), rp.scale);

@@ -56,6 +56,7 @@ class DeviceLayer:
     correction_bias: Optional["torch.Tensor"]     # [E] f32
     arena: Optional["torch.Tensor"] = None
     shared_expert_gate: Optional["torch.Tensor"] = None  # [H] int16 BF16 (QWEN36 shared expert)
+    hash_experts: Optional["torch.Tensor"] = None  # [vocab, k] int64 tid2eid (sqrt-softplus)
 
     @staticmethod
     def from_host(host: C.HostLayer, device="cuda") -> "DeviceLayer":
@@ -68,7 +69,8 @@ class DeviceLayer:
         gate = None
         if host.shared_expert_gate is not None:
             gate = torch.from_numpy(host.shared_expert_gate.view(np.int16)).to(device)
-        return DeviceLayer(host.spec, rw, ex, sh, bias, shared_expert_gate=gate)
+        return DeviceLayer(host.spec, rw, ex, sh, bias, shared_expert_gate=gate,
+                           hash_experts=up(host.hash_experts))
 
     @staticmethod
     def synthesize(spec: C.LayerSpec, base_seed: int = synth.BASE_SEED,
@@ -171,7 +173,7 @@ class DeviceLayer:
         gate = None
         if self.shared_expert_gate is not None:
             gate = self.shared_expert_gate.cpu().numpy().view(np.uint16).reshape(-1)
-        return C.HostLayer(self.spec, rw, ex, sh, bias, gate)
+        return C.HostLayer(self.spec, rw, ex, sh, bias, gate, down(self.hash_experts))
 
 
 class MoeLayer:
@@ -205,33 +207,51 @@ class MoeLayer:
                       spec.n_group, spec.topk_group, int(spec.normalize),
                       float(spec.routed_scaling_factor), max_tokens,
                       float(spec.swiglu_limit))
+        # tid2eid [vocab, k] int64, in the memory the source names (checked and copied)
+        table = getattr(layer, "hash_experts", None)
+        self.hashed = table is not None
+        if table is not None and source == N.SOURCE_HOST:
+            table = np.ascontiguousarray(table, dtype=np.int64)
         w = N.Weights(_ptr(layer.router_weight), _ptr(layer.correction_bias),
                       ctypes.addressof(mats), None if shared is None else ctypes.addressof(shared),
-                      _ptr(getattr(layer, "shared_expert_gate", None)))
+                      _ptr(getattr(layer, "shared_expert_gate", None)), _ptr(table),
+                      0 if table is None else int(table.shape[0]))
         ctx = ctypes.c_void_p()
         st = lib.urb_moe_create(ctypes.byref(desc), ctypes.byref(w), source, ctypes.byref(ctx))
         N.check(st, "urb_moe_create")
         self._ctx = ctx
 
     # -- stream-ordered form ------------------------------------------------------------
-    def forward_into(self, x, y, ids=None, weights=None, stream=None) -> None:
+    def forward_into(self, x, y, ids=None, weights=None, stream=None, token_ids=None) -> None:
+        """``token_ids`` [T] (int32/uint32 device tensor): the tokens' ids, which a layer with a
+        hash table routes by (``urb_moe_forward_tokens``)."""
         T = x.shape[0]
-        N.check(N.moe_lib().urb_moe_forward(self._ctx, _ptr(x), T, _ptr(y), _ptr(ids),
-                                            _ptr(weights), _stream_handle(stream)),
-                "urb_moe_forward")
+        if x.dtype != torch.float32 or not x.is_contiguous() or x.shape[-1] != self.spec.hidden:
+            raise ValueError("x must be a contiguous float32 [T, hidden] tensor")
+        if token_ids is None:
+            N.check(N.moe_lib().urb_moe_forward(self._ctx, _ptr(x), T, _ptr(y), _ptr(ids),
+                                                _ptr(weights), _stream_handle(stream)),
+                    "urb_moe_forward")
+            return
+        if token_ids.numel() != T or token_ids.element_size() != 4:
+            raise ValueError("token_ids must hold one 32-bit id per token")
+        N.check(N.moe_lib().urb_moe_forward_tokens(self._ctx, _ptr(x), _ptr(token_ids), T,
+                                                   _ptr(y), _ptr(ids), _ptr(weights),
+                                                   _stream_handle(stream)),
+                "urb_moe_forward_tokens")
 
     def sync(self, stream=None) -> None:
         N.check(N.moe_lib().urb_moe_sync(self._ctx, _stream_handle(stream)), "urb_moe_sync")
 
     # -- Result-shaped form (the reference's call signature) ---------------------------
-    def forward(self, x: "torch.Tensor"):
+    def forward(self, x: "torch.Tensor", token_ids: Optional["torch.Tensor"] = None):
         """x [T, H] f32 on the device -> (y [T, H], ids [T, k], weights [T, k]); raises
-        UrbError like the reference's Err."""
+        UrbError like the reference's Err.  ``token_ids`` [T]: see ``forward_into``."""
         T = x.shape[0]
         y = torch.empty((T, self.spec.hidden), dtype=torch.float32, device=x.device)
         ids = torch.empty((T, self.spec.top_k), dtype=torch.int32, device=x.device)
         w = torch.empty((T, self.spec.top_k), dtype=torch.float32, device=x.device)
-        self.forward_into(x, y, ids, w)
+        self.forward_into(x, y, ids, w, token_ids=token_ids)
         self.sync()
         return y, ids, w
 
@@ -248,13 +268,18 @@ class MoeLayer:
         self.sync()
         return out, ids, w
 
-    def route(self, x: "torch.Tensor"):
+    def route(self, x: "torch.Tensor", token_ids: Optional["torch.Tensor"] = None):
         T = x.shape[0]
         logits = torch.empty((T, self.spec.n_experts), dtype=torch.float32, device=x.device)
         ids = torch.empty((T, self.spec.top_k), dtype=torch.int32, device=x.device)
         w = torch.empty((T, self.spec.top_k), dtype=torch.float32, device=x.device)
-        N.check(N.moe_lib().urb_moe_route(self._ctx, _ptr(x), T, _ptr(logits), _ptr(ids),
-                                          _ptr(w), _stream_handle()), "urb_moe_route")
+        if token_ids is None:
+            N.check(N.moe_lib().urb_moe_route(self._ctx, _ptr(x), T, _ptr(logits), _ptr(ids),
+                                              _ptr(w), _stream_handle()), "urb_moe_route")
+        else:
+            N.check(N.moe_lib().urb_moe_route_tokens(self._ctx, _ptr(x), _ptr(token_ids), T,
+                                                     _ptr(logits), _ptr(ids), _ptr(w),
+                                                     _stream_handle()), "urb_moe_route_tokens")
         self.sync()
         return logits, ids, w
 
@@ -315,14 +340,17 @@ def zc_rms_norm_bf16(x, weight, eps: float):
     return out
 
 
-def quantize_e4m3(x):
+def quantize_e4m3(x, block: int = 32):
     """simulate_e4m3_activation of a [rows, cols] f32 device tensor as (E4M3 codes, E8M0
-    scales) device tensors, blocks of 32 along each row."""
+    scales) device tensors, blocks of ``block`` (32 or 128) values along each row."""
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("quantize_e4m3 takes a contiguous float32 tensor")
     rows, cols = x.shape
     codes = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
-    scales = torch.empty((rows, cols // 32), dtype=torch.uint8, device=x.device)
-    N.check(N.moe_lib().urb_quantize_e4m3(_ptr(x), rows, cols, _ptr(codes), _ptr(scales),
-                                          _stream_handle()), "urb_quantize_e4m3")
+    scales = torch.empty((rows, cols // block), dtype=torch.uint8, device=x.device)
+    N.check(N.moe_lib().urb_quantize_e4m3_blocks(_ptr(x), rows, cols, block, _ptr(codes),
+                                                 _ptr(scales), _stream_handle()),
+            "urb_quantize_e4m3_blocks")
     return codes, scales
 
 

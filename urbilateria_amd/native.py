@@ -23,7 +23,8 @@ EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_rout
            "urb_moe_sync", "urb_dequant_rows", "urb_moe_memory", "urb_status_string",
            "urb_moe_profile", "urb_moe_profile_read", "urb_pack_matrix", "urb_quantize_e4m3",
            "urb_expert_views", "urb_moe_forward_block", "urb_zc_rms_norm_bf16",
-           "urb_moe_set_expert")
+           "urb_moe_set_expert", "urb_moe_forward_tokens", "urb_moe_route_tokens",
+           "urb_quantize_e4m3_blocks")
 STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
@@ -60,7 +61,8 @@ class Desc(ctypes.Structure):
 class Weights(ctypes.Structure):
     _fields_ = [("router_weight", ctypes.c_void_p), ("correction_bias", ctypes.c_void_p),
                 ("experts", ctypes.c_void_p), ("shared", ctypes.c_void_p),
-                ("shared_expert_gate", ctypes.c_void_p)]
+                ("shared_expert_gate", ctypes.c_void_p),
+                ("hash_experts", ctypes.c_void_p), ("hash_vocab", ctypes.c_uint32)]
 
 
 _moe = None
@@ -91,6 +93,10 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_moe_forward.restype = ctypes.c_int
         lib.urb_moe_route.argtypes = [P, P, u32, P, P, P, P]
         lib.urb_moe_route.restype = ctypes.c_int
+        lib.urb_moe_forward_tokens.argtypes = [P, P, P, u32, P, P, P, P]
+        lib.urb_moe_forward_tokens.restype = ctypes.c_int
+        lib.urb_moe_route_tokens.argtypes = [P, P, P, u32, P, P, P, P]
+        lib.urb_moe_route_tokens.restype = ctypes.c_int
         lib.urb_moe_sync.argtypes = [P, P]
         lib.urb_moe_sync.restype = ctypes.c_int
         lib.urb_dequant_rows.argtypes = [ctypes.c_int, P, P, u32, u32, u32, u32, P, P]
@@ -106,6 +112,8 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_pack_matrix.restype = ctypes.c_int
         lib.urb_quantize_e4m3.argtypes = [P, u32, u32, P, P, P]
         lib.urb_quantize_e4m3.restype = ctypes.c_int
+        lib.urb_quantize_e4m3_blocks.argtypes = [P, u32, u32, u32, P, P, P]
+        lib.urb_quantize_e4m3_blocks.restype = ctypes.c_int
         lib.urb_moe_set_expert.argtypes = [P, u32, P, P]
         lib.urb_moe_set_expert.restype = ctypes.c_int
         lib.urb_moe_forward_block.argtypes = [P, P, P, ctypes.c_float, u32, P, P, P, P]
