@@ -45,22 +45,24 @@ __global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E8, in
 // 16-element chain batches in flight per lane (8 x 32 B = 64 VGPRs of weights).
 constexpr int kLane8Ring = 8;
 
-template <int kLane8Tokens>
-__global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __restrict__ w8,
-                                                          int E, int H,
-                                                          const float* __restrict__ x, int T,
-                                                          float* __restrict__ logits,
-                                                          int round_bf16, int* status) {
+// WAVES waves per workgroup, wave w running the chains of expert group WAVES blockIdx.x + w:
+// the staged token row is shared by 8 WAVES experts.
+template <int kLane8Tokens, int WAVES = 1>
+__global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
+    const uint16_t* __restrict__ w8, int E, int H, const float* __restrict__ x, int T,
+    float* __restrict__ logits, int round_bf16, int* status) {
   // [tok][8][H8 + 4] transposed chains: the pad of 4 floats puts the 8 chains of a column in
   // different LDS banks and keeps 16-byte alignment.  H is a multiple of 128.
   extern __shared__ float xs[];
   const int H8 = H / 8, H8p = H8 + 4;
   const int t0 = blockIdx.y * kLane8Tokens;
   const int nt = min(kLane8Tokens, T - t0);
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int el = lane >> 3, j = lane & 7;
-  const int e = blockIdx.x * 8 + el;
-  const uint16_t* chains = w8 + (size_t)blockIdx.x * 8 * H + 8 * lane;
+  const int g = blockIdx.x * WAVES + wave;
+  const bool live = g < (E + 7) / 8;
+  const int e = g * 8 + el;
+  const uint16_t* chains = w8 + (size_t)(live ? g : 0) * 8 * H + 8 * lane;
   const int nb = H8 / 16;
   // The first kLane8Ring batches are requested before the activations are staged.
   uint4 ring[kLane8Ring][2];
@@ -73,7 +75,7 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
   // Stage x with coalesced float4 loads, transposed into per-lane chains.
   bool bad = false;
   const int n4 = nt * H / 4;
-  for (int i = lane; i < n4; i += 64) {
+  for (int i = threadIdx.x; i < n4; i += 64 * WAVES) {
     const float4 v4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H)[i];
     const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
@@ -85,6 +87,7 @@ __global__ __launch_bounds__(64) void router_lane8_kernel(const uint16_t* __rest
   }
   if (bad) flag(status, kStatusNonFinite);
   __syncthreads();
+  if (!live) return;
   float acc[kLane8Tokens];
 #pragma unroll
   for (int tt = 0; tt < kLane8Tokens; ++tt) acc[tt] = 0.0f;
@@ -759,23 +762,24 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int round_bf16, int* status, hipStream_t s) {
+  const size_t per_tok = (size_t)8 * (H / 8 + 4) * sizeof(float);
   if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
-    const size_t per_tok = (size_t)8 * (H / 8 + 4) * sizeof(float);
     router_lane8_kernel<1><<<dim3((E + 7) / 8, T), 64, per_tok, s>>>(w8, E, H, x, T, logits,
                                                                      round_bf16, status);
     return;
   }
-  // ... and the tiled kernel shares each staged activation chunk between 32 experts' chains
-  // (one token per workgroup up to 512 tokens: measured on MI355X at 128 x 128 x 2048, 13.8 ->
-  // 11.8 us; 256 tokens 17.7 -> 14.2 us; slower below 64 tokens), and beyond 512 tokens divides
+  // ... from 64 tokens four waves share one staged token row (32 experts' chains per
+  // workgroup; measured on MI355X at 128 tokens x 128 experts x 2048, 13.8 us with 64-thread
+  // workgroups, 11.8 us with the chunked tiled kernel, 9.7 us with the whole row staged at
+  // once; 128 x 256 x 2048, 22-26 -> 15-19 us), and beyond 512 tokens the tiled kernel divides
   // the weight traffic by streaming each chain batch for 8 or 16 tokens (bound by LDS reads of
   // the staged activations instead: 1024 tokens x 384 experts x 7168 from 1.74 ms to 0.29 ms).
   const int eg = (E + 31) / 32;
   if (T <= 512)
-    router_lane8_tiled_kernel<1><<<dim3(eg, T), 256, 0, s>>>(w8, E, H, x, T, logits, round_bf16,
-                                                             status);
+    router_lane8_kernel<1, 4><<<dim3(eg, T), 256, per_tok, s>>>(w8, E, H, x, T, logits,
+                                                                round_bf16, status);
   else if ((long)eg * ((T + 15) / 16) >= 256)
     router_lane8_tiled_kernel<16><<<dim3(eg, (T + 15) / 16), 256, 0, s>>>(w8, E, H, x, T, logits,
                                                                         round_bf16, status);
