@@ -234,15 +234,18 @@ def run_one(name, T, args, want_cpu, cpu_budget):
     }
     if w.zipf_s:
         rec["zipf_bias_beta"] = float(beta)
+    cpu_job = None
     if want_cpu:
+        # run after every GPU measurement, so no GPU timing follows seconds of host-only work
         threads = min(16, os.cpu_count() or 1)
-        rec["cpu_baseline"] = cpu_baseline(name, spec, C, first, x, cpu_budget, threads, tok)
+        cpu_job = (lambda dev=first, xx=x, tt=tok:
+                   cpu_baseline(name, spec, C, dev, xx, cpu_budget, threads, tt))
     for l in layers:
         l.close()
     del layers, devs, first, x, y
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
-    return rec
+    return rec, cpu_job
 
 
 def main():
@@ -264,16 +267,23 @@ def main():
         del src, dst
     runs = RUNS if args.configs == "all" else [
         (c.split(":")[0], int(c.split(":")[1])) for c in args.configs.split(",")]
-    results = []
+    results, jobs = [], []
     for name, T in runs:
         log(f"run {name} T={T}")
         head = (name, T) == HEADLINE
         budget = args.cpu_seconds * (4.0 if head else 1.0)
-        rec = run_one(name, T, args, not args.no_cpu, budget)
+        rec, job = run_one(name, T, args, not args.no_cpu, budget)
+        jobs.append((rec, job))
         log(f"  {rec['tokens_per_s']:.1f} tok/s, {rec['ms_per_call']:.3f} ms, "
             f"{rec['GBps']:.0f} GB/s ({100 * rec['hbm_frac']:.1f}% HBM), dominant "
             f"{rec['dominant_stage']}")
         results.append(rec)
+    for rec, job in jobs:
+        if job is not None:
+            log(f"cpu baseline {rec['workload']} T={rec['tokens']}")
+            rec["cpu_baseline"] = job()
+            log(f"  {rec['cpu_baseline']['value']:.1f} tokens/s on "
+                f"{rec['cpu_baseline']['cores']} threads")
     head = next((r for r in results if (r["workload"], r["tokens"]) == HEADLINE), results[0])
     dom = head["stages"].get(head["dominant_stage"], {})
     line = {
