@@ -140,7 +140,8 @@ class DeviceLayer:
     @staticmethod
     def from_consolidated(spec: C.LayerSpec, router_weight, gate_up, gate_up_scales, down,
                           down_scales, shared: Optional[List[Pair]] = None,
-                          correction_bias=None, shared_expert_gate=None) -> "DeviceLayer":
+                          correction_bias=None, shared_expert_gate=None,
+                          hash_experts=None) -> "DeviceLayer":
         """A layer over consolidated expert tensors, used in place: gate_up [E, 2I, H] (each
         expert's gate rows, then its up rows) and down [E, H, I] in the on-disk layouts, scales
         [E, 2I, H/32] and [E, H, I/32] for the MX formats (None for BF16) -- the Qwen3.6 packed
@@ -156,7 +157,7 @@ class DeviceLayer:
             ds = None if down_scales is None else down_scales[e]
             ex.append([(gate_up[e, :I], gs), (gate_up[e, I:], us), (down[e], ds)])
         return DeviceLayer(spec, router_weight, ex, shared, correction_bias,
-                           shared_expert_gate=shared_expert_gate)
+                           shared_expert_gate=shared_expert_gate, hash_experts=hash_experts)
 
     def to_host(self, experts: Optional[List[int]] = None) -> C.HostLayer:
         """Copies (a subset of) the layer back to host memory for the CPU oracle."""
@@ -369,7 +370,7 @@ def packed_layer(layer: "DeviceLayer") -> "DeviceLayer":
               for m, (d, sc) in enumerate(layer.shared)]
     torch.cuda.current_stream().synchronize()
     return DeviceLayer(spec, layer.router_weight, ex, sh, layer.correction_bias, None,
-                       layer.shared_expert_gate)
+                       layer.shared_expert_gate, layer.hash_experts)
 
 
 def dequant_rows(fmt: int, data, scales, rows: int, cols: int, row0: int = 0,

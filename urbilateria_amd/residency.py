@@ -357,7 +357,8 @@ class StreamedMoeLayer:
         placeholder = moe.DeviceLayer(spec, _to_device(layer.router_weight),
                                       [self._slot_mats[0]] * spec.n_experts, shared,
                                       _to_device(layer.correction_bias), None,
-                                      _to_device(getattr(layer, "shared_expert_gate", None)))
+                                      _to_device(getattr(layer, "shared_expert_gate", None)),
+                                      _to_device(getattr(layer, "hash_experts", None)))
         self.layer = moe.MoeLayer(placeholder, max_tokens, source=N.SOURCE_DEVICE_BORROW)
         self.cache = cache if cache is not None else LayerLruCache(layer_index + 1, slots)
         self.telemetry = Telemetry()
@@ -399,11 +400,12 @@ class StreamedMoeLayer:
                 raise RuntimeError("unexpected load")
         self.cache.access_with_evicted(self.telemetry, layer, key, load)
 
-    def forward(self, x):
-        """x [T, H] f32 (device) -> (y, ids, weights) of the resident layer."""
+    def forward(self, x, token_ids=None):
+        """x [T, H] f32 (device) -> (y, ids, weights) of the resident layer; ``token_ids`` [T]
+        for a layer with a hash table."""
         import torch
         T, k = x.shape[0], self.spec.top_k
-        _, ids, _ = self.layer.route(x)
+        _, ids, _ = self.layer.route(x, token_ids=token_ids)
         ids = ids.cpu().tolist()
         runs, start, seen = [], 0, set()
         for t in range(T):
@@ -419,7 +421,8 @@ class StreamedMoeLayer:
             for t in range(a, b):
                 for key in sorted(ids[t]):
                     self._access(key)
-            y, i, w = self.layer.forward(x[a:b].contiguous())
+            y, i, w = self.layer.forward(
+                x[a:b].contiguous(), token_ids=None if token_ids is None else token_ids[a:b])
             ys.append(y)
             idl.append(i)
             wl.append(w)
