@@ -125,6 +125,20 @@ def test_benchmark_byte_accounting():
     assert C.shared_bytes(W["c3_mxfp4_decode"].spec) == 88_080_384
 
 
+def test_synthetic_hash_table_rows_are_distinct_in_range_and_seeded():
+    for vocab, E, k in ((129280, 256, 6), (50, 32, 6), (40, 24, 8), (7, 6, 6), (3, 1, 1)):
+        t = C.hash_table(vocab, E, k)
+        assert t.shape == (vocab, k) and t.dtype == np.int64
+        assert t.min() >= 0 and t.max() < E
+        srt = np.sort(t, axis=1)
+        assert not np.any(srt[:, 1:] == srt[:, :-1])  # distinct within each row
+        assert np.array_equal(t, C.hash_table(vocab, E, k))
+    assert not np.array_equal(C.hash_table(50, 32, 6), C.hash_table(50, 32, 6, base_seed=7))
+    w = C.workload("dsv4_flash_hash")
+    assert w.hash_vocab == 129280 and w.spec.composition == C.COMPOSE_DSV4
+    assert C.workload("dsv4_flash").spec.top_k == 6
+
+
 def test_zipf_bias_is_monotone_in_rank():
     b = C.zipf_bias(384, 1.1, 0.1)
     assert b.shape == (384,) and np.all(np.isfinite(b))
