@@ -71,6 +71,7 @@ struct urb_moe_ctx {
   uint32_t chunk = 0;                  // tokens per internal launch sequence
   void* arena = nullptr;               // router, bias and (unless borrowed) the expert weights
   size_t arena_bytes = 0, weight_bytes = 0;
+  size_t shared_weight_bytes = 0;      // payload bytes of the shared expert's three matrices
   void* work = nullptr;
   size_t work_bytes = 0;
   const uint16_t* router = nullptr;    // [E, H] BF16 (rows zero-padded to router_rows(E))
@@ -295,6 +296,11 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   // Matrix geometry: gate [I, H], up [I, H], down [H, I].
   const size_t dims[3][2] = {{I, H}, {I, H}, {H, I}};
   const size_t sdims[3][2] = {{Is, H}, {Is, H}, {H, Is}};
+  if (has_shared)
+    for (int m = 0; m < 3; ++m) {
+      size_t sb, db = matrix_bytes(d->shared_format, sdims[m][0], sdims[m][1], &sb);
+      c->shared_weight_bytes += db + sb;
+    }
 
   // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
   const size_t Ep = urb::router_rows((int)E);
@@ -534,6 +540,18 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
   return URB_OK;
 }
 
+// The stream the shared expert runs on: the side stream, concurrently with routing and the
+// routed experts, except for one-token calls with a small shared expert, whose kernels run in
+// line on the caller's stream ahead of the routing.  Measured on MI355X (one token): the
+// Qwen3.6 release layer (6 MB shared expert) 71-75 -> 51 us and the DeepSeek-V4 Flash layer
+// (13 MB) 71-72 -> 60 us in line; with 23 MB shared experts (C3 MXFP4, C5 DeepSeek-V4.1
+// shapes) the overlap wins (80 -> 87 us and 93 -> 96 us in line), as it does for every batch
+// of 32 tokens measured.
+constexpr size_t kSharedInlineBytes = 16u << 20;
+static hipStream_t shared_stream(const urb_moe_ctx* c, int n, hipStream_t s) {
+  return n == 1 && c->shared_weight_bytes <= kSharedInlineBytes ? s : c->side;
+}
+
 // The MX-activation compositions for one chunk of n tokens: Hy4 MoeWeights::forward
 // (src/models/hy4/runtime.rs:1371-1447), DeepSeek-V4.1 MoeWeights::forward
 // (src/models/deepseek_v41/runtime.rs:1963-2019) and DeepSeek-V4 MoeWeights::forward{,_batch}
@@ -548,6 +566,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const bool dsv = d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4;
+  hipStream_t ss = shared_stream(c, n, s);
   const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;  // activation block width
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
   // Hy4's shared DenseMlp is a plain BF16 SwiGLU; DeepSeek's shared expert is a routed expert
@@ -558,33 +577,35 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
   urb::launch_quantize(xc, (size_t)n, (size_t)H, ws.xq, nullptr, nullptr, ws.status, s, 0,
                        nullptr, nullptr, block);
   if (has_shared) {
-    URB_HIP(hipEventRecord(c->fork, s));
-    URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
+    if (ss != s) {
+      URB_HIP(hipEventRecord(c->fork, s));
+      URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
+    }
     Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
     const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
     {
-      Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
+      Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
       if (n > 1)
         urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                 ws.xq, ws.shared_act, dense_mlp, ws.status, c->side);
+                                 ws.xq, ws.shared_act, dense_mlp, ws.status, ss);
       else
         urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xq,
-                                 ws.shared_act, dense_mlp, ws.status, c->side);
+                                 ws.shared_act, dense_mlp, ws.status, ss);
       // the down projection re-quantizes its input (Hy4 mx_linear, runtime.rs:1321, 2425-2428;
       // DeepSeek `linear` after the BF16 step, deepseek_v41/runtime.rs:2258-2260)
       urb::launch_quantize(ws.shared_act, (size_t)n, (size_t)Is, ws.shared_act, nullptr, nullptr,
-                           ws.status, c->side, dsv ? 1 : 0, nullptr, nullptr, block);
+                           ws.status, ss, dsv ? 1 : 0, nullptr, nullptr, block);
     }
     {
-      Span span(c, URB_STAGE_SHARED_DOWN, c->side);
+      Span span(c, URB_STAGE_SHARED_DOWN, ss);
       if (n > 1)
         urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                              ws.shared_act, ws.shared_out, dense_mlp, ws.status, c->side);
+                              ws.shared_act, ws.shared_out, dense_mlp, ws.status, ss);
       else
         urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_act,
-                              ws.shared_out, dense_mlp, ws.status, c->side);
+                              ws.shared_out, dense_mlp, ws.status, ss);
     }
-    URB_HIP(hipEventRecord(c->join, c->side));
+    if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
   }
   route_chunk(c, xc, tokens, n, ws.logits, idc, wc, s);
   Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles,
@@ -613,7 +634,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
                          s, dsv ? 1 : 0, dsv ? wc : nullptr, dsv ? slot : nullptr, block);
   }
   if (n == 1 && urb::down_combine_fits(K, I)) {
-    if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+    if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {
       Span span(c, URB_STAGE_DOWN, s);
       urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I, ws.act,
@@ -632,7 +653,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
       urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act, ws.y_perm,
                             routed, ws.status, s);
   }
-  if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+  if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
   {
     Span span(c, URB_STAGE_COMBINE, s);
     urb::launch_combine_hy4(ws.y_perm, pos, dsv ? nullptr : wc, ws.asc,
@@ -677,6 +698,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
     int32_t* idc = ids ? ids + (size_t)c0 * K : ws.ids;
     float* wc = weights ? weights + (size_t)c0 * K : ws.weights;
     const uint32_t* tc = token_ids ? token_ids + c0 : nullptr;
+    hipStream_t ss = shared_stream(c, n, s);
     if (mx_activation(d.composition)) {
       urb_status st = forward_mx(c, xc, tc, n, yc, idc, wc, s);
       if (st) return st;
@@ -687,33 +709,35 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       // router, top-k and permutation run here.  GLM: GatedMlp (src/models/glm/runtime/moe.rs:
       // 162).  QWEN36: a Qwen38Expert and its gate logit linear(shared_expert_gate) -- the
       // router's 8-lane FP32 tree with BF16 output, one row (qwen3_6/runtime.rs:1417-1435).
-      URB_HIP(hipEventRecord(c->fork, s));
-      URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
+      if (ss != s) {
+        URB_HIP(hipEventRecord(c->fork, s));
+        URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
+      }
       const urb::Epi sepi = qwen ? epi : gated;
       Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
       const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
       {
-        Span span(c, URB_STAGE_SHARED_GATE_UP, c->side);
+        Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
         if (qwen)
           urb::launch_router_lane8(c->shared_gate8, 1, H, xc, n, ws.gate_logit, 1, ws.status,
-                                   c->side);
+                                   ss);
         if (n > 1)
           urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                   xc, ws.shared_act, sepi, ws.status, c->side);
+                                   xc, ws.shared_act, sepi, ws.status, ss);
         else
           urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, xc,
-                                   ws.shared_act, sepi, ws.status, c->side);
+                                   ws.shared_act, sepi, ws.status, ss);
       }
       {
-        Span span(c, URB_STAGE_SHARED_DOWN, c->side);
+        Span span(c, URB_STAGE_SHARED_DOWN, ss);
         if (n > 1)
           urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                ws.shared_act, ws.shared_out, sepi, ws.status, c->side);
+                                ws.shared_act, ws.shared_out, sepi, ws.status, ss);
         else
           urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is,
-                                ws.shared_act, ws.shared_out, sepi, ws.status, c->side);
+                                ws.shared_act, ws.shared_out, sepi, ws.status, ss);
       }
-      URB_HIP(hipEventRecord(c->join, c->side));
+      if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
     }
     route_chunk(c, xc, tc, n, ws.logits, idc, wc, s);
     // One token: the GEMVs read the ranked ids directly (slot a at permuted position a).
@@ -740,7 +764,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
     if (n == 1 && urb::down_combine_fits(K, I)) {
       // One token: the down projection and the combine run as one kernel (it reads the shared
       // expert's output, so it waits for the side stream first).
-      if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+      if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
       {
         Span span(c, URB_STAGE_DOWN, s);
         urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
@@ -763,7 +787,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
         urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act,
                               ws.y_perm, epi, ws.status, s);
     }
-    if (has_shared) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+    if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {
       Span span(c, URB_STAGE_COMBINE, s);
       if (qwen)

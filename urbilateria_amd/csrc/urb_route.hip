@@ -44,10 +44,14 @@ __global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E8, in
 
 // 16-element chain batches in flight per lane (8 x 32 B = 64 VGPRs of weights).
 constexpr int kLane8Ring = 8;
+#ifndef LANE8_RING
+#define LANE8_RING 8
+#endif
 
 // WAVES waves per workgroup, wave w running the chains of expert group WAVES blockIdx.x + w:
-// the staged token row is shared by 8 WAVES experts.
-template <int kLane8Tokens, int WAVES = 1>
+// the staged token row is shared by 8 WAVES experts.  RING chain batches are in flight per
+// lane.
+template <int kLane8Tokens, int WAVES = 1, int RING = kLane8Ring>
 __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
     const uint16_t* __restrict__ w8, int E, int H, const float* __restrict__ x, int T,
     float* __restrict__ logits, int round_bf16, int* status) {
@@ -64,10 +68,10 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
   const int e = g * 8 + el;
   const uint16_t* chains = w8 + (size_t)(live ? g : 0) * 8 * H + 8 * lane;
   const int nb = H8 / 16;
-  // The first kLane8Ring batches are requested before the activations are staged.
-  uint4 ring[kLane8Ring][2];
+  // The first RING batches are requested before the activations are staged.
+  uint4 ring[RING][2];
 #pragma unroll
-  for (int d = 0; d < kLane8Ring; ++d)
+  for (int d = 0; d < RING; ++d)
     if (d < nb) {
       ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d) * 512);
       ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d + 1) * 512);
@@ -92,15 +96,15 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
 #pragma unroll
   for (int tt = 0; tt < kLane8Tokens; ++tt) acc[tt] = 0.0f;
   const float* xj = xs + j * H8p;
-  for (int b0 = 0; b0 < nb; b0 += kLane8Ring) {
+  for (int b0 = 0; b0 < nb; b0 += RING) {
 #pragma unroll
-    for (int d = 0; d < kLane8Ring; ++d) {
+    for (int d = 0; d < RING; ++d) {
       const int b = b0 + d;
       if (b >= nb) break;
       const uint4 qa = ring[d][0], qb = ring[d][1];
-      if (b + kLane8Ring < nb) {
-        ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + kLane8Ring)) * 512);
-        ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + kLane8Ring) + 1) * 512);
+      if (b + RING < nb) {
+        ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + RING)) * 512);
+        ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + RING) + 1) * 512);
       }
       const float wv[16] = {bf16_lo(qa.x), bf16_hi(qa.x), bf16_lo(qa.y), bf16_hi(qa.y),
                             bf16_lo(qa.z), bf16_hi(qa.z), bf16_lo(qa.w), bf16_hi(qa.w),
@@ -766,8 +770,8 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
   if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
-    router_lane8_kernel<1><<<dim3((E + 7) / 8, T), 64, per_tok, s>>>(w8, E, H, x, T, logits,
-                                                                     round_bf16, status);
+    router_lane8_kernel<1, 1, LANE8_RING><<<dim3((E + 7) / 8, T), 64, per_tok, s>>>(
+        w8, E, H, x, T, logits, round_bf16, status);
     return;
   }
   // ... from 64 tokens four waves share one staged token row (32 experts' chains per
