@@ -114,6 +114,11 @@ constexpr int kRouterMaxSlices = 16;
 int router_slices(int E, int H, int T);
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
                         int slices, int* status, hipStream_t s);
+// One token: the f64 partial slices part[z][0][e] of the row-major router [E, H] from a GEMV
+// (router_gemv_slices(E) slices, exact products summed in f64).
+int router_gemv_slices(int E);
+void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, double* part,
+                            int slices, int* status, hipStream_t s);
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s);
 // Top-k routing, one wavefront per token (logits is an output when p.part is set).
 void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,

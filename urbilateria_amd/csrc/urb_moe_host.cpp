@@ -234,6 +234,7 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
     size_t most = 0;  // largest slices x tokens any call can need
     for (size_t t = 1; t <= C; ++t)
       most = std::max(most, (size_t)urb::router_slices((int)E, (int)H, (int)t) * t);
+    most = std::max(most, (size_t)urb::router_gemv_slices((int)E));
     w.router_part = b.take<double>(most * urb::router_rows((int)E));
   }
   w.ids = b.take<int32_t>(C * K);
@@ -524,6 +525,12 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
     if (c->router_lane8) {
       urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status,
                                s);
+    } else if (n == 1) {
+      // one token: a GEMV over the row-major router beats the 32-token MFMA tile
+      rp.slices = urb::router_gemv_slices(E);
+      rp.part = c->ws.router_part;
+      urb::launch_router_gemv_f64(c->router, E, H, x, c->ws.router_part, rp.slices,
+                                  c->ws.status, s);
     } else {
       rp.slices = urb::router_slices(E, H, n);
       rp.part = c->ws.router_part;

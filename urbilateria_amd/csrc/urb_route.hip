@@ -44,9 +44,6 @@ __global__ void relayout_lane8_kernel(const uint16_t* __restrict__ w, int E8, in
 
 // 16-element chain batches in flight per lane (8 x 32 B = 64 VGPRs of weights).
 constexpr int kLane8Ring = 8;
-#ifndef LANE8_RING
-#define LANE8_RING 8
-#endif
 
 // WAVES waves per workgroup, wave w running the chains of expert group WAVES blockIdx.x + w:
 // the staged token row is shared by 8 WAVES experts.  RING chain batches are in flight per
@@ -749,6 +746,52 @@ int router_slices(int E, int H, int T) {
   return (steps + per - 1) / per;
 }
 
+// One token: the same f64 partial slices from a GEMV, one wavefront per (expert, slice) over
+// the row-major router.  Lane l accumulates in f64 the exact products of its 8-column units
+// l, l + 64, ... of the slice; the lanes' sums are then added in a fixed butterfly order.
+__global__ __launch_bounds__(64) void router_gemv_f64_kernel(const uint16_t* __restrict__ w,
+                                                             int E, int H,
+                                                             const float* __restrict__ x,
+                                                             int units_per_slice,
+                                                             double* __restrict__ part,
+                                                             int* status) {
+  const int e = blockIdx.x, z = blockIdx.y, lane = threadIdx.x;
+  const int units = H / 8;
+  const int u0 = z * units_per_slice, u1 = min(units, u0 + units_per_slice);
+  const uint16_t* wr = w + (size_t)e * H;
+  double acc = 0.0;
+  bool bad = false;
+  for (int u = u0 + lane; u < u1; u += 64) {
+    const uint4 q = *reinterpret_cast<const uint4*>(wr + 8 * u);
+    const float4 a = *reinterpret_cast<const float4*>(x + 8 * u);
+    const float4 b = *reinterpret_cast<const float4*>(x + 8 * u + 4);
+    const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const float wv[8] = {bf16_lo(q.x), bf16_hi(q.x), bf16_lo(q.y), bf16_hi(q.y),
+                         bf16_lo(q.z), bf16_hi(q.z), bf16_lo(q.w), bf16_hi(q.w)};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      bad |= !finite(xv[k]);
+      acc += (double)wv[k] * (double)xv[k];
+    }
+  }
+  if (bad) flag(status, kStatusNonFinite);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane == 0) part[(size_t)z * router_rows(E) + e] = acc;
+}
+
+int router_gemv_slices(int E) {
+  // enough waves to cover the chip four times over, at most kRouterMaxSlices
+  return std::max(1, std::min(kRouterMaxSlices, (4 * 256 + E - 1) / E));
+}
+
+void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, double* part,
+                            int slices, int* status, hipStream_t s) {
+  const int units = H / 8;
+  const int per = (units + slices - 1) / slices;
+  router_gemv_f64_kernel<<<dim3(E, slices), 64, 0, s>>>(w, E, H, x, per, part, status);
+}
+
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
                         int slices, int* status, hipStream_t s) {
   const int steps = H / kKS;
@@ -770,8 +813,8 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
   if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
-    router_lane8_kernel<1, 1, LANE8_RING><<<dim3((E + 7) / 8, T), 64, per_tok, s>>>(
-        w8, E, H, x, T, logits, round_bf16, status);
+    router_lane8_kernel<1><<<dim3((E + 7) / 8, T), 64, per_tok, s>>>(w8, E, H, x, T, logits,
+                                                                     round_bf16, status);
     return;
   }
   // ... from 64 tokens four waves share one staged token row (32 experts' chains per
