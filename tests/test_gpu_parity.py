@@ -703,6 +703,28 @@ def test_streamed_residency_layer_equals_resident_layer(name):
     resident.close()
 
 
+def test_streamed_hash_routed_layer_equals_resident_layer():
+    # A DeepSeek-V4 hash layer streamed through 10 HBM slots: the token ids reach the routing of
+    # every run, and each run equals the resident layer's call bit for bit
+    from urbilateria_amd import residency as R
+    host = _dsv4_hash_layer(n_experts=16, vocab=30)
+    streamed = R.StreamedMoeLayer(host, slots=10, max_tokens=6)
+    resident = moe_mod().MoeLayer(host, max_tokens=6)
+    for call, T in enumerate((1, 4, 6)):
+        x = torch.from_numpy(synth.activations(f"x.stream.hash.{call}", T,
+                                               host.spec.hidden)).cuda()
+        tok = torch.tensor([(7 * call + 5 * t) % 30 for t in range(T)], dtype=torch.int32,
+                           device="cuda")
+        y, ids, w = streamed.forward(x, token_ids=tok)
+        assert np.array_equal(ids.cpu().numpy(), host.hash_experts[tok.cpu().numpy()])
+        parts = [resident.forward(x[a:b].contiguous(), token_ids=tok[a:b])
+                 for a, b in streamed.last_runs]
+        assert torch.equal(y, torch.cat([p[0] for p in parts]))
+        assert torch.equal(w, torch.cat([p[2] for p in parts]))
+    streamed.close()
+    resident.close()
+
+
 def test_set_expert_validates_and_needs_a_borrowed_context():
     host = _small_layer("c3_mxfp4_decode")
     dev = moe_mod().DeviceLayer.from_host(host)
