@@ -295,6 +295,16 @@ urb_status urb_moe_memory(const urb_moe_ctx *ctx, size_t *weight_bytes, size_t *
 
 const char *urb_status_string(urb_status status);
 
+/* Diagnostic, host only, no reference counterpart: the grouped GEMM's workgroup placement for
+ * a launch over `tiles` row tiles of a [rows, cols] projection in `format` (pair != 0: the
+ * gate+up pair), with dense_tokens > 0 for one dense expert (the shared expert) over that many
+ * tokens.  Writes the row tile and panel group of each of the first `capacity` workgroups (-1
+ * for a workgroup with no work) and returns the grid size.  Lets a test check that every XCD
+ * gets work and every (tile, group) pair is covered once. */
+uint32_t urb_gemm_placement(urb_format format, int pair, uint32_t dense_tokens, uint32_t tiles,
+                            uint32_t rows, uint32_t cols, int32_t *tile_of_block,
+                            int32_t *group_of_block, uint32_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,11 @@
  *
  * Loads go through a callback that returns 0 on success and any other value on failure; a
  * failing load's code is returned unchanged by the access call.
+ *
+ * Layer indices are checked (the reference indexes a Vec and panics): with a layer outside
+ * [0, layers), or a required pointer NULL, the access calls return URB_ERR_ARGUMENT before
+ * changing anything, queries return their empty answer (not resident, capacity 0, no entries,
+ * every key a projected miss, no plan), and the other calls change nothing.
  */
 #ifndef URB_RESIDENCY_H
 #define URB_RESIDENCY_H
@@ -90,7 +95,9 @@ size_t urb_lru_projected_misses(const urb_lru *lru, uint32_t layer, const uint64
  * or 0 (None). */
 int urb_lru_grouped_access_order(const urb_lru *lru, uint32_t layer, const uint64_t *keys,
                                  size_t n, uint64_t *order_out, size_t *order_n);
-/* finish_grouped_accesses (cache.rs:251-261), after the grouped keys were accessed. */
+/* finish_grouped_accesses (cache.rs:251-261), after the grouped keys were accessed: the clock
+ * then stands `groups` accesses after the schedule began.  A clock below `groups` (the
+ * reference's subtraction would underflow) leaves everything unchanged. */
 void urb_lru_finish_grouped_accesses(urb_lru *lru, uint32_t layer, const uint64_t *keys, size_t n,
                                      size_t groups);
 

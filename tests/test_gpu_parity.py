@@ -703,6 +703,57 @@ def test_streamed_residency_layer_equals_resident_layer(name):
     resident.close()
 
 
+def test_streamed_layer_survives_a_failed_load():
+    # A host expert with an E8M0 NaN scale fails its load after the LRU evicted a victim and
+    # after its bytes were packed into a slot.  The call raises; once the expert is repaired,
+    # every later call equals the resident layer bit for bit -- no resident expert's slot was
+    # reused by the failed load or handed out twice afterwards.
+    from urbilateria_amd import residency as R
+    host = _small_layer("c3_mxfp4_decode")
+    spec = host.spec
+    resident = moe_mod().MoeLayer(host, max_tokens=6)
+    xs = [torch.from_numpy(synth.activations(f"x.stream.fail.{c}", 6, spec.hidden)).cuda()
+          for c in range(6)]
+    _, ids1, _ = resident.forward(xs[1])
+    bad_expert = int(ids1[0, 0])
+    good = host.experts[bad_expert][0]
+    broken = good[1].copy()
+    broken[3] = 0xFF
+    experts = [list(e) for e in host.experts]
+    experts[bad_expert][0] = (good[0], broken)
+    streamed = R.StreamedMoeLayer(replace(host, experts=experts), slots=10, max_tokens=6)
+    streamed.forward(xs[0])  # fills slots (the bad expert may load here only if routed)
+    if streamed.cache.contains(0, bad_expert):
+        pytest.skip("the damaged expert was routed by the warm-up call")
+    with pytest.raises(R.LoadError):
+        streamed.forward(xs[1])
+    experts[bad_expert][0] = good  # repaired in the host store the layer streams from
+    for x in xs[1:] + xs[:1]:
+        y, ids, w = streamed.forward(x)
+        parts = [resident.forward(x[a:b].contiguous()) for a, b in streamed.last_runs]
+        assert torch.equal(y, torch.cat([p[0] for p in parts]))
+        assert torch.equal(ids, torch.cat([p[1] for p in parts]))
+        assert torch.equal(w, torch.cat([p[2] for p in parts]))
+        slots = [e.value for e in streamed.cache.entries(0)]
+        assert len(slots) == len(set(slots)) and all(0 <= s < 10 for s in slots)
+    streamed.close()
+    resident.close()
+
+
+def test_streamed_layer_refuses_a_cache_of_another_capacity():
+    from urbilateria_amd import residency as R
+    host = _small_layer("c3_mxfp4_decode")
+    with pytest.raises(ValueError):
+        R.StreamedMoeLayer(host, slots=10, max_tokens=2, cache=R.LayerLruCache(1, 12))
+    cache = R.LayerLruCache(2, 10)
+    streamed = R.StreamedMoeLayer(host, slots=10, max_tokens=2, layer_index=1, cache=cache)
+    cache.lend_unused_capacity(1, 16)  # the other layer's 10 unused slots are lent here
+    x = torch.from_numpy(synth.activations("x.stream.lend", 2, host.spec.hidden)).cuda()
+    with pytest.raises(ValueError):
+        streamed.forward(x)
+    streamed.close()
+
+
 def test_streamed_hash_routed_layer_equals_resident_layer():
     # A DeepSeek-V4 hash layer streamed through 10 HBM slots: the token ids reach the routing of
     # every run, and each run equals the resident layer's call bit for bit

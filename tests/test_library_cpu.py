@@ -185,3 +185,43 @@ def test_expert_views_rejects_bad_arguments():
     assert lib.urb_expert_views(C.FMT_MXFP8, 1, 250, 128, 16, 16, 16, 16, a) == N.ERR_SHAPE
     assert lib.urb_expert_views(C.FMT_BF16, 0, 256, 128, 16, None, 16, None, a) == N.ERR_ARGUMENT
     assert lib.urb_expert_views(C.FMT_BF16, 1, 256, 128, 16, None, 16, None, a) == N.OK
+
+
+def _placement(fmt, pair, dense, tiles, rows, cols):
+    lib = N.moe_lib()
+    n = lib.urb_gemm_placement(fmt, pair, dense, tiles, rows, cols, None, None, 0)
+    assert n > 0
+    t = np.empty(n, np.int32)
+    g = np.empty(n, np.int32)
+    assert lib.urb_gemm_placement(fmt, pair, dense, tiles, rows, cols, t.ctypes.data,
+                                  g.ctypes.data, n) == n
+    return t, g
+
+
+def _groups(fmt, rows):
+    np_ = 1 if fmt == C.FMT_BF16 else 2 if fmt == C.FMT_MXFP8 else (4 if rows % 256 == 0 else 2)
+    return rows // (64 * np_)
+
+
+@pytest.mark.parametrize("fmt,rows,cols", [(C.FMT_BF16, 2048, 7168), (C.FMT_BF16, 7168, 2048),
+                                           (C.FMT_MXFP4, 2048, 7168), (C.FMT_MXFP8, 6144, 2048),
+                                           (C.FMT_BF16, 768, 2048)])
+def test_grouped_gemm_placement_covers_every_pair_once_and_every_xcd(fmt, rows, cols):
+    # The grouped GEMM's workgroup -> (row tile, panel group) mapping, replayed on the host from
+    # the same placement function the kernel runs: every (tile, group) pair is computed by
+    # exactly one workgroup, and (workgroups go to the XCDs round robin, block % 8) every XCD
+    # has work -- for a dense batch (the shared expert) of any size, where one or two tiles
+    # used to land on one XCD, and for routed tile lists of any length >= 8.
+    groups = _groups(fmt, rows)
+    cases = [(T, (T + 31) // 32) for T in list(range(1, 65)) + [96, 128, 200, 256, 1024]]
+    cases += [(0, n) for n in (8, 9, 13, 40, 163, 550)]
+    for dense, tiles in cases:
+        for pair in (0, 1):
+            t, g = _placement(fmt, pair, dense, tiles, rows, cols)
+            work = t >= 0
+            pairs = list(zip(t[work].tolist(), g[work].tolist()))
+            assert len(pairs) == len(set(pairs)) == tiles * groups, (dense, tiles)
+            assert set(pairs) == {(a, b) for a in range(tiles) for b in range(groups)}
+            if groups >= 8 or tiles >= 8:
+                xcds = set((np.nonzero(work)[0] % 8).tolist())
+                assert xcds == set(range(8)), (dense, tiles, pair, sorted(xcds))

@@ -171,15 +171,32 @@ def test_mxfp8_compact_within_reference_contract():
 
 
 def test_mxfp8_compact_lane_order_kat():
-    # lane 0 gets columns 0, 8 (1x32 block: groups of 8 columns feed lanes 0..7).
-    cols = 32
-    codes = np.zeros(cols, np.uint8)
+    # The compact kernel (mxfp.rs:1113-1157): lane j FMA-accumulates the columns == j (mod 8)
+    # in column order across blocks, then the eight lanes are added in lane order.  Values sit
+    # at 2^24, where adding 1 rounds back to 2^24, so each plausible other order gives another
+    # exact result.
     e = lambda v: O.encode_e4m3fn_finite(v)
-    codes[0], codes[1], codes[8] = e(256.0), e(-256.0), e(2.0 ** -8)
-    scales = np.array([127 + 16], np.uint8)   # x 2^16 -> 2^24, -2^24, 2^8
-    x = np.ones(cols, np.float32)
-    # lanes: l0 = fma(2^24,1,0)=2^24 then fma(2^8,1,2^24)=2^24+2^8 (exact), l1 = -2^24.
-    assert O.matvec_rows(O.FMT_MXFP8, codes, scales, 1, cols, x)[0] == 2.0 ** 8
+    prev = O.set_mxfp8_fma_host(True)
+    try:
+        cols = 64
+        x = np.ones(cols, np.float32)
+        # (1) in-lane order and lane assignment: block 0 (scale 2^16) puts +-2^24 in lanes 0
+        # and 1; block 1 (scale 1) adds 1.0 twice more to lane 0 (columns 32 and 40).  Lane
+        # tree: 2^24 + 1 + 1 = 2^24 in lane 0, cancelled by lane 1 -> 0.  A sequential or f64
+        # sum gives 2, and so does lane 0 in reverse column order.
+        codes = np.zeros(cols, np.uint8)
+        codes[0], codes[1], codes[32], codes[40] = e(256.0), e(-256.0), e(1.0), e(1.0)
+        scales = np.array([127 + 16, 127], np.uint8)
+        assert O.matvec_rows(O.FMT_MXFP8, codes, scales, 1, cols, x)[0] == 0.0
+        assert O.mxfp8_matvec_rows_f64(codes, scales, 1, cols, x)[0] == 2.0
+        # (2) the lane sum runs in lane order: lanes (2^24, 1, 1, -2^24, 0, ...) give 0 in
+        # order 0..7, 1 pairwise ((l0 + l1) + (l2 + l3)) and 2 in reverse order.
+        codes = np.zeros(cols, np.uint8)
+        codes[0], codes[3], codes[33], codes[34] = e(256.0), e(-256.0), e(1.0), e(1.0)
+        assert O.matvec_rows(O.FMT_MXFP8, codes, scales, 1, cols, x)[0] == 0.0
+        assert O.mxfp8_matvec_rows_f64(codes, scales, 1, cols, x)[0] == 2.0
+    finally:
+        O.set_mxfp8_fma_host(prev)
 
 
 def test_mxfp8_validation_order():

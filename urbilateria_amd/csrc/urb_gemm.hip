@@ -28,13 +28,7 @@ namespace urb {
 // NP panels per wave (the workgroup covers 4 NP panels = 64 NP weight rows): every staged
 // activation fragment feeds NP (x2 for gate+up) MFMAs.  MT tokens per tile (32 or 64; 64 for
 // large dense batches, so each weight byte feeds twice the MFMAs before it is re-read).
-//
-// Placement: workgroups go to the eight XCDs round robin (blockIdx.x % 8), and each XCD has its
-// own L2.  XCD c = cx + xsplit cy takes the contiguous run cy (of 8 / xsplit) of the tile list
-// and the run cx (of xsplit) of the panel groups, tile by tile.  Tiles are in expert order, so
-// the tiles of an expert, which read the same weight panels, share one L2, and so do the
-// workgroups of a tile, which read the same activation rows.  xsplit > 1 (a dense batch, one
-// expert) trades weight re-reads across XCDs for activation re-reads.
+// Placement: gemm_place (urb_kernels.hpp); xsplit > 1 only for a dense batch (one expert).
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
                                                       Perm perm, int max_tiles, int xsplit,
@@ -48,16 +42,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   __shared__ __attribute__((aligned(16))) u16 a_lo[2][MT * kALd];
 
   // ---- which tile and panel group
-  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
-  const int cx = xcd % xsplit, cy = xcd / xsplit, ysplit = 8 / xsplit;
   const int groups = rows / (kNT * NP);
-  const int g0 = cx * groups / xsplit, width = (cx + 1) * groups / xsplit - g0;
   const int ntiles = min(perm.dense_tokens > 0 ? (perm.dense_tokens + MT - 1) / MT : perm.meta[1],
                          max_tiles);
-  const int t1 = (cy + 1) * ntiles / ysplit;
-  const int w = cy * ntiles / ysplit + local / width;
-  if (w >= t1) return;
-  const int group = g0 + local % width;
+  int w, group;
+  if (!gemm_place(blockIdx.x, ntiles, groups, xsplit, &w, &group)) return;
   int expert, base, count, m0;
   if (perm.dense_tokens > 0) {
     expert = 0;
@@ -230,31 +219,31 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   if (bad) flag(status, kStatusNonFinite);
 }
 
-// Panel-group split across XCDs: 1 for routed experts (each expert's weights once, from the
-// XCD holding its tiles); for one dense expert the split that minimises weight re-reads
-// (8 / xsplit times) plus activation re-reads (xsplit times).
-template <int FMT, bool PAIR, int NP>
-static int xcd_split(const Perm& perm, int max_tiles, int rows, int K) {
-  const int groups = rows / (kNT * NP);
-  if (perm.dense_tokens <= 0 || max_tiles < 8) return 1;
-  const double wbytes = (PAIR ? 2.0 : 1.0) * rows * (double)panel_row_bytes<FMT>(K);
-  const double abytes = (double)perm.dense_tokens * K * 4;
+int gemm_xsplit(int dense_tokens, int ntiles, int groups, double wbytes, double abytes) {
+  if (dense_tokens <= 0 || ntiles <= 0) return 1;
   int best = 1;
-  double best_cost = 8 * wbytes + abytes;
-  for (int x = 2; x <= 8 && x <= groups; x *= 2) {
-    const double cost = 8.0 / x * wbytes + x * abytes;
-    if (cost < best_cost) best = x, best_cost = cost;
+  double best_time = 0.0;
+  for (int x = 1; x <= 8 && x <= groups; x *= 2) {
+    const int runs = std::min(8 / x, ntiles);  // non-empty tile runs
+    const double bytes = runs * wbytes + x * abytes;
+    const double time = bytes / (x * runs);   // per busy XCD
+    if (x == 1 || time < best_time) best = x, best_time = time;
   }
   return best;
+}
+
+template <int FMT, bool PAIR, int NP>
+static int xcd_split(const Perm& perm, int max_tiles, int rows, int K) {
+  const double wbytes = (PAIR ? 2.0 : 1.0) * rows * (double)panel_row_bytes<FMT>(K);
+  const double abytes = (double)std::max(perm.dense_tokens, 0) * K * 4;
+  return gemm_xsplit(perm.dense_tokens, max_tiles, rows / (kNT * NP), wbytes, abytes);
 }
 
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                          const float* in, float* out, Epi epi, int* status, hipStream_t s) {
   const int xsplit = xcd_split<FMT, PAIR, NP>(perm, max_tiles, rows, K);
-  const int groups = rows / (kNT * NP), ysplit = 8 / xsplit;
-  // per XCD: at most ceil(tiles / ysplit) tiles times ceil(groups / xsplit) panel groups
-  const int per_xcd = (max_tiles + ysplit - 1) / ysplit * ((groups + xsplit - 1) / xsplit);
+  const int per_xcd = gemm_blocks_per_xcd(max_tiles, rows / (kNT * NP), xsplit);
   gemm_kernel<FMT, PAIR, DEPTH, NP, MT><<<dim3(8 * per_xcd), 256, 0, s>>>(
       mats, perm, max_tiles, xsplit, rows, K, in, out, epi, status);
 }
@@ -270,10 +259,33 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
     launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
   else if constexpr (FMT == kFmtMXFP8)
     launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
-  else if (rows % (kNT * 4) == 0)
+  else if (gemm_panels_per_wave(FMT, rows) == 4)
     launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
   else
     launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
+}
+
+int gemm_panels_per_wave(int fmt, int rows) {
+  if (fmt == kFmtBF16) return 1;
+  if (fmt == kFmtMXFP8) return 2;
+  return rows % (kNT * 4) == 0 ? 4 : 2;
+}
+
+int gemm_placement(int fmt, bool pair, int dense_tokens, int max_tiles, int rows, int K,
+                   int32_t* tile_of_block, int32_t* group_of_block, int capacity) {
+  const int np = gemm_panels_per_wave(fmt, rows);
+  const int groups = rows / (kNT * np);
+  const double rb = fmt == kFmtBF16 ? 2.0 * K : fmt == kFmtMXFP4 ? K / 2.0 : (double)K;
+  const int xsplit = gemm_xsplit(dense_tokens, max_tiles, groups, (pair ? 2.0 : 1.0) * rows * rb,
+                                 (double)dense_tokens * K * 4);
+  const int blocks = 8 * gemm_blocks_per_xcd(max_tiles, groups, xsplit);
+  for (int b = 0; b < blocks && b < capacity; ++b) {
+    int t = -1, g = -1;
+    if (!gemm_place(b, max_tiles, groups, xsplit, &t, &g)) t = g = -1;
+    tile_of_block[b] = t;
+    group_of_block[b] = g;
+  }
+  return blocks;
 }
 
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,

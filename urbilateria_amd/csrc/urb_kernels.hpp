@@ -75,6 +75,43 @@ inline int gemm_max_tiles(int n, int k, int E) {
   int a = n * k < E ? n * k : E;
   return a + (n * k + kGemmMTile - 1) / kGemmMTile;
 }
+
+// Workgroup placement of the grouped GEMM.  Workgroups go to the eight XCDs round robin
+// (block % 8) and each XCD has its own L2.  XCD c = cx + xsplit cy takes the contiguous run cy
+// (of 8 / xsplit) of the tile list and the run cx (of xsplit) of the panel groups, tile by tile:
+// an expert's tiles (tiles are in expert order), which read the same weight panels, share one
+// L2, and so do a tile's workgroups, which read the same activation rows.  Returns false for a
+// workgroup with nothing to do.  The grid has 8 * gemm_blocks_per_xcd(...) workgroups.
+__host__ __device__ inline bool gemm_place(int block, int ntiles, int groups, int xsplit,
+                                           int* tile, int* group) {
+  const int xcd = block & 7, local = block >> 3;
+  const int cx = xcd % xsplit, cy = xcd / xsplit, ysplit = 8 / xsplit;
+  const int g0 = cx * groups / xsplit, width = (cx + 1) * groups / xsplit - g0;
+  if (width <= 0) return false;
+  const int t1 = (cy + 1) * ntiles / ysplit;
+  const int w = cy * ntiles / ysplit + local / width;
+  if (w >= t1) return false;
+  *tile = w;
+  *group = g0 + local % width;
+  return true;
+}
+__host__ __device__ inline int gemm_blocks_per_xcd(int max_tiles, int groups, int xsplit) {
+  const int ysplit = 8 / xsplit;
+  return (max_tiles + ysplit - 1) / ysplit * ((groups + xsplit - 1) / xsplit);
+}
+// The panel-group split across XCDs.  Routed tiles (dense_tokens == 0): 1, so each expert's
+// weights come from the one XCD holding its tiles.  One dense expert over `ntiles` tiles: the
+// split with the least estimated time, taking time as the HBM bytes the launch moves (weights
+// once per non-empty tile run, `wbytes` each; the activations once per split, `abytes` each)
+// spread over the XCDs that have work -- so a batch of one or two tiles spreads its panel
+// groups over all eight XCDs instead of leaving most of them idle.
+int gemm_xsplit(int dense_tokens, int ntiles, int groups, double wbytes, double abytes);
+// Weight panels per wave of the grouped GEMM for a format and row count.
+int gemm_panels_per_wave(int fmt, int rows);
+// Host-side replay of a launch's placement (urb_gemm_placement): the grid size, and the tile and
+// panel group of each of the first `capacity` workgroups (-1 when idle).
+int gemm_placement(int fmt, bool pair, int dense_tokens, int max_tiles, int rows, int K,
+                   int32_t* tile_of_block, int32_t* group_of_block, int capacity);
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
                          int I, const float* x, float* act, Epi epi, int* status,
                          hipStream_t s);

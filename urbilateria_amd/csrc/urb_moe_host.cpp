@@ -1021,6 +1021,17 @@ urb_status urb_moe_set_expert(urb_moe_ctx* c, uint32_t expert, const urb_matrix*
   return URB_OK;
 }
 
+uint32_t urb_gemm_placement(urb_format format, int pair, uint32_t dense_tokens, uint32_t tiles,
+                            uint32_t rows, uint32_t cols, int32_t* tile_of_block,
+                            int32_t* group_of_block, uint32_t capacity) {
+  if (format != URB_FMT_BF16 && format != URB_FMT_MXFP4 && format != URB_FMT_MXFP8) return 0;
+  if (!urb::panel_shape_ok(rows, cols) || rows % urb::kGemmNTile || tiles == 0) return 0;
+  if (capacity && (!tile_of_block || !group_of_block)) return 0;
+  return (uint32_t)urb::gemm_placement((int)format, pair != 0, (int)dense_tokens, (int)tiles,
+                                       (int)rows, (int)cols, tile_of_block, group_of_block,
+                                       (int)capacity);
+}
+
 urb_status urb_moe_memory(const urb_moe_ctx* c, size_t* weight_bytes, size_t* workspace_bytes) {
   if (!c) return URB_ERR_ARGUMENT;
   if (weight_bytes) *weight_bytes = c->weight_bytes;

@@ -58,7 +58,12 @@ struct urb_lru {
   uint64_t budget = 0;
   uint64_t clock = 0;
 
+  // Layer indices come from the caller: every entry point checks them before indexing (the
+  // reference indexes its Vec and panics; here an out-of-range layer is refused).
+  bool has(uint32_t layer) const { return layer < layers.size(); }
+
   bool contains(uint32_t layer, uint64_t key) const {
+    if (!has(layer)) return false;
     for (const Entry& e : layers[layer])
       if (e.key == key) return true;
     return false;
@@ -135,6 +140,8 @@ void urb_lru_destroy(urb_lru* lru) { delete lru; }
 int urb_lru_access(urb_lru* c, urb_lru_telemetry* t, uint32_t layer, uint64_t key,
                    urb_lru_load_fn load, void* user, uint64_t* value, uint64_t* evicted,
                    int* has_evicted) {
+  if (!c || !t || !value || !evicted || !has_evicted || !load || !c->has(layer))
+    return URB_ERR_ARGUMENT;
   *has_evicted = 0;
   c->clock = sat_add(c->clock, 1);
   auto& entries = c->layers[layer];
@@ -176,10 +183,11 @@ int urb_lru_access(urb_lru* c, urb_lru_telemetry* t, uint32_t layer, uint64_t ke
 }
 
 int urb_lru_contains(const urb_lru* c, uint32_t layer, uint64_t key) {
-  return c->contains(layer, key) ? 1 : 0;
+  return c && c->contains(layer, key) ? 1 : 0;
 }
 
 int urb_lru_peek(const urb_lru* c, uint32_t layer, uint64_t key, uint64_t* value) {
+  if (!c || !value || !c->has(layer)) return 0;
   for (const Entry& e : c->layers[layer])
     if (e.key == key) {
       *value = e.value;
@@ -189,14 +197,18 @@ int urb_lru_peek(const urb_lru* c, uint32_t layer, uint64_t key, uint64_t* value
 }
 
 int urb_lru_layer_is_empty(const urb_lru* c, uint32_t layer) {
-  return c->layers[layer].empty() ? 1 : 0;
+  return !c || !c->has(layer) || c->layers[layer].empty() ? 1 : 0;
 }
 
 uint32_t urb_lru_layer_capacity(const urb_lru* c, uint32_t layer) {
-  return c->capacities[layer];
+  return c && c->has(layer) ? c->capacities[layer] : 0;
 }
 
 void urb_lru_residency(const urb_lru* c, uint32_t layer, uint64_t* experts, uint64_t* bytes) {
+  if (!experts || !bytes) return;
+  *experts = 0;
+  *bytes = 0;
+  if (!c || !c->has(layer)) return;
   uint64_t b = 0;
   for (const Entry& e : c->layers[layer]) b = sat_add(b, e.bytes);
   *experts = c->layers[layer].size();
@@ -205,6 +217,7 @@ void urb_lru_residency(const urb_lru* c, uint32_t layer, uint64_t* experts, uint
 
 size_t urb_lru_entries(const urb_lru* c, uint32_t layer, uint64_t* keys, uint64_t* last_used,
                        uint64_t* values) {
+  if (!c || !c->has(layer)) return 0;
   const auto& entries = c->layers[layer];
   for (size_t i = 0; i < entries.size(); ++i) {
     if (keys) keys[i] = entries[i].key;
@@ -214,11 +227,14 @@ size_t urb_lru_entries(const urb_lru* c, uint32_t layer, uint64_t* keys, uint64_
   return entries.size();
 }
 
-uint64_t urb_lru_clock(const urb_lru* c) { return c->clock; }
-void urb_lru_set_clock(urb_lru* c, uint64_t clock) { c->clock = clock; }
+uint64_t urb_lru_clock(const urb_lru* c) { return c ? c->clock : 0; }
+void urb_lru_set_clock(urb_lru* c, uint64_t clock) {
+  if (c) c->clock = clock;
+}
 
 size_t urb_lru_drain_layer(urb_lru* c, urb_lru_telemetry* t, uint32_t layer,
                            uint64_t* values_out) {
+  if (!c || !t || !c->has(layer)) return 0;
   std::vector<Entry> entries;
   entries.swap(c->layers[layer]);
   uint64_t bytes = 0;
@@ -234,6 +250,7 @@ size_t urb_lru_drain_layer(urb_lru* c, urb_lru_telemetry* t, uint32_t layer,
 
 int urb_lru_can_insert_without_eviction(const urb_lru* c, uint32_t layer, const uint64_t* keys,
                                         size_t n) {
+  if (!c || !c->has(layer) || (n && !keys)) return 0;
   const size_t cap = c->capacities[layer];
   if (cap == 0) return 0;
   std::vector<uint64_t> missing;
@@ -246,11 +263,13 @@ int urb_lru_can_insert_without_eviction(const urb_lru* c, uint32_t layer, const 
 
 size_t urb_lru_projected_misses(const urb_lru* c, uint32_t layer, const uint64_t* keys,
                                 size_t n) {
+  if (!c || !c->has(layer) || (n && !keys)) return n;
   return c->projected(layer, keys, n).second;
 }
 
 int urb_lru_grouped_access_order(const urb_lru* c, uint32_t layer, const uint64_t* keys,
                                  size_t n, uint64_t* order_out, size_t* order_n) {
+  if (!c || !c->has(layer) || !order_out || !order_n || (n && !keys)) return 0;
   // once timestamps would saturate, key order no longer stands for recency
   if (c->clock > kMax - (uint64_t)n) return 0;
   const std::vector<uint64_t> grouped = last_use_order(keys, n);
@@ -265,6 +284,10 @@ int urb_lru_grouped_access_order(const urb_lru* c, uint32_t layer, const uint64_
 
 void urb_lru_finish_grouped_accesses(urb_lru* c, uint32_t layer, const uint64_t* keys, size_t n,
                                      size_t groups) {
+  // the clock advanced once per group access since the schedule began, so it is at least
+  // `groups`; a call that breaks this (or names another layer) changes nothing
+  if (!c || !c->has(layer) || (n && !keys) || c->clock < groups) return;
+  if (c->clock - groups > kMax - n) return;
   const uint64_t initial = c->clock - groups;
   c->clock = initial + n;
   for (Entry& e : c->layers[layer])
@@ -277,6 +300,7 @@ void urb_lru_finish_grouped_accesses(urb_lru* c, uint32_t layer, const uint64_t*
 
 urb_lru_plan* urb_lru_grouped_access_plan(const urb_lru* c, uint32_t layer, const uint64_t* keys,
                                           size_t n) {
+  if (!c || !c->has(layer) || !keys) return nullptr;
   if (c->capacities[layer] == 0 || n == 0) return nullptr;
   if (c->clock > kMax - (uint64_t)n) return nullptr;
   std::vector<uint64_t> order = last_use_order(keys, n);
@@ -303,6 +327,7 @@ urb_lru_plan* urb_lru_grouped_access_plan(const urb_lru* c, uint32_t layer, cons
 void urb_lru_plan_destroy(urb_lru_plan* plan) { delete plan; }
 
 size_t urb_lru_plan_order(const urb_lru_plan* plan, uint64_t* order_out) {
+  if (!plan || !order_out) return 0;
   std::copy(plan->order.begin(), plan->order.end(), order_out);
   return plan->order.size();
 }
@@ -310,6 +335,8 @@ size_t urb_lru_plan_order(const urb_lru_plan* plan, uint64_t* order_out) {
 int urb_lru_access_grouped(urb_lru* c, urb_lru_telemetry* t, const urb_lru_plan* plan,
                            uint64_t key, urb_lru_load_fn load, void* user, uint64_t* value,
                            uint64_t* evicted, int* has_evicted) {
+  if (!c || !t || !plan || !load || !value || !evicted || !has_evicted || !c->has(plan->layer))
+    return URB_ERR_ARGUMENT;
   const uint32_t layer = plan->layer;
   if (c->contains(layer, key))
     return urb_lru_access(c, t, layer, key, load, user, value, evicted, has_evicted);
@@ -342,6 +369,7 @@ int urb_lru_access_grouped(urb_lru* c, urb_lru_telemetry* t, const urb_lru_plan*
 }
 
 void urb_lru_finish_grouped_plan(urb_lru* c, const urb_lru_plan* plan) {
+  if (!c || !plan || !c->has(plan->layer)) return;
   // after the schedule only final keys are resident
   for (Entry& e : c->layers[plan->layer])
     if (plan->retains(e.key)) e.last_used = plan->retained_use(e.key);
@@ -351,6 +379,7 @@ void urb_lru_finish_grouped_plan(urb_lru* c, const urb_lru_plan* plan) {
 int urb_lru_prepare_ordered_batch(urb_lru* c, urb_lru_telemetry* t, uint32_t layer,
                                   const uint64_t* keys, size_t n, uint64_t* evicted_out,
                                   size_t* n_evicted) {
+  if (!c || !t || !c->has(layer) || !evicted_out || !n_evicted || (n && !keys)) return 0;
   const size_t cap = c->capacities[layer];
   if (cap == 0 || n == 0 || n > cap) return 0;
   for (size_t i = 0; i < n; ++i)
@@ -379,6 +408,12 @@ int urb_lru_prepare_ordered_batch(urb_lru* c, urb_lru_telemetry* t, uint32_t lay
   }
   for (uint64_t k : victims)
     if (!c->contains(layer, k)) return 0;
+  // Once the clock saturates, timestamps tie and an original entry the batch reloaded can be
+  // evicted a second time (the reference's "every simulated eviction refers to an original
+  // entry" then panics): refuse the batch, changing nothing.
+  for (size_t i = 0; i < victims.size(); ++i)
+    for (size_t j = 0; j < i; ++j)
+      if (victims[i] == victims[j]) return 0;
   auto& entries = c->layers[layer];
   size_t m = 0;
   for (uint64_t k : victims) {
@@ -393,6 +428,7 @@ int urb_lru_prepare_ordered_batch(urb_lru* c, urb_lru_telemetry* t, uint32_t lay
 }
 
 uint32_t urb_lru_lend_unused_capacity(urb_lru* c, uint32_t layer, uint32_t maximum) {
+  if (!c || !c->has(layer)) return 0;
   const uint32_t steady = c->capacities[layer];
   uint64_t elsewhere = 0;
   for (size_t l = 0; l < c->layers.size(); ++l)
@@ -404,6 +440,7 @@ uint32_t urb_lru_lend_unused_capacity(urb_lru* c, uint32_t layer, uint32_t maxim
 
 size_t urb_lru_restore_layer_capacity(urb_lru* c, urb_lru_telemetry* t, uint32_t layer,
                                       uint32_t capacity, uint64_t* evicted_out) {
+  if (!c || !t || !c->has(layer)) return 0;
   c->capacities[layer] = capacity;
   auto& entries = c->layers[layer];
   size_t m = 0;

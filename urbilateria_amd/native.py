@@ -24,7 +24,7 @@ EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_rout
            "urb_moe_profile", "urb_moe_profile_read", "urb_pack_matrix", "urb_quantize_e4m3",
            "urb_expert_views", "urb_moe_forward_block", "urb_zc_rms_norm_bf16",
            "urb_moe_set_expert", "urb_moe_forward_tokens", "urb_moe_route_tokens",
-           "urb_quantize_e4m3_blocks")
+           "urb_quantize_e4m3_blocks", "urb_gemm_placement")
 STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
@@ -122,6 +122,9 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_zc_rms_norm_bf16.restype = ctypes.c_int
         lib.urb_expert_views.argtypes = [ctypes.c_int, u32, u32, u32, P, P, P, P, P]
         lib.urb_expert_views.restype = ctypes.c_int
+        lib.urb_gemm_placement.argtypes = [ctypes.c_int, ctypes.c_int, u32, u32, u32, u32, P, P,
+                                           u32]
+        lib.urb_gemm_placement.restype = u32
         lib.urb_status_string.argtypes = [ctypes.c_int]
         lib.urb_status_string.restype = ctypes.c_char_p
         for f in EXPORTS:

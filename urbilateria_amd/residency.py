@@ -361,8 +361,25 @@ class StreamedMoeLayer:
                                       _to_device(getattr(layer, "hash_experts", None)))
         self.layer = moe.MoeLayer(placeholder, max_tokens, source=N.SOURCE_DEVICE_BORROW)
         self.cache = cache if cache is not None else LayerLruCache(layer_index + 1, slots)
+        self._check_capacity()
         self.telemetry = Telemetry()
-        self._free = list(range(slots))
+
+    def _check_capacity(self) -> None:
+        # one slot per resident expert: a layer capacity other than `slots` (another cache, or
+        # capacity lent by lend_unused_capacity) would admit experts with no slot to hold them
+        cap = self.cache.layer_capacity(self.layer_index)
+        if cap != self.slots:
+            raise ValueError(f"the cache holds {cap} experts of layer {self.layer_index}, the "
+                             f"layer has {self.slots} HBM slots")
+
+    def _free_slot(self) -> int:
+        """A slot no resident expert of the layer holds.  Called from the load, after the access
+        evicted its victim, so the cache's own entries say which slots are in use."""
+        used = {e.value for e in self.cache.entries(self.layer_index)}
+        for slot in range(self.slots):
+            if slot not in used:
+                return slot
+        raise RuntimeError("no free HBM slot although the cache has room")
 
     def _pack(self, expert: int, slot: int) -> None:
         from . import moe
@@ -383,28 +400,23 @@ class StreamedMoeLayer:
                                                moe._stream_handle()), "urb_moe_set_expert")
 
     def _access(self, key: int) -> None:
-        layer = self.layer_index
-        if not self.cache.contains(layer, key):
-            if self._free:
-                slot = self._free.pop()
-            else:  # the victim the access is about to evict frees its slot
-                ents = self.cache.entries(layer)
-                slot = min(ents, key=lambda e: (e.last_used, e.key)).value
-
-            def load(key=key, slot=slot):
-                self._pack(key, slot)
-                self._point(key, slot)
-                return slot, self._slot_bytes, self._slot_bytes
-        else:
-            def load():  # never called on a hit
-                raise RuntimeError("unexpected load")
-        self.cache.access_with_evicted(self.telemetry, layer, key, load)
+        """One expert access through the policy.  A miss packs the expert into a free slot (never
+        one a resident expert uses) and repoints the table after validating it; a failed load
+        (bad payload, pack error) leaves every resident expert and its slot untouched, and the
+        slot it wrote stays free, so later calls are unaffected."""
+        def load(key=key):
+            slot = self._free_slot()
+            self._pack(key, slot)
+            self._point(key, slot)
+            return slot, self._slot_bytes, self._slot_bytes
+        self.cache.access_with_evicted(self.telemetry, self.layer_index, key, load)
 
     def forward(self, x, token_ids=None):
         """x [T, H] f32 (device) -> (y, ids, weights) of the resident layer; ``token_ids`` [T]
         for a layer with a hash table."""
         import torch
-        T, k = x.shape[0], self.spec.top_k
+        self._check_capacity()
+        T = x.shape[0]
         _, ids, _ = self.layer.route(x, token_ids=token_ids)
         ids = ids.cpu().tolist()
         runs, start, seen = [], 0, set()
