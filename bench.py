@@ -1,10 +1,13 @@
 #!/usr/bin/env python3
 """MoE-layer benchmark on one MI355X: the five seeded workloads, HBM-resident inputs.
 
-Prints ONE JSON line.  ``value`` is the prefill throughput of the BF16 layer with 128 tokens
-(H 2048, 128 experts, top-8, I 768); every workload's tokens/s, HBM and MFMA fractions and CPU
-baseline are listed under ``all_configs``.  ``roofline`` describes the dominant kernel of the
-headline workload, its duration measured with HIP events on the stream it runs on.
+Prints ONE JSON line.  ``value`` is the prefill throughput of the largest workload, the Kimi-scale
+MXFP4 layer with 1024 tokens and Zipf(1.1)-skewed routing (H 7168, 384 experts, top-8, I 2048,
+BF16 shared expert).  Every workload's tokens/s, HBM and MFMA fractions, its own ``roofline``
+block and its CPU baseline are listed under ``all_configs``.  A ``roofline`` block describes the
+workload's dominant kernel: algorithmic bytes per launch over its average duration, measured
+with HIP events on the stream the kernel runs on, and the HBM bytes the rocprofv3 counters
+measured for it (profiles/hbm_traffic.json).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs a,b] [--cpu-seconds S]
 """
@@ -24,10 +27,12 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE-layer decode tok/s + % HBM peak; prefill tok/s + % MFMA peak, 1 GPU"
 HBM_PEAK = 8.0e12                                            # B/s
 MFMA_PEAK = {"bf16": 2.5e15, "fp8": 5.0e15, "fp4": 10.1e15}  # dense FLOP/s
-HEADLINE = ("c2_bf16_prefill", 128)
+HEADLINE = ("c5_mxfp4_zipf_prefill", 1024)
 RUNS = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
         ("c3_mxfp4_decode", 32), ("c4_mxfp8", 1), ("c4_mxfp8", 512),
-        ("c5_mxfp4_zipf_prefill", 1024)]
+        ("c5_mxfp4_zipf_prefill", 1024), ("c5_mxfp4_zipf_hot", 1024)]
+# the projection stages a roofline block may name (routing kernels are latency-bound)
+PROJECTIONS = ("gate_up", "down", "shared_gate_up", "shared_down")
 MALL_BYTES = 256 << 20   # Infinity Cache: rotate enough layer copies to stream past it
 
 
@@ -67,6 +72,14 @@ def layer_flops(spec, tokens):
     return 2 * tokens * (E * H + k * 3 * H * I + 3 * H * Is)
 
 
+def stage_flops(spec, stage, tokens):
+    """FLOPs of one launch of a projection stage (2 per multiply-add)."""
+    H, I, k, Is = spec.hidden, spec.intermediate, spec.top_k, spec.shared_intermediate
+    return {"gate_up": 2 * tokens * k * 2 * H * I, "down": 2 * tokens * k * H * I,
+            "shared_gate_up": 2 * tokens * 2 * H * Is,
+            "shared_down": 2 * tokens * H * Is}.get(stage, 0)
+
+
 def stage_bytes(spec, C, stage, tokens, distinct):
     """Algorithmic HBM bytes of one launch of a stage (weights touched once, f32 activations)."""
     H, I, E, k, Is = spec.hidden, spec.intermediate, spec.n_experts, spec.top_k, \
@@ -104,38 +117,99 @@ def measured_traffic(workload, tokens, stage):
     return None
 
 
-def cpu_baseline(name, spec, C, dev, x, budget_s, threads, tok=None):
+def host_disclosure(workers):
+    """The CPU the baseline ran on: model, sockets, physical cores and logical CPUs of the
+    allowed set, AVX2/FMA (which select the reference's BF16 and MXFP8 kernels), workers."""
+    from oracle import oracle as O
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    allowed = sorted(os.sched_getaffinity(0))
+    packages = set()
+    for c in allowed:
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id") as f:
+                packages.add(int(f.read()))
+        except (OSError, ValueError):
+            pass
+    return {"cpu_model": model, "sockets": len(packages), "physical_cores": O.physical_cores(),
+            "logical_cpus": len(allowed), "avx2": "avx2" in flags, "fma": "fma" in flags,
+            "workers": workers, "pinned": "physical-core-first, one worker per core"}
+
+
+def cpu_workers():
+    """One worker per physical core of the allowed CPU set (src/execution.rs:254-263), capped
+    at the CPU share this process is given (OMP_NUM_THREADS on a shared GPU host)."""
+    from oracle import oracle as O
+    physical = max(1, O.physical_cores())
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return min(physical, share) if share > 0 else physical
+
+
+def cpu_baseline(name, spec, C, dev, x, budget_s, tok=None):
     """The CPU oracle (a C++ restatement of the reference's CPU path) timed on a bounded
-    sample of the same workload's tokens, one worker per core."""
+    sample of the same workload's tokens, with the reference's execution contract: one worker
+    per physical core, pinned physical-core-first (src/execution.rs:254-394)."""
     import numpy as np
     from oracle import oracle as O
     T = x.shape[0]
     host = dev.to_host()
     xs = x.cpu().numpy()
     ts = None if tok is None else tok.cpu().numpy().astype(np.uint32)
+    threads = cpu_workers()
+    prev = O.set_pinning(True)
 
     def call(n):
         O.moe_forward(spec, host.experts, host.router_weight, xs[:n], host.correction_bias,
                       host.shared, threads=threads, shared_expert_gate=host.shared_expert_gate,
                       token_ids=None if ts is None else ts[:n], hash_experts=host.hash_experts)
-    call(1)  # warm pool and page cache
-    t0 = time.perf_counter()
-    call(1)
-    one = time.perf_counter() - t0
-    # tokens per call: the whole batch when a call fits the budget, else a prefix that does;
-    # whole calls repeat until the budget is spent
-    n = int(max(1, min(T, budget_s / max(one, 1e-6))))
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        call(n)
-        reps += 1
-        if time.perf_counter() - t0 >= budget_s or reps >= 5000:
-            break
-    dt = (time.perf_counter() - t0) / reps
+    try:
+        call(1)  # warm pool and page cache
+        t0 = time.perf_counter()
+        call(1)
+        one = time.perf_counter() - t0
+        # tokens per call: the whole batch when a call fits the budget, else a prefix that
+        # does; whole calls repeat until the budget is spent
+        n = int(max(1, min(T, budget_s / max(one, 1e-6))))
+        reps = 0
+        t0 = time.perf_counter()
+        while True:
+            call(n)
+            reps += 1
+            if time.perf_counter() - t0 >= budget_s or reps >= 5000:
+                break
+        dt = (time.perf_counter() - t0) / reps
+    finally:
+        O.set_pinning(prev)
     return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{name}: first {n} of {T} tokens x{reps}, {dt * 1e3:.1f} ms per call, "
-                      f"C++ restatement of the reference CPU path, {threads} threads"}
+                      f"C++ restatement of the reference CPU path, {threads} pinned workers",
+            "host": host_disclosure(threads)}
+
+
+def roofline_block(rec, spec, C, workload, tokens):
+    """The dominant projection kernel of a run: algorithmic bytes per launch over its average
+    launch duration (HIP events on its stream), against 8 TB/s; its MFMA rate against the
+    dense BF16 peak; and the counter-measured HBM bytes per launch when profiles/ holds them."""
+    stages = rec["stages"]
+    cands = [k for k in PROJECTIONS if k in stages]
+    if not cands:
+        return None
+    dom = max(cands, key=lambda k: stages[k]["avg_us"])
+    st = stages[dom]
+    achieved = st["bytes"] / (st["avg_us"] * 1e-6) / 1e9
+    return {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s", "frac": achieved / (HBM_PEAK / 1e9),
+            "traffic": measured_traffic(workload, tokens, dom),
+            "bytes_per_launch": st["bytes"], "avg_launch_us": st["avg_us"],
+            "mfma_frac_bf16": st.get("flops", 0) / (st["avg_us"] * 1e-6) / MFMA_PEAK["bf16"]}
 
 
 def run_one(name, T, args, want_cpu, cpu_budget):
@@ -146,14 +220,7 @@ def run_one(name, T, args, want_cpu, cpu_budget):
 
     w = C.workload(name)
     spec = w.spec
-    bias = None
-    if w.zipf_s:
-        from urbilateria_amd import synth
-        # logit std of a BF16 N(0, 0.02) router row on N(0, 1) inputs is 0.02 * sqrt(H)
-        std = np.full(spec.n_experts, 0.02 * math.sqrt(spec.hidden))
-        beta = C.calibrate_zipf_beta(spec.n_experts, spec.top_k, w.zipf_s, std,
-                                     router=spec.router)
-        bias = C.zipf_bias(spec.n_experts, w.zipf_s, beta)
+    beta, bias = C.workload_bias(w)
     table = tok = None
     if w.hash_vocab:
         from urbilateria_amd import synth
@@ -215,7 +282,8 @@ def run_one(name, T, args, want_cpu, cpu_budget):
         if n:
             avg = tms / n
             b = stage_bytes(spec, C, k, T, distinct)
-            stage_rows[k] = {"avg_us": avg * 1e3, "bytes": b, "GBps": b / (avg * 1e-3) / 1e9}
+            stage_rows[k] = {"avg_us": avg * 1e3, "bytes": b, "GBps": b / (avg * 1e-3) / 1e9,
+                             "flops": stage_flops(spec, k, T)}
     dom = max(stage_rows, key=lambda k: stage_rows[k]["avg_us"]) if stage_rows else None
     flops = layer_flops(spec, T)
     fmt = C.FORMAT_NAMES[spec.expert_format]
@@ -234,12 +302,12 @@ def run_one(name, T, args, want_cpu, cpu_budget):
     }
     if w.zipf_s:
         rec["zipf_bias_beta"] = float(beta)
+    rec["roofline"] = roofline_block(rec, spec, C, name, T)
     cpu_job = None
     if want_cpu:
         # run after every GPU measurement, so no GPU timing follows seconds of host-only work
-        threads = min(16, os.cpu_count() or 1)
         cpu_job = (lambda dev=first, xx=x, tt=tok:
-                   cpu_baseline(name, spec, C, dev, xx, cpu_budget, threads, tt))
+                   cpu_baseline(name, spec, C, dev, xx, cpu_budget, tt))
     for l in layers:
         l.close()
     del layers, devs, first, x, y
@@ -285,7 +353,10 @@ def main():
             log(f"  {rec['cpu_baseline']['value']:.1f} tokens/s on "
                 f"{rec['cpu_baseline']['cores']} threads")
     head = next((r for r in results if (r["workload"], r["tokens"]) == HEADLINE), results[0])
-    dom = head["stages"].get(head["dominant_stage"], {})
+    fmt = head["workload"]
+    dtype = ("bf16 weights x f32 activations" if "bf16" in fmt else
+             "mxfp8 weights x f32 activations" if "mxfp8" in fmt else
+             "mxfp4 weights x f32 activations") + " (bf16 MFMA, f32 accumulation)"
     line = {
         "metric": METRIC,
         "value": head["tokens_per_s"],
@@ -297,19 +368,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if "bf16" in head["workload"] else "f32-accumulated MX",
+        "dtype": dtype,
         "data": "synthetic (seeded SplitMix64 weights and activations)",
         "config": {"workload": f"{head['workload']}: {head['description']}",
                    "tokens": head["tokens"], "parallelism": "single GPU"},
         "hbm_frac": head["hbm_frac"],
         "mfma_frac": head["mfma_frac_bf16"],
-        "roofline": {
-            "kernel": head["dominant_stage"], "bound": "hbm",
-            "achieved": dom.get("GBps"), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": (dom.get("GBps") or 0) / (HBM_PEAK / 1e9),
-            "traffic": measured_traffic(head["workload"], head["tokens"], head["dominant_stage"]),
-            "bytes_per_launch": dom.get("bytes"), "avg_launch_us": dom.get("avg_us"),
-        },
+        "roofline": head.get("roofline"),
         "cpu_baseline": head.get("cpu_baseline"),
         "all_configs": results,
     }

@@ -68,6 +68,12 @@ def _load():
     lib.urbo_moe_forward_tokens.argtypes = [P, P, P, ctypes.c_uint32, P, P, P, P, ctypes.c_int]
     lib.urbo_dsv4_expert.argtypes = [ctypes.c_int, P, ctypes.c_uint32, ctypes.c_uint32, P,
                                      ctypes.c_uint32, ctypes.c_float, P, P, ctypes.c_int]
+    lib.urbo_physical_cores.argtypes = []
+    lib.urbo_physical_cores.restype = ctypes.c_int
+    lib.urbo_cpu_order.argtypes = [P, sz]
+    lib.urbo_cpu_order.restype = sz
+    lib.urbo_set_pinning.argtypes = [ctypes.c_int]
+    lib.urbo_set_pinning.restype = ctypes.c_int
     return lib
 
 
@@ -326,6 +332,24 @@ def gated_mlp(fmt: int, triple, hidden: int, intermediate: int, x: np.ndarray,
     _check(_lib.urbo_gated_mlp(fmt, ctypes.addressof(mats), hidden, intermediate, _ptr(x),
                                x.shape[0], _ptr(y), threads))
     return y
+
+
+def physical_cores() -> int:
+    """recommended_worker_threads (src/execution.rs:254-263): physical cores in the allowed set."""
+    return int(_lib.urbo_physical_cores())
+
+
+def cpu_order() -> list:
+    """The allowed logical CPUs, one per physical core first (src/execution.rs:270-330)."""
+    buf = (ctypes.c_int * 8192)()
+    n = _lib.urbo_cpu_order(buf, 8192)
+    return [buf[i] for i in range(min(n, 8192))]
+
+
+def set_pinning(enable: bool) -> bool:
+    """Pin pool worker i to cpu_order()[i] (the reference pool's start_handler); returns the
+    previous setting."""
+    return bool(_lib.urbo_set_pinning(int(enable)))
 
 
 def set_mxfp8_fma_host(fma_host: bool) -> bool:

@@ -8,14 +8,21 @@
 
 #include "urb_oracle.h"
 
+#include <sched.h>
+
 #include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <condition_variable>
 #include <cstring>
+#include <fstream>
 #include <functional>
 #include <mutex>
+#include <set>
+#include <sstream>
+#include <string>
 #include <thread>
+#include <tuple>
 #include <vector>
 
 namespace {
@@ -83,10 +90,102 @@ inline bool rne_bf16(float value, float *out) {
 // ------------------------------------------------------------------------------------------
 constexpr size_t kParallelMinWork = 64 * 1024;
 
+// ------------------------------------------------------------------------------------------
+// CPU topology and pinning: src/execution.rs:254-394.  The logical CPUs of the allowed set
+// (/proc/self/status Cpus_allowed_list) with their (package, core) ids from sysfs, ordered so
+// every physical core gets one CPU before any SMT sibling (physical_core_first); the default
+// pool width is the number of physical cores (recommended_worker_threads), and worker i is
+// pinned to the i-th CPU of that order (the pool's start_handler).
+// ------------------------------------------------------------------------------------------
+bool parse_cpu_list(const std::string &value, std::vector<int> *out) {
+    std::stringstream ss(value);
+    std::string part;
+    while (std::getline(ss, part, ',')) {
+        const size_t dash = part.find('-');
+        try {
+            const int a = std::stoi(part.substr(0, dash));
+            const int b = dash == std::string::npos ? a : std::stoi(part.substr(dash + 1));
+            if (b < a) return false;
+            for (int c = a; c <= b; ++c) out->push_back(c);
+        } catch (...) {
+            return false;
+        }
+    }
+    return true;
+}
+
+// (cpu, package, core) of the allowed logical CPUs, sorted by cpu (available_cpu_topology).
+std::vector<std::tuple<int, int, int>> cpu_topology() {
+    std::set<int> allowed;
+    bool have_allowed = false;
+    std::ifstream status("/proc/self/status");
+    for (std::string line; std::getline(status, line);) {
+        const std::string key = "Cpus_allowed_list:";
+        if (line.compare(0, key.size(), key) == 0) {
+            std::vector<int> cpus;
+            std::string v = line.substr(key.size());
+            v.erase(0, v.find_first_not_of(" \t"));
+            if (parse_cpu_list(v, &cpus)) {
+                allowed.insert(cpus.begin(), cpus.end());
+                have_allowed = true;
+            }
+        }
+    }
+    std::vector<std::tuple<int, int, int>> topo;
+    for (int cpu = 0; cpu < 4096; ++cpu) {
+        const std::string base = "/sys/devices/system/cpu/cpu" + std::to_string(cpu) + "/topology/";
+        std::ifstream pk(base + "physical_package_id"), co(base + "core_id");
+        int package, core;
+        if (!(pk >> package) || !(co >> core)) continue;
+        if (have_allowed && !allowed.count(cpu)) continue;
+        topo.emplace_back(cpu, package, core);
+    }
+    return topo;
+}
+
+std::vector<int> physical_core_first_order() {
+    std::set<std::pair<int, int>> seen;
+    std::vector<int> primary, siblings;
+    for (const auto &t : cpu_topology()) {
+        if (seen.insert({std::get<1>(t), std::get<2>(t)}).second)
+            primary.push_back(std::get<0>(t));
+        else
+            siblings.push_back(std::get<0>(t));
+    }
+    primary.insert(primary.end(), siblings.begin(), siblings.end());
+    return primary;
+}
+
+int physical_core_count() {
+    std::set<std::pair<int, int>> cores;
+    for (const auto &t : cpu_topology()) cores.insert({std::get<1>(t), std::get<2>(t)});
+    return (int)cores.size();
+}
+
+void pin_current_thread(int cpu) {  // best effort, as the reference
+    if (cpu < 0 || cpu >= CPU_SETSIZE) return;
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    CPU_SET(cpu, &set);
+    (void)sched_setaffinity(0, sizeof(set), &set);
+}
+
+std::atomic<int> g_pin_workers{0};
+
+// The pool: n worker threads run every parallel loop while the caller waits, as calls entering
+// the reference's Rayon pool (install) do.  With pinning on, worker i runs on the i-th CPU of
+// the physical-core-first order.
 class Pool {
   public:
-    explicit Pool(int n) : n_(n) {
-        for (int i = 1; i < n_; ++i) workers_.emplace_back([this] { loop(); });
+    Pool(int n, bool pin) : n_(n), pin_(pin) {
+        const std::vector<int> order = pin ? physical_core_first_order() : std::vector<int>();
+        for (int i = 0; i < n_ && n_ > 1; ++i) {
+            const int cpu = i < (int)order.size() ? order[i] : -1;
+            workers_.emplace_back([this, cpu] {
+                if (cpu >= 0) pin_current_thread(cpu);
+                loop();
+            });
+        }
     }
     ~Pool() {
         { std::lock_guard<std::mutex> g(m_); stop_ = true; }
@@ -94,22 +193,19 @@ class Pool {
         for (auto &t : workers_) t.join();
     }
     int size() const { return n_; }
+    bool pinned() const { return pin_; }
     void run(size_t items, const std::function<void(size_t)> &fn) {
         if (n_ <= 1 || items <= 1) {
             for (size_t i = 0; i < items; ++i) fn(i);
             return;
         }
-        {
-            std::lock_guard<std::mutex> g(m_);
-            fn_ = &fn;
-            items_ = items;
-            next_.store(0);
-            active_ = (int)workers_.size();
-            ++generation_;
-        }
-        cv_.notify_all();
-        drain();
         std::unique_lock<std::mutex> g(m_);
+        fn_ = &fn;
+        items_ = items;
+        next_.store(0);
+        active_ = (int)workers_.size();
+        ++generation_;
+        cv_.notify_all();
         done_cv_.wait(g, [this] { return active_ == 0; });
         fn_ = nullptr;
     }
@@ -139,6 +235,7 @@ class Pool {
         }
     }
     int n_;
+    bool pin_;
     std::vector<std::thread> workers_;
     std::mutex m_;
     std::condition_variable cv_, done_cv_;
@@ -156,9 +253,10 @@ Pool *g_pool = nullptr;
 Pool &pool(int threads) {
     std::lock_guard<std::mutex> g(g_pool_mutex);
     if (threads < 1) threads = 1;
-    if (!g_pool || g_pool->size() != threads) {
+    const bool pin = g_pin_workers.load() != 0;
+    if (!g_pool || g_pool->size() != threads || g_pool->pinned() != pin) {
         delete g_pool;
-        g_pool = new Pool(threads);
+        g_pool = new Pool(threads, pin);
     }
     return *g_pool;
 }
@@ -736,6 +834,16 @@ int urbo_route_sqrt_softplus_hashed(const float *logits, const float *bias, cons
 }
 
 float urbo_silu(float value) { return silu_f(value); }
+
+int urbo_physical_cores(void) { return physical_core_count(); }
+
+size_t urbo_cpu_order(int *cpus, size_t capacity) {
+    const std::vector<int> order = physical_core_first_order();
+    for (size_t i = 0; i < order.size() && i < capacity; ++i) cpus[i] = order[i];
+    return order.size();
+}
+
+int urbo_set_pinning(int enable) { return g_pin_workers.exchange(enable ? 1 : 0); }
 
 int urbo_set_mxfp8_fma_host(int fma_host) {
     int old = g_mxfp8_fma_host;

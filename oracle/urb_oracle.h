@@ -90,6 +90,14 @@ int urbo_route_sqrt_softplus_hashed(const float *logits, const float *bias, cons
                                     size_t n, size_t top_k, float scale, int32_t *ids,
                                     float *weights, float *selection_out);
 float urbo_silu(float value);
+/* The reference's execution contract (src/execution.rs:254-394): the number of physical cores
+ * in the allowed CPU set (recommended_worker_threads), and the allowed logical CPUs in
+ * physical-core-first order (room for `capacity`; returns the count).  With pinning on, worker i
+ * of the row-parallel pool runs pinned to the i-th CPU of that order; returns the previous
+ * setting.  Default off. */
+int urbo_physical_cores(void);
+size_t urbo_cpu_order(int *cpus, size_t capacity);
+int urbo_set_pinning(int enable);
 /* Selects MxFp8Matrix::matvec_rows's host kernel for layer calls (src/math/mxfp.rs:720-765):
  * 1 = compact 8-lane FMA (AVX2+FMA hosts, the default), 0 = ordered f64.  Returns the previous. */
 int urbo_set_mxfp8_fma_host(int fma_host);

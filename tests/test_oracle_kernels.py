@@ -1043,3 +1043,42 @@ def test_qwen_shared_expert_requires_bf16_and_its_gate():
     with pytest.raises(O.OracleError) as e:
         O.moe_forward(layer.spec, layer.experts, layer.router_weight, x, None, layer.shared)
     assert e.value.status == 1
+
+
+def _sysfs_core(cpu):
+    base = f"/sys/devices/system/cpu/cpu{cpu}/topology/"
+    return (int(open(base + "physical_package_id").read()), int(open(base + "core_id").read()))
+
+
+def test_cpu_order_is_physical_core_first_over_the_allowed_set():
+    # src/execution.rs:254-330: one worker per physical core of the allowed CPU set, CPUs
+    # ordered so every physical core appears once before any SMT sibling
+    order = O.cpu_order()
+    allowed = sorted(os.sched_getaffinity(0))
+    assert sorted(order) == allowed
+    cores = [_sysfs_core(c) for c in order]
+    n = O.physical_cores()
+    assert n == len(set(cores))
+    assert len(set(cores[:n])) == n  # the first n CPUs are n distinct physical cores
+
+
+def test_pinned_pool_gives_identical_results():
+    # pinning only places the workers; every row keeps its reduction order, so a pinned
+    # 4-worker pool, an unpinned one and one worker agree bit for bit
+    rng = np.random.default_rng(5)
+    H, I = 512, 256
+
+    def bf16_matrix(rows, cols):
+        v = np.array([O.round_to_bf16(float(a)) for a in rng.standard_normal(rows * cols) * 0.05],
+                     np.float32)
+        return ((v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8), None)
+    triple = [bf16_matrix(I, H), bf16_matrix(I, H), bf16_matrix(H, I)]
+    x = rng.standard_normal((3, H)).astype(np.float32)
+    one = O.gated_mlp(O.FMT_BF16, triple, H, I, x, threads=1)
+    loose = O.gated_mlp(O.FMT_BF16, triple, H, I, x, threads=4)
+    prev = O.set_pinning(True)
+    try:
+        pinned = O.gated_mlp(O.FMT_BF16, triple, H, I, x, threads=4)
+    finally:
+        O.set_pinning(prev)
+    assert np.array_equal(one, loose) and np.array_equal(one, pinned)

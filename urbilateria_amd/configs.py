@@ -98,6 +98,9 @@ class Workload:
     zipf_s: Optional[float] = None
     description: str = ""
     hash_vocab: int = 0   # > 0: routed by a synthetic tid2eid table of this many token ids
+    # > 0: the Zipf bias's beta is set so the hottest expert takes this share of the tokens,
+    # instead of by the log-log slope fit
+    zipf_top_share: float = 0.0
 
 
 # The five benchmark configurations (shapes, routers, formats and value distributions).
@@ -137,6 +140,19 @@ WORKLOADS: Dict[str, Workload] = {
         (1024,), zipf_s=1.1,
         description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias I2048 + BF16 shared, "
                     "prefill 1024"),
+    # C5 with the load imbalance the Zipf(1.1) popularity model predicts for top-8 selection
+    # without replacement: the hottest expert routed by ~850 of 1024 tokens.  (Fitting the
+    # log-log slope of the whole frequency curve, as c5_mxfp4_zipf_prefill does, lets the
+    # Gaussian tail of the logits dominate and gives a much flatter head.)
+    "c5_mxfp4_zipf_hot": Workload(
+        "c5_mxfp4_zipf_hot",
+        LayerSpec(hidden=7168, n_experts=384, top_k=8, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_BF16,
+                  router=ROUTER_SIGMOID_NOAUX_TC, composition=COMPOSE_GLM, n_group=1,
+                  topk_group=1, normalize=True, routed_scaling_factor=1.0),
+        (1024,), zipf_s=1.1, zipf_top_share=850.0 / 1024.0,
+        description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias, hottest expert ~850 of "
+                    "1024 tokens, I2048 + BF16 shared, prefill 1024"),
 }
 
 # The MX-activation mode on the shapes of C4 and C5: Hy4's composition (E4M3 activations per
@@ -302,9 +318,9 @@ def zipf_bias(n_experts: int, s: float, beta: float, base_seed: int = synth.BASE
 
 def calibrate_zipf_beta(n_experts: int, top_k: int, s: float, logit_std: np.ndarray,
                         tokens: int = 4096, base_seed: int = synth.BASE_SEED,
-                        router: int = ROUTER_SIGMOID_NOAUX_TC) -> float:
+                        router: int = ROUTER_SIGMOID_NOAUX_TC, top_target: float = 0.0) -> float:
     """Bisection on beta so the log-log slope of expert selection frequency against popularity
-    rank is -s.  Router logits are drawn as independent N(0, logit_std[e]^2), the distribution
+    rank is -s (top_target > 0: so the hottest expert is selected by that share of tokens).  Router logits are drawn as independent N(0, logit_std[e]^2), the distribution
     a BF16 N(0, 0.02) router produces on N(0, 1) activations (logit_std[e] = ||w_e||); the
     selection score is the router's: sigmoid, or sqrt(softplus) for ROUTER_SQRT_SOFTPLUS."""
     z = synth.normals(synth.stream_seed("zipf.calibration", base_seed), tokens * n_experts)
@@ -325,14 +341,39 @@ def calibrate_zipf_beta(n_experts: int, top_k: int, s: float, logit_std: np.ndar
         ok = freq > 0
         return float(np.polyfit(np.log(rank[ok]), np.log(freq[ok]), 1)[0])
 
+    def top_share(beta: float) -> float:
+        bias = zipf_bias(n_experts, s, beta, base_seed).astype(np.float64)
+        sel = gates + bias[None, :]
+        top = np.argpartition(-sel, top_k - 1, axis=1)[:, :top_k]
+        return float(np.bincount(top.ravel(), minlength=n_experts).max()) / tokens
+
     lo, hi = 0.0, 4.0
     for _ in range(40):
         mid = 0.5 * (lo + hi)
-        if slope(mid) > -s:
+        if (top_share(mid) < top_target) if top_target else (slope(mid) > -s):
             lo = mid
         else:
             hi = mid
     return 0.5 * (lo + hi)
+
+
+_BIAS_CACHE: Dict[str, Tuple[float, np.ndarray]] = {}
+
+
+def workload_bias(w: Workload) -> Tuple[Optional[float], Optional[np.ndarray]]:
+    """(beta, correction bias [E]) of a Zipf workload, calibrated as the benchmark runs it
+    (None, None without a Zipf bias).  The logit std of a BF16 N(0, 0.02) router row on N(0, 1)
+    inputs is 0.02 sqrt(H)."""
+    if not w.zipf_s:
+        return None, None
+    if w.name not in _BIAS_CACHE:
+        spec = w.spec
+        std = np.full(spec.n_experts, 0.02 * np.sqrt(spec.hidden))
+        beta = calibrate_zipf_beta(spec.n_experts, spec.top_k, w.zipf_s, std,
+                                   router=spec.router, top_target=w.zipf_top_share)
+        _BIAS_CACHE[w.name] = (beta, zipf_bias(spec.n_experts, w.zipf_s, beta))
+    beta, bias = _BIAS_CACHE[w.name]
+    return beta, bias.copy()
 
 
 def with_tokens(w: Workload, tokens: int) -> Tuple[LayerSpec, int]:
