@@ -715,17 +715,22 @@ def test_streamed_layer_survives_a_failed_load():
     resident = moe_mod().MoeLayer(host, max_tokens=6)
     xs = [torch.from_numpy(synth.activations(f"x.stream.fail.{c}", 6, spec.hidden)).cuda()
           for c in range(6)]
+    warm = xs[0][:1].contiguous()  # one token: 8 of the 10 slots
+    _, ids0, _ = resident.forward(warm)
     _, ids1, _ = resident.forward(xs[1])
-    bad_expert = int(ids1[0, 0])
+    warm_set = set(ids0.ravel().tolist())
+    cands = [e for e in ids1.ravel().tolist() if e not in warm_set]
+    if not cands:
+        pytest.skip("every expert of the second call is routed by the warm-up token")
+    bad_expert = cands[0]
     good = host.experts[bad_expert][0]
     broken = good[1].copy()
     broken[3] = 0xFF
     experts = [list(e) for e in host.experts]
     experts[bad_expert][0] = (good[0], broken)
     streamed = R.StreamedMoeLayer(replace(host, experts=experts), slots=10, max_tokens=6)
-    streamed.forward(xs[0])  # fills slots (the bad expert may load here only if routed)
-    if streamed.cache.contains(0, bad_expert):
-        pytest.skip("the damaged expert was routed by the warm-up call")
+    streamed.forward(warm)
+    assert not streamed.cache.contains(0, bad_expert)
     with pytest.raises(R.LoadError):
         streamed.forward(xs[1])
     experts[bad_expert][0] = good  # repaired in the host store the layer streams from

@@ -70,7 +70,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nb
                                                        uint8_t* __restrict__ scales, int* status,
                                                        int round_first,
                                                        const float* __restrict__ row_w,
-                                                       const int32_t* __restrict__ row_slot) {
+                                                       const int32_t* __restrict__ row_slot,
+                                                       uint16_t* __restrict__ pieces) {
   const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   const size_t blk = gid >> 5;
   const size_t e0 = gid * VPT;  // first element of this lane
@@ -110,16 +111,25 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nb
   uint32_t code[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) code[j] = encode_e4m3(v[j] / scale);
-  if (values) {
+  if (values || pieces) {
     // E4M3 code -> value via the conversion instruction (exact), times the power of two
     float d[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j)
       d[j] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(code[j], 1.0f, false)[0] * scale;
-    if constexpr (VPT == 4)
-      *reinterpret_cast<float4*>(values + e0) = make_float4(d[0], d[1], d[2], d[3]);
-    else
-      values[e0] = d[0];
+    if (values) {
+      if constexpr (VPT == 4)
+        *reinterpret_cast<float4*>(values + e0) = make_float4(d[0], d[1], d[2], d[3]);
+      else
+        values[e0] = d[0];
+    }
+    if (pieces) {
+      const size_t row = e0 / (size_t)cols;
+      const int col = (int)(e0 - row * (size_t)cols);
+#pragma unroll
+      for (int j = 0; j < VPT; ++j)
+        store_piece_value(pieces + row * (size_t)(cols / 8) * kPieceUnit, col + j, d[j]);
+    }
   }
   if (codes)
 #pragma unroll
@@ -129,16 +139,16 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* x, size_t nb
 
 void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
                      uint8_t* scales, int* status, hipStream_t s, int round_first,
-                     const float* row_w, const int32_t* row_slot, int block) {
+                     const float* row_w, const int32_t* row_slot, int block, uint16_t* pieces) {
   const size_t nblocks = rows * cols / block;
   const size_t threads = nblocks * 32;
   const unsigned grid = (unsigned)((threads + 255) / 256);
   if (block == 128)
     quantize_kernel<4><<<grid, 256, 0, s>>>(x, nblocks, (int)cols, values, codes, scales, status,
-                                            round_first, row_w, row_slot);
+                                            round_first, row_w, row_slot, pieces);
   else
     quantize_kernel<1><<<grid, 256, 0, s>>>(x, nblocks, (int)cols, values, codes, scales, status,
-                                            round_first, row_w, row_slot);
+                                            round_first, row_w, row_slot, pieces);
 }
 
 // ------------------------------------------------------------------------------------------

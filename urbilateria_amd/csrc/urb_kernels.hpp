@@ -140,8 +140,9 @@ struct RouteParams {
 
 // Router logits.
 // Router logits, the reference's 8-lane FP32 tree (BF16-rounded when round_bf16).
+// With `xp` (T = 1 only), the kernel also writes the token's BF16 piece vector there.
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
-                         int round_bf16, int* status, hipStream_t s);
+                         int round_bf16, int* status, hipStream_t s, uint16_t* xp = nullptr);
 
 // GLM router logits: MFMA BF16 with f64 accumulation of 32-k partials, split over K into
 // f64 partial slices.  The router weight is packed in the panel layout with router_rows(E)
@@ -155,7 +156,7 @@ void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, 
 // (router_gemv_slices(E) slices, exact products summed in f64).
 int router_gemv_slices(int E);
 void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, double* part,
-                            int slices, int* status, hipStream_t s);
+                            int slices, int* status, hipStream_t s, uint16_t* xp = nullptr);
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s);
 // Top-k routing, one wavefront per token (logits is an output when p.part is set).
 void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,
@@ -166,6 +167,23 @@ constexpr int kMaxChunkTokens = 1024;
 void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int32_t* active,
                     int32_t* offsets, int32_t* counts, int32_t* perm_token, int32_t* pos_of_slot,
                     int32_t* tiles, int32_t* slot_of_pos, hipStream_t s);
+// One-token projections on the matrix cores (urb_decode.hip).  Inputs and activations are BF16
+// piece vectors (urb_panel.hpp): `xp` [H / 8 units] for the token, `act_xp` [slot][I / 8 units].
+// gate_up writes the activation as f32 (`act`, may be null) and/or pieces (`act_xp`).
+void launch_gemv_mfma_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
+                              int H, int I, const uint16_t* xp, float* act, uint16_t* act_xp,
+                              Epi epi, int* status, hipStream_t s);
+void launch_gemv_mfma_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
+                           int H, int I, const uint16_t* act_xp, float* y, Epi epi, int* status,
+                           hipStream_t s);
+bool mfma_down_combine_fits(int K);
+bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
+                                   const float* weights, const int32_t* asc, int K, int H, int I,
+                                   const uint16_t* act_xp, const float* shared, int comp, Epi epi,
+                                   float* out, int* status, hipStream_t s,
+                                   const float* residual = nullptr, const float* gate = nullptr);
+void launch_split_pieces(const float* x, size_t rows, size_t cols, uint16_t* out, hipStream_t s);
+constexpr int kPieceUnit = 32;  // u16 per 8-value unit of a piece vector
 // Decode projections (GEMV family, one token per active expert): gate+up with the activation
 // epilogue, then down.
 void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
@@ -203,10 +221,12 @@ void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const f
 // With `round_first`, each value is first multiplied by its row's weight (row_w[row_slot[row]],
 // row_w[row] when row_slot is null, none when row_w is null) and rounded to BF16 (DeepSeek
 // V4.1's weighted, BF16-materialised SwiGLU output).
+// `pieces` (may be null): the simulated values as BF16 piece vectors [rows][cols / 8 units]
+// (exact in the first piece).
 void launch_quantize(const float* x, size_t rows, size_t cols, float* values, uint8_t* codes,
                      uint8_t* scales, int* status, hipStream_t s, int round_first = 0,
                      const float* row_w = nullptr, const int32_t* row_slot = nullptr,
-                     int block = 32);
+                     int block = 32, uint16_t* pieces = nullptr);
 // Hy4 combine: ascending expert id, f32, + shared, BF16 (weights null: the plain sum of DeepSeek
 // V4.1, whose experts already applied their route weight).
 void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const float* weights,

@@ -48,6 +48,11 @@ struct Workspace {
   float* xq = nullptr;  // HY4, DSV41, DSV4: the simulated E4M3 token activations [chunk, H]
   float* xn = nullptr;  // QWEN36 block calls: the normalized BF16 token activations [chunk, H]
   float* gate_logit = nullptr;  // QWEN36 shared expert: bf16(shared_expert_gate . x) [chunk]
+  // one-token calls: BF16 piece vectors (urb_panel.hpp) of the token, the k SwiGLU rows and
+  // the shared expert's SwiGLU row, the decode GEMVs' A operands
+  uint16_t* xp = nullptr;
+  uint16_t* act_xp = nullptr;
+  uint16_t* shared_xp = nullptr;
   int* status = nullptr;  // [0] latched numerical failures, [1] validation flags
 };
 
@@ -256,6 +261,10 @@ static void carve_workspace(urb_moe_ctx* c, Bump& b) {
   if (mx_activation(d.composition)) w.xq = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36) w.xn = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36 && d.shared_intermediate) w.gate_logit = b.take<float>(C);
+  w.xp = b.take<uint16_t>(H / 8 * urb::kPieceUnit);
+  w.act_xp = b.take<uint16_t>(K * (I / 8) * urb::kPieceUnit);
+  w.shared_xp = b.take<uint16_t>(std::max<size_t>(d.shared_intermediate, 8) / 8 *
+                                 urb::kPieceUnit);
 }
 
 static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
@@ -512,8 +521,11 @@ void urb_moe_destroy(urb_moe_ctx* ctx) {
   destroy_ctx(ctx);
 }
 
+// Router and top-k for one chunk.  `xp` (one token): the router also writes the token's piece
+// vector.  `after_router` (may be null): recorded on `s` between the router and the routing.
 static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* tokens, int n,
-                              float* logits, int32_t* ids, float* weights, hipStream_t s) {
+                              float* logits, int32_t* ids, float* weights, hipStream_t s,
+                              uint16_t* xp = nullptr, hipEvent_t after_router = nullptr) {
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
@@ -524,13 +536,13 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
     Span span(c, URB_STAGE_ROUTER, s);
     if (c->router_lane8) {
       urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status,
-                               s);
+                               s, n == 1 ? xp : nullptr);
     } else if (n == 1) {
       // one token: a GEMV over the row-major router beats the 32-token MFMA tile
       rp.slices = urb::router_gemv_slices(E);
       rp.part = c->ws.router_part;
       urb::launch_router_gemv_f64(c->router, E, H, x, c->ws.router_part, rp.slices,
-                                  c->ws.status, s);
+                                  c->ws.status, s, xp);
     } else {
       rp.slices = urb::router_slices(E, H, n);
       rp.part = c->ws.router_part;
@@ -538,6 +550,7 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
                               c->ws.status, s);
     }
   }
+  if (after_router) URB_HIP(hipEventRecord(after_router, s));
   {
     Span span(c, URB_STAGE_ROUTE, s);
     const bool ascending = d.composition != URB_COMPOSE_GLM;
@@ -559,6 +572,118 @@ static hipStream_t shared_stream(const urb_moe_ctx* c, int n, hipStream_t s) {
   return n == 1 && c->shared_weight_bytes <= kSharedInlineBytes ? s : c->side;
 }
 
+// One token, GLM and QWEN36 compositions: the projections run on the matrix cores from BF16
+// piece vectors (urb_decode.hip).  The router writes the token's pieces, so the shared expert
+// (side stream, or in line when small) starts after the router; its output and the k routed
+// rows meet in the fused down projection + combine.
+static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* tokens, float* yc,
+                              int32_t* idc, float* wc, const float* resid, hipStream_t s) {
+  const urb_moe_desc& d = c->desc;
+  const bool qwen = d.composition == URB_COMPOSE_QWEN36;
+  const bool has_shared = d.shared_intermediate != 0;
+  const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
+  const int Is = (int)d.shared_intermediate;
+  Workspace& ws = c->ws;
+  const urb::Epi epi{qwen ? urb::kEpiQwen : urb::kEpiGated, 0.0f};
+  hipStream_t ss = shared_stream(c, 1, s);
+  const bool side = has_shared && ss != s;
+  route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp, side ? c->fork : nullptr);
+  if (has_shared) {
+    // GLM: GatedMlp (src/models/glm/runtime/moe.rs:162).  QWEN36: a Qwen38Expert and its gate
+    // logit linear(shared_expert_gate) (qwen3_6/runtime.rs:1417-1435).
+    if (side) URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
+    Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
+    {
+      Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
+      if (qwen)
+        urb::launch_router_lane8(c->shared_gate8, 1, H, xc, 1, ws.gate_logit, 1, ws.status, ss);
+      urb::launch_gemv_mfma_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xp,
+                                    nullptr, ws.shared_xp, epi, ws.status, ss);
+    }
+    {
+      Span span(c, URB_STAGE_SHARED_DOWN, ss);
+      urb::launch_gemv_mfma_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_xp,
+                                 ws.shared_out, epi, ws.status, ss);
+    }
+    if (side) URB_HIP(hipEventRecord(c->join, ss));
+  }
+  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
+  {
+    Span span(c, URB_STAGE_GATE_UP, s);
+    urb::launch_gemv_mfma_gate_up(d.expert_format, c->table, perm, std::min(E, K), H, I, ws.xp,
+                                  nullptr, ws.act_xp, epi, ws.status, s);
+  }
+  if (side) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+  {
+    Span span(c, URB_STAGE_DOWN, s);
+    urb::launch_gemv_mfma_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
+                                       ws.act_xp, has_shared ? ws.shared_out : nullptr,
+                                       qwen ? 0 : 1, epi, yc, ws.status, s, resid,
+                                       ws.gate_logit);
+  }
+  if (c->profiling) return collect_spans(c);
+  return URB_OK;
+}
+
+// One token, MX-activation compositions: the quantizer writes the token's pieces (exact in the
+// first piece); the projections run on the matrix cores; between them the SwiGLU output is
+// re-quantized into pieces.
+static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t* tokens,
+                                 float* yc, int32_t* idc, float* wc, hipStream_t s) {
+  const urb_moe_desc& d = c->desc;
+  const bool has_shared = d.shared_intermediate != 0;
+  const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
+  const int Is = (int)d.shared_intermediate;
+  Workspace& ws = c->ws;
+  const bool dsv = d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4;
+  hipStream_t ss = shared_stream(c, 1, s);
+  const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;
+  const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
+  const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
+  urb::launch_quantize(xc, 1, (size_t)H, nullptr, nullptr, nullptr, ws.status, s, 0, nullptr,
+                       nullptr, block, ws.xp);
+  if (has_shared) {
+    if (ss != s) {
+      URB_HIP(hipEventRecord(c->fork, s));
+      URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
+    }
+    Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
+    {
+      Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
+      urb::launch_gemv_mfma_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xp,
+                                    ws.shared_act, nullptr, dense_mlp, ws.status, ss);
+      urb::launch_quantize(ws.shared_act, 1, (size_t)Is, nullptr, nullptr, nullptr, ws.status,
+                           ss, dsv ? 1 : 0, nullptr, nullptr, block, ws.shared_xp);
+    }
+    {
+      Span span(c, URB_STAGE_SHARED_DOWN, ss);
+      urb::launch_gemv_mfma_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_xp,
+                                 ws.shared_out, dense_mlp, ws.status, ss);
+    }
+    if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
+  }
+  route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s);
+  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
+  {
+    Span span(c, URB_STAGE_GATE_UP, s);
+    urb::launch_gemv_mfma_gate_up(d.expert_format, c->table, perm, std::min(E, K), H, I, ws.xp,
+                                  ws.act, nullptr, routed, ws.status, s);
+    // Hy4 re-quantizes the SwiGLU output (expert.rs:677); DeepSeek first scales each row by
+    // its route weight and rounds to BF16 (runtime.rs:2254-2258); one token: slot = row
+    urb::launch_quantize(ws.act, (size_t)K, (size_t)I, nullptr, nullptr, nullptr, ws.status, s,
+                         dsv ? 1 : 0, dsv ? wc : nullptr, nullptr, block, ws.act_xp);
+  }
+  if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+  {
+    Span span(c, URB_STAGE_DOWN, s);
+    urb::launch_gemv_mfma_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
+                                       ws.act_xp, has_shared ? ws.shared_out : nullptr,
+                                       dsv ? 3 : 2, routed, yc, ws.status, s);
+  }
+  if (c->profiling) return collect_spans(c);
+  return URB_OK;
+}
+
 // The MX-activation compositions for one chunk of n tokens: Hy4 MoeWeights::forward
 // (src/models/hy4/runtime.rs:1371-1447), DeepSeek-V4.1 MoeWeights::forward
 // (src/models/deepseek_v41/runtime.rs:1963-2019) and DeepSeek-V4 MoeWeights::forward{,_batch}
@@ -567,6 +692,7 @@ static hipStream_t shared_stream(const urb_moe_ctx* c, int n, hipStream_t s) {
 // run them with the Hy4 epilogues.
 static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* tokens, int n,
                               float* yc, int32_t* idc, float* wc, hipStream_t s) {
+  if (n == 1) return forward_mx_one(c, xc, tokens, yc, idc, wc, s);
   const urb_moe_desc& d = c->desc;
   const bool has_shared = d.shared_intermediate != 0;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
@@ -708,6 +834,11 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
     hipStream_t ss = shared_stream(c, n, s);
     if (mx_activation(d.composition)) {
       urb_status st = forward_mx(c, xc, tc, n, yc, idc, wc, s);
+      if (st) return st;
+      continue;
+    }
+    if (n == 1) {
+      urb_status st = forward_one(c, xc, tc, yc, idc, wc, resid, s);
       if (st) return st;
       continue;
     }

@@ -51,7 +51,7 @@ constexpr int kLane8Ring = 8;
 template <int kLane8Tokens, int WAVES = 1, int RING = kLane8Ring>
 __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
     const uint16_t* __restrict__ w8, int E, int H, const float* __restrict__ x, int T,
-    float* __restrict__ logits, int round_bf16, int* status) {
+    float* __restrict__ logits, int round_bf16, int* status, uint16_t* __restrict__ xp) {
   // [tok][8][H8 + 4] transposed chains: the pad of 4 floats puts the 8 chains of a column in
   // different LDS banks and keeps 16-byte alignment.  H is a multiple of 128.
   extern __shared__ float xs[];
@@ -87,6 +87,9 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
     }
   }
   if (bad) flag(status, kStatusNonFinite);
+  // one token: the workgroups also write its BF16 piece vector (the decode GEMVs' input)
+  if (xp && T == 1)
+    split_vector(x, H / 8, xp, blockIdx.x * blockDim.x + threadIdx.x, gridDim.x * blockDim.x);
   __syncthreads();
   if (!live) return;
   float acc[kLane8Tokens];
@@ -754,7 +757,8 @@ __global__ __launch_bounds__(64) void router_gemv_f64_kernel(const uint16_t* __r
                                                              const float* __restrict__ x,
                                                              int units_per_slice,
                                                              double* __restrict__ part,
-                                                             int* status) {
+                                                             int* status,
+                                                             uint16_t* __restrict__ xp) {
   const int e = blockIdx.x, z = blockIdx.y, lane = threadIdx.x;
   const int units = H / 8;
   const int u0 = z * units_per_slice, u1 = min(units, u0 + units_per_slice);
@@ -778,6 +782,10 @@ __global__ __launch_bounds__(64) void router_gemv_f64_kernel(const uint16_t* __r
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
   if (lane == 0) part[(size_t)z * router_rows(E) + e] = acc;
+  // the token's BF16 piece vector (the decode GEMVs' input), spread over the workgroups
+  if (xp)
+    split_vector(x, units, xp, (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane,
+                 gridDim.x * gridDim.y * 64);
 }
 
 int router_gemv_slices(int E) {
@@ -786,10 +794,10 @@ int router_gemv_slices(int E) {
 }
 
 void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, double* part,
-                            int slices, int* status, hipStream_t s) {
+                            int slices, int* status, hipStream_t s, uint16_t* xp) {
   const int units = H / 8;
   const int per = (units + slices - 1) / slices;
-  router_gemv_f64_kernel<<<dim3(E, slices), 64, 0, s>>>(w, E, H, x, per, part, status);
+  router_gemv_f64_kernel<<<dim3(E, slices), 64, 0, s>>>(w, E, H, x, per, part, status, xp);
 }
 
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
@@ -808,13 +816,13 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 }
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
-                         int round_bf16, int* status, hipStream_t s) {
+                         int round_bf16, int* status, hipStream_t s, uint16_t* xp) {
   const size_t per_tok = (size_t)8 * (H / 8 + 4) * sizeof(float);
   if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
     router_lane8_kernel<1><<<dim3((E + 7) / 8, T), 64, per_tok, s>>>(w8, E, H, x, T, logits,
-                                                                     round_bf16, status);
+                                                                     round_bf16, status, xp);
     return;
   }
   // ... from 64 tokens four waves share one staged token row (32 experts' chains per
@@ -826,7 +834,7 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
   const int eg = (E + 31) / 32;
   if (T <= 512)
     router_lane8_kernel<1, 4><<<dim3(eg, T), 256, per_tok, s>>>(w8, E, H, x, T, logits,
-                                                                round_bf16, status);
+                                                                round_bf16, status, nullptr);
   else if ((long)eg * ((T + 15) / 16) >= 256)
     router_lane8_tiled_kernel<16><<<dim3(eg, (T + 15) / 16), 256, 0, s>>>(w8, E, H, x, T, logits,
                                                                         round_bf16, status);
