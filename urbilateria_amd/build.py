@@ -19,7 +19,7 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-MOE_SOURCES = ["urb_route.hip", "urb_panel.hip", "urb_gemv.hip", "urb_gemm.hip", "urb_hy4.hip",
+MOE_SOURCES = ["urb_route.hip", "urb_panel.hip", "urb_combine.hip", "urb_gemm.hip", "urb_hy4.hip",
                "urb_decode.hip",
                "urb_block.hip",
                "urb_moe_host.cpp", "urb_residency.cpp"]

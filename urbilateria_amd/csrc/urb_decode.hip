@@ -1,21 +1,21 @@
 // urb_decode.hip -- one-token expert projections on the matrix cores (decode).
 //
 // A decode projection is a GEMV: every weight byte is used once, so the kernel's job is to keep
-// HBM busy while spending as few instructions as possible per byte.  Dot products on the FMA
-// lanes cost two VALU operations per MXFP4 weight (decode + FMA) plus an LDS read of the input
-// per weight, which at 8 TB/s is more than a CU can issue.  Here the weights go to
-// v_mfma_f32_16x16x32_bf16 as the B operand straight from the panel layout (BF16 as loaded; MX
-// blocks through the scaled CDNA4 conversions, exact), and the A operand holds the input vector
-// split into BF16 pieces (hi, mid, lo: the f32 value to 2^-24, urb_panel.hpp), one piece per A
-// row.  C rows 0..2 of lane (ln, 0) are then the three pieces' partial sums of weight row ln,
-// added in f32: the result is the f32 dot product with MFMA accumulation.  15 of the 16 A rows
-// are padding, but the matrix cores have ~5x the throughput this needs, and the VALU is left
-// with the MX decode alone.
+// enough bytes in flight to saturate HBM while spending few instructions per byte.  Dot
+// products on the FMA lanes cost two VALU operations per MXFP4 weight (decode + FMA) plus an
+// LDS read of the input per weight, more than a CU can issue at HBM speed.  Here the weights go
+// to v_mfma_f32_16x16x32_bf16 as the B operand straight from the panel layout (BF16 as loaded;
+// MX blocks through the scaled CDNA4 conversions, exact), and the A operand holds the input
+// vector as BF16 pieces (hi, lo: 16 significant bits, urb_panel.hpp), one piece per A row.
+// C rows 0 and 1 of lane (ln, 0) are the two pieces' partial sums of weight row ln, added in
+// f32.  15 of the 16 A rows are padding, but the matrix cores have ~5x the throughput this
+// needs, and the VALU is left with the MX decode alone.
 //
-// Work: a workgroup of max(4, KSPLIT) waves is max(4, KSPLIT) / KSPLIT groups of NP consecutive
-// 16-row panels times KSPLIT parts of K.  Each wave sweeps its panels' part front to back with DEPTH steps of
-// weights (and input pieces, read through L1/L2) in flight; the K parts meet in LDS and are
-// added in part order, then the epilogue runs on 16 lanes per panel.
+// Bytes in flight: a workgroup stages its input pieces in LDS once, so the only vector-memory
+// loads in the main loop are weights.  (Vector-memory loads complete in order: an input load
+// sharing the counter with the weight loads would make every step wait for all older weight
+// loads, capping the useful prefetch at the input's distance.)  Each wave keeps DW weight steps
+// in flight in a register ring of DW + 1 slots, the step loop unrolled DW + 1 times.
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
 #include "urb_panel.hpp"
@@ -24,13 +24,19 @@
 
 namespace urb {
 
-// The input pieces lane (ln, lq) feeds MFMA j of step s: piece ln % 4 of the unit holding
-// k = 128 s + frag_k(j, lq) .. + 8.  `xrow` already points at piece ln % 4 of unit 0.
+// The A fragment lane (ln, lq) feeds MFMA j of step s: piece ln % 2 of the unit holding
+// k = 128 s + frag_k(j, lq) .. + 8, from a piece vector staged in LDS (16 B per piece).
 template <int FMT>
-__device__ __forceinline__ uint4 load_piece(const uint16_t* __restrict__ xrow, int s, int j,
-                                            int lq) {
-  const int k = kGemmKStep * s + frag_k<FMT>(j, lq);
-  return ldg16(xrow + (size_t)(k >> 3) * kPieceUnit);
+__device__ __forceinline__ bf16x8 lds_piece(const uint4* xs, int s, int j, int lq, int piece) {
+  const int u = (kGemmKStep * s + frag_k<FMT>(j, lq)) >> 3;
+  return __builtin_bit_cast(bf16x8, xs[2 * u + piece]);
+}
+
+// Copies `units` piece units (32 B each) from global memory to LDS, all threads.
+__device__ __forceinline__ void stage_pieces(const uint16_t* __restrict__ src, uint4* dst,
+                                             int units) {
+  const uint4* s4 = reinterpret_cast<const uint4*>(src);
+  for (int i = threadIdx.x; i < 2 * units; i += blockDim.x) dst[i] = s4[i];
 }
 
 // Slot a -> (expert, permuted position) of a one-token call: the ranked ids (perm.direct) or
@@ -48,70 +54,72 @@ __device__ __forceinline__ bool decode_slot(const Perm& perm, int a, int& expert
   return true;
 }
 
-constexpr int kDecodeMaxSplit = 8;
+constexpr int kDecodeMaxWaves = 16;
 
-template <int FMT, bool PAIR, int NP, int DEPTH>
-__global__ __launch_bounds__(64 * kDecodeMaxSplit) void gemv_mfma_kernel(
+// A workgroup of W waves (blockDim.x / 64) is W / KSPLIT groups of NP consecutive 16-row panels
+// times KSPLIT parts of K, for one slot (blockIdx.y).  Dynamic LDS: the slot's input pieces,
+// cols / 8 units of 32 B.
+template <int FMT, bool PAIR, int NP, int DW, int WMAX>
+__global__ __launch_bounds__(64 * WMAX) void gemv_mfma_kernel(
     const ExpertMats* __restrict__ mats, Perm perm, int rows, int cols, int ksplit,
     const uint16_t* __restrict__ xp, float* __restrict__ out, uint16_t* __restrict__ out_xp,
     Epi epi, int* status) {
-  __shared__ float red[kDecodeMaxSplit][NP][16][2];
+  extern __shared__ uint4 xs[];
+  __shared__ float red[WMAX][NP][16][2];
   int expert, pos;
   if (!decode_slot(perm, blockIdx.y, expert, pos)) return;
   const ExpertMats m = mats[expert];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ln = lane & 15, lq = lane >> 4;
+  const int ln = lane & 15, lq = lane >> 4, piece = ln & 1;
   const int part = wave % ksplit;
   const int groups = (int)(blockDim.x >> 6) / ksplit;  // panel groups per workgroup
   const int panel0 = (blockIdx.x * groups + wave / ksplit) * NP;
   const bool valid = panel0 < rows / kPanelRows;
   const int steps = cols / kGemmKStep;
-  const int s_begin = steps * part / ksplit, s_end = steps * (part + 1) / ksplit;
+  const int s_begin = steps * part / ksplit, n = steps * (part + 1) / ksplit - s_begin;
   const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(cols);
   const size_t pscales = (size_t)kPanelRows * (cols / 32);
-  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + (valid ? panel0 : 0) * pbytes;
-  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr
-                                       : m.scales[PAIR ? 0 : 2] + (valid ? panel0 : 0) * pscales;
-  const uint8_t* pd1 = PAIR ? m.data[1] + (valid ? panel0 : 0) * pbytes : nullptr;
-  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + (valid ? panel0 : 0) * pscales
-                                                 : nullptr;
+  const int pv = valid ? panel0 : 0;
+  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + pv * pbytes;
+  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + pv * pscales;
+  const uint8_t* pd1 = PAIR ? m.data[1] + pv * pbytes : nullptr;
+  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + pv * pscales : nullptr;
   const uint32_t doff = 16u * lane, soff = lane;
-  // gate/up read the token's input row (one token: row 0); down reads the slot's activation row
-  const uint16_t* xrow = xp + (size_t)(PAIR ? 0 : pos) * (cols / 8) * kPieceUnit + (ln & 3) * 8;
+
+  constexpr int R = DW + 1;
+  BRaw<FMT> r0[R][NP], r1[R][NP];
+  auto fetch = [&](int slot, int s) {
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      load_b<FMT, true>(r0[slot][q], pd0 + q * pbytes, doff, ps0 + q * pscales, soff, s);
+      if constexpr (PAIR)
+        load_b<FMT, true>(r1[slot][q], pd1 + q * pbytes, doff, ps1 + q * pscales, soff, s);
+    }
+  };
+  // the first weight steps go out before the input is staged, so the two latencies overlap;
+  // gate/up read the token's input (row 0), down the slot's activation row
+  if (valid) {
+#pragma unroll
+    for (int d = 0; d < DW; ++d)
+      if (d < n) fetch(d, s_begin + d);
+  }
+  stage_pieces(xp + (size_t)(PAIR ? 0 : pos) * (cols / 8) * kPieceUnit, xs, cols / 8);
+  __syncthreads();
 
   f32x4 acc0[NP], acc1[NP];
 #pragma unroll
   for (int q = 0; q < NP; ++q) acc0[q] = acc1[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   if (valid) {
-    // ring of R = DEPTH + 1 slots, the step loop unrolled R times (no register copies)
-    constexpr int R = DEPTH + 1;
-    BRaw<FMT> r0[R][NP], r1[R][NP];
-    uint4 xa[R][4];
-    auto fetch = [&](int slot, int s) {
-#pragma unroll
-      for (int q = 0; q < NP; ++q) {
-        load_b<FMT, true>(r0[slot][q], pd0 + q * pbytes, doff, ps0 + q * pscales, soff, s);
-        if constexpr (PAIR)
-          load_b<FMT, true>(r1[slot][q], pd1 + q * pbytes, doff, ps1 + q * pscales, soff, s);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xa[slot][j] = load_piece<FMT>(xrow, s, j, lq);
-    };
-    const int n = s_end - s_begin;
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d)
-      if (d < n) fetch(d, s_begin + d);
     for (int i0 = 0; i0 < n; i0 += R) {
 #pragma unroll
       for (int d = 0; d < R; ++d) {
         const int i = i0 + d;
         if (i >= n) break;
-        if (i + DEPTH < n) fetch((d + DEPTH) % R, s_begin + i + DEPTH);
+        if (i + DW < n) fetch((d + DW) % R, s_begin + i + DW);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const bf16x8 a = __builtin_bit_cast(bf16x8, xa[d][j]);
+          const bf16x8 a = lds_piece<FMT>(xs, s_begin + i, j, lq, piece);
 #pragma unroll
           for (int q = 0; q < NP; ++q) {
             acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, decode_b<FMT>(r0[d][q], j),
@@ -124,12 +132,12 @@ __global__ __launch_bounds__(64 * kDecodeMaxSplit) void gemv_mfma_kernel(
       }
     }
   }
-  // lane (ln, 0): rows 0..2 are the hi, mid and lo partial sums of weight row ln
+  // lane (ln, 0): rows 0 and 1 are the hi and lo partial sums of weight row ln
   float v0[NP], v1[NP];
 #pragma unroll
   for (int q = 0; q < NP; ++q) {
-    v0[q] = (acc0[q][0] + acc0[q][1]) + acc0[q][2];
-    v1[q] = (acc1[q][0] + acc1[q][1]) + acc1[q][2];
+    v0[q] = acc0[q][0] + acc0[q][1];
+    v1[q] = acc1[q][0] + acc1[q][1];
   }
   if (ksplit > 1) {
     if (lq == 0)
@@ -162,25 +170,36 @@ __global__ __launch_bounds__(64 * kDecodeMaxSplit) void gemv_mfma_kernel(
   if (bad) flag(status, kStatusNonFinite);
 }
 
-// Weight steps in flight per wave, and panels per wave, per format.
+// Weight steps in flight per wave, panels per wave and the largest workgroup (waves).  Measured
+// on MI355X (one token, every weight from HBM): two steps in flight beat one, four, six and
+// eight; with the input in LDS, a deeper ring only costs occupancy.
+template <int FMT, bool PAIR>
+constexpr int decode_depth() { return 2; }
+template <int FMT, bool PAIR>
+constexpr int decode_panels() { return 1; }
+template <int FMT, bool PAIR>
+constexpr int decode_max_waves() { return PAIR ? 8 : kDecodeMaxWaves; }
+
 template <int FMT, bool PAIR>
 static void launch_gemv_mfma(const ExpertMats* mats, const Perm& perm, int max_active, int rows,
                              int cols, const uint16_t* xp, float* out, uint16_t* out_xp, Epi epi,
                              int* status, hipStream_t s) {
-  constexpr int NP = 1;
-  constexpr int D = FMT == kFmtBF16 ? 1 : 2;
+  constexpr int NP = decode_panels<FMT, PAIR>();
+  constexpr int D = decode_depth<FMT, PAIR>();
+  constexpr int WMAX = decode_max_waves<FMT, PAIR>();
   const int panels = rows / kPanelRows, steps = cols / kGemmKStep;
-  // split K until the launch has ~4096 waves (16 per CU), keeping at least 2 DEPTH steps a
-  // part; a workgroup holds max(4, ksplit) waves
+  // split K until the launch has ~8192 waves, keeping at least two steps a part; a workgroup
+  // holds max(4, ksplit) waves
   int ksplit = 1;
-  while (ksplit < kDecodeMaxSplit && (long)panels / NP * max_active * ksplit < 4096 &&
-         steps / (2 * ksplit) >= D)
+  while (ksplit < WMAX && (long)panels / NP * max_active * ksplit < 8192 &&
+         steps / (2 * ksplit) >= 1)
     ksplit *= 2;
   const int waves = std::max(4, ksplit);
   const int per_wg = waves / ksplit * NP;
   const dim3 grid((panels + per_wg - 1) / per_wg, max_active);
-  gemv_mfma_kernel<FMT, PAIR, NP, D><<<grid, 64 * waves, 0, s>>>(mats, perm, rows, cols, ksplit,
-                                                                 xp, out, out_xp, epi, status);
+  const size_t lds = (size_t)cols / 8 * 32;
+  gemv_mfma_kernel<FMT, PAIR, NP, D, WMAX><<<grid, 64 * waves, lds, s>>>(
+      mats, perm, rows, cols, ksplit, xp, out, out_xp, epi, status);
 }
 
 void launch_gemv_mfma_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
@@ -207,65 +226,56 @@ void launch_gemv_mfma_down(int fmt, const ExpertMats* mats, const Perm& perm, in
 
 // ------------------------------------------------------------------------------------------
 // The down projection of the k routed experts fused with the combine (one token).  A
-// workgroup owns one 16-row output panel; its tasks are (slot a, K part z), a * ksplit + z,
-// spread over its waves.  Task partials meet in LDS; 16 threads add each slot's parts in
-// order, apply the down epilogue and combine the slots in the composition's order -- the
-// per-slot outputs never leave the chip and no combine kernel runs.  `comp` = composition
-// (0 QWEN36, 1 GLM, 2 HY4, 3 DSV41).
+// workgroup owns one 16-row output panel; its waves are tasks (slot a, K part z),
+// a * ksplit + z, one each.  The k SwiGLU rows' pieces are staged in LDS once; task partials
+// meet in LDS; 16 threads add each slot's parts in order, apply the down epilogue and combine
+// the slots in the composition's order -- the per-slot outputs never leave the chip and no
+// combine kernel runs.  `comp` = composition (0 QWEN36, 1 GLM, 2 HY4, 3 DSV41).
 // ------------------------------------------------------------------------------------------
-constexpr int kDownTasks = 128;  // K x ksplit
-
-template <int FMT, int DEPTH>
-__global__ __launch_bounds__(1024) void gemv_mfma_down_combine_kernel(
+template <int FMT, int DW>
+__global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_kernel(
     const ExpertMats* __restrict__ mats, const int32_t* __restrict__ ids,
     const float* __restrict__ w, const int32_t* __restrict__ asc, int K, int H, int I, int ksplit,
     const uint16_t* __restrict__ act_xp, const float* __restrict__ shared, int comp, Epi epi,
     const float* __restrict__ residual, const float* __restrict__ gate, float* __restrict__ out,
     int* status) {
-  __shared__ float red[kDownTasks][16];
+  extern __shared__ uint4 xs[];  // K x I / 8 piece units
+  __shared__ float red[kDecodeMaxWaves][16];
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int W = blockDim.x >> 6;
-  const int ln = lane & 15, lq = lane >> 4;
+  const int t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's task
+  const int ln = lane & 15, lq = lane >> 4, piece = ln & 1;
   const int panel = blockIdx.x;
   const int steps = I / kGemmKStep;
   const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(I);
   const size_t pscales = (size_t)kPanelRows * (I / 32);
   const uint32_t doff = 16u * lane, soff = lane;
-  const int tasks = K * ksplit;
-  for (int t = wave; t < tasks; t += W) {
-    const int a = t / ksplit, z = t - a * ksplit;
-    const int s_begin = steps * z / ksplit, n = steps * (z + 1) / ksplit - s_begin;
-    const ExpertMats m = mats[ids[a]];
-    const uint8_t* pd = m.data[2] + (size_t)panel * pbytes;
-    const uint8_t* ps = FMT == kFmtBF16 ? nullptr : m.scales[2] + (size_t)panel * pscales;
-    const uint16_t* xrow = act_xp + (size_t)a * (I / 8) * kPieceUnit + (ln & 3) * 8;
-    constexpr int R = DEPTH + 1;
-    BRaw<FMT> r[R];
-    uint4 xa[R][4];
-    auto fetch = [&](int slot, int s) {
-      load_b<FMT, true>(r[slot], pd, doff, ps, soff, s);
+  const int a = t / ksplit, z = t - a * ksplit;
+  const int s_begin = steps * z / ksplit, n = steps * (z + 1) / ksplit - s_begin;
+  const ExpertMats m = mats[ids[a]];
+  const uint8_t* pd = m.data[2] + (size_t)panel * pbytes;
+  const uint8_t* ps = FMT == kFmtBF16 ? nullptr : m.scales[2] + (size_t)panel * pscales;
+  constexpr int R = DW + 1;
+  BRaw<FMT> r[R];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xa[slot][j] = load_piece<FMT>(xrow, s, j, lq);
-    };
+  for (int d = 0; d < DW; ++d)
+    if (d < n) load_b<FMT, true>(r[d], pd, doff, ps, soff, s_begin + d);
+  stage_pieces(act_xp, xs, K * (I / 8));
+  __syncthreads();
+  const uint4* xa = xs + (size_t)a * (I / 8) * 2;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i0 = 0; i0 < n; i0 += R) {
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d)
-      if (d < n) fetch(d, s_begin + d);
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int i0 = 0; i0 < n; i0 += R) {
+    for (int d = 0; d < R; ++d) {
+      const int i = i0 + d;
+      if (i >= n) break;
+      if (i + DW < n) load_b<FMT, true>(r[(d + DW) % R], pd, doff, ps, soff, s_begin + i + DW);
 #pragma unroll
-      for (int d = 0; d < R; ++d) {
-        const int i = i0 + d;
-        if (i >= n) break;
-        if (i + DEPTH < n) fetch((d + DEPTH) % R, s_begin + i + DEPTH);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[d][j]),
-                                                        decode_b<FMT>(r[d], j), acc, 0, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_piece<FMT>(xa, s_begin + i, j, lq, piece),
+                                                      decode_b<FMT>(r[d], j), acc, 0, 0, 0);
     }
-    if (lq == 0) red[t][ln] = (acc[0] + acc[1]) + acc[2];
   }
+  if (lq == 0) red[t][ln] = acc[0] + acc[1];
   __syncthreads();
 
   if (threadIdx.x < 16) {
@@ -325,28 +335,35 @@ __global__ __launch_bounds__(1024) void gemv_mfma_down_combine_kernel(
   }
 }
 
-bool mfma_down_combine_fits(int K) { return K <= 32; }
+// The k SwiGLU rows' pieces (4 I bytes each) must fit the LDS the fused kernel stages, and its
+// tasks one wave each.
+constexpr size_t kDownComboLds = 96 * 1024;
+bool mfma_down_combine_fits(int K, int I) {
+  return K <= kDecodeMaxWaves && (size_t)K * I * 4 <= kDownComboLds;
+}
 
 bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                                    const float* weights, const int32_t* asc, int K, int H, int I,
                                    const uint16_t* act_xp, const float* shared, int comp, Epi epi,
                                    float* out, int* status, hipStream_t s,
                                    const float* residual, const float* gate) {
-  if (!mfma_down_combine_fits(K)) return false;
+  if (!mfma_down_combine_fits(K, I)) return false;
   const int steps = I / kGemmKStep;
-  // split K so a workgroup has ~16 tasks, keeping 2+ steps per part
+  // one task per wave: split K while the workgroup stays within 16 waves, 2+ steps a part
   int ksplit = 1;
-  while (K * ksplit * 2 <= 16 && steps / (2 * ksplit) >= 2 && K * ksplit * 2 <= kDownTasks)
-    ksplit *= 2;
-  const int waves = std::min(16, K * ksplit);
-  const dim3 grid(H / kPanelRows), block(64 * waves);
+  while (K * ksplit * 2 <= kDecodeMaxWaves && steps / (2 * ksplit) >= 2) ksplit *= 2;
+  const dim3 grid(H / kPanelRows), block(64 * K * ksplit);
+  const size_t lds = (size_t)K * I * 4;
   auto go = [&](auto kernel) {
-    kernel<<<grid, block, 0, s>>>(mats, ids, weights, asc, K, H, I, ksplit, act_xp, shared, comp,
-                                  epi, residual, gate, out, status);
+    // dynamic LDS beyond 64 KiB must be allowed per kernel
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kDownComboLds);
+    kernel<<<grid, block, lds, s>>>(mats, ids, weights, asc, K, H, I, ksplit, act_xp, shared,
+                                    comp, epi, residual, gate, out, status);
   };
-  if (fmt == kFmtBF16) go(gemv_mfma_down_combine_kernel<kFmtBF16, 1>);
-  else if (fmt == kFmtMXFP4) go(gemv_mfma_down_combine_kernel<kFmtMXFP4, 2>);
-  else go(gemv_mfma_down_combine_kernel<kFmtMXFP8, 2>);
+  if (fmt == kFmtBF16) go(gemv_mfma_down_combine_kernel<kFmtBF16, decode_depth<kFmtBF16, false>()>);
+  else if (fmt == kFmtMXFP4) go(gemv_mfma_down_combine_kernel<kFmtMXFP4, decode_depth<kFmtMXFP4, false>()>);
+  else go(gemv_mfma_down_combine_kernel<kFmtMXFP8, decode_depth<kFmtMXFP8, false>()>);
   return true;
 }
 

@@ -169,42 +169,23 @@ void launch_permute(const int32_t* ids, int T, int E, int K, int32_t* meta, int3
                     int32_t* tiles, int32_t* slot_of_pos, hipStream_t s);
 // One-token projections on the matrix cores (urb_decode.hip).  Inputs and activations are BF16
 // piece vectors (urb_panel.hpp): `xp` [H / 8 units] for the token, `act_xp` [slot][I / 8 units].
-// gate_up writes the activation as f32 (`act`, may be null) and/or pieces (`act_xp`).
+// gate_up writes the activation as f32 (`act`, may be null) and/or pieces (`act_xp`); down
+// writes f32 rows y [slot][H].  The fused down + combine runs when mfma_down_combine_fits
+// (otherwise it returns false and launches nothing).
 void launch_gemv_mfma_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
                               int H, int I, const uint16_t* xp, float* act, uint16_t* act_xp,
                               Epi epi, int* status, hipStream_t s);
 void launch_gemv_mfma_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
                            int H, int I, const uint16_t* act_xp, float* y, Epi epi, int* status,
                            hipStream_t s);
-bool mfma_down_combine_fits(int K);
+bool mfma_down_combine_fits(int K, int I);
 bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                                    const float* weights, const int32_t* asc, int K, int H, int I,
                                    const uint16_t* act_xp, const float* shared, int comp, Epi epi,
                                    float* out, int* status, hipStream_t s,
                                    const float* residual = nullptr, const float* gate = nullptr);
 void launch_split_pieces(const float* x, size_t rows, size_t cols, uint16_t* out, hipStream_t s);
-constexpr int kPieceUnit = 32;  // u16 per 8-value unit of a piece vector
-// Decode projections (GEMV family, one token per active expert): gate+up with the activation
-// epilogue, then down.
-void launch_gemv_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
-                         int H, int I, const float* x, float* act, Epi epi, int* status,
-                         hipStream_t s);
-void launch_gemv_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active, int H,
-                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s);
-// One token: the down projection of the k routed experts fused with the combine of the
-// composition (comp: 0 QWEN36, 1 GLM, 2 HY4, 3 DSV41); ids/weights/asc are the token's routes, act the
-// k SwiGLU rows [k, I] in slot order, shared the shared expert's output or null.  Only when
-// down_combine_fits (the k activation rows fit the kernel's LDS budget); returns false and
-// launches nothing otherwise.
-bool down_combine_fits(int K, int I);
-// QWEN36 (comp 0) with `shared`: the shared expert's output enters with scale
-// bf16(sigmoid(gate[0])) after the routes.  With `residual` [H] (not null), out =
-// bf16(residual + combined) (the decoder layer's residual add with BF16 activations).
-bool launch_gemv_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
-                              const float* weights, const int32_t* asc, int K, int H, int I,
-                              const float* act, const float* shared, int comp, Epi epi,
-                              float* out, int* status, hipStream_t s,
-                              const float* residual = nullptr, const float* gate = nullptr);
+constexpr int kPieceUnit = 16;  // u16 per 8-value unit of a piece vector (hi, lo)
 // Combines: Qwen BF16 ascending-id, GLM f64 ranking order.  Qwen with `shared` [T, H]: the
 // gated shared expert (scale bf16(sigmoid(gate[t]))) added last; with `residual` [T, H]:
 // out = bf16(residual + combined).

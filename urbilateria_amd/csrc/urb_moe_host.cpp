@@ -613,13 +613,28 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
     urb::launch_gemv_mfma_gate_up(d.expert_format, c->table, perm, std::min(E, K), H, I, ws.xp,
                                   nullptr, ws.act_xp, epi, ws.status, s);
   }
-  if (side) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
-  {
+  if (urb::mfma_down_combine_fits(K, I)) {
+    if (side) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     Span span(c, URB_STAGE_DOWN, s);
     urb::launch_gemv_mfma_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
                                        ws.act_xp, has_shared ? ws.shared_out : nullptr,
                                        qwen ? 0 : 1, epi, yc, ws.status, s, resid,
                                        ws.gate_logit);
+  } else {
+    // k SwiGLU rows beyond the fused kernel's LDS: per-slot outputs, then the combine
+    {
+      Span span(c, URB_STAGE_DOWN, s);
+      urb::launch_gemv_mfma_down(d.expert_format, c->table, perm, std::min(E, K), H, I,
+                                 ws.act_xp, ws.y_perm, epi, ws.status, s);
+    }
+    if (side) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+    Span span(c, URB_STAGE_COMBINE, s);
+    if (qwen)
+      urb::launch_combine_qwen(ws.y_perm, nullptr, wc, ws.asc, 1, K, H, yc, ws.status, s, resid,
+                               has_shared ? ws.shared_out : nullptr, ws.gate_logit);
+    else
+      urb::launch_combine_glm(ws.y_perm, nullptr, wc, has_shared ? ws.shared_out : nullptr, 1, K,
+                              H, yc, s);
   }
   if (c->profiling) return collect_spans(c);
   return URB_OK;
@@ -673,12 +688,22 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
     urb::launch_quantize(ws.act, (size_t)K, (size_t)I, nullptr, nullptr, nullptr, ws.status, s,
                          dsv ? 1 : 0, dsv ? wc : nullptr, nullptr, block, ws.act_xp);
   }
-  if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
-  {
+  if (urb::mfma_down_combine_fits(K, I)) {
+    if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     Span span(c, URB_STAGE_DOWN, s);
     urb::launch_gemv_mfma_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
                                        ws.act_xp, has_shared ? ws.shared_out : nullptr,
                                        dsv ? 3 : 2, routed, yc, ws.status, s);
+  } else {
+    {
+      Span span(c, URB_STAGE_DOWN, s);
+      urb::launch_gemv_mfma_down(d.expert_format, c->table, perm, std::min(E, K), H, I,
+                                 ws.act_xp, ws.y_perm, routed, ws.status, s);
+    }
+    if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+    Span span(c, URB_STAGE_COMBINE, s);
+    urb::launch_combine_hy4(ws.y_perm, nullptr, dsv ? nullptr : wc, ws.asc,
+                            has_shared ? ws.shared_out : nullptr, 1, K, H, yc, ws.status, s);
   }
   if (c->profiling) return collect_spans(c);
   return URB_OK;
@@ -718,12 +743,8 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
     const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
     {
       Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
-      if (n > 1)
-        urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                 ws.xq, ws.shared_act, dense_mlp, ws.status, ss);
-      else
-        urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xq,
-                                 ws.shared_act, dense_mlp, ws.status, ss);
+      urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is, ws.xq,
+                               ws.shared_act, dense_mlp, ws.status, ss);
       // the down projection re-quantizes its input (Hy4 mx_linear, runtime.rs:1321, 2425-2428;
       // DeepSeek `linear` after the BF16 step, deepseek_v41/runtime.rs:2258-2260)
       urb::launch_quantize(ws.shared_act, (size_t)n, (size_t)Is, ws.shared_act, nullptr, nullptr,
@@ -731,65 +752,39 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
     }
     {
       Span span(c, URB_STAGE_SHARED_DOWN, ss);
-      if (n > 1)
-        urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                              ws.shared_act, ws.shared_out, dense_mlp, ws.status, ss);
-      else
-        urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_act,
-                              ws.shared_out, dense_mlp, ws.status, ss);
+      urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                            ws.shared_act, ws.shared_out, dense_mlp, ws.status, ss);
     }
     if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
   }
   route_chunk(c, xc, tokens, n, ws.logits, idc, wc, s);
-  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles,
-            n == 1 ? idc : nullptr, K};
-  if (n > 1) {
+  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, nullptr, K};
+  {
     Span span(c, URB_STAGE_PERMUTE, s);
     urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token,
                         ws.pos_of_slot, ws.tiles, ws.slot_of_pos, s);
   }
-  const int32_t* pos = n == 1 ? nullptr : ws.pos_of_slot;
-  const int32_t* slot = n == 1 ? nullptr : ws.slot_of_pos;  // one token: position = slot
-  const int max_active = std::min(E, n * K);
   const int max_tiles = urb::gemm_max_tiles(n, K, E);
   {
     Span span(c, URB_STAGE_GATE_UP, s);
-    if (n > 1)
-      urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, ws.xq, ws.act,
-                               routed, ws.status, s);
-    else
-      urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, ws.xq, ws.act,
-                               routed, ws.status, s);
+    urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, ws.xq, ws.act,
+                             routed, ws.status, s);
     // the SwiGLU output re-quantized for the down projection (Hy4 activate_gate_up,
     // expert.rs:677); DeepSeek first scales each row by its route weight and rounds to BF16
     // (runtime.rs:2254-2258)
     urb::launch_quantize(ws.act, (size_t)n * K, (size_t)I, ws.act, nullptr, nullptr, ws.status,
-                         s, dsv ? 1 : 0, dsv ? wc : nullptr, dsv ? slot : nullptr, block);
-  }
-  if (n == 1 && urb::down_combine_fits(K, I)) {
-    if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
-    {
-      Span span(c, URB_STAGE_DOWN, s);
-      urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I, ws.act,
-                                    has_shared ? ws.shared_out : nullptr, dsv ? 3 : 2, routed, yc,
-                                    ws.status, s);
-    }
-    if (c->profiling) return collect_spans(c);
-    return URB_OK;
+                         s, dsv ? 1 : 0, dsv ? wc : nullptr, dsv ? ws.slot_of_pos : nullptr,
+                         block);
   }
   {
     Span span(c, URB_STAGE_DOWN, s);
-    if (n > 1)
-      urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act, ws.y_perm,
-                            routed, ws.status, s);
-    else
-      urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act, ws.y_perm,
-                            routed, ws.status, s);
+    urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act, ws.y_perm,
+                          routed, ws.status, s);
   }
   if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
   {
     Span span(c, URB_STAGE_COMBINE, s);
-    urb::launch_combine_hy4(ws.y_perm, pos, dsv ? nullptr : wc, ws.asc,
+    urb::launch_combine_hy4(ws.y_perm, ws.pos_of_slot, dsv ? nullptr : wc, ws.asc,
                             has_shared ? ws.shared_out : nullptr, n, K, H, yc, ws.status, s);
   }
   if (c->profiling) return collect_spans(c);
@@ -859,81 +854,44 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
         if (qwen)
           urb::launch_router_lane8(c->shared_gate8, 1, H, xc, n, ws.gate_logit, 1, ws.status,
                                    ss);
-        if (n > 1)
-          urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                   xc, ws.shared_act, sepi, ws.status, ss);
-        else
-          urb::launch_gemv_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, xc,
-                                   ws.shared_act, sepi, ws.status, ss);
+        urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is, xc,
+                                 ws.shared_act, sepi, ws.status, ss);
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, ss);
-        if (n > 1)
-          urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                                ws.shared_act, ws.shared_out, sepi, ws.status, ss);
-        else
-          urb::launch_gemv_down(d.shared_format, c->shared_table, dense, 1, H, Is,
-                                ws.shared_act, ws.shared_out, sepi, ws.status, ss);
+        urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                              ws.shared_act, ws.shared_out, sepi, ws.status, ss);
       }
       if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
     }
     route_chunk(c, xc, tc, n, ws.logits, idc, wc, s);
-    // One token: the GEMVs read the ranked ids directly (slot a at permuted position a).
-    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles,
-              n == 1 ? idc : nullptr, K};
-    if (n > 1) {
+    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, nullptr, K};
+    {
       Span span(c, URB_STAGE_PERMUTE, s);
       urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts,
                           ws.perm_token, ws.pos_of_slot, ws.tiles, nullptr, s);
     }
-    const int32_t* pos = n == 1 ? nullptr : ws.pos_of_slot;
-    const int max_active = std::min(E, n * K);
     const int max_tiles = urb::gemm_max_tiles(n, K, E);
-    // One token: row-parallel GEMV.  Several: grouped MFMA GEMM over the row tiles.
+    // grouped MFMA GEMMs over the row tiles
     {
       Span span(c, URB_STAGE_GATE_UP, s);
-      if (n > 1)
-        urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act,
-                                 epi, ws.status, s);
-      else
-        urb::launch_gemv_gate_up(d.expert_format, c->table, perm, max_active, H, I, xc, ws.act,
-                                 epi, ws.status, s);
-    }
-    if (n == 1 && urb::down_combine_fits(K, I)) {
-      // One token: the down projection and the combine run as one kernel (it reads the shared
-      // expert's output, so it waits for the side stream first).
-      if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
-      {
-        Span span(c, URB_STAGE_DOWN, s);
-        urb::launch_gemv_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
-                                      ws.act, has_shared ? ws.shared_out : nullptr,
-                                      qwen ? 0 : 1, epi, yc, ws.status, s, resid,
-                                      ws.gate_logit);
-      }
-      if (c->profiling) {
-        urb_status st = collect_spans(c);
-        if (st) return st;
-      }
-      continue;
+      urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act, epi,
+                               ws.status, s);
     }
     {
       Span span(c, URB_STAGE_DOWN, s);
-      if (n > 1)
-        urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act,
-                              ws.y_perm, epi, ws.status, s);
-      else
-        urb::launch_gemv_down(d.expert_format, c->table, perm, max_active, H, I, ws.act,
-                              ws.y_perm, epi, ws.status, s);
+      urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act, ws.y_perm,
+                            epi, ws.status, s);
     }
     if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {
       Span span(c, URB_STAGE_COMBINE, s);
       if (qwen)
-        urb::launch_combine_qwen(ws.y_perm, pos, wc, ws.asc, n, K, H, yc, ws.status, s, resid,
-                                 has_shared ? ws.shared_out : nullptr, ws.gate_logit);
+        urb::launch_combine_qwen(ws.y_perm, ws.pos_of_slot, wc, ws.asc, n, K, H, yc, ws.status, s,
+                                 resid, has_shared ? ws.shared_out : nullptr, ws.gate_logit);
       else
-        urb::launch_combine_glm(ws.y_perm, pos, wc, has_shared ? ws.shared_out : nullptr, n, K,
-                                H, yc, s);
+        urb::launch_combine_glm(ws.y_perm, ws.pos_of_slot, wc, has_shared ? ws.shared_out : nullptr,
+                                n, K, H, yc, s);
     }
     if (c->profiling) {
       urb_status st = collect_spans(c);

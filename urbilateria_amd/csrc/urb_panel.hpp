@@ -266,44 +266,36 @@ template <int N>
 using Int = std::integral_constant<int, N>;
 
 // ---- BF16 pieces of f32 vectors: the A operand of the decode MFMA GEMVs ----
-// An f32 value v is the sum of three BF16 values: hi = bf16(v), mid = bf16(v - hi),
-// lo = bf16(v - hi - mid) (round to nearest even; each difference is exact in f32), and
-// v - (hi + mid + lo) is below 2^-24 |v| -- the product of a BF16-exact weight with the three
-// pieces, summed in f32, is the f32 product.  A vector of K values (K % 8 == 0) is stored as
-// K / 8 units of 64 B: unit u = pieces 0..3 (hi, mid, lo, 0) of values 8 u .. 8 u + 7, 8 BF16
-// each.  Lane (ln, lq) of an MFMA reads 16 B, piece ln % 4 of one unit, so A row r holds
-// piece r % 4 and C rows 0..3 are the three pieces' partial sums (rows 4..15 repeat them).
+// An f32 value v is carried as two BF16 values: hi = bf16(v) and lo = bf16(v - hi) (round to
+// nearest even; v - hi is exact in f32), so hi + lo keeps 16 significant bits of v, like the
+// hi/lo split of the grouped GEMMs' activations.  A vector of K values (K % 8 == 0) is stored
+// as K / 8 units of 32 B: unit u = hi and lo of values 8 u .. 8 u + 7, 8 BF16 each.  Lane
+// (ln, lq) of an MFMA reads 16 B, piece ln % 2 of one unit, so A row r holds piece r % 2 and C
+// rows 0 and 1 are the two pieces' partial sums (rows 2..15 repeat them).
 
-// The three pieces of two values, packed in pairs (value a in the low halves).
-__device__ __forceinline__ void split3_pair(float a, float b, uint32_t& hi, uint32_t& mid,
-                                            uint32_t& lo) {
+// The two pieces of two values, packed in pairs (value a in the low halves).
+__device__ __forceinline__ void split2_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
   hi = pk_bf16(a, b);
-  const float ra = a - u2f(hi << 16), rb = b - u2f(hi & 0xffff0000u);
-  mid = pk_bf16(ra, rb);
-  lo = pk_bf16(ra - u2f(mid << 16), rb - u2f(mid & 0xffff0000u));
+  lo = pk_bf16(a - u2f(hi << 16), b - u2f(hi & 0xffff0000u));
 }
 
-// The unit of values v[0..8): 4 x 16 B, pieces in order.
+// The unit of values v[0..8): 2 x 16 B, pieces in order.
 __device__ __forceinline__ void store_piece_unit(const float* v, uint16_t* unit) {
-  uint32_t h[4], m[4], l[4];
+  uint32_t h[4], l[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) split3_pair(v[2 * i], v[2 * i + 1], h[i], m[i], l[i]);
+  for (int i = 0; i < 4; ++i) split2_pair(v[2 * i], v[2 * i + 1], h[i], l[i]);
   uint4* d = reinterpret_cast<uint4*>(unit);
   d[0] = make_uint4(h[0], h[1], h[2], h[3]);
-  d[1] = make_uint4(m[0], m[1], m[2], m[3]);
-  d[2] = make_uint4(l[0], l[1], l[2], l[3]);
-  d[3] = make_uint4(0u, 0u, 0u, 0u);
+  d[1] = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
 // One value k of a piece vector (scattered 2-byte stores; for epilogues that own one value).
 __device__ __forceinline__ void store_piece_value(uint16_t* vec, int k, float v) {
-  uint32_t h, m, l;
-  split3_pair(v, 0.0f, h, m, l);
+  uint32_t h, l;
+  split2_pair(v, 0.0f, h, l);
   uint16_t* u = vec + (size_t)(k >> 3) * kPieceUnit + (k & 7);
   u[0] = (uint16_t)h;
-  u[8] = (uint16_t)m;
-  u[16] = (uint16_t)l;
-  u[24] = 0;
+  u[8] = (uint16_t)l;
 }
 
 // Units [first, units) step `stride` of the piece vector of x[0..8 units) (f32).
