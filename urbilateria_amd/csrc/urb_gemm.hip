@@ -29,7 +29,7 @@ namespace urb {
 // activation fragment feeds NP (x2 for gate+up) MFMAs.  MT tokens per tile (32 or 64; 64 for
 // large dense batches, so each weight byte feeds twice the MFMAs before it is re-read).
 // Placement: gemm_place (urb_kernels.hpp); xsplit > 1 only for a dense batch (one expert).
-template <int FMT, bool PAIR, int DEPTH, int NP, int MT>
+template <int FMT, bool PAIR, int DEPTH, int NP, int MT, int AD = 1>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
                                                       Perm perm, int max_tiles, int xsplit,
                                                       int rows, int K,
@@ -161,25 +161,44 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d)
       if (d < steps) fetch(d, d);
-    AStage as[RG];
+    // activations: step t's rows are loaded into ring slot t % AD, AD steps before they are
+    // staged in LDS (at the end of step t - 1); the step loop is unrolled lcm(R, AD) times so
+    // both rings are indexed by compile-time slots
+    constexpr int U = (R % AD == 0) ? R : R * AD;
+    AStage as[AD][RG];
 #pragma unroll
-    for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], true, 0);
-    bool lo_any = __syncthreads_or(stage(as, 0));
-    for (int s0 = 0; s0 < steps; s0 += R) {
+    for (int g = 0; g < RG; ++g) load_a(as[0][g], a_src[g], true, 0);
+    bool lo_any = __syncthreads_or(stage(as[0], 0));
+    if constexpr (AD > 1) {
 #pragma unroll
-      for (int d = 0; d < R; ++d) {
+      for (int e = 1; e <= AD; ++e)
+        if (e < steps)
+#pragma unroll
+          for (int g = 0; g < RG; ++g) load_a(as[e % AD][g], a_src[g], true, e * kKS);
+    }
+    for (int s0 = 0; s0 < steps; s0 += U) {
+#pragma unroll
+      for (int d = 0; d < U; ++d) {
         const int s = s0 + d;
         if (s >= steps) break;
         const int buf = s & 1;
         const bool more = s + 1 < steps;
-        if (more) {
+        if constexpr (AD == 1) {
+          if (more) {
 #pragma unroll
-          for (int g = 0; g < RG; ++g) load_a(as[g], a_src[g], true, (s + 1) * kKS);
+            for (int g = 0; g < RG; ++g) load_a(as[0][g], a_src[g], true, (s + 1) * kKS);
+          }
         }
         // refill the slot step s - 1 used, DEPTH steps ahead
         if (s + DEPTH < steps) fetch((d + DEPTH) % R, s + DEPTH);
-        mma(d, a_hi[buf], a_lo[buf], lo_any);
-        if (more) lo_any = __syncthreads_or(stage(as, buf ^ 1));
+        mma(d % R, a_hi[buf], a_lo[buf], lo_any);
+        if (more) lo_any = __syncthreads_or(stage(as[(d + 1) % AD], buf ^ 1));
+        if constexpr (AD > 1) {
+          if (s + 1 + AD < steps)
+#pragma unroll
+            for (int g = 0; g < RG; ++g)
+              load_a(as[(d + 1) % AD][g], a_src[g], true, (s + 1 + AD) * kKS);
+        }
       }
     }
   };
@@ -239,12 +258,12 @@ static int xcd_split(const Perm& perm, int max_tiles, int rows, int K) {
   return gemm_xsplit(perm.dense_tokens, max_tiles, rows / (kNT * NP), wbytes, abytes);
 }
 
-template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT>
+template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT, int AD = 1>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                          const float* in, float* out, Epi epi, int* status, hipStream_t s) {
   const int xsplit = xcd_split<FMT, PAIR, NP>(perm, max_tiles, rows, K);
   const int per_xcd = gemm_blocks_per_xcd(max_tiles, rows / (kNT * NP), xsplit);
-  gemm_kernel<FMT, PAIR, DEPTH, NP, MT><<<dim3(8 * per_xcd), 256, 0, s>>>(
+  gemm_kernel<FMT, PAIR, DEPTH, NP, MT, AD><<<dim3(8 * per_xcd), 256, 0, s>>>(
       mats, perm, max_tiles, xsplit, rows, K, in, out, epi, status);
 }
 
@@ -255,12 +274,23 @@ static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles
 template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                    const float* in, float* out, Epi epi, int* status, hipStream_t s) {
-  if constexpr (FMT == kFmtBF16)
-    launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
+  if constexpr (FMT == kFmtBF16) {
+    // a dense batch (the shared expert) of more than 64 tokens: 64-token tiles, each weight
+    // fragment feeding four MFMA blocks (C5's 1024-token shared gate/up in isolation:
+    // 201 -> 148 us)
+    if (PAIR && perm.dense_tokens > 64)
+      launch_shape<FMT, PAIR, 1, 1, 64>(mats, perm, (perm.dense_tokens + 63) / 64, rows, K, in,
+                                        out, epi, status, s);
+    else
+      launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
+  }
   else if constexpr (FMT == kFmtMXFP8)
     launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
   else if (gemm_panels_per_wave(FMT, rows) == 4)
-    launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
+    // the gate/up pair gathers its activation rows two steps ahead (C5 gate/up in isolation:
+    // 1417 -> 1253 us)
+    launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                      status, s);
   else
     launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
 }
