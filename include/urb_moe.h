@@ -295,6 +295,43 @@ urb_status urb_moe_memory(const urb_moe_ctx *ctx, size_t *weight_bytes, size_t *
 
 const char *urb_status_string(urb_status status);
 
+/* safetensors element types of the tensors expert matrices are stored in. */
+typedef enum {
+  URB_DTYPE_BF16 = 0,
+  URB_DTYPE_F16 = 1,
+  URB_DTYPE_F32 = 2,
+  URB_DTYPE_F8_E4M3 = 3,
+  URB_DTYPE_I8 = 4,
+  URB_DTYPE_U8 = 5,
+  URB_DTYPE_F8_E8M0 = 6,
+  URB_DTYPE_OTHER = 7
+} urb_dtype;
+
+/* A tensor's safetensors header entry: dtype, shape (ndim <= 2 used) and payload bytes. */
+typedef struct {
+  urb_dtype dtype;
+  uint32_t ndim;
+  uint64_t shape[2];
+  uint64_t data_len;
+} urb_tensor_meta;
+
+/* Replaces inspect_weight_matrix (src/storage/weight.rs:118-330) for the formats this layer
+ * takes, from metadata only (no payload read): the format of a logical [rows, cols] matrix
+ * stored as `weight` with its MX scale sidecar `scale` (NULL when the checkpoint has none;
+ * the caller finds it as find_native_scale_name does, weight.rs:645-653), and `packed_name`
+ * != 0 when the weight's name ends in ".weight_packed".  Selection as the reference:
+ * plain BF16 [rows, cols] without a sidecar -> URB_FMT_BF16; F8_E4M3 [rows, cols] with a U8
+ * [rows, ceil(cols/32)] sidecar (ModelOpt 1x32) -> URB_FMT_MXFP8; I8 (F8_E8M0 sidecar) or U8
+ * ".weight_packed" (U8 sidecar) [rows, ceil(cols/2)] with a [rows, ceil(cols/32)] sidecar ->
+ * URB_FMT_MXFP4.  *resident_bytes = payload + sidecar bytes.  Errors: rows or cols 0, or a
+ * shape or sidecar that does not match the format the dtypes select -> URB_ERR_SHAPE
+ * (InvalidShape); layouts the reference reads but this layer does not take -> URB_ERR_ARGUMENT
+ * (F16/F32 plain matrices, E4M3 with 32x32 or 128x128 E8M0 block scales or without a sidecar,
+ * Colibri INT4/INT8 and other dtypes: the reference's other formats and Unsupported). */
+urb_status urb_inspect_matrix(const urb_tensor_meta *weight, const urb_tensor_meta *scale,
+                              int packed_name, uint32_t rows, uint32_t cols, urb_format *format,
+                              uint64_t *resident_bytes);
+
 /* Diagnostic, host only, no reference counterpart: the grouped GEMM's workgroup placement for
  * a launch over `tiles` row tiles of a [rows, cols] projection in `format` (pair != 0: the
  * gate+up pair), with dense_tokens > 0 for one dense expert (the shared expert) over that many

@@ -225,3 +225,52 @@ def test_grouped_gemm_placement_covers_every_pair_once_and_every_xcd(fmt, rows, 
             if groups >= 8 or tiles >= 8:
                 xcds = set((np.nonzero(work)[0] % 8).tolist())
                 assert xcds == set(range(8)), (dense, tiles, pair, sorted(xcds))
+
+
+def _meta(dtype, shape, elem=1):
+    n = int(np.prod(shape)) * elem
+    return {"dtype": dtype, "shape": list(shape), "data_len": n}
+
+
+def test_inspect_matrix_selects_formats_from_metadata_like_the_reference():
+    # inspect_weight_matrix (src/storage/weight.rs:118-330): the reference's own fixtures --
+    # Kimi native MXFP4 `expert.w1.weight_packed` U8 [2, 1] + U8 scale [2, 1] -> 4 resident
+    # bytes (weight.rs:1035-1053); ModelOpt MXFP8 E4M3 [2, 33] + U8 [2, 2] -> 70 bytes
+    # (weight.rs:1056-1077) -- then DeepSeek-style I8 + F8_E8M0 MXFP4 and plain BF16
+    F = N.inspect_matrix
+    assert F(_meta("U8", (2, 1)), _meta("U8", (2, 1)), 2, 2, packed_name=True) == (C.FMT_MXFP4, 4)
+    assert F(_meta("F8_E4M3", (2, 33)), _meta("U8", (2, 2)), 2, 33) == (C.FMT_MXFP8, 70)
+    assert F(_meta("I8", (2048, 3584)), _meta("F8_E8M0", (2048, 224)), 2048, 7168) == \
+        (C.FMT_MXFP4, 2048 * 3584 + 2048 * 224)
+    assert F(_meta("BF16", (2, 2), 2), None, 2, 2) == (C.FMT_BF16, 8)
+
+
+@pytest.mark.parametrize("weight,scale,rows,cols,packed,status", [
+    # E4M3 with DeepSeek-V4.1 32x32 or DeepSeek-V4 128x128 E8M0 block scales: a format the
+    # reference reads (MxFp8E4M3 32x32 / 128x128) that this layer does not take
+    (("F8_E4M3", (64, 64)), ("F8_E8M0", (2, 2)), 64, 64, False, N.ERR_ARGUMENT),
+    (("F8_E4M3", (129, 129)), ("F8_E8M0", (2, 2)), 129, 129, False, N.ERR_ARGUMENT),
+    # E4M3 without a sidecar: require_mx_scale's Unsupported
+    (("F8_E4M3", (2, 32)), None, 2, 32, False, N.ERR_ARGUMENT),
+    # a sidecar of no known geometry, a weight of the wrong shape: InvalidShape
+    (("F8_E4M3", (2, 33)), ("U8", (2, 1)), 2, 33, False, N.ERR_SHAPE),
+    (("F8_E4M3", (1, 129)), ("U8", (2, 5)), 2, 129, False, N.ERR_SHAPE),
+    # MXFP4: I8 payload wants an F8_E8M0 sidecar, U8 `.weight_packed` a U8 one
+    (("I8", (2, 16)), ("U8", (2, 1)), 2, 32, False, N.ERR_SHAPE),
+    (("U8", (2, 16)), ("F8_E8M0", (2, 1)), 2, 32, True, N.ERR_SHAPE),
+    (("I8", (2, 15)), ("F8_E8M0", (2, 1)), 2, 32, False, N.ERR_SHAPE),
+    # U8 not named `.weight_packed`: Colibri INT4/INT8 with an F32 sidecar, not taken here
+    (("U8", (2, 16)), ("U8", (2, 1)), 2, 32, False, N.ERR_ARGUMENT),
+    # plain F32 / F16 matrices, plain matrices of the wrong shape, empty matrices
+    (("F32", (2, 2)), None, 2, 2, False, N.ERR_ARGUMENT),
+    (("F16", (2, 2)), None, 2, 2, False, N.ERR_ARGUMENT),
+    (("BF16", (2, 3)), None, 2, 2, False, N.ERR_SHAPE),
+    (("BF16", (0, 2)), None, 0, 2, False, N.ERR_SHAPE),
+])
+def test_inspect_matrix_errors(weight, scale, rows, cols, packed, status):
+    esize = {"BF16": 2, "F16": 2, "F32": 4}.get(weight[0], 1)
+    w = _meta(weight[0], weight[1], esize)
+    s = None if scale is None else _meta(scale[0], scale[1])
+    with pytest.raises(N.UrbError) as e:
+        N.inspect_matrix(w, s, rows, cols, packed_name=packed)
+    assert e.value.status == status

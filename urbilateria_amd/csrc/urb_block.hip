@@ -2,7 +2,8 @@
 //
 // The post-attention zero-centred RMSNorm with its BF16 cast feeds the router and the experts
 // (src/models/qwen3_6/runtime.rs:1053-1057); the residual add after the combine
-// (runtime.rs:1060) is fused into the combine kernels (urb_gemv.hip).
+// (runtime.rs:1060) is fused into the combine kernels (urb_combine.hip, and the one-token
+// down + combine kernel in urb_decode.hip).
 //
 // zero_centered_rms_norm (src/models/qwen3_8/norm.rs:38-52, 176-186): the mean square is the
 // reference's left-to-right f32 sum of x*x divided by H, so one lane adds the products in index

@@ -1,5 +1,5 @@
 // urb_hy4.hip -- the MX-activation mode (Hy4 composition): the activation quantizer and the
-// combine.  The projections run on the BF16 MFMA kernels (urb_gemm.hip, urb_gemv.hip): a
+// combine.  The projections run on the BF16 MFMA kernels (urb_gemm.hip, urb_decode.hip): a
 // simulated E4M3 activation is an E4M3 code times a power of two, exactly a BF16 value, so
 // the A operand needs no low half and every product is exact; the f32 accumulation of those
 // kernels then stays within f32 rounding of the reference's sums.

@@ -229,10 +229,11 @@ static void destroy_ctx(urb_moe_ctx* c) {
   delete c;
 }
 
-static void carve_workspace(urb_moe_ctx* c, Bump& b) {
+// The per-call buffers for chunks of up to `chunk` tokens, carved from one region into `w`
+// (a Bump with a null base only sizes the region: every pointer it hands out is null).
+static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspace& w) {
   const urb_moe_desc& d = c->desc;
-  const size_t C = c->chunk, E = d.n_experts, K = d.top_k, H = d.hidden, I = d.intermediate;
-  Workspace& w = c->ws;
+  const size_t C = chunk, E = d.n_experts, K = d.top_k, H = d.hidden, I = d.intermediate;
   w.status = b.take<int>(4);
   w.logits = b.take<float>(C * E);
   if (d.composition != URB_COMPOSE_QWEN36) {
@@ -439,12 +440,13 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   URB_HIP(hipMemcpy(c->shared_table, &shared, sizeof(ExpertMats), hipMemcpyHostToDevice));
 
   // ---- workspace
+  Workspace unsized;
   Bump sizing{nullptr};
-  carve_workspace(c, sizing);
+  carve_workspace(c, sizing, c->chunk, unsized);
   URB_HIP(hipMalloc(&c->work, sizing.off));
   c->work_bytes = sizing.off;
   Bump wb{static_cast<char*>(c->work)};
-  carve_workspace(c, wb);
+  carve_workspace(c, wb, c->chunk, c->ws);
   urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
 
   // ---- one validation pass over every payload
@@ -1108,6 +1110,54 @@ urb_status urb_moe_set_expert(urb_moe_ctx* c, uint32_t expert, const urb_matrix*
   URB_HIP(hipMemcpyAsync(c->table + expert, &e, sizeof(ExpertMats), hipMemcpyHostToDevice, s));
   URB_HIP(hipStreamSynchronize(s));
   return URB_OK;
+}
+
+urb_status urb_inspect_matrix(const urb_tensor_meta* weight, const urb_tensor_meta* scale,
+                              int packed_name, uint32_t rows, uint32_t cols, urb_format* format,
+                              uint64_t* resident_bytes) {
+  if (!weight || !format || !resident_bytes) return URB_ERR_ARGUMENT;
+  if (rows == 0 || cols == 0) return URB_ERR_SHAPE;
+  const uint64_t R = rows, Cc = cols, blocks = (Cc + 31) / 32;
+  auto is2d = [](const urb_tensor_meta* t, uint64_t a, uint64_t b) {
+    return t->ndim == 2 && t->shape[0] == a && t->shape[1] == b;
+  };
+  const urb_dtype wt = weight->dtype;
+  if ((wt == URB_DTYPE_BF16 || wt == URB_DTYPE_F16 || wt == URB_DTYPE_F32) && !scale) {
+    // a plain matrix (weight.rs:157-170)
+    const uint64_t esize = wt == URB_DTYPE_F32 ? 4 : 2;
+    if (!is2d(weight, R, Cc) || weight->data_len != R * Cc * esize) return URB_ERR_SHAPE;
+    if (wt != URB_DTYPE_BF16) return URB_ERR_ARGUMENT;
+    *format = URB_FMT_BF16;
+    *resident_bytes = weight->data_len;
+    return URB_OK;
+  }
+  if (wt == URB_DTYPE_F8_E4M3) {
+    // MXFP8 (weight.rs:171-254): the sidecar's dtype and shape select the block geometry
+    if (!scale) return URB_ERR_ARGUMENT;  // require_mx_scale: Unsupported
+    const bool modelopt = scale->dtype == URB_DTYPE_U8 && is2d(scale, R, blocks);
+    const bool block32 = scale->dtype == URB_DTYPE_F8_E8M0 && is2d(scale, (R + 31) / 32, blocks);
+    const bool block128 = scale->dtype == URB_DTYPE_F8_E8M0 &&
+                          is2d(scale, (R + 127) / 128, (Cc + 127) / 128);
+    if (!modelopt && !block32 && !block128) return URB_ERR_SHAPE;
+    if (!is2d(weight, R, Cc) || weight->data_len != R * Cc) return URB_ERR_SHAPE;
+    if (!modelopt) return URB_ERR_ARGUMENT;  // 32x32 / 128x128 blocks: not taken here
+    *format = URB_FMT_MXFP8;
+    *resident_bytes = weight->data_len + scale->data_len;
+    return URB_OK;
+  }
+  const bool native_mxfp4 = wt == URB_DTYPE_I8 || (wt == URB_DTYPE_U8 && packed_name);
+  if (native_mxfp4 && scale) {
+    // MXFP4 (weight.rs:261-286): packed nibbles, E8M0 per 32 (U8-typed for U8 weights)
+    const urb_dtype sdt = wt == URB_DTYPE_U8 ? URB_DTYPE_U8 : URB_DTYPE_F8_E8M0;
+    const uint64_t pc = (Cc + 1) / 2;
+    if (!is2d(weight, R, pc) || weight->data_len != R * pc || scale->dtype != sdt ||
+        !is2d(scale, R, blocks))
+      return URB_ERR_SHAPE;
+    *format = URB_FMT_MXFP4;
+    *resident_bytes = weight->data_len + scale->data_len;
+    return URB_OK;
+  }
+  return URB_ERR_ARGUMENT;  // Colibri INT4/INT8, block-FP8 and other dtypes
 }
 
 uint32_t urb_gemm_placement(urb_format format, int pair, uint32_t dense_tokens, uint32_t tiles,

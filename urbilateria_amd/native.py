@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+from typing import Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 MOE_LIB = os.path.join(_HERE, "liburb_moe.so")
@@ -24,7 +25,7 @@ EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_rout
            "urb_moe_profile", "urb_moe_profile_read", "urb_pack_matrix", "urb_quantize_e4m3",
            "urb_expert_views", "urb_moe_forward_block", "urb_zc_rms_norm_bf16",
            "urb_moe_set_expert", "urb_moe_forward_tokens", "urb_moe_route_tokens",
-           "urb_quantize_e4m3_blocks", "urb_gemm_placement")
+           "urb_quantize_e4m3_blocks", "urb_gemm_placement", "urb_inspect_matrix")
 STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
@@ -56,6 +57,14 @@ class Desc(ctypes.Structure):
         ("normalize", ctypes.c_int32), ("routed_scaling_factor", ctypes.c_float),
         ("max_tokens", ctypes.c_uint32), ("swiglu_limit", ctypes.c_float),
     ]
+
+
+DTYPES = {"BF16": 0, "F16": 1, "F32": 2, "F8_E4M3": 3, "I8": 4, "U8": 5, "F8_E8M0": 6}
+
+
+class TensorMeta(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("ndim", ctypes.c_uint32),
+                ("shape", ctypes.c_uint64 * 2), ("data_len", ctypes.c_uint64)]
 
 
 class Weights(ctypes.Structure):
@@ -122,6 +131,10 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_zc_rms_norm_bf16.restype = ctypes.c_int
         lib.urb_expert_views.argtypes = [ctypes.c_int, u32, u32, u32, P, P, P, P, P]
         lib.urb_expert_views.restype = ctypes.c_int
+        lib.urb_inspect_matrix.argtypes = [P, P, ctypes.c_int, u32, u32,
+                                           ctypes.POINTER(ctypes.c_int),
+                                           ctypes.POINTER(ctypes.c_uint64)]
+        lib.urb_inspect_matrix.restype = ctypes.c_int
         lib.urb_gemm_placement.argtypes = [ctypes.c_int, ctypes.c_int, u32, u32, u32, u32, P, P,
                                            u32]
         lib.urb_gemm_placement.restype = u32
@@ -162,3 +175,21 @@ def synth_lib() -> ctypes.CDLL:
 def check(status: int, where: str = "") -> None:
     if status != OK:
         raise UrbError(status, where)
+
+
+def inspect_matrix(weight: dict, scale: Optional[dict], rows: int, cols: int,
+                   packed_name: bool = False):
+    """urb_inspect_matrix on safetensors header entries ({"dtype", "shape", "data_offsets"} or
+    {"dtype", "shape", "data_len"}): (urb_format, resident bytes); raises UrbError."""
+    def meta(e):
+        shape = list(e["shape"])
+        n = e["data_len"] if "data_len" in e else e["data_offsets"][1] - e["data_offsets"][0]
+        return TensorMeta(DTYPES.get(e["dtype"], 7), len(shape),
+                          (ctypes.c_uint64 * 2)(*(shape + [0, 0])[:2]), n)
+    w = meta(weight)
+    s = meta(scale) if scale is not None else None
+    fmt, rb = ctypes.c_int(), ctypes.c_uint64()
+    check(moe_lib().urb_inspect_matrix(ctypes.byref(w), None if s is None else ctypes.byref(s),
+                                       int(packed_name), rows, cols, ctypes.byref(fmt),
+                                       ctypes.byref(rb)), "urb_inspect_matrix")
+    return fmt.value, rb.value
