@@ -172,6 +172,21 @@ urb_status urb_moe_forward_tokens(urb_moe_ctx *ctx, const float *x, const uint32
                                   uint32_t tokens, float *y, int32_t *ids, float *weights,
                                   void *stream);
 
+/* No counterpart in the reference: urb_moe_forward for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid it).  The
+ * call allocates nothing: its buffers (logits, routes, permutation, activations, per-slot
+ * outputs) come from a static 32 MiB scratch array each GPU holds until the process ends,
+ * instead of the context's workspace.  Same kernels, results and status reporting as
+ * urb_moe_forward (failures latch in the context, returned by urb_moe_sync).  Limits: 1 <=
+ * tokens <= the context's max_tokens chunk, and the call's buffers must fit the scratch, else
+ * URB_ERR_SHAPE: one token fits every supported shape; an H 7168, E 384, top-8, I 2048 layer
+ * with a 2048-wide shared expert takes up to 88 tokens, an H 2048, E 128, top-8, I 768 one 312.
+ * Contexts with a hash table return URB_ERR_ARGUMENT (use urb_moe_forward_tokens).  Every call on a GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (other streams, other threads, other contexts) race and must be
+ * serialised by the caller. */
+urb_status urb_moe_forward_noalloc(urb_moe_ctx *ctx, const float *x, uint32_t tokens, float *y,
+                                   int32_t *ids, float *weights, void *stream);
+
 /* Router only: logits [tokens, E] (device, may be NULL), ids/weights as above.  Replaces
  * `linear(router)` + route_softmax_top_k (src/models/qwen3_8/math.rs:10-26,
  * src/models/qwen3_8/moe.rs:91-159) and router.matvec + route_noaux_tc

@@ -224,6 +224,11 @@ void launch_validate(int fmt, const uint8_t* data, size_t data_bytes, const uint
 void launch_dequant(int fmt, const uint8_t* data, const uint8_t* scales, int rows, int cols,
                     int row0, int count, float* out, hipStream_t s);
 void launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t s);
+
+// The allocation-free layer call's scratch (urb_scratch.hip): kScratchBytes of device memory per
+// GPU, held until the process ends; the current device's address.
+constexpr size_t kScratchBytes = 32u << 20;
+hipError_t scratch_region(void** out);
 void launch_check_finite(const float* x, size_t n, int* status, hipStream_t s);
 
 }  // namespace urb

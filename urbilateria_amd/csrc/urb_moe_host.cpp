@@ -910,6 +910,31 @@ urb_status urb_moe_forward(urb_moe_ctx* c, const float* x, uint32_t tokens, floa
   return forward_impl(c, x, nullptr, tokens, y, ids, weights, stream, nullptr);
 }
 
+urb_status urb_moe_forward_noalloc(urb_moe_ctx* c, const float* x, uint32_t tokens, float* y,
+                                   int32_t* ids, float* weights, void* stream) {
+  if (!c || !x || !y) return URB_ERR_ARGUMENT;
+  if (c->hash) return URB_ERR_ARGUMENT;  // hash routing reads token ids
+  if (tokens == 0 || tokens > c->chunk) return URB_ERR_SHAPE;
+  // this call's buffers, carved from the GPU's static scratch instead of the context workspace
+  Workspace ws;
+  Bump sizing{nullptr};
+  carve_workspace(c, sizing, tokens, ws);
+  if (sizing.off > urb::kScratchBytes) return URB_ERR_SHAPE;
+  void* region = nullptr;
+  URB_HIP(urb::scratch_region(&region));
+  Bump b{static_cast<char*>(region)};
+  carve_workspace(c, b, tokens, ws);
+  ws.status = c->ws.status;  // failures still latch in the context's status word
+  const Workspace own = c->ws;
+  const uint32_t chunk = c->chunk;
+  c->ws = ws;
+  c->chunk = tokens;  // one chunk: the scratch buffers are sized for `tokens`
+  const urb_status st = forward_impl(c, x, nullptr, tokens, y, ids, weights, stream, nullptr);
+  c->chunk = chunk;
+  c->ws = own;
+  return st;
+}
+
 urb_status urb_moe_forward_tokens(urb_moe_ctx* c, const float* x, const uint32_t* token_ids,
                                   uint32_t tokens, float* y, int32_t* ids, float* weights,
                                   void* stream) {

@@ -25,7 +25,8 @@ EXPORTS = ("urb_moe_create", "urb_moe_destroy", "urb_moe_forward", "urb_moe_rout
            "urb_moe_profile", "urb_moe_profile_read", "urb_pack_matrix", "urb_quantize_e4m3",
            "urb_expert_views", "urb_moe_forward_block", "urb_zc_rms_norm_bf16",
            "urb_moe_set_expert", "urb_moe_forward_tokens", "urb_moe_route_tokens",
-           "urb_quantize_e4m3_blocks", "urb_gemm_placement", "urb_inspect_matrix")
+           "urb_quantize_e4m3_blocks", "urb_gemm_placement", "urb_moe_forward_noalloc",
+           "urb_inspect_matrix")
 STAGES = ("router", "route", "permute", "gate_up", "down", "shared_gate_up", "shared_down",
           "combine")
 SYNTH_EXPORTS = ("urb_synth_bf16", "urb_synth_activations", "urb_synth_fp4", "urb_synth_fp8",
@@ -102,6 +103,8 @@ def moe_lib() -> ctypes.CDLL:
         lib.urb_moe_forward.restype = ctypes.c_int
         lib.urb_moe_route.argtypes = [P, P, u32, P, P, P, P]
         lib.urb_moe_route.restype = ctypes.c_int
+        lib.urb_moe_forward_noalloc.argtypes = [P, P, u32, P, P, P, P]
+        lib.urb_moe_forward_noalloc.restype = ctypes.c_int
         lib.urb_moe_forward_tokens.argtypes = [P, P, P, u32, P, P, P, P]
         lib.urb_moe_forward_tokens.restype = ctypes.c_int
         lib.urb_moe_route_tokens.argtypes = [P, P, P, u32, P, P, P, P]
