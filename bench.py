@@ -32,7 +32,10 @@ RUNS = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
         ("c3_mxfp4_decode", 32), ("c4_mxfp8", 1), ("c4_mxfp8", 512),
         ("c5_mxfp4_zipf_prefill", 1024), ("c5_mxfp4_zipf_hot", 1024)]
 # the projection stages a roofline block may name (routing kernels are latency-bound)
-PROJECTIONS = ("gate_up", "down", "shared_gate_up", "shared_down")
+# The routed projections run on the caller's stream, on the critical path of the call; the
+# shared expert's run beside them on a side stream (batches), where their spans include the
+# time they wait for CUs, so the dominant kernel is the slower routed projection.
+PROJECTIONS = ("gate_up", "down")
 MALL_BYTES = 256 << 20   # Infinity Cache: rotate enough layer copies to stream past it
 
 
@@ -284,7 +287,9 @@ def run_one(name, T, args, want_cpu, cpu_budget):
             b = stage_bytes(spec, C, k, T, distinct)
             stage_rows[k] = {"avg_us": avg * 1e3, "bytes": b, "GBps": b / (avg * 1e-3) / 1e9,
                              "flops": stage_flops(spec, k, T)}
-    dom = max(stage_rows, key=lambda k: stage_rows[k]["avg_us"]) if stage_rows else None
+    # the longest span on the caller's stream (the shared expert's spans overlap the others')
+    main = [k for k in stage_rows if not k.startswith("shared_")]
+    dom = max(main, key=lambda k: stage_rows[k]["avg_us"]) if main else None
     flops = layer_flops(spec, T)
     fmt = C.FORMAT_NAMES[spec.expert_format]
     mfma_dtype = {"bf16": "bf16", "mxfp8": "fp8", "mxfp4": "fp4"}[fmt]

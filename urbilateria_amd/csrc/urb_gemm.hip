@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
                                                       int rows, int K,
                                                       const float* __restrict__ in,
                                                       float* __restrict__ out, Epi epi,
-                                                      int* status) {
+                                                      int* status, int block0) {
   constexpr int RG = MT / 32;       // staging rows per thread
   constexpr int MBMAX = MT / 16;    // 16-token MFMA blocks per tile
   __shared__ __attribute__((aligned(16))) u16 a_hi[2][MT * kALd];
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   const int ntiles = min(perm.dense_tokens > 0 ? (perm.dense_tokens + MT - 1) / MT : perm.meta[1],
                          max_tiles);
   int w, group;
-  if (!gemm_place(blockIdx.x, ntiles, groups, xsplit, &w, &group)) return;
+  if (!gemm_place(block0 + blockIdx.x, ntiles, groups, xsplit, &w, &group)) return;
   int expert, base, count, m0;
   if (perm.dense_tokens > 0) {
     expert = 0;
@@ -258,13 +258,23 @@ static int xcd_split(const Perm& perm, int max_tiles, int rows, int K) {
   return gemm_xsplit(perm.dense_tokens, max_tiles, rows / (kNT * NP), wbytes, abytes);
 }
 
+// Workgroups per XCD (32 CUs) of one launch of a dense batch: one per CU.
+constexpr int kDenseBlocksPerXcd = 32;
+
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT, int AD = 1>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                          const float* in, float* out, Epi epi, int* status, hipStream_t s) {
   const int xsplit = xcd_split<FMT, PAIR, NP>(perm, max_tiles, rows, K);
   const int per_xcd = gemm_blocks_per_xcd(max_tiles, rows / (kNT * NP), xsplit);
-  gemm_kernel<FMT, PAIR, DEPTH, NP, MT, AD><<<dim3(8 * per_xcd), 256, 0, s>>>(
-      mats, perm, max_tiles, xsplit, rows, K, in, out, epi, status);
+  // A dense batch (the shared expert, on the side stream beside the routing kernels) runs as
+  // launches of at most one workgroup per CU, so those kernels keep the other slots; a launch
+  // of B workgroups takes placement slots block0 .. block0 + B - 1 (B a multiple of 8, so a
+  // slot keeps its XCD).
+  const int step = perm.dense_tokens > 0 ? kDenseBlocksPerXcd : per_xcd;
+  for (int b0 = 0; b0 < per_xcd; b0 += step)
+    gemm_kernel<FMT, PAIR, DEPTH, NP, MT, AD><<<dim3(8 * std::min(step, per_xcd - b0)), 256, 0,
+                                                s>>>(mats, perm, max_tiles, xsplit, rows, K, in,
+                                                     out, epi, status, 8 * b0);
 }
 
 // Weight steps in flight per wave (DEPTH) and panels per wave (NP), per format.  BF16 steps are

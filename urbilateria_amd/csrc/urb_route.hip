@@ -310,6 +310,14 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
   float v[EPL];
   bool open[EPL];
   bool bad = false;
+  // the selection bias is loaded first, so its latency overlaps the logits' (one token's routing
+  // is a chain of dependent steps; this kernel is on the critical path of every decode call)
+  float bias[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    bias[i] = (MODE != 0 && rp.bias && e < E) ? rp.bias[e] : 0.0f;
+  }
   if (rp.part) {
     // logit = (f32) sum of the router's f64 partial slices, in slice order
     const size_t pitch = (size_t)router_rows(E), slice = (size_t)T * pitch;
@@ -418,7 +426,6 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
     int32_t key[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      const int e = lane + 64 * i;
       float sp = 0.0f;
       if (open[i]) {
         const float x = v[i];
@@ -427,8 +434,7 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
         sp = x > 0.0f ? __fadd_rn(x, l1) : l1;
       }
       score[i] = open[i] ? sqrtf(sp) : 0.0f;  // correctly rounded (not the native root)
-      const float b = (open[i] && rp.bias) ? rp.bias[e] : 0.0f;
-      key[i] = total_key(__fadd_rn(score[i], b));
+      key[i] = total_key(__fadd_rn(score[i], bias[i]));
     }
     if (rp.hash) {
       // the tid2eid row of the token (deepseek_v4/runtime.rs:2664-2681); lane r < K reads the
@@ -466,8 +472,7 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
     for (int i = 0; i < EPL; ++i) {
       const int e = lane + 64 * i;
       g[i] = open[i] ? 1.0f / (1.0f + exp_f32(-v[i])) : 0.0f;
-      const float b = (open[i] && rp.bias) ? rp.bias[e] : 0.0f;
-      sc[i] = __fadd_rn(g[i], b);
+      sc[i] = __fadd_rn(g[i], bias[i]);
       key[i] = total_key(sc[i]);
       if (open[i]) sh[e] = sc[i];
     }
