@@ -59,7 +59,57 @@ def parse():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run a device-to-device copy of this many MiB (a known-size "
                          "kernel for calibrating HBM byte counters)")
+    ap.add_argument("--pack-cost", action="store_true",
+                    help="instead of the layer runs, time the ingest conversion of checkpoint "
+                         "matrices into the panel layout (urb_pack_matrix, HBM to HBM) and a "
+                         "pinned host-to-HBM copy of the same bytes; prints one JSON line")
     return ap.parse_args()
+
+
+def pack_cost(steps):
+    """The cost of converting checkpoint-layout expert matrices into the panel layout at ingest:
+    urb_pack_matrix on one [2048, 7168] projection per format (a C3/C5 expert matrix), HBM to
+    HBM, against a pinned host-to-HBM copy of the same checkpoint bytes (the copy every ingest
+    makes anyway)."""
+    import torch
+    from urbilateria_amd import configs as C
+    from urbilateria_amd import moe
+    rows, cols = 2048, 7168
+    out = []
+    for fmt, name in ((C.FMT_BF16, "bf16"), (C.FMT_MXFP4, "mxfp4"), (C.FMT_MXFP8, "mxfp8")):
+        nbytes = rows * cols * 2 if fmt == C.FMT_BF16 else rows * cols // (2 if fmt == C.FMT_MXFP4 else 1)
+        # any bytes: the conversion moves bytes without decoding them (E8M0 scales 127 = 1.0)
+        data = torch.randint(0, 120, (nbytes,), dtype=torch.uint8, device="cuda")
+        scales = (None if fmt == C.FMT_BF16 else
+                  torch.full((rows * cols // 32,), 127, dtype=torch.uint8, device="cuda"))
+        total = nbytes + (0 if scales is None else scales.numel())
+        for _ in range(3):
+            moe.pack_matrix(fmt, data, scales, rows, cols)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            moe.pack_matrix(fmt, data, scales, rows, cols)
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / steps
+        host = torch.empty(total, dtype=torch.uint8, pin_memory=True)
+        dev = torch.empty(total, dtype=torch.uint8, device="cuda")
+        dev.copy_(host, non_blocking=True)
+        torch.cuda.synchronize()
+        t0.record()
+        for _ in range(steps):
+            dev.copy_(host, non_blocking=True)
+        t1.record()
+        torch.cuda.synchronize()
+        h2d = t0.elapsed_time(t1) * 1e3 / steps
+        out.append({"format": name, "rows": rows, "cols": cols, "checkpoint_bytes": total,
+                    "pack_us": us, "pack_GBps": total / (us * 1e-6) / 1e9,
+                    "h2d_pinned_us": h2d, "h2d_pinned_GBps": total / (h2d * 1e-6) / 1e9,
+                    "pack_over_h2d": us / h2d})
+        log(f"pack {name} [{rows}, {cols}]: {us:.1f} us ({total / (us * 1e-6) / 1e9:.0f} GB/s); "
+            f"pinned H2D {h2d:.1f} us ({total / (h2d * 1e-6) / 1e9:.1f} GB/s)")
+    print(json.dumps({"pack_cost": out}), flush=True)
 
 
 def layer_bytes(spec, C, tokens, distinct):
@@ -329,6 +379,9 @@ def main():
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.pack_cost:
+        pack_cost(args.steps)
+        return
     if args.copy_probe_mib:
         n = args.copy_probe_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device="cuda")

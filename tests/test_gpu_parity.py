@@ -154,6 +154,50 @@ def test_mfma_scale_16x16x128_operands(fmt):
     assert np.array_equal(got, ref), float(np.abs(got - ref).max())
 
 
+@pytest.mark.parametrize("fmt", [C.FMT_MXFP4, C.FMT_MXFP8])
+def test_mfma_scale_16x16x128_accumulates_below_f32_accuracy(fmt):
+    # Why the MX-activation compositions run on the BF16 MFMA instead of
+    # v_mfma_scale_f32_16x16x128_f8f6f4: on full-range operands (every finite E4M3 code, E2M1 or
+    # E4M3 weights, E8M0 scales 2^-10 .. 2^10) its 128-term dot products miss the exact sum by
+    # more than any f32 summation order can (a sequential f32 sum of 128 exact products is off
+    # by at most 127 * 2^-24 of the sum of their magnitudes).  200 random steps; the error is
+    # |C - exact| / sum_k |a_k b_k| per output.
+    rng = np.random.default_rng(11)
+    fin8 = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    dec8 = np.array([O.decode_e4m3fn(c) for c in range(256)], np.float64)
+    dec4 = np.array([O.decode_e2m1(c) for c in range(16)], np.float64)
+    worst, errs = 0.0, []
+    for _ in range(200):
+        A = rng.choice(fin8, (16, 128)).astype(np.uint8)
+        sa = rng.integers(117, 138, (16, 4)).astype(np.uint8)
+        sb = rng.integers(117, 138, (16, 4)).astype(np.uint8)
+        if fmt == C.FMT_MXFP8:
+            Bc = rng.choice(fin8, (16, 128)).astype(np.uint8)
+            Bv, Bbytes = dec8[Bc], Bc
+        else:
+            Bc = rng.integers(0, 16, (16, 128)).astype(np.uint8)
+            Bv = dec4[Bc]
+            Bbytes = (Bc[:, 0::2] | (Bc[:, 1::2] << 4)).astype(np.uint8)
+        Av = dec8[A] * np.exp2(np.repeat(sa.astype(np.float64) - 127, 32, axis=1))
+        Bv = Bv * np.exp2(np.repeat(sb.astype(np.float64) - 127, 32, axis=1))
+        dev = [torch.from_numpy(np.ascontiguousarray(v)).cuda() for v in (A, sa, Bbytes, sb)]
+        c = torch.zeros((16, 16), device="cuda")
+        N.check(N.synth_lib().urb_probe_mfma_scale_16x16x128(
+            fmt, *(d.data_ptr() for d in dev), c.data_ptr(), None))
+        torch.cuda.synchronize()
+        got = c.cpu().numpy().astype(np.float64)
+        mag = np.abs(Av) @ np.abs(Bv).T
+        e = np.abs(got - Av @ Bv.T) / np.where(mag > 0, mag, 1.0)
+        errs.append(float(e.max()))
+    worst = max(errs)
+    f32_bound = 127 * 2.0 ** -24
+    print(f"\nscaled MFMA 16x16x128 ({'E4M3 x E2M1' if fmt == C.FMT_MXFP4 else 'E4M3 x E4M3'}): "
+          f"max error {worst:.3g}, median of step maxima {np.median(errs):.3g} of sum|a b|; "
+          f"f32 sequential-sum bound {f32_bound:.3g}")
+    assert worst > f32_bound
+    assert worst < 1e-3
+
+
 def _bf16_rne_bits(x):
     """Round-to-nearest-even BF16 bits of finite float32 values (the textbook bit formula)."""
     b = x.view(np.uint32).astype(np.uint64)

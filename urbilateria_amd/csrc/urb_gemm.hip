@@ -263,14 +263,15 @@ constexpr int kDenseBlocksPerXcd = 32;
 
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT, int AD = 1>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
-                         const float* in, float* out, Epi epi, int* status, hipStream_t s) {
+                         const float* in, float* out, Epi epi, int* status, hipStream_t s,
+                         bool beside) {
   const int xsplit = xcd_split<FMT, PAIR, NP>(perm, max_tiles, rows, K);
   const int per_xcd = gemm_blocks_per_xcd(max_tiles, rows / (kNT * NP), xsplit);
-  // A dense batch (the shared expert, on the side stream beside the routing kernels) runs as
+  // A dense batch beside the routing kernels (the shared expert on the side stream) runs as
   // launches of at most one workgroup per CU, so those kernels keep the other slots; a launch
   // of B workgroups takes placement slots block0 .. block0 + B - 1 (B a multiple of 8, so a
   // slot keeps its XCD).
-  const int step = perm.dense_tokens > 0 ? kDenseBlocksPerXcd : per_xcd;
+  const int step = beside && perm.dense_tokens > 0 ? kDenseBlocksPerXcd : per_xcd;
   for (int b0 = 0; b0 < per_xcd; b0 += step)
     gemm_kernel<FMT, PAIR, DEPTH, NP, MT, AD><<<dim3(8 * std::min(step, per_xcd - b0)), 256, 0,
                                                 s>>>(mats, perm, max_tiles, xsplit, rows, K, in,
@@ -283,26 +284,26 @@ static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles
 // Rows are multiples of 128 (urb_moe_create), so NP = 2 always tiles them.
 template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
-                   const float* in, float* out, Epi epi, int* status, hipStream_t s) {
+                   const float* in, float* out, Epi epi, int* status, hipStream_t s, bool beside) {
   if constexpr (FMT == kFmtBF16) {
     // a dense batch (the shared expert) of more than 64 tokens: 64-token tiles, each weight
     // fragment feeding four MFMA blocks (C5's 1024-token shared gate/up in isolation:
     // 201 -> 148 us)
     if (PAIR && perm.dense_tokens > 64)
       launch_shape<FMT, PAIR, 1, 1, 64>(mats, perm, (perm.dense_tokens + 63) / 64, rows, K, in,
-                                        out, epi, status, s);
+                                        out, epi, status, s, beside);
     else
-      launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
+      launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   }
   else if constexpr (FMT == kFmtMXFP8)
-    launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
+    launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   else if (gemm_panels_per_wave(FMT, rows) == 4)
     // the gate/up pair gathers its activation rows two steps ahead (C5 gate/up in isolation:
     // 1417 -> 1253 us)
     launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                      status, s);
+                                                      status, s, beside);
   else
-    launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s);
+    launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
 }
 
 int gemm_panels_per_wave(int fmt, int rows) {
@@ -330,17 +331,24 @@ int gemm_placement(int fmt, bool pair, int dense_tokens, int max_tiles, int rows
 
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
                          int I, const float* x, float* act, Epi epi, int* status,
-                         hipStream_t s) {
-  if (fmt == kFmtBF16) launch<kFmtBF16, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s);
-  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s);
-  else launch<kFmtMXFP8, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s);
+                         hipStream_t s, bool beside) {
+  if (fmt == kFmtBF16)
+    launch<kFmtBF16, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s, beside);
+  else if (fmt == kFmtMXFP4)
+    launch<kFmtMXFP4, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s, beside);
+  else
+    launch<kFmtMXFP8, true>(mats, perm, max_tiles, I, H, x, act, epi, status, s, beside);
 }
 
 void launch_gemm_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
-                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s) {
-  if (fmt == kFmtBF16) launch<kFmtBF16, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s);
-  else if (fmt == kFmtMXFP4) launch<kFmtMXFP4, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s);
-  else launch<kFmtMXFP8, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s);
+                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s,
+                      bool beside) {
+  if (fmt == kFmtBF16)
+    launch<kFmtBF16, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s, beside);
+  else if (fmt == kFmtMXFP4)
+    launch<kFmtMXFP4, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s, beside);
+  else
+    launch<kFmtMXFP8, false>(mats, perm, max_tiles, H, I, act, y, epi, status, s, beside);
 }
 
 }  // namespace urb

@@ -112,11 +112,14 @@ int gemm_panels_per_wave(int fmt, int rows);
 // panel group of each of the first `capacity` workgroups (-1 when idle).
 int gemm_placement(int fmt, bool pair, int dense_tokens, int max_tiles, int rows, int K,
                    int32_t* tile_of_block, int32_t* group_of_block, int capacity);
+// beside: a dense batch running on a side stream next to other work (launched at most one
+// workgroup per CU at a time, so that work keeps the other slots).
 void launch_gemm_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
                          int I, const float* x, float* act, Epi epi, int* status,
-                         hipStream_t s);
+                         hipStream_t s, bool beside = false);
 void launch_gemm_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_tiles, int H,
-                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s);
+                      int I, const float* act, float* y, Epi epi, int* status, hipStream_t s,
+                      bool beside = false);
 
 struct RouteParams {
   int router;        // 0 softmax top-k, 1 sigmoid noaux_tc, 2 sqrt-softplus

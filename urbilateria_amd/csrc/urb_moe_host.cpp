@@ -563,15 +563,22 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
 }
 
 // The stream the shared expert runs on: the side stream, concurrently with routing and the
-// routed experts, except for one-token calls with a small shared expert, whose kernels run in
-// line on the caller's stream ahead of the routing.  Measured on MI355X (one token): the
-// Qwen3.6 release layer (6 MB shared expert) 71-75 -> 51 us and the DeepSeek-V4 Flash layer
-// (13 MB) 71-72 -> 60 us in line; with 23 MB shared experts (C3 MXFP4, C5 DeepSeek-V4.1
-// shapes) the overlap wins (80 -> 87 us and 93 -> 96 us in line), as it does for every batch
-// of 32 tokens measured.
+// routed experts, except
+//  * one-token calls with a small shared expert, whose kernels run in line on the caller's
+//    stream ahead of the routing.  Measured on MI355X (one token): the Qwen3.6 release layer
+//    (6 MB shared expert) 71-75 -> 51 us and the DeepSeek-V4 Flash layer (13 MB) 71-72 -> 60 us
+//    in line; with 23 MB shared experts (C3 MXFP4, C5 DeepSeek-V4.1 shapes) the overlap wins
+//    (80 -> 87 us and 93 -> 96 us in line), as it does for every batch of 32 tokens measured;
+//  * batches of 256+ tokens of the f32-activation compositions (mx == false), whose dense
+//    shared GEMMs fill the GPU on their own: beside the MFMA router and the routed GEMMs they
+//    only contend (C5, 1024 tokens: 2.53 -> 2.48 ms in line).  The MX-activation compositions
+//    keep the overlap: their 8-lane FP32 router is LDS-bound and hides under the shared GEMMs
+//    (1024 tokens in line: DeepSeek-V4.1 C5 shape 2.56 -> 2.67 ms, V4 Flash 1.09 -> 1.13 ms).
 constexpr size_t kSharedInlineBytes = 16u << 20;
-static hipStream_t shared_stream(const urb_moe_ctx* c, int n, hipStream_t s) {
-  return n == 1 && c->shared_weight_bytes <= kSharedInlineBytes ? s : c->side;
+constexpr int kSharedInlineTokens = 256;
+static hipStream_t shared_stream(const urb_moe_ctx* c, int n, hipStream_t s, bool mx) {
+  if (n == 1) return c->shared_weight_bytes <= kSharedInlineBytes ? s : c->side;
+  return !mx && n >= kSharedInlineTokens ? s : c->side;
 }
 
 // One token, GLM and QWEN36 compositions: the projections run on the matrix cores from BF16
@@ -587,7 +594,7 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const urb::Epi epi{qwen ? urb::kEpiQwen : urb::kEpiGated, 0.0f};
-  hipStream_t ss = shared_stream(c, 1, s);
+  hipStream_t ss = shared_stream(c, 1, s, false);
   const bool side = has_shared && ss != s;
   route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp, side ? c->fork : nullptr);
   if (has_shared) {
@@ -653,7 +660,7 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const bool dsv = d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4;
-  hipStream_t ss = shared_stream(c, 1, s);
+  hipStream_t ss = shared_stream(c, 1, s, false);
   const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
   const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
@@ -726,7 +733,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const bool dsv = d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4;
-  hipStream_t ss = shared_stream(c, n, s);
+  hipStream_t ss = shared_stream(c, n, s, true);
   const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;  // activation block width
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
   // Hy4's shared DenseMlp is a plain BF16 SwiGLU; DeepSeek's shared expert is a routed expert
@@ -746,7 +753,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
     {
       Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
       urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is, ws.xq,
-                               ws.shared_act, dense_mlp, ws.status, ss);
+                               ws.shared_act, dense_mlp, ws.status, ss, ss != s);
       // the down projection re-quantizes its input (Hy4 mx_linear, runtime.rs:1321, 2425-2428;
       // DeepSeek `linear` after the BF16 step, deepseek_v41/runtime.rs:2258-2260)
       urb::launch_quantize(ws.shared_act, (size_t)n, (size_t)Is, ws.shared_act, nullptr, nullptr,
@@ -755,7 +762,7 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
     {
       Span span(c, URB_STAGE_SHARED_DOWN, ss);
       urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                            ws.shared_act, ws.shared_out, dense_mlp, ws.status, ss);
+                            ws.shared_act, ws.shared_out, dense_mlp, ws.status, ss, ss != s);
     }
     if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
   }
@@ -828,7 +835,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
     int32_t* idc = ids ? ids + (size_t)c0 * K : ws.ids;
     float* wc = weights ? weights + (size_t)c0 * K : ws.weights;
     const uint32_t* tc = token_ids ? token_ids + c0 : nullptr;
-    hipStream_t ss = shared_stream(c, n, s);
+    hipStream_t ss = shared_stream(c, n, s, mx_activation(d.composition));
     if (mx_activation(d.composition)) {
       urb_status st = forward_mx(c, xc, tc, n, yc, idc, wc, s);
       if (st) return st;
@@ -857,12 +864,12 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
           urb::launch_router_lane8(c->shared_gate8, 1, H, xc, n, ws.gate_logit, 1, ws.status,
                                    ss);
         urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is, xc,
-                                 ws.shared_act, sepi, ws.status, ss);
+                                 ws.shared_act, sepi, ws.status, ss, ss != s);
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, ss);
         urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                              ws.shared_act, ws.shared_out, sepi, ws.status, ss);
+                              ws.shared_act, ws.shared_out, sepi, ws.status, ss, ss != s);
       }
       if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
     }
