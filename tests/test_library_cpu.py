@@ -198,8 +198,11 @@ def _placement(fmt, pair, dense, tiles, rows, cols):
     return t, g
 
 
-def _groups(fmt, rows):
-    np_ = 1 if fmt == C.FMT_BF16 else 2 if fmt == C.FMT_MXFP8 else (4 if rows % 256 == 0 else 2)
+def _groups(fmt, rows, pair, dense):
+    if fmt == C.FMT_BF16:
+        np_ = 1 if dense <= 64 else (4 if not pair and rows % 256 == 0 else 2)
+    else:
+        np_ = 2 if fmt == C.FMT_MXFP8 else (4 if rows % 256 == 0 else 2)
     return rows // (64 * np_)
 
 
@@ -212,11 +215,11 @@ def test_grouped_gemm_placement_covers_every_pair_once_and_every_xcd(fmt, rows, 
     # exactly one workgroup, and (workgroups go to the XCDs round robin, block % 8) every XCD
     # has work -- for a dense batch (the shared expert) of any size, where one or two tiles
     # used to land on one XCD, and for routed tile lists of any length >= 8.
-    groups = _groups(fmt, rows)
     cases = [(T, (T + 31) // 32) for T in list(range(1, 65)) + [96, 128, 200, 256, 1024]]
     cases += [(0, n) for n in (8, 9, 13, 40, 163, 550)]
     for dense, tiles in cases:
         for pair in (0, 1):
+            groups = _groups(fmt, rows, pair, dense)
             t, g = _placement(fmt, pair, dense, tiles, rows, cols)
             work = t >= 0
             pairs = list(zip(t[work].tolist(), g[work].tolist()))

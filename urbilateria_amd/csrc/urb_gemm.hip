@@ -286,18 +286,26 @@ template <int FMT, bool PAIR>
 static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                    const float* in, float* out, Epi epi, int* status, hipStream_t s, bool beside) {
   if constexpr (FMT == kFmtBF16) {
-    // a dense batch (the shared expert) of more than 64 tokens: 64-token tiles, each weight
-    // fragment feeding four MFMA blocks (C5's 1024-token shared gate/up in isolation:
-    // 201 -> 148 us)
-    if (PAIR && perm.dense_tokens > 64)
-      launch_shape<FMT, PAIR, 1, 1, 64>(mats, perm, (perm.dense_tokens + 63) / 64, rows, K, in,
-                                        out, epi, status, s, beside);
+    // a dense batch (the shared expert) of more than 64 tokens: two (gate+up) or four (down)
+    // panels per wave, each staged activation fragment feeding as many weight panels (C5's
+    // 1024-token shared expert in isolation: gate+up 136-140 -> 117-121 us against 64-token
+    // tiles, down 120-125 -> 81-84 us against one panel)
+    const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
+    if constexpr (!PAIR) {
+      if (np == 4) {
+        launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                      beside);
+        return;
+      }
+    }
+    if (np == 2)
+      launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
     else
       launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   }
   else if constexpr (FMT == kFmtMXFP8)
     launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
-  else if (gemm_panels_per_wave(FMT, rows) == 4)
+  else if (gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens) == 4)
     // the gate/up pair gathers its activation rows two steps ahead (C5 gate/up in isolation:
     // 1417 -> 1253 us)
     launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out, epi,
@@ -306,15 +314,18 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
     launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
 }
 
-int gemm_panels_per_wave(int fmt, int rows) {
-  if (fmt == kFmtBF16) return 1;
+int gemm_panels_per_wave(int fmt, int rows, bool pair, int dense_tokens) {
+  if (fmt == kFmtBF16) {
+    if (dense_tokens <= 64) return 1;
+    return !pair && rows % (kNT * 4) == 0 ? 4 : 2;
+  }
   if (fmt == kFmtMXFP8) return 2;
   return rows % (kNT * 4) == 0 ? 4 : 2;
 }
 
 int gemm_placement(int fmt, bool pair, int dense_tokens, int max_tiles, int rows, int K,
                    int32_t* tile_of_block, int32_t* group_of_block, int capacity) {
-  const int np = gemm_panels_per_wave(fmt, rows);
+  const int np = gemm_panels_per_wave(fmt, rows, pair, dense_tokens);
   const int groups = rows / (kNT * np);
   const double rb = fmt == kFmtBF16 ? 2.0 * K : fmt == kFmtMXFP4 ? K / 2.0 : (double)K;
   const int xsplit = gemm_xsplit(dense_tokens, max_tiles, groups, (pair ? 2.0 : 1.0) * rows * rb,

@@ -106,8 +106,9 @@ __host__ __device__ inline int gemm_blocks_per_xcd(int max_tiles, int groups, in
 // spread over the XCDs that have work -- so a batch of one or two tiles spreads its panel
 // groups over all eight XCDs instead of leaving most of them idle.
 int gemm_xsplit(int dense_tokens, int ntiles, int groups, double wbytes, double abytes);
-// Weight panels per wave of the grouped GEMM for a format and row count.
-int gemm_panels_per_wave(int fmt, int rows);
+// Weight panels per wave of the grouped GEMM for a format, row count, projection (pair: gate+up)
+// and dense batch size (0: routed tiles).
+int gemm_panels_per_wave(int fmt, int rows, bool pair, int dense_tokens);
 // Host-side replay of a launch's placement (urb_gemm_placement): the grid size, and the tile and
 // panel group of each of the first `capacity` workgroups (-1 when idle).
 int gemm_placement(int fmt, bool pair, int dense_tokens, int max_tiles, int rows, int K,
