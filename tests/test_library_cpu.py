@@ -201,13 +201,16 @@ def _placement(fmt, pair, dense, tiles, rows, cols):
 def _groups(fmt, rows, pair, dense):
     if fmt == C.FMT_BF16:
         np_ = 1 if dense <= 64 else (4 if not pair and rows % 256 == 0 else 2)
+    elif fmt == C.FMT_MXFP8:
+        np_ = 4 if not pair and rows % 256 == 0 else 2
     else:
-        np_ = 2 if fmt == C.FMT_MXFP8 else (4 if rows % 256 == 0 else 2)
+        np_ = 8 if not pair and rows % 512 == 0 else 4 if rows % 256 == 0 else 2
     return rows // (64 * np_)
 
 
 @pytest.mark.parametrize("fmt,rows,cols", [(C.FMT_BF16, 2048, 7168), (C.FMT_BF16, 7168, 2048),
-                                           (C.FMT_MXFP4, 2048, 7168), (C.FMT_MXFP8, 6144, 2048),
+                                           (C.FMT_MXFP4, 2048, 7168), (C.FMT_MXFP4, 7168, 2048),
+                                           (C.FMT_MXFP4, 4224, 2048), (C.FMT_MXFP8, 6144, 2048),
                                            (C.FMT_BF16, 768, 2048)])
 def test_grouped_gemm_placement_covers_every_pair_once_and_every_xcd(fmt, rows, cols):
     # The grouped GEMM's workgroup -> (row tile, panel group) mapping, replayed on the host from

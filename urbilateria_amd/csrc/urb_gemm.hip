@@ -129,30 +129,28 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
       const bool LO = with_lo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        bf16x8 f0[NP], f1[NP];
-#pragma unroll
-        for (int q = 0; q < NP; ++q) {
-          f0[q] = decode_b<FMT>(r0[slot][q], j);
-          if constexpr (PAIR) f1[q] = decode_b<FMT>(r1[slot][q], j);
-        }
         const int kf = frag_k<FMT>(j, lq);
+        bf16x8 ah[NMB], al[NMB];
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
-          const bf16x8 ah = lds_frag(hi, mb * 16 + ln, kf);
-          bf16x8 al;
-          if (LO) al = lds_frag(lo, mb * 16 + ln, kf);
+          ah[mb] = lds_frag(hi, mb * 16 + ln, kf);
+          if (LO) al[mb] = lds_frag(lo, mb * 16 + ln, kf);
+        }
+        // one panel's operands decoded at a time: few registers live beside the ring
 #pragma unroll
-          for (int q = 0; q < NP; ++q) {
-            acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f0[q], acc0[q][mb], 0, 0, 0);
+        for (int q = 0; q < NP; ++q) {
+          const bf16x8 f0 = decode_b<FMT>(r0[slot][q], j);
+          bf16x8 f1;
+          if constexpr (PAIR) f1 = decode_b<FMT>(r1[slot][q], j);
+#pragma unroll
+          for (int mb = 0; mb < NMB; ++mb) {
+            acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[mb], f0, acc0[q][mb], 0, 0, 0);
             if constexpr (PAIR)
-              acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, f1[q], acc1[q][mb], 0, 0, 0);
-          }
-          if (LO) {
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f0[q], acc0[q][mb], 0, 0, 0);
+              acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[mb], f1, acc1[q][mb], 0, 0, 0);
+            if (LO) {
+              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[mb], f0, acc0[q][mb], 0, 0, 0);
               if constexpr (PAIR)
-                acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, f1[q], acc1[q][mb], 0, 0, 0);
+                acc1[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[mb], f1, acc1[q][mb], 0, 0, 0);
             }
           }
         }
@@ -303,15 +301,38 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
     else
       launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   }
-  else if constexpr (FMT == kFmtMXFP8)
+  else if constexpr (FMT == kFmtMXFP8) {
+    // down: four panels per wave where the rows allow (C4 down in isolation: 449-473 -> 443-447
+    // us against two; four panels for gate+up were 60 % slower)
+    if constexpr (!PAIR) {
+      if (gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens) == 4) {
+        launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                      beside);
+        return;
+      }
+    }
     launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
-  else if (gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens) == 4)
-    // the gate/up pair gathers its activation rows two steps ahead (C5 gate/up in isolation:
-    // 1417 -> 1253 us)
-    launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                      status, s, beside);
-  else
-    launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
+  }
+  else {
+    const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
+    if constexpr (!PAIR) {
+      // the down projection: eight panels per wave where the rows allow (C5 down in isolation:
+      // 797-808 -> 755-770 us against four)
+      if (np == 8) {
+        launch_shape<FMT, PAIR, 1, 8>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                      beside);
+        return;
+      }
+    }
+    if (np == 4)
+      // the gate/up pair gathers its activation rows two steps ahead (C5 gate/up in isolation:
+      // 1417 -> 1253 us)
+      launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out,
+                                                        epi, status, s, beside);
+    else
+      launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                    beside);
+  }
 }
 
 int gemm_panels_per_wave(int fmt, int rows, bool pair, int dense_tokens) {
@@ -319,7 +340,8 @@ int gemm_panels_per_wave(int fmt, int rows, bool pair, int dense_tokens) {
     if (dense_tokens <= 64) return 1;
     return !pair && rows % (kNT * 4) == 0 ? 4 : 2;
   }
-  if (fmt == kFmtMXFP8) return 2;
+  if (fmt == kFmtMXFP8) return !pair && rows % (kNT * 4) == 0 ? 4 : 2;
+  if (!pair && rows % (kNT * 8) == 0) return 8;
   return rows % (kNT * 4) == 0 ? 4 : 2;
 }
 
