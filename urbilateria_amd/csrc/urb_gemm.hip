@@ -40,6 +40,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
   constexpr int MBMAX = MT / 16;    // 16-token MFMA blocks per tile
   __shared__ __attribute__((aligned(16))) u16 a_hi[2][MT * kALd];
   __shared__ __attribute__((aligned(16))) u16 a_lo[2][MT * kALd];
+  __shared__ __attribute__((aligned(16))) int lo_flag[2][4];  // per staging buffer, per wave
 
   // ---- which tile and panel group
   const int groups = rows / (kNT * NP);
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     AStage as[AD][RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g) load_a(as[0][g], a_src[g], true, 0);
-    bool lo_any = __syncthreads_or(stage(as[0], 0));
+    bool lo_any = barrier_or4(stage(as[0], 0), lo_flag[0]);
     if constexpr (AD > 1) {
 #pragma unroll
       for (int e = 1; e <= AD; ++e)
@@ -190,7 +191,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
         // refill the slot step s - 1 used, DEPTH steps ahead
         if (s + DEPTH < steps) fetch((d + DEPTH) % R, s + DEPTH);
         mma(d % R, a_hi[buf], a_lo[buf], lo_any);
-        if (more) lo_any = __syncthreads_or(stage(as[(d + 1) % AD], buf ^ 1));
+        if (more) lo_any = barrier_or4(stage(as[(d + 1) % AD], buf ^ 1), lo_flag[buf ^ 1]);
         if constexpr (AD > 1) {
           if (s + 1 + AD < steps)
 #pragma unroll

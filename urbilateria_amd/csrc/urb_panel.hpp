@@ -209,6 +209,19 @@ __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
   return (lor & 0x7fff7fffu) != 0;
 }
 
+// A workgroup barrier that also ORs a per-thread flag over the four waves of a 256-thread
+// workgroup, with one s_barrier: each wave's lane 0 writes the wave's OR into its slot before
+// the barrier and every wave reads the four slots after it.  (HIP's __syncthreads_or reduces
+// through one LDS word with an atomic, three barriers.)  `slots` (4 ints, 16-byte aligned) must
+// not be rewritten before the next barrier: double-buffer them with the data they describe.
+__device__ __forceinline__ bool barrier_or4(bool pred, int* slots) {
+  const bool any = __ballot(pred) != 0;
+  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = any;
+  __syncthreads();
+  const int4 v = *reinterpret_cast<const int4*>(slots);
+  return (v.x | v.y | v.z | v.w) != 0;
+}
+
 __device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + m * kALd + k));
 }

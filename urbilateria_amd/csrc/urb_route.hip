@@ -664,6 +664,7 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
                                                              int* status) {
   __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
   __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
+  __shared__ __attribute__((aligned(16))) int lo_flag[2][4];  // per staging buffer, per wave
   const int m0 = blockIdx.y * kMT;
   const int mrows = min(kMT, T - m0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -697,7 +698,7 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
     AStage as;
     load_a(as, a_src, a_valid, s_begin * kKS);
     check(as);
-    bool lo_any = __syncthreads_or(store_a(as, a_hi[0], a_lo[0]));
+    bool lo_any = barrier_or4(store_a(as, a_hi[0], a_lo[0]), lo_flag[0]);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = s_begin; s0 < s_end; s0 += DEPTH) {
 #pragma unroll
@@ -726,7 +727,7 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
         }
         if (more) {
           check(as);
-          lo_any = __syncthreads_or(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]));
+          lo_any = barrier_or4(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]), lo_flag[buf ^ 1]);
         }
       }
     }
