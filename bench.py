@@ -68,9 +68,9 @@ def parse():
 
 def pack_cost(steps):
     """The cost of converting checkpoint-layout expert matrices into the panel layout at ingest:
-    urb_pack_matrix on one [2048, 7168] projection per format (a C3/C5 expert matrix), HBM to
-    HBM, against a pinned host-to-HBM copy of the same checkpoint bytes (the copy every ingest
-    makes anyway)."""
+    urb_pack_matrix on one [2048, 7168] projection per format (an expert matrix of the c3 and c5
+    workloads), HBM to HBM, against a pinned host-to-HBM copy of the same checkpoint bytes (the
+    copy every ingest makes anyway)."""
     import torch
     from urbilateria_amd import configs as C
     from urbilateria_amd import moe

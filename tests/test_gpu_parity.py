@@ -1003,7 +1003,7 @@ def test_shape_and_geometry_errors():
 
 
 # ------------------------------------------------------------------------------- full size
-# The five configurations at their benchmark sizes, plus C5 with the hot-expert skew, with the
+# The five configurations at their benchmark sizes, plus c5 with the hot-expert skew, with the
 # benchmark's own calibrated Zipf bias: every token's ids and outputs against the oracle.
 FULL = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
         ("c3_mxfp4_decode", 32), ("c4_mxfp8", 1), ("c4_mxfp8", 512),

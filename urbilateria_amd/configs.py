@@ -140,7 +140,8 @@ WORKLOADS: Dict[str, Workload] = {
         (1024,), zipf_s=1.1,
         description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias I2048 + BF16 shared, "
                     "prefill 1024"),
-    # C5 with the load imbalance the Zipf(1.1) popularity model predicts for top-8 selection
+    # c5_mxfp4_zipf_prefill with the load imbalance the Zipf(1.1) popularity model predicts for
+    # top-8 selection
     # without replacement: the hottest expert routed by ~850 of 1024 tokens.  (Fitting the
     # log-log slope of the whole frequency curve, as c5_mxfp4_zipf_prefill does, lets the
     # Gaussian tail of the logits dominate and gives a much flatter head.)
@@ -155,11 +156,12 @@ WORKLOADS: Dict[str, Workload] = {
                     "1024 tokens, I2048 + BF16 shared, prefill 1024"),
 }
 
-# The MX-activation mode on the shapes of C4 and C5: Hy4's composition (E4M3 activations per
+# The MX-activation mode on the shapes of c4_mxfp8 and c5_mxfp4_zipf_prefill: Hy4's
+# composition (E4M3 activations per
 # 32 values into every MX projection, BF16 boundaries, bounded SwiGLU with limit 7, f32
 # ascending-id combine) and DeepSeek-V4.1's (the same activations, FP32-accumulated
-# projections, route weight applied before the down projection, sqrt-softplus router).  C5's
-# shared expert is MXFP4 here: the mode feeds MX weights only.
+# projections, route weight applied before the down projection, sqrt-softplus router).  The
+# shared expert of the c5 shape is MXFP4 here: the mode feeds MX weights only.
 MX_ACTIVATION_WORKLOADS: Dict[str, Workload] = {
     "c4_mxfp8_mx_activation": Workload(
         "c4_mxfp8_mx_activation",
@@ -191,7 +193,7 @@ MX_ACTIVATION_WORKLOADS: Dict[str, Workload] = {
 
 # The Qwen3.6 release MoE geometry (src/models/qwen3_6/expert_store.rs:180-190: H 2048, 256
 # experts of I 512, BF16) with its sigmoid-gated BF16 shared expert (I 512), top-8: the full
-# QWEN36 composition the C1/C2 shapes leave the shared expert out of.
+# QWEN36 composition the c1/c2 shapes leave the shared expert out of.
 QWEN36_RELEASE_WORKLOADS: Dict[str, Workload] = {
     "qwen36_release": Workload(
         "qwen36_release",

@@ -286,9 +286,9 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
                    const float* in, float* out, Epi epi, int* status, hipStream_t s, bool beside) {
   if constexpr (FMT == kFmtBF16) {
     // a dense batch (the shared expert) of more than 64 tokens: two (gate+up) or four (down)
-    // panels per wave, each staged activation fragment feeding as many weight panels (C5's
-    // 1024-token shared expert in isolation: gate+up 136-140 -> 117-121 us against 64-token
-    // tiles, down 120-125 -> 81-84 us against one panel)
+    // panels per wave, each staged activation fragment feeding as many weight panels (a
+    // 1024-token batch through a 2048 x 7168 BF16 shared expert, in isolation: gate+up 136-140
+    // -> 117-121 us against 64-token tiles, down 120-125 -> 81-84 us against one panel)
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
     if constexpr (!PAIR) {
       if (np == 4) {
@@ -303,8 +303,9 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
       launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   }
   else if constexpr (FMT == kFmtMXFP8) {
-    // down: four panels per wave where the rows allow (C4 down in isolation: 449-473 -> 443-447
-    // us against two; four panels for gate+up were 60 % slower)
+    // down: four panels per wave where the rows allow (512 tokens over 160 experts of 6144 x
+    // 2048, in isolation: 449-473 -> 443-447 us against two; four panels for gate+up were 60 %
+    // slower)
     if constexpr (!PAIR) {
       if (gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens) == 4) {
         launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
@@ -317,8 +318,8 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
   else {
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
     if constexpr (!PAIR) {
-      // the down projection: eight panels per wave where the rows allow (C5 down in isolation:
-      // 797-808 -> 755-770 us against four)
+      // the down projection: eight panels per wave where the rows allow (1024 tokens, top-8 over
+      // 384 experts of 7168 x 2048, in isolation: 797-808 -> 755-770 us against four)
       if (np == 8) {
         launch_shape<FMT, PAIR, 1, 8>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
                                       beside);
@@ -326,8 +327,8 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
       }
     }
     if (np == 4)
-      // the gate/up pair gathers its activation rows two steps ahead (C5 gate/up in isolation:
-      // 1417 -> 1253 us)
+      // the gate/up pair gathers its activation rows two steps ahead (the same 1024-token
+      // batch's gate/up in isolation: 1417 -> 1253 us)
       launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out,
                                                         epi, status, s, beside);
     else

@@ -567,13 +567,15 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
 //  * one-token calls with a small shared expert, whose kernels run in line on the caller's
 //    stream ahead of the routing.  Measured on MI355X (one token): the Qwen3.6 release layer
 //    (6 MB shared expert) 71-75 -> 51 us and the DeepSeek-V4 Flash layer (13 MB) 71-72 -> 60 us
-//    in line; with 23 MB shared experts (C3 MXFP4, C5 DeepSeek-V4.1 shapes) the overlap wins
-//    (80 -> 87 us and 93 -> 96 us in line), as it does for every batch of 32 tokens measured;
+//    in line; with 23 MB shared experts (the 7168 x 2048 layers of c3_mxfp4_decode and
+//    c5_mxfp4_dsv41) the overlap wins (80 -> 87 us and 93 -> 96 us in line), as it does for
+//    every batch of 32 tokens measured;
 //  * batches of 256+ tokens of the f32-activation compositions (mx == false), whose dense
 //    shared GEMMs fill the GPU on their own: beside the MFMA router and the routed GEMMs they
-//    only contend (C5, 1024 tokens: 2.53 -> 2.48 ms in line).  The MX-activation compositions
-//    keep the overlap: their 8-lane FP32 router is LDS-bound and hides under the shared GEMMs
-//    (1024 tokens in line: DeepSeek-V4.1 C5 shape 2.56 -> 2.67 ms, V4 Flash 1.09 -> 1.13 ms).
+//    only contend (c5_mxfp4_zipf_prefill, 1024 tokens: 2.53 -> 2.48 ms in line).  The
+//    MX-activation compositions keep the overlap: their 8-lane FP32 router is LDS-bound and
+//    hides under the shared GEMMs (1024 tokens in line: c5_mxfp4_dsv41 2.56 -> 2.67 ms,
+//    dsv4_flash 1.09 -> 1.13 ms).
 constexpr size_t kSharedInlineBytes = 16u << 20;
 constexpr int kSharedInlineTokens = 256;
 static hipStream_t shared_stream(const urb_moe_ctx* c, int n, hipStream_t s, bool mx) {
