@@ -320,6 +320,25 @@ def test_router_logits_match_oracle(name):
     layer.close()
 
 
+@pytest.mark.parametrize("E,groups,topk_group", [(64, 32, 5), (64, 16, 3), (64, 8, 4),
+                                                 (128, 8, 3), (256, 8, 4), (256, 4, 2),
+                                                 (160, 8, 4), (384, 4, 2)])
+def test_group_limited_routing_matches_oracle(E, groups, topk_group):
+    # groups of 2 .. 64 experts are scored by a lane butterfly, groups of 20 and 96 by a scan
+    # over the scores in LDS; one token and a batch of nine take the same per-token routine
+    spec = replace(C.small_spec(C.workload("c3_mxfp4_decode").spec, hidden=256, n_experts=E,
+                                intermediate=128), n_group=groups, topk_group=topk_group)
+    host = C.make_host_layer(spec, bias=C.zipf_bias(E, 1.1, 0.05))
+    for T in (1, 9):
+        x = synth.activations(f"x.groups.{E}.{groups}.{T}", T, spec.hidden)
+        layer = moe_mod().MoeLayer(host, max_tokens=T)
+        _, ids, w = layer.route(torch.from_numpy(x).cuda())
+        ref = _oracle(host, x)
+        assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+        assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+        layer.close()
+
+
 @pytest.mark.parametrize("name,T", [(n, T) for n in ("c3_mxfp4_decode", "c4_mxfp8")
                                      for T in (1, 5, 40)])
 def test_sqrt_softplus_router_layer_matches_oracle(name, T):

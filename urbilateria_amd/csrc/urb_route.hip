@@ -276,6 +276,29 @@ __device__ __forceinline__ float rdl(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// The float whose total-order key is k (total_key is an involution on the bits).
+__device__ __forceinline__ float key_value(int32_t k) {
+  return __int_as_float(k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1));
+}
+// (k1 >= k2) := the two largest keys of this lane's set merged with the partner lane's
+// (disjoint) set; the partner is the DPP lane CTRL, a ds_swizzle pattern, or lane ^ 32.
+__device__ __forceinline__ void top2_fold(int32_t& k1, int32_t& k2, int32_t p1, int32_t p2) {
+  k2 = max(min(k1, p1), max(k2, p2));
+  k1 = max(k1, p1);
+}
+template <int CTRL>
+__device__ __forceinline__ void top2_merge(int32_t& k1, int32_t& k2) {
+  top2_fold(k1, k2, __builtin_amdgcn_update_dpp(k1, k1, CTRL, 0xf, 0xf, false),
+            __builtin_amdgcn_update_dpp(k2, k2, CTRL, 0xf, 0xf, false));
+}
+template <int PATTERN>
+__device__ __forceinline__ void top2_merge_swz(int32_t& k1, int32_t& k2) {
+  top2_fold(k1, k2, __builtin_amdgcn_ds_swizzle(k1, PATTERN), __builtin_amdgcn_ds_swizzle(k2, PATTERN));
+}
+__device__ __forceinline__ void top2_merge_x32(int32_t& k1, int32_t& k2) {
+  top2_fold(k1, k2, __shfl_xor(k1, 32, 64), __shfl_xor(k2, 32, 64));
+}
+
 // One ranking round over the lane's untaken slots: returns the winner id (uniform) and sets
 // `val` (uniform) to the winner's `score2` value.
 template <int EPL>
@@ -470,28 +493,66 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
     int32_t key[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      const int e = lane + 64 * i;
       g[i] = open[i] ? 1.0f / (1.0f + exp_f32(-v[i])) : 0.0f;
       sc[i] = __fadd_rn(g[i], bias[i]);
       key[i] = total_key(sc[i]);
-      if (open[i]) sh[e] = sc[i];
     }
     if (rp.topk_group < rp.n_group) {
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      // group score = sum of the two largest selection scores (:104-111).  (Equal keys are
+      // equal values, so the order in which a group's members are visited does not change
+      // the two values.)
       const int per = E / rp.n_group;
-      // group score = sum of the two largest selection scores (:104-111)
-      if (lane < rp.n_group) {
-        int32_t k1 = INT32_MIN, k2 = INT32_MIN;
-        float b1 = 0.0f, b2 = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < per; ++i) {
-          const float sv = sh[lane * per + i];
-          const int32_t k = total_key(sv);
-          if (k > k1) { k2 = k1; b2 = b1; k1 = k; b1 = sv; }
-          else if (k > k2) { k2 = k; b2 = sv; }
+      if (per >= 2 && 64 % per == 0) {
+        // A group is an aligned run of `per` lanes of one slot: a butterfly of top-2 merges
+        // over that run leaves the group's two largest keys in every lane of it.
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+          int32_t k1 = open[i] ? key[i] : INT32_MIN, k2 = INT32_MIN;
+          top2_merge<0xB1>(k1, k2);                        // quad_perm 1,0,3,2
+          if (per > 2) top2_merge<0x4E>(k1, k2);           // quad_perm 2,3,0,1
+          if (per > 4) top2_merge<0x141>(k1, k2);          // row_half_mirror
+          if (per > 8) top2_merge<0x140>(k1, k2);          // row_mirror
+          if (per > 16) top2_merge_swz<0x401F>(k1, k2);    // lane ^ 16
+          if (per > 32) top2_merge_x32(k1, k2);            // lane ^ 32
+          const int e = lane + 64 * i;
+          if (open[i] && e % per == 0)
+            grpw[e / per] = __fadd_rn(key_value(k1), key_value(k2));
         }
-        grpw[lane] = __fadd_rn(b1, b2);
+      } else {
+        // Lane g scans group g in batches of eight independent LDS reads, starting at its
+        // own offset g so the lanes read different banks.
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          if (open[i]) sh[lane + 64 * i] = sc[i];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (lane < rp.n_group) {
+          int32_t k1 = INT32_MIN, k2 = INT32_MIN;
+          float b1 = 0.0f, b2 = 0.0f;
+          const float* row = sh + lane * per;
+          const int start = lane % per;
+          for (int i0 = 0; i0 < per; i0 += 8) {
+            float sv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              int i = i0 + j + start;  // the group's slots in rotated order
+              i = i >= per ? i - per : i;
+              i = i0 + j < per ? i : 0;  // past the group's end: any valid slot, unused
+              sv[j] = row[i];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              if (i0 + j >= per) break;
+              const int32_t k = total_key(sv[j]);
+              const bool gt1 = k > k1, gt2 = k > k2;
+              k2 = gt1 ? k1 : (gt2 ? k : k2);
+              b2 = gt1 ? b1 : (gt2 ? sv[j] : b2);
+              k1 = gt1 ? k : k1;
+              b1 = gt1 ? sv[j] : b1;
+            }
+          }
+          grpw[lane] = __fadd_rn(b1, b2);
+        }
       }
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
