@@ -76,7 +76,6 @@ struct urb_moe_ctx {
   uint32_t chunk = 0;                  // tokens per internal launch sequence
   void* arena = nullptr;               // router, bias and (unless borrowed) the expert weights
   size_t arena_bytes = 0, weight_bytes = 0;
-  size_t shared_weight_bytes = 0;      // payload bytes of the shared expert's three matrices
   void* work = nullptr;
   size_t work_bytes = 0;
   const uint16_t* router = nullptr;    // [E, H] BF16 (rows zero-padded to router_rows(E))
@@ -307,11 +306,6 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   // Matrix geometry: gate [I, H], up [I, H], down [H, I].
   const size_t dims[3][2] = {{I, H}, {I, H}, {H, I}};
   const size_t sdims[3][2] = {{Is, H}, {Is, H}, {H, Is}};
-  if (has_shared)
-    for (int m = 0; m < 3; ++m) {
-      size_t sb, db = matrix_bytes(d->shared_format, sdims[m][0], sdims[m][1], &sb);
-      c->shared_weight_bytes += db + sb;
-    }
 
   // ---- arena: router, lane-chain router, bias, then the expert payloads (unless borrowed)
   const size_t Ep = urb::router_rows((int)E);
@@ -524,10 +518,10 @@ void urb_moe_destroy(urb_moe_ctx* ctx) {
 }
 
 // Router and top-k for one chunk.  `xp` (one token): the router also writes the token's piece
-// vector.  `after_router` (may be null): recorded on `s` between the router and the routing.
+// vector.
 static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* tokens, int n,
                               float* logits, int32_t* ids, float* weights, hipStream_t s,
-                              uint16_t* xp = nullptr, hipEvent_t after_router = nullptr) {
+                              uint16_t* xp = nullptr) {
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
   const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
@@ -552,7 +546,6 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
                               c->ws.status, s);
     }
   }
-  if (after_router) URB_HIP(hipEventRecord(after_router, s));
   {
     Span span(c, URB_STAGE_ROUTE, s);
     const bool ascending = d.composition != URB_COMPOSE_GLM;
@@ -564,29 +557,28 @@ static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* to
 
 // The stream the shared expert runs on: the side stream, concurrently with routing and the
 // routed experts, except
-//  * one-token calls with a small shared expert, whose kernels run in line on the caller's
-//    stream ahead of the routing.  Measured on MI355X (one token): the Qwen3.6 release layer
-//    (6 MB shared expert) 71-75 -> 51 us and the DeepSeek-V4 Flash layer (13 MB) 71-72 -> 60 us
-//    in line; with 23 MB shared experts (the 7168 x 2048 layers of c3_mxfp4_decode and
-//    c5_mxfp4_dsv41) the overlap wins (80 -> 87 us and 93 -> 96 us in line), as it does for
-//    every batch of 32 tokens measured;
+//  * one-token calls, whose shared-expert kernels run in line on the caller's stream ahead of
+//    the routing.  The fork and join cost the host ~23 us per call (two event records and two
+//    stream waits, measured on MI355X), more than a one-token call's GPU work leaves to hide
+//    it: with 4-6 kernel launches the call becomes host-bound.  Measured (one token, every
+//    weight from HBM): c3_mxfp4_decode (88 MB BF16 shared expert) 75.5 -> 70-72 us in line,
+//    the Qwen3.6 release layer (6 MB) 71-75 -> 51 us, DeepSeek-V4 Flash (13 MB) 71-72 -> 60 us;
 //  * batches of 256+ tokens of the f32-activation compositions (mx == false), whose dense
 //    shared GEMMs fill the GPU on their own: beside the MFMA router and the routed GEMMs they
 //    only contend (c5_mxfp4_zipf_prefill, 1024 tokens: 2.53 -> 2.48 ms in line).  The
 //    MX-activation compositions keep the overlap: their 8-lane FP32 router is LDS-bound and
 //    hides under the shared GEMMs (1024 tokens in line: c5_mxfp4_dsv41 2.56 -> 2.67 ms,
 //    dsv4_flash 1.09 -> 1.13 ms).
-constexpr size_t kSharedInlineBytes = 16u << 20;
 constexpr int kSharedInlineTokens = 256;
 static hipStream_t shared_stream(const urb_moe_ctx* c, int n, hipStream_t s, bool mx) {
-  if (n == 1) return c->shared_weight_bytes <= kSharedInlineBytes ? s : c->side;
+  if (n == 1) return s;
   return !mx && n >= kSharedInlineTokens ? s : c->side;
 }
 
 // One token, GLM and QWEN36 compositions: the projections run on the matrix cores from BF16
-// piece vectors (urb_decode.hip).  The router writes the token's pieces, so the shared expert
-// (side stream, or in line when small) starts after the router; its output and the k routed
-// rows meet in the fused down projection + combine.
+// piece vectors (urb_decode.hip).  The router writes the token's pieces; the shared expert runs
+// in line after the routing, and its output and the k routed rows meet in the fused down
+// projection + combine.
 static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* tokens, float* yc,
                               int32_t* idc, float* wc, const float* resid, hipStream_t s) {
   const urb_moe_desc& d = c->desc;
@@ -596,27 +588,24 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const urb::Epi epi{qwen ? urb::kEpiQwen : urb::kEpiGated, 0.0f};
-  hipStream_t ss = shared_stream(c, 1, s, false);
-  const bool side = has_shared && ss != s;
-  route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp, side ? c->fork : nullptr);
+  route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp);
   if (has_shared) {
     // GLM: GatedMlp (src/models/glm/runtime/moe.rs:162).  QWEN36: a Qwen38Expert and its gate
     // logit linear(shared_expert_gate) (qwen3_6/runtime.rs:1417-1435).
-    if (side) URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
+    // in line on the caller's stream (one token: see shared_stream)
     Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
     {
-      Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
+      Span span(c, URB_STAGE_SHARED_GATE_UP, s);
       if (qwen)
-        urb::launch_router_lane8(c->shared_gate8, 1, H, xc, 1, ws.gate_logit, 1, ws.status, ss);
+        urb::launch_router_lane8(c->shared_gate8, 1, H, xc, 1, ws.gate_logit, 1, ws.status, s);
       urb::launch_gemv_mfma_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xp,
-                                    nullptr, ws.shared_xp, epi, ws.status, ss);
+                                    nullptr, ws.shared_xp, epi, ws.status, s);
     }
     {
-      Span span(c, URB_STAGE_SHARED_DOWN, ss);
+      Span span(c, URB_STAGE_SHARED_DOWN, s);
       urb::launch_gemv_mfma_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_xp,
-                                 ws.shared_out, epi, ws.status, ss);
+                                 ws.shared_out, epi, ws.status, s);
     }
-    if (side) URB_HIP(hipEventRecord(c->join, ss));
   }
   Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
   {
@@ -625,7 +614,6 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
                                   nullptr, ws.act_xp, epi, ws.status, s);
   }
   if (urb::mfma_down_combine_fits(K, I)) {
-    if (side) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     Span span(c, URB_STAGE_DOWN, s);
     urb::launch_gemv_mfma_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
                                        ws.act_xp, has_shared ? ws.shared_out : nullptr,
@@ -638,7 +626,6 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
       urb::launch_gemv_mfma_down(d.expert_format, c->table, perm, std::min(E, K), H, I,
                                  ws.act_xp, ws.y_perm, epi, ws.status, s);
     }
-    if (side) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     Span span(c, URB_STAGE_COMBINE, s);
     if (qwen)
       urb::launch_combine_qwen(ws.y_perm, nullptr, wc, ws.asc, 1, K, H, yc, ws.status, s, resid,
@@ -662,31 +649,26 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const bool dsv = d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4;
-  hipStream_t ss = shared_stream(c, 1, s, false);
   const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
   const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
   urb::launch_quantize(xc, 1, (size_t)H, nullptr, nullptr, nullptr, ws.status, s, 0, nullptr,
                        nullptr, block, ws.xp);
   if (has_shared) {
-    if (ss != s) {
-      URB_HIP(hipEventRecord(c->fork, s));
-      URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
-    }
+    // in line on the caller's stream (one token: see shared_stream)
     Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
     {
-      Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
+      Span span(c, URB_STAGE_SHARED_GATE_UP, s);
       urb::launch_gemv_mfma_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xp,
-                                    ws.shared_act, nullptr, dense_mlp, ws.status, ss);
+                                    ws.shared_act, nullptr, dense_mlp, ws.status, s);
       urb::launch_quantize(ws.shared_act, 1, (size_t)Is, nullptr, nullptr, nullptr, ws.status,
-                           ss, dsv ? 1 : 0, nullptr, nullptr, block, ws.shared_xp);
+                           s, dsv ? 1 : 0, nullptr, nullptr, block, ws.shared_xp);
     }
     {
-      Span span(c, URB_STAGE_SHARED_DOWN, ss);
+      Span span(c, URB_STAGE_SHARED_DOWN, s);
       urb::launch_gemv_mfma_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_xp,
-                                 ws.shared_out, dense_mlp, ws.status, ss);
+                                 ws.shared_out, dense_mlp, ws.status, s);
     }
-    if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
   }
   route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s);
   Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
@@ -700,7 +682,6 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
                          dsv ? 1 : 0, dsv ? wc : nullptr, nullptr, block, ws.act_xp);
   }
   if (urb::mfma_down_combine_fits(K, I)) {
-    if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     Span span(c, URB_STAGE_DOWN, s);
     urb::launch_gemv_mfma_down_combine(d.expert_format, c->table, idc, wc, ws.asc, K, H, I,
                                        ws.act_xp, has_shared ? ws.shared_out : nullptr,
@@ -711,7 +692,6 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
       urb::launch_gemv_mfma_down(d.expert_format, c->table, perm, std::min(E, K), H, I,
                                  ws.act_xp, ws.y_perm, routed, ws.status, s);
     }
-    if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     Span span(c, URB_STAGE_COMBINE, s);
     urb::launch_combine_hy4(ws.y_perm, nullptr, dsv ? nullptr : wc, ws.asc,
                             has_shared ? ws.shared_out : nullptr, 1, K, H, yc, ws.status, s);

@@ -311,7 +311,11 @@ __device__ __forceinline__ int argmax_round(const int32_t (&key)[EPL], const flo
   for (int i = 0; i < EPL; ++i)
     if (open[i] && key[i] > bk) { bk = key[i]; bid = lane + 64 * i; }
   const int kmax = dpp_max_i32(bk);
-  const int id = dpp_min_i32(bk == kmax ? bid : INT32_MAX);
+  // the lowest id among the lanes holding the maximum: one lane (the usual case) names it
+  const uint64_t at_max = __ballot(bk == kmax);
+  const int id = __popcll(at_max) == 1
+                     ? __builtin_amdgcn_readlane(bid, (int)__builtin_ctzll(at_max))
+                     : dpp_min_i32(bk == kmax ? bid : INT32_MAX);
   float mine = 0.0f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i)
@@ -370,7 +374,6 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
       const int e = lane + 64 * i;
       open[i] = e < E;
       v[i] = (float)acc[i];
-      if (open[i]) lt[e] = v[i];
     }
   } else {
 #pragma unroll
@@ -502,6 +505,8 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
       // equal values, so the order in which a group's members are visited does not change
       // the two values.)
       const int per = E / rp.n_group;
+      const bool pow2 = (per & (per - 1)) == 0;
+      const int lg = __builtin_ctz(per);
       if (per >= 2 && 64 % per == 0) {
         // A group is an aligned run of `per` lanes of one slot: a butterfly of top-2 merges
         // over that run leaves the group's two largest keys in every lane of it.
@@ -515,8 +520,8 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
           if (per > 16) top2_merge_swz<0x401F>(k1, k2);    // lane ^ 16
           if (per > 32) top2_merge_x32(k1, k2);            // lane ^ 32
           const int e = lane + 64 * i;
-          if (open[i] && e % per == 0)
-            grpw[e / per] = __fadd_rn(key_value(k1), key_value(k2));
+          if (open[i] && (e & (per - 1)) == 0)
+            grpw[e >> lg] = __fadd_rn(key_value(k1), key_value(k2));
         }
       } else {
         // Lane g scans group g in batches of eight independent LDS reads, starting at its
@@ -556,20 +561,21 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
       }
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      // keep the top `topk_group` groups (score desc, id asc)
+      // keep the top `topk_group` groups (score desc, id asc): a group's rank is the number
+      // of groups ahead of it in that order
       const bool is_group = lane < rp.n_group;
       const int32_t gk = is_group ? total_key(grpw[lane]) : INT32_MIN;
-      bool gopen = is_group, gsel = false;
-      for (int r = 0; r < rp.topk_group; ++r) {
-        const int32_t cand = gopen ? gk : INT32_MIN;
-        const int32_t kmax = dpp_max_i32(cand);
-        const int gid = dpp_min_i32(gopen && gk == kmax ? lane : INT32_MAX);
-        if (lane == gid) { gopen = false; gsel = true; }
+      int rank = 0;
+      for (int h = 0; h < rp.n_group; ++h) {
+        const int32_t kh = __builtin_amdgcn_readlane(gk, h);
+        rank += (kh > gk || (kh == gk && h < lane)) ? 1 : 0;
       }
-      const uint64_t gmask = __ballot(gsel);
+      const uint64_t gmask = __ballot(is_group && rank < rp.topk_group);
 #pragma unroll
-      for (int i = 0; i < EPL; ++i)
-        if (open[i] && !((gmask >> ((lane + 64 * i) / per)) & 1ull)) open[i] = false;
+      for (int i = 0; i < EPL; ++i) {
+        const int e = lane + 64 * i;
+        if (open[i] && !((gmask >> (pow2 ? e >> lg : e / per)) & 1ull)) open[i] = false;
+      }
     }
     for (int r = 0; r < K; ++r) {
       float val;
@@ -581,6 +587,13 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
     den = __fadd_rn(den, 1e-20f);
     if (rp.normalize && !finite(den)) bad = true;
     w = __fmul_rn(rp.normalize ? my_val / den : my_val, rp.scale);
+  }
+  if (rp.part) {
+    // the logits are stored last: a store counts against the same counter as the loads, so
+    // an earlier store would be waited on by every later wait for a load
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i < E) lt[lane + 64 * i] = v[i];
   }
   if (bad) flag(status, kStatusNonFinite);
   if (lane < K) {
