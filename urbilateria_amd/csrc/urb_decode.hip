@@ -16,190 +16,29 @@
 // sharing the counter with the weight loads would make every step wait for all older weight
 // loads, capping the useful prefetch at the input's distance.)  Each wave keeps DW weight steps
 // in flight in a register ring of DW + 1 slots, the step loop unrolled DW + 1 times.
-#include "urb_device.hpp"
-#include "urb_kernels.hpp"
-#include "urb_panel.hpp"
-
-#include <algorithm>
+#include "urb_decode.hpp"
 
 namespace urb {
 
-// The A fragment lane (ln, lq) feeds MFMA j of step s: piece ln % 2 of the unit holding
-// k = 128 s + frag_k(j, lq) .. + 8, from a piece vector staged in LDS (16 B per piece).
-template <int FMT>
-__device__ __forceinline__ bf16x8 lds_piece(const uint4* xs, int s, int j, int lq, int piece) {
-  const int u = (kGemmKStep * s + frag_k<FMT>(j, lq)) >> 3;
-  return __builtin_bit_cast(bf16x8, xs[2 * u + piece]);
-}
-
-// Copies `units` piece units (32 B each) from global memory to LDS, all threads.
-__device__ __forceinline__ void stage_pieces(const uint16_t* __restrict__ src, uint4* dst,
-                                             int units) {
-  const uint4* s4 = reinterpret_cast<const uint4*>(src);
-  for (int i = threadIdx.x; i < 2 * units; i += blockDim.x) dst[i] = s4[i];
-}
-
-// Slot a -> (expert, permuted position) of a one-token call: the ranked ids (perm.direct) or
-// the dense expert (the shared expert, table entry 0).
-__device__ __forceinline__ bool decode_slot(const Perm& perm, int a, int& expert, int& pos) {
-  if (perm.dense_tokens > 0) {
-    if (a != 0) return false;
-    expert = 0;
-    pos = 0;
-    return true;
-  }
-  if (a >= perm.direct_k) return false;
-  expert = perm.direct[a];
-  pos = a;
-  return true;
-}
-
-constexpr int kDecodeMaxWaves = 16;
-
-// A workgroup of W waves (blockDim.x / 64) is W / KSPLIT groups of NP consecutive 16-row panels
-// times KSPLIT parts of K, for one slot (blockIdx.y).  Dynamic LDS: the slot's input pieces,
-// cols / 8 units of 32 B.
+// The MFMA GEMV of one slot's panel groups (gemv_mfma_body, urb_decode.hpp) as a kernel.
 template <int FMT, bool PAIR, int NP, int DW, int WMAX>
 __global__ __launch_bounds__(64 * WMAX) void gemv_mfma_kernel(
     const ExpertMats* __restrict__ mats, Perm perm, int rows, int cols, int ksplit,
     const uint16_t* __restrict__ xp, float* __restrict__ out, uint16_t* __restrict__ out_xp,
     Epi epi, int* status) {
   extern __shared__ uint4 xs[];
-  __shared__ float red[WMAX][NP][16][2];
-  int expert, pos;
-  if (!decode_slot(perm, blockIdx.y, expert, pos)) return;
-  const ExpertMats m = mats[expert];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ln = lane & 15, lq = lane >> 4, piece = ln & 1;
-  const int part = wave % ksplit;
-  const int groups = (int)(blockDim.x >> 6) / ksplit;  // panel groups per workgroup
-  const int panel0 = (blockIdx.x * groups + wave / ksplit) * NP;
-  const bool valid = panel0 < rows / kPanelRows;
-  const int steps = cols / kGemmKStep;
-  const int s_begin = steps * part / ksplit, n = steps * (part + 1) / ksplit - s_begin;
-  const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(cols);
-  const size_t pscales = (size_t)kPanelRows * (cols / 32);
-  const int pv = valid ? panel0 : 0;
-  const uint8_t* pd0 = m.data[PAIR ? 0 : 2] + pv * pbytes;
-  const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + pv * pscales;
-  const uint8_t* pd1 = PAIR ? m.data[1] + pv * pbytes : nullptr;
-  const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + pv * pscales : nullptr;
-  const uint32_t doff = 16u * lane, soff = lane;
-
-  constexpr int R = DW + 1;
-  BRaw<FMT> r0[R][NP], r1[R][NP];
-  auto fetch = [&](int slot, int s) {
-#pragma unroll
-    for (int q = 0; q < NP; ++q) {
-      load_b<FMT, true>(r0[slot][q], pd0 + q * pbytes, doff, ps0 + q * pscales, soff, s);
-      if constexpr (PAIR)
-        load_b<FMT, true>(r1[slot][q], pd1 + q * pbytes, doff, ps1 + q * pscales, soff, s);
-    }
-  };
-  // the first weight steps go out before the input is staged, so the two latencies overlap;
-  // gate/up read the token's input (row 0), down the slot's activation row
-  if (valid) {
-#pragma unroll
-    for (int d = 0; d < DW; ++d)
-      if (d < n) fetch(d, s_begin + d);
-  }
-  stage_pieces(xp + (size_t)(PAIR ? 0 : pos) * (cols / 8) * kPieceUnit, xs, cols / 8);
-  __syncthreads();
-
-  f32x4 acc0[NP], acc1[NP];
-#pragma unroll
-  for (int q = 0; q < NP; ++q) acc0[q] = acc1[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (valid) {
-    for (int i0 = 0; i0 < n; i0 += R) {
-#pragma unroll
-      for (int d = 0; d < R; ++d) {
-        const int i = i0 + d;
-        if (i >= n) break;
-        if (i + DW < n) fetch((d + DW) % R, s_begin + i + DW);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8 a = lds_piece<FMT>(xs, s_begin + i, j, lq, piece);
-#pragma unroll
-          for (int q = 0; q < NP; ++q) {
-            acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, decode_b<FMT>(r0[d][q], j),
-                                                              acc0[q], 0, 0, 0);
-            if constexpr (PAIR)
-              acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, decode_b<FMT>(r1[d][q], j),
-                                                                acc1[q], 0, 0, 0);
-          }
-        }
-      }
-    }
-  }
-  // lane (ln, 0): rows 0 and 1 are the hi and lo partial sums of weight row ln
-  float v0[NP], v1[NP];
-#pragma unroll
-  for (int q = 0; q < NP; ++q) {
-    v0[q] = acc0[q][0] + acc0[q][1];
-    v1[q] = acc1[q][0] + acc1[q][1];
-  }
-  if (ksplit > 1) {
-    if (lq == 0)
-#pragma unroll
-      for (int q = 0; q < NP; ++q) {
-        red[wave][q][ln][0] = v0[q];
-        red[wave][q][ln][1] = v1[q];
-      }
-    __syncthreads();
-    if (part == 0 && lq == 0)
-#pragma unroll
-      for (int q = 0; q < NP; ++q) {
-        v0[q] = 0.0f;
-        v1[q] = 0.0f;
-        for (int z = 0; z < ksplit; ++z) {  // K parts in order
-          v0[q] += red[wave + z][q][ln][0];
-          v1[q] += red[wave + z][q][ln][1];
-        }
-      }
-  }
-  if (!valid || part != 0 || lq != 0) return;
-  bool bad = false;
-#pragma unroll
-  for (int q = 0; q < NP; ++q) {
-    const int r = (panel0 + q) * kPanelRows + ln;
-    const float v = PAIR ? epi_gate_up(epi, v0[q], v1[q], bad) : epi_down<FMT>(epi, v0[q], bad);
-    if (out) out[(size_t)pos * rows + r] = v;
-    if (out_xp) store_piece_value(out_xp + (size_t)pos * (rows / 8) * kPieceUnit, r, v);
-  }
-  if (bad) flag(status, kStatusNonFinite);
+  gemv_mfma_body<FMT, PAIR, NP, DW, WMAX>(mats, perm, rows, cols, ksplit, xp, out, out_xp, epi,
+                                          status, xs);
 }
-
-// Weight steps in flight per wave, panels per wave and the largest workgroup (waves).  Measured
-// on MI355X (one token, every weight from HBM): two steps in flight beat one, four, six and
-// eight; with the input in LDS, a deeper ring only costs occupancy.
-template <int FMT, bool PAIR>
-constexpr int decode_depth() { return 2; }
-template <int FMT, bool PAIR>
-constexpr int decode_panels() { return 1; }
-template <int FMT, bool PAIR>
-constexpr int decode_max_waves() { return PAIR ? 8 : kDecodeMaxWaves; }
 
 template <int FMT, bool PAIR>
 static void launch_gemv_mfma(const ExpertMats* mats, const Perm& perm, int max_active, int rows,
                              int cols, const uint16_t* xp, float* out, uint16_t* out_xp, Epi epi,
                              int* status, hipStream_t s) {
-  constexpr int NP = decode_panels<FMT, PAIR>();
-  constexpr int D = decode_depth<FMT, PAIR>();
-  constexpr int WMAX = decode_max_waves<FMT, PAIR>();
-  const int panels = rows / kPanelRows, steps = cols / kGemmKStep;
-  // split K until the launch has ~8192 waves, keeping at least two steps a part; a workgroup
-  // holds max(4, ksplit) waves
-  int ksplit = 1;
-  while (ksplit < WMAX && (long)panels / NP * max_active * ksplit < 8192 &&
-         steps / (2 * ksplit) >= 1)
-    ksplit *= 2;
-  const int waves = std::max(4, ksplit);
-  const int per_wg = waves / ksplit * NP;
-  const dim3 grid((panels + per_wg - 1) / per_wg, max_active);
-  const size_t lds = (size_t)cols / 8 * 32;
-  gemv_mfma_kernel<FMT, PAIR, NP, D, WMAX><<<grid, 64 * waves, lds, s>>>(
-      mats, perm, rows, cols, ksplit, xp, out, out_xp, epi, status);
+  const GemvShape g = gemv_mfma_shape<FMT, PAIR>(rows, cols, max_active);
+  gemv_mfma_kernel<FMT, PAIR, decode_panels<FMT, PAIR>(), decode_depth<FMT, PAIR>(),
+                   decode_max_waves<FMT, PAIR>()><<<g.grid, 64 * g.waves, g.lds, s>>>(
+      mats, perm, rows, cols, g.ksplit, xp, out, out_xp, epi, status);
 }
 
 void launch_gemv_mfma_gate_up(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,

@@ -142,7 +142,17 @@ struct RouteParams {
 };
 
 
-// Router logits.
+// The top-k routing of a one-token call's token 0 of `logits` with `rp` into ids / weights /
+// asc, run beside another kernel's work in its launch.
+struct RouteJob {
+  float* logits;
+  int K;
+  RouteParams rp;
+  int32_t* ids;
+  float* weights;
+  int32_t* asc;
+};
+
 // Router logits, the reference's 8-lane FP32 tree (BF16-rounded when round_bf16).
 // With `xp` (T = 1 only), the kernel also writes the token's BF16 piece vector there.
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
@@ -182,6 +192,11 @@ void launch_gemv_mfma_gate_up(int fmt, const ExpertMats* mats, const Perm& perm,
 void launch_gemv_mfma_down(int fmt, const ExpertMats* mats, const Perm& perm, int max_active,
                            int H, int I, const uint16_t* act_xp, float* y, Epi epi, int* status,
                            hipStream_t s);
+// The shared expert's gate_up (the dense table entry 0, as launch_gemv_mfma_gate_up) and the
+// routing of the token (`job`, E <= 512 experts) in one launch (urb_route.hip).
+void launch_shared_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
+                                 const uint16_t* xp, float* act, uint16_t* act_xp, Epi epi,
+                                 int* status, hipStream_t s, int E, const RouteJob& job);
 bool mfma_down_combine_fits(int K, int I);
 bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                                    const float* weights, const int32_t* asc, int K, int H, int I,

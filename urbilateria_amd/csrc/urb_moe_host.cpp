@@ -517,41 +517,47 @@ void urb_moe_destroy(urb_moe_ctx* ctx) {
   destroy_ctx(ctx);
 }
 
+// Router logits for one chunk (the routing parameters returned carry the partial slices when
+// the router writes them).  `xp` (one token): the router also writes the token's piece vector.
+static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
+                                            const uint32_t* tokens, int n, float* logits,
+                                            hipStream_t s, uint16_t* xp = nullptr) {
+  const urb_moe_desc& d = c->desc;
+  const bool qwen = d.composition == URB_COMPOSE_QWEN36;
+  const int E = (int)d.n_experts, H = (int)d.hidden;
+  urb::RouteParams rp{(int)d.router, qwen ? 1 : 0, (int)d.n_group, (int)d.topk_group,
+                      d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias, nullptr, 0,
+                      c->hash, tokens, c->hash_vocab};
+  Span span(c, URB_STAGE_ROUTER, s);
+  if (c->router_lane8) {
+    urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status, s,
+                             n == 1 ? xp : nullptr);
+  } else if (n == 1) {
+    // one token: a GEMV over the row-major router beats the 32-token MFMA tile
+    rp.slices = urb::router_gemv_slices(E);
+    rp.part = c->ws.router_part;
+    urb::launch_router_gemv_f64(c->router, E, H, x, c->ws.router_part, rp.slices, c->ws.status,
+                                s, xp);
+  } else {
+    rp.slices = urb::router_slices(E, H, n);
+    rp.part = c->ws.router_part;
+    urb::launch_router_mfma(c->router_panel, E, H, x, n, c->ws.router_part, rp.slices,
+                            c->ws.status, s);
+  }
+  return rp;
+}
+
 // Router and top-k for one chunk.  `xp` (one token): the router also writes the token's piece
 // vector.
 static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* tokens, int n,
                               float* logits, int32_t* ids, float* weights, hipStream_t s,
                               uint16_t* xp = nullptr) {
   const urb_moe_desc& d = c->desc;
-  const bool qwen = d.composition == URB_COMPOSE_QWEN36;
-  const int E = (int)d.n_experts, H = (int)d.hidden, K = (int)d.top_k;
-  urb::RouteParams rp{(int)d.router, qwen ? 1 : 0, (int)d.n_group, (int)d.topk_group,
-                      d.normalize ? 1 : 0, d.routed_scaling_factor, c->bias, nullptr, 0,
-                      c->hash, tokens, c->hash_vocab};
-  {
-    Span span(c, URB_STAGE_ROUTER, s);
-    if (c->router_lane8) {
-      urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status,
-                               s, n == 1 ? xp : nullptr);
-    } else if (n == 1) {
-      // one token: a GEMV over the row-major router beats the 32-token MFMA tile
-      rp.slices = urb::router_gemv_slices(E);
-      rp.part = c->ws.router_part;
-      urb::launch_router_gemv_f64(c->router, E, H, x, c->ws.router_part, rp.slices,
-                                  c->ws.status, s, xp);
-    } else {
-      rp.slices = urb::router_slices(E, H, n);
-      rp.part = c->ws.router_part;
-      urb::launch_router_mfma(c->router_panel, E, H, x, n, c->ws.router_part, rp.slices,
-                              c->ws.status, s);
-    }
-  }
-  {
-    Span span(c, URB_STAGE_ROUTE, s);
-    const bool ascending = d.composition != URB_COMPOSE_GLM;
-    urb::launch_route(logits, n, E, K, rp, ids, weights, ascending ? c->ws.asc : nullptr,
-                      c->ws.status, s);
-  }
+  const urb::RouteParams rp = launch_router_chunk(c, x, tokens, n, logits, s, xp);
+  Span span(c, URB_STAGE_ROUTE, s);
+  const bool ascending = d.composition != URB_COMPOSE_GLM;
+  urb::launch_route(logits, n, (int)d.n_experts, (int)d.top_k, rp, ids, weights,
+                    ascending ? c->ws.asc : nullptr, c->ws.status, s);
   return URB_OK;
 }
 
@@ -588,24 +594,28 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const urb::Epi epi{qwen ? urb::kEpiQwen : urb::kEpiGated, 0.0f};
-  route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp);
   if (has_shared) {
     // GLM: GatedMlp (src/models/glm/runtime/moe.rs:162).  QWEN36: a Qwen38Expert and its gate
-    // logit linear(shared_expert_gate) (qwen3_6/runtime.rs:1417-1435).
-    // in line on the caller's stream (one token: see shared_stream)
+    // logit linear(shared_expert_gate) (qwen3_6/runtime.rs:1417-1435).  In line on the caller's
+    // stream (one token: see shared_stream); the routing runs beside the shared gate+up, in
+    // its launch.
+    const urb::RouteParams rp = launch_router_chunk(c, xc, tokens, 1, ws.logits, s, ws.xp);
     Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
     {
       Span span(c, URB_STAGE_SHARED_GATE_UP, s);
       if (qwen)
         urb::launch_router_lane8(c->shared_gate8, 1, H, xc, 1, ws.gate_logit, 1, ws.status, s);
-      urb::launch_gemv_mfma_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xp,
-                                    nullptr, ws.shared_xp, epi, ws.status, s);
+      const urb::RouteJob job{ws.logits, K, rp, idc, wc, qwen ? ws.asc : nullptr};
+      urb::launch_shared_gate_up_route(d.shared_format, c->shared_table, H, Is, ws.xp, nullptr,
+                                       ws.shared_xp, epi, ws.status, s, E, job);
     }
     {
       Span span(c, URB_STAGE_SHARED_DOWN, s);
       urb::launch_gemv_mfma_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_xp,
                                  ws.shared_out, epi, ws.status, s);
     }
+  } else {
+    route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp);
   }
   Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
   {

@@ -1,4 +1,5 @@
 // urb_route.hip -- router GEMV/GEMM, top-k routing and the token->expert permutation.
+#include "urb_decode.hpp"
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
 #include "urb_panel.hpp"
@@ -622,6 +623,79 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
   if (t >= T) return;
   route_token<EPL, MODE>(t, logits, T, E, K, rp, ids, weights, asc, status, lds[wave],
                             grp[wave]);
+}
+
+// ------------------------------------------------------------------------------------------
+// One-token calls with a shared expert: the shared expert's gate+up GEMV and the token's top-k
+// routing in one launch.  The grid is the GEMV's plus one workgroup, whose first wave routes
+// the token while the others stream the shared expert's weights.  The two read the router's
+// output (logits or partial slices, and the token's pieces) and share nothing else, so no
+// workgroup waits for another; the routing's latency hides under the GEMV.  The routing
+// handles up to 64 * EPL experts.
+// ------------------------------------------------------------------------------------------
+template <int FMT, int EPL, int MODE>
+__global__ __launch_bounds__(64 * 8) void gemv_gate_up_route_kernel(
+    const ExpertMats* __restrict__ mats, Perm perm, int rows, int cols, int ksplit,
+    const uint16_t* __restrict__ xp, float* __restrict__ out, uint16_t* __restrict__ out_xp,
+    Epi epi, int* status, RouteJob job, int E) {
+  static_assert(decode_max_waves<FMT, true>() == 8, "workgroup bound of the gate_up GEMV");
+  extern __shared__ uint4 pieces_lds[];
+  if (blockIdx.x == gridDim.x - 1) {
+    // the LDS of the GEMV's input pieces holds the routing's scratch (the launch sizes it)
+    float* sh = reinterpret_cast<float*>(pieces_lds);
+    if (threadIdx.x < 64)
+      route_token<EPL, MODE>(0, job.logits, 1, E, job.K, job.rp, job.ids, job.weights, job.asc,
+                             status, sh, sh + kMaxExperts);
+    return;
+  }
+  gemv_mfma_body<FMT, true, decode_panels<FMT, true>(), decode_depth<FMT, true>(),
+                 decode_max_waves<FMT, true>()>(mats, perm, rows, cols, ksplit, xp, out, out_xp,
+                                                epi, status, pieces_lds);
+}
+
+template <int FMT, int EPL, int MODE>
+static void launch_gate_up_route_as(const ExpertMats* mats, int H, int I, const uint16_t* xp,
+                                    float* act, uint16_t* act_xp, Epi epi, int* status,
+                                    hipStream_t s, int E, const RouteJob& job) {
+  const Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
+  GemvShape g = gemv_mfma_shape<FMT, true>(I, H, 1);
+  g.grid.x += 1;
+  g.lds = std::max(g.lds, (size_t)(kMaxExperts + 64) * sizeof(float));
+  gemv_gate_up_route_kernel<FMT, EPL, MODE><<<g.grid, 64 * g.waves, g.lds, s>>>(
+      mats, dense, I, H, g.ksplit, xp, act, act_xp, epi, status, job, E);
+}
+
+template <int FMT, int EPL>
+static void launch_gate_up_route_epl(const ExpertMats* mats, int H, int I, const uint16_t* xp,
+                                     float* act, uint16_t* act_xp, Epi epi, int* status,
+                                     hipStream_t s, int E, const RouteJob& job) {
+  if (job.rp.router == 0)
+    launch_gate_up_route_as<FMT, EPL, 0>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+  else if (job.rp.router == 1)
+    launch_gate_up_route_as<FMT, EPL, 1>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+  else
+    launch_gate_up_route_as<FMT, EPL, 2>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+}
+
+template <int FMT>
+static void launch_gate_up_route_fmt(const ExpertMats* mats, int H, int I, const uint16_t* xp,
+                                     float* act, uint16_t* act_xp, Epi epi, int* status,
+                                     hipStream_t s, int E, const RouteJob& job) {
+  if (E <= 256)
+    launch_gate_up_route_epl<FMT, 4>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+  else
+    launch_gate_up_route_epl<FMT, 8>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+}
+
+void launch_shared_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
+                                 const uint16_t* xp, float* act, uint16_t* act_xp, Epi epi,
+                                 int* status, hipStream_t s, int E, const RouteJob& job) {
+  if (fmt == kFmtBF16)
+    launch_gate_up_route_fmt<kFmtBF16>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+  else if (fmt == kFmtMXFP4)
+    launch_gate_up_route_fmt<kFmtMXFP4>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+  else
+    launch_gate_up_route_fmt<kFmtMXFP8>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
 }
 
 // ------------------------------------------------------------------------------------------
