@@ -140,7 +140,11 @@ def stage_bytes(spec, C, stage, tokens, distinct):
     eb = lambda fmt, r, c: sum(C.matrix_bytes(fmt, r, c))
     ef = spec.expert_format
     if stage == "gate_up":
-        return distinct * 2 * eb(ef, I, H) + tokens * H * 4 + tokens * k * I * 4
+        routed = distinct * 2 * eb(ef, I, H) + tokens * H * 4 + tokens * k * I * 4
+        if tokens == 1 and Is and spec.composition in (C.COMPOSE_GLM, C.COMPOSE_QWEN36):
+            # one token: the shared expert's down projection runs in the routed gate+up launch
+            routed += stage_bytes(spec, C, "shared_down", tokens, distinct)
+        return routed
     if stage == "down":
         return distinct * eb(ef, H, I) + tokens * k * I * 4 + tokens * k * H * 4
     if stage == "shared_gate_up":

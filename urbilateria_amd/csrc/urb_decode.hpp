@@ -44,23 +44,23 @@ __device__ __forceinline__ bool decode_slot(const Perm& perm, int a, int& expert
 constexpr int kDecodeMaxWaves = 16;
 
 // A workgroup of W waves (blockDim.x / 64) is W / KSPLIT groups of NP consecutive 16-row panels
-// times KSPLIT parts of K, for one slot (blockIdx.y), workgroup blockIdx.x of the slot's panel
+// times KSPLIT parts of K, for one slot (`by`), workgroup `bx` of the slot's panel
 // groups.  xs (LDS): the slot's input pieces, cols / 8 units of 32 B.
 template <int FMT, bool PAIR, int NP, int DW, int WMAX>
 __device__ __forceinline__ void gemv_mfma_body(
     const ExpertMats* __restrict__ mats, const Perm& perm, int rows, int cols, int ksplit,
     const uint16_t* __restrict__ xp, float* __restrict__ out, uint16_t* __restrict__ out_xp,
-    Epi epi, int* status, uint4* xs) {
+    Epi epi, int* status, uint4* xs, int bx, int by) {
   __shared__ float red[WMAX][NP][16][2];
   int expert, pos;
-  if (!decode_slot(perm, blockIdx.y, expert, pos)) return;
+  if (!decode_slot(perm, by, expert, pos)) return;
   const ExpertMats m = mats[expert];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, lq = lane >> 4, piece = ln & 1;
   const int part = wave % ksplit;
   const int groups = (int)(blockDim.x >> 6) / ksplit;  // panel groups per workgroup
-  const int panel0 = (blockIdx.x * groups + wave / ksplit) * NP;
+  const int panel0 = (bx * groups + wave / ksplit) * NP;
   const bool valid = panel0 < rows / kPanelRows;
   const int steps = cols / kGemmKStep;
   const int s_begin = steps * part / ksplit, n = steps * (part + 1) / ksplit - s_begin;

@@ -594,13 +594,14 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
   const int Is = (int)d.shared_intermediate;
   Workspace& ws = c->ws;
   const urb::Epi epi{qwen ? urb::kEpiQwen : urb::kEpiGated, 0.0f};
+  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
   if (has_shared) {
     // GLM: GatedMlp (src/models/glm/runtime/moe.rs:162).  QWEN36: a Qwen38Expert and its gate
     // logit linear(shared_expert_gate) (qwen3_6/runtime.rs:1417-1435).  In line on the caller's
-    // stream (one token: see shared_stream); the routing runs beside the shared gate+up, in
-    // its launch.
+    // stream (one token: see shared_stream), each shared projection in the launch of the
+    // routed work beside it: the routing beside the shared gate+up, the routed gate+up beside
+    // the shared down.
     const urb::RouteParams rp = launch_router_chunk(c, xc, tokens, 1, ws.logits, s, ws.xp);
-    Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
     {
       Span span(c, URB_STAGE_SHARED_GATE_UP, s);
       if (qwen)
@@ -609,16 +610,13 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
       urb::launch_shared_gate_up_route(d.shared_format, c->shared_table, H, Is, ws.xp, nullptr,
                                        ws.shared_xp, epi, ws.status, s, E, job);
     }
-    {
-      Span span(c, URB_STAGE_SHARED_DOWN, s);
-      urb::launch_gemv_mfma_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_xp,
-                                 ws.shared_out, epi, ws.status, s);
-    }
+    Span span(c, URB_STAGE_GATE_UP, s);
+    urb::launch_gemv_mfma_gate_up_and_shared_down(d.expert_format, c->table, perm, std::min(E, K),
+                                                  H, I, ws.xp, ws.act_xp, d.shared_format,
+                                                  c->shared_table, Is, ws.shared_xp,
+                                                  ws.shared_out, epi, ws.status, s);
   } else {
     route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp);
-  }
-  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
-  {
     Span span(c, URB_STAGE_GATE_UP, s);
     urb::launch_gemv_mfma_gate_up(d.expert_format, c->table, perm, std::min(E, K), H, I, ws.xp,
                                   nullptr, ws.act_xp, epi, ws.status, s);

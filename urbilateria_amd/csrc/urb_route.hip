@@ -650,7 +650,8 @@ __global__ __launch_bounds__(64 * 8) void gemv_gate_up_route_kernel(
   }
   gemv_mfma_body<FMT, true, decode_panels<FMT, true>(), decode_depth<FMT, true>(),
                  decode_max_waves<FMT, true>()>(mats, perm, rows, cols, ksplit, xp, out, out_xp,
-                                                epi, status, pieces_lds);
+                                                epi, status, pieces_lds, blockIdx.x,
+                                                blockIdx.y);
 }
 
 template <int FMT, int EPL, int MODE>
