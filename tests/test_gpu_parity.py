@@ -698,6 +698,31 @@ def _qwen_shared_layer(hidden=256, n_experts=16, intermediate=128):
     return C.make_host_layer(spec)
 
 
+@pytest.mark.parametrize("fmt,shared_fmt,hidden,inter",
+                         [(f, g, 256, 128) for f in (C.FMT_BF16, C.FMT_MXFP4, C.FMT_MXFP8)
+                          for g in (C.FMT_BF16, C.FMT_MXFP4, C.FMT_MXFP8)]
+                         + [(C.FMT_MXFP4, C.FMT_BF16, 2048, 1024),
+                            (C.FMT_MXFP8, C.FMT_MXFP4, 2048, 1024)])
+def test_one_token_shared_expert_launches_match_oracle(fmt, shared_fmt, hidden, inter):
+    # One token with a shared expert: the routing runs beside the shared gate+up and the shared
+    # down beside the routed gate+up, for every pair of weight formats; H 2048 splits K in both
+    spec = C.LayerSpec(hidden=hidden, n_experts=64, top_k=8, intermediate=inter,
+                       shared_intermediate=inter, expert_format=fmt, shared_format=shared_fmt,
+                       router=C.ROUTER_SIGMOID_NOAUX_TC, composition=C.COMPOSE_GLM, n_group=8,
+                       topk_group=4, normalize=True, routed_scaling_factor=2.5)
+    host = C.make_host_layer(spec, bias=C.zipf_bias(64, 1.1, 0.05))
+    x = synth.activations(f"x.one.{fmt}.{shared_fmt}.{hidden}", 1, hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=1)
+    for _ in range(2):  # a second call reuses the workspace
+        y, ids, w = layer.forward(torch.from_numpy(x).cuda())
+        ref = _oracle(host, x)
+        assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+        assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+        err = rel_l2(y.cpu().numpy(), ref.output)
+        assert err < REL_L2_BAR, err
+    layer.close()
+
+
 @pytest.mark.parametrize("T", [1, 5, 40])
 def test_qwen_gated_shared_expert_matches_oracle(T):
     # T = 1 takes the fused down+combine kernel, T > 1 the grouped GEMMs and combine kernel;
