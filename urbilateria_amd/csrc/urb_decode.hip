@@ -76,29 +76,30 @@ constexpr int kPairWaves = 8;
 template <int FR, int FS>
 __global__ __launch_bounds__(64 * kPairWaves) void gemv_gate_up_and_down_kernel(
     const ExpertMats* __restrict__ mats_r, Perm perm, int I, int H, int ksplit_r, int gx_r,
-    int slots, const uint16_t* __restrict__ xp, uint16_t* __restrict__ act_xp,
-    const ExpertMats* __restrict__ mats_s, int Is, int ksplit_s,
-    const uint16_t* __restrict__ shared_xp, float* __restrict__ shared_out, Epi epi,
-    int* status) {
+    int slots, const uint16_t* __restrict__ xp, float* __restrict__ act,
+    uint16_t* __restrict__ act_xp, const ExpertMats* __restrict__ mats_s, int Is, int ksplit_s,
+    const uint16_t* __restrict__ shared_xp, float* __restrict__ shared_out, Epi epi_r,
+    Epi epi_s, int* status) {
   extern __shared__ uint4 xs[];
   const int nr = gx_r * slots;
   if ((int)blockIdx.x < nr) {
     gemv_mfma_body<FR, true, decode_panels<FR, true>(), decode_depth<FR, true>(), kPairWaves>(
-        mats_r, perm, I, H, ksplit_r, xp, nullptr, act_xp, epi, status, xs, blockIdx.x % gx_r,
+        mats_r, perm, I, H, ksplit_r, xp, act, act_xp, epi_r, status, xs, blockIdx.x % gx_r,
         blockIdx.x / gx_r);
   } else {
     const Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
     gemv_mfma_body<FS, false, decode_panels<FS, false>(), decode_depth<FS, false>(),
                    kPairWaves>(mats_s, dense, H, Is, ksplit_s, shared_xp, shared_out, nullptr,
-                               epi, status, xs, blockIdx.x - nr, 0);
+                               epi_s, status, xs, blockIdx.x - nr, 0);
   }
 }
 
 template <int FR, int FS>
 static void launch_gate_up_and_down(const ExpertMats* mats_r, const Perm& perm, int slots, int H,
-                                    int I, const uint16_t* xp, uint16_t* act_xp,
+                                    int I, const uint16_t* xp, float* act, uint16_t* act_xp,
                                     const ExpertMats* mats_s, int Is, const uint16_t* shared_xp,
-                                    float* shared_out, Epi epi, int* status, hipStream_t s) {
+                                    float* shared_out, Epi epi_r, Epi epi_s, int* status,
+                                    hipStream_t s) {
   static_assert(decode_panels<FR, true>() == 1 && decode_panels<FS, false>() == 1,
                 "one panel per wave");
   const int kr = std::min(gemv_mfma_shape<FR, true>(I, H, slots).ksplit, kPairWaves);
@@ -108,42 +109,46 @@ static void launch_gate_up_and_down(const ExpertMats* mats_r, const Perm& perm, 
   const int gx_s = (H / kPanelRows + per_s - 1) / per_s;
   const size_t lds = (size_t)std::max(H, Is) / 8 * 32;
   gemv_gate_up_and_down_kernel<FR, FS><<<gx_r * slots + gx_s, 64 * kPairWaves, lds, s>>>(
-      mats_r, perm, I, H, kr, gx_r, slots, xp, act_xp, mats_s, Is, ks, shared_xp, shared_out,
-      epi, status);
+      mats_r, perm, I, H, kr, gx_r, slots, xp, act, act_xp, mats_s, Is, ks, shared_xp,
+      shared_out, epi_r, epi_s, status);
 }
 
 template <int FR>
 static void launch_gate_up_and_down_fr(int fs, const ExpertMats* mats_r, const Perm& perm,
-                                       int slots, int H, int I, const uint16_t* xp,
+                                       int slots, int H, int I, const uint16_t* xp, float* act,
                                        uint16_t* act_xp, const ExpertMats* mats_s, int Is,
-                                       const uint16_t* shared_xp, float* shared_out, Epi epi,
-                                       int* status, hipStream_t s) {
+                                       const uint16_t* shared_xp, float* shared_out, Epi epi_r,
+                                       Epi epi_s, int* status, hipStream_t s) {
   if (fs == kFmtBF16)
-    launch_gate_up_and_down<FR, kFmtBF16>(mats_r, perm, slots, H, I, xp, act_xp, mats_s, Is,
-                                          shared_xp, shared_out, epi, status, s);
+    launch_gate_up_and_down<FR, kFmtBF16>(mats_r, perm, slots, H, I, xp, act, act_xp, mats_s,
+                                          Is, shared_xp, shared_out, epi_r, epi_s, status, s);
   else if (fs == kFmtMXFP4)
-    launch_gate_up_and_down<FR, kFmtMXFP4>(mats_r, perm, slots, H, I, xp, act_xp, mats_s, Is,
-                                           shared_xp, shared_out, epi, status, s);
+    launch_gate_up_and_down<FR, kFmtMXFP4>(mats_r, perm, slots, H, I, xp, act, act_xp, mats_s,
+                                           Is, shared_xp, shared_out, epi_r, epi_s, status, s);
   else
-    launch_gate_up_and_down<FR, kFmtMXFP8>(mats_r, perm, slots, H, I, xp, act_xp, mats_s, Is,
-                                           shared_xp, shared_out, epi, status, s);
+    launch_gate_up_and_down<FR, kFmtMXFP8>(mats_r, perm, slots, H, I, xp, act, act_xp, mats_s,
+                                           Is, shared_xp, shared_out, epi_r, epi_s, status, s);
 }
 
 void launch_gemv_mfma_gate_up_and_shared_down(int fmt, const ExpertMats* mats, const Perm& perm,
                                               int max_active, int H, int I, const uint16_t* xp,
-                                              uint16_t* act_xp, int shared_fmt,
-                                              const ExpertMats* shared_mats, int Is,
-                                              const uint16_t* shared_xp, float* shared_out,
-                                              Epi epi, int* status, hipStream_t s) {
+                                              float* act, uint16_t* act_xp, Epi epi,
+                                              int shared_fmt, const ExpertMats* shared_mats,
+                                              int Is, const uint16_t* shared_xp,
+                                              float* shared_out, Epi shared_epi, int* status,
+                                              hipStream_t s) {
   if (fmt == kFmtBF16)
-    launch_gate_up_and_down_fr<kFmtBF16>(shared_fmt, mats, perm, max_active, H, I, xp, act_xp,
-                                         shared_mats, Is, shared_xp, shared_out, epi, status, s);
+    launch_gate_up_and_down_fr<kFmtBF16>(shared_fmt, mats, perm, max_active, H, I, xp, act,
+                                         act_xp, shared_mats, Is, shared_xp, shared_out, epi,
+                                         shared_epi, status, s);
   else if (fmt == kFmtMXFP4)
-    launch_gate_up_and_down_fr<kFmtMXFP4>(shared_fmt, mats, perm, max_active, H, I, xp, act_xp,
-                                          shared_mats, Is, shared_xp, shared_out, epi, status, s);
+    launch_gate_up_and_down_fr<kFmtMXFP4>(shared_fmt, mats, perm, max_active, H, I, xp, act,
+                                          act_xp, shared_mats, Is, shared_xp, shared_out, epi,
+                                          shared_epi, status, s);
   else
-    launch_gate_up_and_down_fr<kFmtMXFP8>(shared_fmt, mats, perm, max_active, H, I, xp, act_xp,
-                                          shared_mats, Is, shared_xp, shared_out, epi, status, s);
+    launch_gate_up_and_down_fr<kFmtMXFP8>(shared_fmt, mats, perm, max_active, H, I, xp, act,
+                                          act_xp, shared_mats, Is, shared_xp, shared_out, epi,
+                                          shared_epi, status, s);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -197,14 +197,16 @@ void launch_gemv_mfma_down(int fmt, const ExpertMats* mats, const Perm& perm, in
 void launch_shared_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
                                  const uint16_t* xp, float* act, uint16_t* act_xp, Epi epi,
                                  int* status, hipStream_t s, int E, const RouteJob& job);
-// The routed gate_up (act_xp pieces only) and the shared expert's down projection (the dense
-// table entry 0, f32 rows into shared_out) in one launch.
+// The routed gate_up (as launch_gemv_mfma_gate_up, epilogue `epi`) and the shared expert's down
+// projection (the dense table entry 0, f32 rows into shared_out, epilogue `shared_epi`) in one
+// launch.
 void launch_gemv_mfma_gate_up_and_shared_down(int fmt, const ExpertMats* mats, const Perm& perm,
                                               int max_active, int H, int I, const uint16_t* xp,
-                                              uint16_t* act_xp, int shared_fmt,
-                                              const ExpertMats* shared_mats, int Is,
-                                              const uint16_t* shared_xp, float* shared_out,
-                                              Epi epi, int* status, hipStream_t s);
+                                              float* act, uint16_t* act_xp, Epi epi,
+                                              int shared_fmt, const ExpertMats* shared_mats,
+                                              int Is, const uint16_t* shared_xp,
+                                              float* shared_out, Epi shared_epi, int* status,
+                                              hipStream_t s);
 bool mfma_down_combine_fits(int K, int I);
 bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_t* ids,
                                    const float* weights, const int32_t* asc, int K, int H, int I,

@@ -612,9 +612,9 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
     }
     Span span(c, URB_STAGE_GATE_UP, s);
     urb::launch_gemv_mfma_gate_up_and_shared_down(d.expert_format, c->table, perm, std::min(E, K),
-                                                  H, I, ws.xp, ws.act_xp, d.shared_format,
-                                                  c->shared_table, Is, ws.shared_xp,
-                                                  ws.shared_out, epi, ws.status, s);
+                                                  H, I, ws.xp, nullptr, ws.act_xp, epi,
+                                                  d.shared_format, c->shared_table, Is,
+                                                  ws.shared_xp, ws.shared_out, epi, ws.status, s);
   } else {
     route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, ws.xp);
     Span span(c, URB_STAGE_GATE_UP, s);
@@ -662,32 +662,39 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
   const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
   urb::launch_quantize(xc, 1, (size_t)H, nullptr, nullptr, nullptr, ws.status, s, 0, nullptr,
                        nullptr, block, ws.xp);
+  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
+  // Hy4 re-quantizes the SwiGLU output (expert.rs:677); DeepSeek first scales each row by its
+  // route weight and rounds to BF16 (runtime.rs:2254-2258); one token: slot = row
+  auto quantize_act = [&] {
+    urb::launch_quantize(ws.act, (size_t)K, (size_t)I, nullptr, nullptr, nullptr, ws.status, s,
+                         dsv ? 1 : 0, dsv ? wc : nullptr, nullptr, block, ws.act_xp);
+  };
   if (has_shared) {
-    // in line on the caller's stream (one token: see shared_stream)
-    Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
+    // In line on the caller's stream (one token: see shared_stream), each shared projection in
+    // the launch of the routed work beside it: the routing beside the shared gate+up, the
+    // routed gate+up beside the shared down.
+    const urb::RouteParams rp = launch_router_chunk(c, xc, tokens, 1, ws.logits, s);
     {
       Span span(c, URB_STAGE_SHARED_GATE_UP, s);
-      urb::launch_gemv_mfma_gate_up(d.shared_format, c->shared_table, dense, 1, H, Is, ws.xp,
-                                    ws.shared_act, nullptr, dense_mlp, ws.status, s);
+      const urb::RouteJob job{ws.logits, K, rp, idc, wc, ws.asc};
+      urb::launch_shared_gate_up_route(d.shared_format, c->shared_table, H, Is, ws.xp,
+                                       ws.shared_act, nullptr, dense_mlp, ws.status, s, E, job);
       urb::launch_quantize(ws.shared_act, 1, (size_t)Is, nullptr, nullptr, nullptr, ws.status,
                            s, dsv ? 1 : 0, nullptr, nullptr, block, ws.shared_xp);
     }
-    {
-      Span span(c, URB_STAGE_SHARED_DOWN, s);
-      urb::launch_gemv_mfma_down(d.shared_format, c->shared_table, dense, 1, H, Is, ws.shared_xp,
-                                 ws.shared_out, dense_mlp, ws.status, s);
-    }
-  }
-  route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s);
-  Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
-  {
+    Span span(c, URB_STAGE_GATE_UP, s);
+    urb::launch_gemv_mfma_gate_up_and_shared_down(d.expert_format, c->table, perm, std::min(E, K),
+                                                  H, I, ws.xp, ws.act, nullptr, routed,
+                                                  d.shared_format, c->shared_table, Is,
+                                                  ws.shared_xp, ws.shared_out, dense_mlp,
+                                                  ws.status, s);
+    quantize_act();
+  } else {
+    route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s);
     Span span(c, URB_STAGE_GATE_UP, s);
     urb::launch_gemv_mfma_gate_up(d.expert_format, c->table, perm, std::min(E, K), H, I, ws.xp,
                                   ws.act, nullptr, routed, ws.status, s);
-    // Hy4 re-quantizes the SwiGLU output (expert.rs:677); DeepSeek first scales each row by
-    // its route weight and rounds to BF16 (runtime.rs:2254-2258); one token: slot = row
-    urb::launch_quantize(ws.act, (size_t)K, (size_t)I, nullptr, nullptr, nullptr, ws.status, s,
-                         dsv ? 1 : 0, dsv ? wc : nullptr, nullptr, block, ws.act_xp);
+    quantize_act();
   }
   if (urb::mfma_down_combine_fits(K, I)) {
     Span span(c, URB_STAGE_DOWN, s);
