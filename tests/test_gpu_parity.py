@@ -698,6 +698,32 @@ def _qwen_shared_layer(hidden=256, n_experts=16, intermediate=128):
     return C.make_host_layer(spec)
 
 
+@pytest.mark.parametrize("comp,T", [(C.COMPOSE_GLM, 256), (C.COMPOSE_GLM, 300),
+                                    (C.COMPOSE_GLM, 520), (C.COMPOSE_QWEN36, 300)])
+def test_dense_shared_batch_matches_oracle(comp, T):
+    # f32-activation batches of 256+ tokens run the BF16 shared expert in line, as dense
+    # 32-token tiles of two (gate+up) or four (down) panels per wave; 300 and 520 end in a
+    # partial tile
+    if comp == C.COMPOSE_GLM:
+        spec = C.LayerSpec(hidden=512, n_experts=16, top_k=4, intermediate=256,
+                           shared_intermediate=256, expert_format=C.FMT_MXFP4,
+                           shared_format=C.FMT_BF16, router=C.ROUTER_SIGMOID_NOAUX_TC,
+                           composition=C.COMPOSE_GLM, n_group=4, topk_group=2, normalize=True,
+                           routed_scaling_factor=2.5)
+        host = C.make_host_layer(spec, bias=C.zipf_bias(16, 1.1, 0.05))
+    else:
+        host = _qwen_shared_layer()
+        spec = host.spec
+    x = synth.activations(f"x.dense.{comp}.{T}", T, spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y, ids, w = layer.forward(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+    err = rel_l2(y.cpu().numpy(), ref.output)
+    assert err < REL_L2_BAR, err
+    layer.close()
+
+
 @pytest.mark.parametrize("fmt,shared_fmt,hidden,inter",
                          [(f, g, 256, 128) for f in (C.FMT_BF16, C.FMT_MXFP4, C.FMT_MXFP8)
                           for g in (C.FMT_BF16, C.FMT_MXFP4, C.FMT_MXFP8)]
