@@ -127,10 +127,15 @@ def layer_flops(spec, tokens):
 
 def stage_flops(spec, stage, tokens):
     """FLOPs of one launch of a projection stage (2 per multiply-add)."""
+    from urbilateria_amd import configs as C
     H, I, k, Is = spec.hidden, spec.intermediate, spec.top_k, spec.shared_intermediate
-    return {"gate_up": 2 * tokens * k * 2 * H * I, "down": 2 * tokens * k * H * I,
-            "shared_gate_up": 2 * tokens * 2 * H * Is,
-            "shared_down": 2 * tokens * H * Is}.get(stage, 0)
+    f = {"gate_up": 2 * tokens * k * 2 * H * I, "down": 2 * tokens * k * H * I,
+         "shared_gate_up": 2 * tokens * 2 * H * Is,
+         "shared_down": 2 * tokens * H * Is}.get(stage, 0)
+    if (stage == "gate_up" and tokens == 1 and Is
+            and spec.composition in (C.COMPOSE_GLM, C.COMPOSE_QWEN36)):
+        f += 2 * H * Is  # the shared down projection runs in the same launch
+    return f
 
 
 def stage_bytes(spec, C, stage, tokens, distinct):
