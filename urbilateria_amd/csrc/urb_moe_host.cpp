@@ -844,10 +844,11 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       continue;
     }
     if (has_shared) {
-      // The shared expert does not depend on the routes: it runs on the side stream while the
-      // router, top-k and permutation run here.  GLM: GatedMlp (src/models/glm/runtime/moe.rs:
-      // 162).  QWEN36: a Qwen38Expert and its gate logit linear(shared_expert_gate) -- the
-      // router's 8-lane FP32 tree with BF16 output, one row (qwen3_6/runtime.rs:1417-1435).
+      // The shared expert does not depend on the routes: below 256 tokens it runs on the side
+      // stream while the router, top-k and permutation run here (shared_stream).  GLM:
+      // GatedMlp (src/models/glm/runtime/moe.rs:162).  QWEN36: a Qwen38Expert and its gate
+      // logit linear(shared_expert_gate) -- the router's 8-lane FP32 tree with BF16 output, one
+      // row (qwen3_6/runtime.rs:1417-1435).
       if (ss != s) {
         URB_HIP(hipEventRecord(c->fork, s));
         URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
