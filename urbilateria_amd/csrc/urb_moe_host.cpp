@@ -843,6 +843,22 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       if (st) return st;
       continue;
     }
+    // The routing and the permutation; with a shared expert in line (batches of 256+ tokens),
+    // they run beside it on the side stream instead, and the routed GEMMs wait for both.
+    const bool route_beside = has_shared && ss == s;
+    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, nullptr, K};
+    auto route_and_permute = [&](hipStream_t rs) {
+      route_chunk(c, xc, tc, n, ws.logits, idc, wc, rs);
+      Span span(c, URB_STAGE_PERMUTE, rs);
+      urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts,
+                          ws.perm_token, ws.pos_of_slot, ws.tiles, nullptr, rs);
+    };
+    if (route_beside) {
+      URB_HIP(hipEventRecord(c->fork, s));
+      URB_HIP(hipStreamWaitEvent(c->side, c->fork, 0));
+      route_and_permute(c->side);
+      URB_HIP(hipEventRecord(c->join, c->side));
+    }
     if (has_shared) {
       // The shared expert does not depend on the routes: below 256 tokens it runs on the side
       // stream while the router, top-k and permutation run here (shared_stream).  GLM:
@@ -871,13 +887,10 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       }
       if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
     }
-    route_chunk(c, xc, tc, n, ws.logits, idc, wc, s);
-    Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, nullptr, K};
-    {
-      Span span(c, URB_STAGE_PERMUTE, s);
-      urb::launch_permute(idc, n, E, K, ws.meta, ws.active, ws.offsets, ws.counts,
-                          ws.perm_token, ws.pos_of_slot, ws.tiles, nullptr, s);
-    }
+    if (route_beside)
+      URB_HIP(hipStreamWaitEvent(s, c->join, 0));
+    else
+      route_and_permute(s);
     const int max_tiles = urb::gemm_max_tiles(n, K, E);
     // grouped MFMA GEMMs over the row tiles
     {
