@@ -157,9 +157,10 @@ void urb_moe_destroy(urb_moe_ctx *ctx);
  * routes per token in ranking order: ids [tokens, k] (device, i32) and weights [tokens, k]
  * (device, f32), either may be NULL.  Replaces execute_streamed_moe / execute_batched_moe
  * (src/models/qwen3_6/runtime.rs:1067-1243) for QWEN36 and RuntimeMoeLayer::forward
- * (src/models/glm/runtime/moe.rs:138-176) for GLM.  Enqueues only: numerical failures the
- * reference reports (non-finite input, activations or outputs) are latched on the device and
- * returned by urb_moe_sync. */
+ * (src/models/glm/runtime/moe.rs:138-176) for GLM.  1 <= tokens <= desc.max_tokens, else
+ * URB_ERR_SHAPE and nothing is enqueued.  Enqueues only: numerical failures the reference
+ * reports (non-finite input, activations or outputs) are latched on the device and returned by
+ * urb_moe_sync. */
 urb_status urb_moe_forward(urb_moe_ctx *ctx, const float *x, uint32_t tokens, float *y,
                            int32_t *ids, float *weights, void *stream);
 

@@ -1069,6 +1069,9 @@ def test_shape_and_geometry_errors():
     with pytest.raises(N.UrbError) as e:
         layer.forward(x)  # more tokens than max_tokens
     assert e.value.status == N.ERR_SHAPE
+    with pytest.raises(N.UrbError) as e:
+        layer.forward(torch.zeros((0, host.spec.hidden), device="cuda"))  # an empty batch
+    assert e.value.status == N.ERR_SHAPE
     layer.close()
 
 
