@@ -1069,9 +1069,10 @@ def test_shape_and_geometry_errors():
     with pytest.raises(N.UrbError) as e:
         layer.forward(x)  # more tokens than max_tokens
     assert e.value.status == N.ERR_SHAPE
-    with pytest.raises(N.UrbError) as e:
-        layer.forward(torch.zeros((0, host.spec.hidden), device="cuda"))  # an empty batch
-    assert e.value.status == N.ERR_SHAPE
+    # an empty batch (valid buffers, 0 tokens): a shape error, nothing enqueued
+    y = torch.empty((1, host.spec.hidden), device="cuda")
+    assert N.moe_lib().urb_moe_forward(layer._ctx, x.data_ptr(), 0, y.data_ptr(), None, None,
+                                       None) == N.ERR_SHAPE
     layer.close()
 
 
