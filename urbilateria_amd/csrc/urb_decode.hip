@@ -155,9 +155,12 @@ void launch_gemv_mfma_gate_up_and_shared_down(int fmt, const ExpertMats* mats, c
 // The down projection of the k routed experts fused with the combine (one token).  A
 // workgroup owns one 16-row output panel; its waves are tasks (slot a, K part z),
 // a * ksplit + z, one each.  The k SwiGLU rows' pieces are staged in LDS once; task partials
-// meet in LDS; 16 threads add each slot's parts in order, apply the down epilogue and combine
-// the slots in the composition's order -- the per-slot outputs never leave the chip and no
-// combine kernel runs.  `comp` = composition (0 QWEN36, 1 GLM, 2 HY4, 3 DSV41).
+// meet in LDS; the first wave of each slot adds the slot's parts in order and applies the down
+// epilogue; 16 threads combine the slots in the composition's order -- the per-slot outputs
+// never leave the chip and no combine kernel runs.  `comp` = composition (0 QWEN36, 1 GLM,
+// 2 HY4, 3 DSV41).  The combine's inputs (route weights and order, shared and residual rows,
+// gate) are loaded while the weights stream, and the combine reads every slot before it adds:
+// with dependent loads per slot, the 16-thread tail cost ~1.3 us of a 14.5 us launch.
 // ------------------------------------------------------------------------------------------
 template <int FMT, int DW>
 __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_kernel(
@@ -168,6 +171,22 @@ __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_k
     int* status) {
   extern __shared__ uint4 xs[];  // K x I / 8 piece units
   __shared__ float red[kDecodeMaxWaves][16];
+  __shared__ float ys[kDecodeMaxWaves][16];  // slot outputs after the down epilogue
+  __shared__ float wl[kDecodeMaxWaves];
+  __shared__ int al[kDecodeMaxWaves];
+  // combine inputs, in flight during the weight stream
+  float wv = 0.0f, sv = 0.0f, rv = 0.0f, gv = 0.0f;
+  int av = 0;
+  if (threadIdx.x < K) {
+    wv = w[threadIdx.x];
+    if (comp != 1) av = asc[threadIdx.x];
+  }
+  if (threadIdx.x < 16) {
+    const int row = blockIdx.x * kPanelRows + threadIdx.x;
+    if (shared) sv = shared[row];
+    if (residual) rv = residual[row];
+    if (gate) gv = gate[0];
+  }
   const int lane = threadIdx.x & 63;
   const int t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's task
   const int ln = lane & 15, lq = lane >> 4, piece = ln & 1;
@@ -203,49 +222,67 @@ __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_k
     }
   }
   if (lq == 0) red[t][ln] = acc[0] + acc[1];
+  if (threadIdx.x < K) {
+    wl[threadIdx.x] = wv;
+    al[threadIdx.x] = av;
+  }
+  __syncthreads();
+  if (z == 0 && lq == 0) {
+    bool bad = false;
+    float v = 0.0f;
+    for (int zz = 0; zz < ksplit; ++zz) v += red[t + zz][ln];  // K parts in order
+    ys[a][ln] = epi_down<FMT>(epi, v, bad);
+    if (bad) flag(status, kStatusNonFinite);
+  }
   __syncthreads();
 
   if (threadIdx.x < 16) {
     const int row = panel * kPanelRows + threadIdx.x;
     bool bad = false;
-    auto y = [&](int a) {
-      float v = 0.0f;
-      for (int z = 0; z < ksplit; ++z) v += red[a * ksplit + z][threadIdx.x];
-      return epi_down<FMT>(epi, v, bad);
-    };
+    // slot j's output and weight in combine order: ranking order (GLM) or ascending id
+    float yv[kDecodeMaxWaves], wr[kDecodeMaxWaves];
+#pragma unroll
+    for (int j = 0; j < kDecodeMaxWaves; ++j) {
+      const int a = j < K ? (comp == 1 ? j : al[j]) : 0;
+      yv[j] = ys[a][threadIdx.x];
+      wr[j] = wl[a];
+    }
     float res;
     if (comp == 1) {
       // GLM (src/models/glm/runtime/moe.rs:162-171): f64 from the shared expert, ranking order
-      double acc = shared ? (double)shared[row] : 0.0;
-      for (int j = 0; j < K; ++j) acc += (double)w[j] * (double)y(j);
+      double acc = shared ? (double)sv : 0.0;
+#pragma unroll
+      for (int j = 0; j < kDecodeMaxWaves; ++j)
+        if (j < K) acc += (double)wr[j] * (double)yv[j];
       res = (float)acc;
     } else {
       float acc = 0.0f;
-      for (int j = 0; j < K; ++j) {
-        const int a = asc[j];
-        const float v = y(a);
+#pragma unroll
+      for (int j = 0; j < kDecodeMaxWaves; ++j) {
+        if (j >= K) break;
+        const float v = yv[j];
         if (comp == 0) {
           // Qwen (src/models/qwen3_6/runtime.rs:1398-1415): c = bf16(w y), acc = bf16(acc + c)
           float c;
-          if (!rne_bf16(w[a] * v, &c)) { bad = true; c = w[a] * v; }
+          if (!rne_bf16(wr[j] * v, &c)) { bad = true; c = wr[j] * v; }
           const float t = acc + c;
           if (!rne_bf16(t, &acc)) { bad = true; acc = t; }
         } else if (comp == 2) {
-          acc = acc + w[a] * v;  // Hy4 (src/models/hy4/runtime.rs:1436-1441): f32
+          acc = acc + wr[j] * v;  // Hy4 (src/models/hy4/runtime.rs:1436-1441): f32
         } else {
           acc = acc + v;  // DeepSeek V4.1 (deepseek_v41/runtime.rs:1995-1998): weight applied
         }
       }
       if (comp == 0 && shared) {
         // the gated shared expert (src/models/qwen3_6/runtime.rs:1436-1461)
-        const float sc = qwen_shared_scale(gate[0], bad);
+        const float sc = qwen_shared_scale(gv, bad);
         float c;
-        if (!rne_bf16(sc * shared[row], &c)) { bad = true; c = sc * shared[row]; }
+        if (!rne_bf16(sc * sv, &c)) { bad = true; c = sc * sv; }
         const float t = acc + c;
         if (!rne_bf16(t, &acc)) { bad = true; acc = t; }
       }
       if (comp >= 2) {
-        if (shared) acc = acc + shared[row];
+        if (shared) acc = acc + sv;
         float b;
         if (!rne_bf16(acc, &b)) { bad = true; b = acc; }
         acc = b;
@@ -254,7 +291,7 @@ __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_k
     }
     if (residual) {
       // add_residual with BF16 activations (src/models/qwen3_6/runtime.rs:1470-1494)
-      const float t = residual[row] + res;
+      const float t = rv + res;
       if (!rne_bf16(t, &res)) { bad = true; res = t; }
     }
     out[row] = res;
