@@ -313,10 +313,11 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
         return;
       }
     }
-    // gate+up gathers its activation rows two steps ahead (512 tokens over 160 experts of
-    // 6144 x 2048, in isolation: 782-787 -> 776-777 us)
-    launch_shape<FMT, PAIR, 1, 2, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                      status, s, beside);
+    // activation rows gathered one step ahead: two steps ahead (as the MXFP4 gate+up) was 1 %
+    // faster in isolation on f32 token rows (512 tokens over 160 experts of 6144 x 2048: 782-787
+    // -> 776-777 us) but 1.5 % slower on BF16-valued rows, which skip the lo-half MFMAs
+    // (774-776 -> 786-787 us in the layer call)
+    launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   }
   else {
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
