@@ -197,6 +197,12 @@ void launch_gemv_mfma_down(int fmt, const ExpertMats* mats, const Perm& perm, in
 void launch_shared_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
                                  const uint16_t* xp, float* act, uint16_t* act_xp, Epi epi,
                                  int* status, hipStream_t s, int E, const RouteJob& job);
+// One token without a shared expert: the routing inside the routed gate+up GEMV (every
+// workgroup routes the token; the first one writes ids, weights, asc and a sliced router's
+// logits).  Returns false (nothing launched) when top_k exceeds the kernel's LDS slots.
+bool launch_routed_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
+                                 const uint16_t* xp, uint16_t* act_xp, Epi epi, int* status,
+                                 hipStream_t s, int E, const RouteJob& job);
 // The routed gate_up (as launch_gemv_mfma_gate_up, epilogue `epi`) and the shared expert's down
 // projection (the dense table entry 0, f32 rows into shared_out, epilogue `shared_epi`) in one
 // launch.

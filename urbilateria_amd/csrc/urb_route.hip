@@ -334,7 +334,7 @@ template <int EPL, int MODE>
 __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int K,
                             const RouteParams& rp, int32_t* __restrict__ ids,
                             float* __restrict__ weights, int32_t* __restrict__ asc, int* status,
-                            float* sh, float* grpw) {
+                            float* sh, float* grpw, bool store_logits = true) {
   const int lane = threadIdx.x & 63;
   float* lt = logits + (size_t)t * E;
   float v[EPL];
@@ -591,7 +591,7 @@ __device__ void route_token(int t, float* __restrict__ logits, int T, int E, int
     if (rp.normalize && !finite(den)) bad = true;
     w = __fmul_rn(rp.normalize ? my_val / den : my_val, rp.scale);
   }
-  if (rp.part) {
+  if (rp.part && store_logits) {
     // the logits are stored last: a store counts against the same counter as the loads, so
     // an earlier store would be waited on by every later wait for a load
 #pragma unroll
@@ -699,6 +699,92 @@ void launch_shared_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
     launch_gate_up_route_fmt<kFmtMXFP4>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
   else
     launch_gate_up_route_fmt<kFmtMXFP8>(mats, H, I, xp, act, act_xp, epi, status, s, E, job);
+}
+
+// ------------------------------------------------------------------------------------------
+// One token without a shared expert: the routing inside the routed gate+up GEMV.  Every
+// workgroup's first wave routes the token from the router's output (logits, or f64 partial
+// slices) into LDS -- the same inputs through the same arithmetic, so every workgroup holds
+// the same routes -- and the GEMV then reads its slot's expert from LDS.  Workgroup (0, 0)
+// also writes the routes, and a sliced router's logits, for the down + combine launch.  Each
+// workgroup spends one routing (its logits read and top-k) before its first weight load; the
+// routing kernel and its launch are gone.
+// ------------------------------------------------------------------------------------------
+constexpr int kRouteMaxK = 32;
+
+template <int FMT, int EPL, int MODE>
+__global__ __launch_bounds__(64 * 8) void gemv_route_gate_up_kernel(
+    const ExpertMats* __restrict__ mats, int rows, int cols, int ksplit,
+    const uint16_t* __restrict__ xp, uint16_t* __restrict__ out_xp, Epi epi, int* status,
+    RouteJob job, int E) {
+  static_assert(decode_max_waves<FMT, true>() == 8, "workgroup bound of the gate_up GEMV");
+  extern __shared__ uint4 pieces_lds[];
+  __shared__ __attribute__((aligned(16))) float rsh[kMaxExperts + 64];
+  __shared__ int32_t ids_l[kRouteMaxK];
+  __shared__ float w_l[kRouteMaxK];
+  __shared__ int32_t asc_l[kRouteMaxK];
+  const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
+  if (threadIdx.x < 64) {
+    route_token<EPL, MODE>(0, job.logits, 1, E, job.K, job.rp, ids_l, w_l,
+                           job.asc ? asc_l : nullptr, status, rsh, rsh + kMaxExperts, lead);
+    if (lead && (int)threadIdx.x < job.K) {
+      job.ids[threadIdx.x] = ids_l[threadIdx.x];
+      job.weights[threadIdx.x] = w_l[threadIdx.x];
+      if (job.asc) job.asc[threadIdx.x] = asc_l[threadIdx.x];
+    }
+  }
+  __syncthreads();
+  const Perm perm{nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr, ids_l, job.K};
+  gemv_mfma_body<FMT, true, decode_panels<FMT, true>(), decode_depth<FMT, true>(),
+                 decode_max_waves<FMT, true>()>(mats, perm, rows, cols, ksplit, xp, nullptr,
+                                                out_xp, epi, status, pieces_lds, blockIdx.x,
+                                                blockIdx.y);
+}
+
+template <int FMT, int EPL, int MODE>
+static void launch_route_gate_up_as(const ExpertMats* mats, int H, int I, const uint16_t* xp,
+                                    uint16_t* act_xp, Epi epi, int* status, hipStream_t s, int E,
+                                    const RouteJob& job) {
+  const GemvShape g = gemv_mfma_shape<FMT, true>(I, H, job.K);
+  gemv_route_gate_up_kernel<FMT, EPL, MODE><<<g.grid, 64 * g.waves, g.lds, s>>>(
+      mats, I, H, g.ksplit, xp, act_xp, epi, status, job, E);
+}
+
+template <int FMT, int EPL>
+static void launch_route_gate_up_epl(const ExpertMats* mats, int H, int I, const uint16_t* xp,
+                                     uint16_t* act_xp, Epi epi, int* status, hipStream_t s, int E,
+                                     const RouteJob& job) {
+  if (job.rp.router == 0)
+    launch_route_gate_up_as<FMT, EPL, 0>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+  else if (job.rp.router == 1)
+    launch_route_gate_up_as<FMT, EPL, 1>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+  else
+    launch_route_gate_up_as<FMT, EPL, 2>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+}
+
+template <int FMT>
+static void launch_route_gate_up_fmt(const ExpertMats* mats, int H, int I, const uint16_t* xp,
+                                     uint16_t* act_xp, Epi epi, int* status, hipStream_t s, int E,
+                                     const RouteJob& job) {
+  if (E <= 128)
+    launch_route_gate_up_epl<FMT, 2>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+  else if (E <= 256)
+    launch_route_gate_up_epl<FMT, 4>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+  else
+    launch_route_gate_up_epl<FMT, 8>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+}
+
+bool launch_routed_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
+                                 const uint16_t* xp, uint16_t* act_xp, Epi epi, int* status,
+                                 hipStream_t s, int E, const RouteJob& job) {
+  if (job.K > kRouteMaxK) return false;
+  if (fmt == kFmtBF16)
+    launch_route_gate_up_fmt<kFmtBF16>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+  else if (fmt == kFmtMXFP4)
+    launch_route_gate_up_fmt<kFmtMXFP4>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+  else
+    launch_route_gate_up_fmt<kFmtMXFP8>(mats, H, I, xp, act_xp, epi, status, s, E, job);
+  return true;
 }
 
 // ------------------------------------------------------------------------------------------
