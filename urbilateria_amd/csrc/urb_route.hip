@@ -708,7 +708,8 @@ void launch_shared_gate_up_route(int fmt, const ExpertMats* mats, int H, int I,
 // the same routes -- and the GEMV then reads its slot's expert from LDS.  Workgroup (0, 0)
 // also writes the routes, and a sliced router's logits, for the down + combine launch.  Each
 // workgroup spends one routing (its logits read and top-k) before its first weight load; the
-// routing kernel and its launch are gone.
+// routing kernel and its launch are gone.  The host uses it after routers that write f32
+// logits: reading a sliced router's f64 partials in every workgroup costs more than the launch.
 // ------------------------------------------------------------------------------------------
 constexpr int kRouteMaxK = 32;
 
