@@ -298,6 +298,30 @@ def test_small_layer_matches_oracle(name, T):
     layer.close()
 
 
+# top_k at its extremes: one expert; 16, the most the fused one-token down + combine takes (one
+# wave per slot); 32, the header's limit (per-slot down projections, then the combine kernel).
+# At T = 1 (the one-token launches) and T = 40 (the grouped GEMMs).
+TOPK = [(name, k, T) for name in ("c1_bf16_decode", "c3_mxfp4_decode", "c4_mxfp8")
+        for k in (1, 16, 32) for T in (1, 40)]
+
+
+@pytest.mark.parametrize("name,k,T", TOPK)
+def test_top_k_extremes_match_oracle(name, k, T):
+    w = C.workload(name)
+    spec = C.small_spec(w.spec, hidden=256, n_experts=64, intermediate=128, top_k=k)
+    bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.05) if w.zipf_s else None
+    host = C.make_host_layer(spec, bias=bias)
+    x = synth.activations(f"x.topk.{k}.{T}", T, spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y, ids, wts = layer.forward(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+    err = rel_l2(y.cpu().numpy(), ref.output)
+    assert err < REL_L2_BAR, err
+    assert np.allclose(wts.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    layer.close()
+
+
 @pytest.mark.parametrize("name", list(C.WORKLOADS))
 def test_router_logits_match_oracle(name):
     host = _small_layer(name, hidden=512, n_experts=64)
