@@ -322,6 +322,33 @@ def test_top_k_extremes_match_oracle(name, k, T):
     layer.close()
 
 
+# The header's largest geometry, one dimension at a time: 512 experts (the routing's lane
+# slots, group-limited for c3), hidden 12288 (the one-token kernels stage 48 KiB of input
+# pieces per workgroup), intermediate 12288 (past the fused down + combine's 96 KiB of SwiGLU
+# rows: per-slot down projections, then the combine kernel).
+LARGEST = [(name, dims, T) for name in ("c1_bf16_decode", "c3_mxfp4_decode", "c4_mxfp8")
+           for dims in ((512, 256, 128), (16, 12288, 128), (16, 256, 12288)) for T in (1, 3)]
+
+
+@pytest.mark.parametrize("name,dims,T", LARGEST,
+                         ids=[f"{n}-E{d[0]}-H{d[1]}-I{d[2]}-T{t}" for n, d, t in LARGEST])
+def test_largest_geometry_matches_oracle(name, dims, T):
+    E, H, I = dims
+    w = C.workload(name)
+    spec = C.small_spec(w.spec, hidden=H, n_experts=E, intermediate=I)
+    bias = C.zipf_bias(spec.n_experts, w.zipf_s, 0.05) if w.zipf_s else None
+    host = C.make_host_layer(spec, bias=bias)
+    x = synth.activations(f"x.largest.{E}.{H}.{I}.{T}", T, spec.hidden)
+    layer = moe_mod().MoeLayer(host, max_tokens=T)
+    y, ids, wts = layer.forward(torch.from_numpy(x).cuda())
+    ref = _oracle(host, x)
+    assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+    err = rel_l2(y.cpu().numpy(), ref.output)
+    assert err < REL_L2_BAR, err
+    assert np.allclose(wts.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
+    layer.close()
+
+
 @pytest.mark.parametrize("name", list(C.WORKLOADS))
 def test_router_logits_match_oracle(name):
     host = _small_layer(name, hidden=512, n_experts=64)
