@@ -298,10 +298,12 @@ def test_small_layer_matches_oracle(name, T):
     layer.close()
 
 
-# top_k at its extremes: one expert; 16, the most the fused one-token down + combine takes (one
-# wave per slot); 32, the header's limit (per-slot down projections, then the combine kernel).
-# At T = 1 (the one-token launches) and T = 40 (the grouped GEMMs).
-TOPK = [(name, k, T) for name in ("c1_bf16_decode", "c3_mxfp4_decode", "c4_mxfp8")
+# top_k at its extremes (plain, MX-activation and gated-shared-expert compositions): one
+# expert; 16, the most the fused one-token down + combine takes (one wave per slot); 32, the
+# header's limit (per-slot down projections, then the combine kernel).  At T = 1 (the one-token
+# launches) and T = 40 (the grouped GEMMs).
+TOPK = [(name, k, T) for name in ("c1_bf16_decode", "c3_mxfp4_decode", "c4_mxfp8",
+                                  "c4_mxfp8_mx_activation", "c5_mxfp4_dsv41", "qwen36_release")
         for k in (1, 16, 32) for T in (1, 40)]
 
 
