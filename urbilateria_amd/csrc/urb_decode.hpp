@@ -46,11 +46,16 @@ constexpr int kDecodeMaxWaves = 16;
 // A workgroup of W waves (blockDim.x / 64) is W / KSPLIT groups of NP consecutive 16-row panels
 // times KSPLIT parts of K, for one slot (`by`), workgroup `bx` of the slot's panel
 // groups.  xs (LDS): the slot's input pieces, cols / 8 units of 32 B.
-template <int FMT, bool PAIR, int NP, int DW, int WMAX>
+// HALF (gate+up, one panel): a group is half a panel pair -- 8 gate rows and the same 8 up rows
+// in one 16-column MFMA operand (lanes ln < 8 read the gate panel, ln >= 8 the up panel) -- so
+// a matrix of R rows offers R / 8 groups instead of R / 16: twice the workgroups for a dense
+// matrix whose R / 16 workgroups would leave half the CUs idle.
+template <int FMT, bool PAIR, int NP, int DW, int WMAX, bool HALF = false>
 __device__ __forceinline__ void gemv_mfma_body(
     const ExpertMats* __restrict__ mats, const Perm& perm, int rows, int cols, int ksplit,
     const uint16_t* __restrict__ xp, float* __restrict__ out, uint16_t* __restrict__ out_xp,
     Epi epi, int* status, uint4* xs, int bx, int by) {
+  static_assert(!HALF || (PAIR && NP == 1), "half panel pairs: gate+up, one panel per wave");
   __shared__ float red[WMAX][NP][16][2];
   int expert, pos;
   if (!decode_slot(perm, by, expert, pos)) return;
@@ -60,7 +65,9 @@ __device__ __forceinline__ void gemv_mfma_body(
   const int ln = lane & 15, lq = lane >> 4, piece = ln & 1;
   const int part = wave % ksplit;
   const int groups = (int)(blockDim.x >> 6) / ksplit;  // panel groups per workgroup
-  const int panel0 = (bx * groups + wave / ksplit) * NP;
+  const int group = bx * groups + wave / ksplit;
+  const int panel0 = HALF ? group >> 1 : group * NP;
+  const int half = HALF ? group & 1 : 0;
   const bool valid = panel0 < rows / kPanelRows;
   const int steps = cols / kGemmKStep;
   const int s_begin = steps * part / ksplit, n = steps * (part + 1) / ksplit - s_begin;
@@ -71,11 +78,20 @@ __device__ __forceinline__ void gemv_mfma_body(
   const uint8_t* ps0 = FMT == kFmtBF16 ? nullptr : m.scales[PAIR ? 0 : 2] + pv * pscales;
   const uint8_t* pd1 = PAIR ? m.data[1] + pv * pbytes : nullptr;
   const uint8_t* ps1 = (PAIR && FMT != kFmtBF16) ? m.scales[1] + pv * pscales : nullptr;
-  const uint32_t doff = 16u * lane, soff = lane;
+  // HALF: lane (ln, lq) takes the panel lane holding row 8 half + ln % 8 at k-quad lq, from the
+  // gate panel (ln < 8) or the up panel (ln >= 8)
+  const int src = HALF ? lq * 16 + half * 8 + (ln & 7) : lane;
+  const uint32_t doff = 16u * src, soff = src;
+  const uint8_t* pdh = HALF && ln >= 8 ? pd1 : pd0;
+  const uint8_t* psh = HALF && ln >= 8 ? ps1 : ps0;
 
   constexpr int R = DW + 1;
   BRaw<FMT> r0[R][NP], r1[R][NP];
   auto fetch = [&](int slot, int s) {
+    if constexpr (HALF) {
+      load_b<FMT, true>(r0[slot][0], pdh, doff, psh, soff, s);
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
       load_b<FMT, true>(r0[slot][q], pd0 + q * pbytes, doff, ps0 + q * pscales, soff, s);
@@ -110,7 +126,7 @@ __device__ __forceinline__ void gemv_mfma_body(
           for (int q = 0; q < NP; ++q) {
             acc0[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, decode_b<FMT>(r0[d][q], j),
                                                               acc0[q], 0, 0, 0);
-            if constexpr (PAIR)
+            if constexpr (PAIR && !HALF)
               acc1[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, decode_b<FMT>(r1[d][q], j),
                                                                 acc1[q], 0, 0, 0);
           }
@@ -143,6 +159,18 @@ __device__ __forceinline__ void gemv_mfma_body(
           v1[q] += red[wave + z][q][ln][1];
         }
       }
+  }
+  if constexpr (HALF) {
+    // column ln < 8: gate row 8 half + ln; its up row is column ln + 8
+    const float up = __shfl_xor(v0[0], 8);
+    if (!valid || part != 0 || lq != 0 || ln >= 8) return;
+    bool bad = false;
+    const int r = panel0 * kPanelRows + half * 8 + ln;
+    const float v = epi_gate_up(epi, v0[0], up, bad);
+    if (out) out[(size_t)pos * rows + r] = v;
+    if (out_xp) store_piece_value(out_xp + (size_t)pos * (rows / 8) * kPieceUnit, r, v);
+    if (bad) flag(status, kStatusNonFinite);
+    return;
   }
   if (!valid || part != 0 || lq != 0) return;
   bool bad = false;

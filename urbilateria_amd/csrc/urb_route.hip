@@ -635,6 +635,9 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
 // workgroup waits for another; the routing's latency hides under the GEMV.  The routing
 // handles up to 64 * EPL experts.
 // ------------------------------------------------------------------------------------------
+template <int FMT>
+constexpr bool kSharedHalfPairs = FMT == kFmtBF16;
+
 template <int FMT, int EPL, int MODE>
 __global__ __launch_bounds__(64 * 8) void gemv_gate_up_route_kernel(
     const ExpertMats* __restrict__ mats, Perm perm, int rows, int cols, int ksplit,
@@ -650,10 +653,13 @@ __global__ __launch_bounds__(64 * 8) void gemv_gate_up_route_kernel(
                              status, sh, sh + kMaxExperts);
     return;
   }
-  gemv_mfma_body<FMT, true, decode_panels<FMT, true>(), decode_depth<FMT, true>(),
-                 decode_max_waves<FMT, true>()>(mats, perm, rows, cols, ksplit, xp, out, out_xp,
-                                                epi, status, pieces_lds, blockIdx.x,
-                                                blockIdx.y);
+  // BF16: half panel pairs, so a dense 2048-row gate+up offers 256 workgroups, one per CU
+  // (C3's 2 x 2048 x 7168 shared gate+up 16.3-17.6 -> 15.3-15.8 us).  The MX formats keep
+  // whole pairs: their steps are 1-2 KiB per panel, and halving them made DeepSeek-V4 Flash's
+  // MXFP4 shared gate+up 12.3 -> 13.7 us.
+  gemv_mfma_body<FMT, true, 1, decode_depth<FMT, true>(), decode_max_waves<FMT, true>(),
+                 kSharedHalfPairs<FMT>>(mats, perm, rows, cols, ksplit, xp, out, out_xp, epi,
+                                        status, pieces_lds, blockIdx.x, blockIdx.y);
 }
 
 template <int FMT, int EPL, int MODE>
@@ -661,7 +667,8 @@ static void launch_gate_up_route_as(const ExpertMats* mats, int H, int I, const 
                                     float* act, uint16_t* act_xp, Epi epi, int* status,
                                     hipStream_t s, int E, const RouteJob& job) {
   const Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
-  GemvShape g = gemv_mfma_shape<FMT, true>(I, H, 1);
+  // half panel pairs: 2 I / 16 groups
+  GemvShape g = gemv_mfma_shape<FMT, true>(kSharedHalfPairs<FMT> ? 2 * I : I, H, 1);
   g.grid.x += 1;
   g.lds = std::max(g.lds, (size_t)(kMaxExperts + 64) * sizeof(float));
   gemv_gate_up_route_kernel<FMT, EPL, MODE><<<g.grid, 64 * g.waves, g.lds, s>>>(
