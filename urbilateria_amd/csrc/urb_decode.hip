@@ -162,7 +162,10 @@ void launch_gemv_mfma_gate_up_and_shared_down(int fmt, const ExpertMats* mats, c
 // gate) are loaded while the weights stream, and the combine reads every slot before it adds:
 // with dependent loads per slot, the 16-thread tail cost ~1.3 us of a 14.5 us launch.
 // ------------------------------------------------------------------------------------------
-template <int FMT, int DW>
+// HALF: a workgroup owns 8 output rows (half a panel; lanes ln >= 8 load the same rows as
+// ln - 8, from the same cache lines, and their MFMA columns are dropped), so H / 8 workgroups
+// keep every CU streaming where H / 16 would not (hidden below 4096).
+template <int FMT, int DW, bool HALF>
 __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_kernel(
     const ExpertMats* __restrict__ mats, const int32_t* __restrict__ ids,
     const float* __restrict__ w, const int32_t* __restrict__ asc, int K, int H, int I, int ksplit,
@@ -181,8 +184,11 @@ __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_k
     wv = w[threadIdx.x];
     if (comp != 1) av = asc[threadIdx.x];
   }
-  if (threadIdx.x < 16) {
-    const int row = blockIdx.x * kPanelRows + threadIdx.x;
+  constexpr int kRows = HALF ? 8 : kPanelRows;  // output rows of this workgroup
+  const int panel = HALF ? blockIdx.x >> 1 : blockIdx.x;
+  const int row0 = panel * kPanelRows + (HALF ? (blockIdx.x & 1) * 8 : 0);
+  if (threadIdx.x < kRows) {
+    const int row = row0 + threadIdx.x;
     if (shared) sv = shared[row];
     if (residual) rv = residual[row];
     if (gate) gv = gate[0];
@@ -190,11 +196,12 @@ __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_k
   const int lane = threadIdx.x & 63;
   const int t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's task
   const int ln = lane & 15, lq = lane >> 4, piece = ln & 1;
-  const int panel = blockIdx.x;
   const int steps = I / kGemmKStep;
   const size_t pbytes = kPanelRows * panel_row_bytes<FMT>(I);
   const size_t pscales = (size_t)kPanelRows * (I / 32);
-  const uint32_t doff = 16u * lane, soff = lane;
+  // HALF: lane (ln, lq) takes the panel lane of row (row0 % 16) + ln % 8 at k-quad lq
+  const int src = HALF ? lq * 16 + (row0 & 15) + (ln & 7) : lane;
+  const uint32_t doff = 16u * src, soff = src;
   const int a = t / ksplit, z = t - a * ksplit;
   const int s_begin = steps * z / ksplit, n = steps * (z + 1) / ksplit - s_begin;
   const ExpertMats m = mats[ids[a]];
@@ -236,8 +243,8 @@ __global__ __launch_bounds__(64 * kDecodeMaxWaves) void gemv_mfma_down_combine_k
   }
   __syncthreads();
 
-  if (threadIdx.x < 16) {
-    const int row = panel * kPanelRows + threadIdx.x;
+  if (threadIdx.x < kRows) {
+    const int row = row0 + threadIdx.x;
     bool bad = false;
     // slot j's output and weight in combine order: ranking order (GLM) or ascending id
     float yv[kDecodeMaxWaves], wr[kDecodeMaxWaves];
@@ -316,7 +323,9 @@ bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_
   // one task per wave: split K while the workgroup stays within 16 waves, 2+ steps a part
   int ksplit = 1;
   while (K * ksplit * 2 <= kDecodeMaxWaves && steps / (2 * ksplit) >= 2) ksplit *= 2;
-  const dim3 grid(H / kPanelRows), block(64 * K * ksplit);
+  // half panels where whole ones leave CUs idle (C1 and Qwen3.6's H 2048: 128 -> 256)
+  const bool half = H / kPanelRows < 256;
+  const dim3 grid(half ? H / 8 : H / kPanelRows), block(64 * K * ksplit);
   const size_t lds = (size_t)K * I * 4;
   auto go = [&](auto kernel) {
     // dynamic LDS beyond 64 KiB must be allowed per kernel
@@ -325,9 +334,14 @@ bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_
     kernel<<<grid, block, lds, s>>>(mats, ids, weights, asc, K, H, I, ksplit, act_xp, shared,
                                     comp, epi, residual, gate, out, status);
   };
-  if (fmt == kFmtBF16) go(gemv_mfma_down_combine_kernel<kFmtBF16, decode_depth<kFmtBF16, false>()>);
-  else if (fmt == kFmtMXFP4) go(gemv_mfma_down_combine_kernel<kFmtMXFP4, decode_depth<kFmtMXFP4, false>()>);
-  else go(gemv_mfma_down_combine_kernel<kFmtMXFP8, decode_depth<kFmtMXFP8, false>()>);
+  auto pick = [&](auto fmtc) {
+    constexpr int F = decltype(fmtc)::value;
+    if (half) go(gemv_mfma_down_combine_kernel<F, decode_depth<F, false>(), true>);
+    else go(gemv_mfma_down_combine_kernel<F, decode_depth<F, false>(), false>);
+  };
+  if (fmt == kFmtBF16) pick(Int<kFmtBF16>{});
+  else if (fmt == kFmtMXFP4) pick(Int<kFmtMXFP4>{});
+  else pick(Int<kFmtMXFP8>{});
   return true;
 }
 
