@@ -155,8 +155,11 @@ struct RouteJob {
 
 // Router logits, the reference's 8-lane FP32 tree (BF16-rounded when round_bf16).
 // With `xp` (T = 1 only), the kernel also writes the token's BF16 piece vector there.
+// w8b / logits_b (optional): a one-row matrix in the same layout (Qwen3.6's shared-expert gate)
+// computed in the same launch below 64 tokens.
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
-                         int round_bf16, int* status, hipStream_t s, uint16_t* xp = nullptr);
+                         int round_bf16, int* status, hipStream_t s, uint16_t* xp = nullptr,
+                         const uint16_t* w8b = nullptr, float* logits_b = nullptr);
 
 // GLM router logits: MFMA BF16 with f64 accumulation of 32-k partials, split over K into
 // f64 partial slices.  The router weight is packed in the panel layout with router_rows(E)

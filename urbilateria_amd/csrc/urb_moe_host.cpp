@@ -521,7 +521,8 @@ void urb_moe_destroy(urb_moe_ctx* ctx) {
 // the router writes them).  `xp` (one token): the router also writes the token's piece vector.
 static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
                                             const uint32_t* tokens, int n, float* logits,
-                                            hipStream_t s, uint16_t* xp = nullptr) {
+                                            hipStream_t s, uint16_t* xp = nullptr,
+                                            float* gate_logit = nullptr) {
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
   const int E = (int)d.n_experts, H = (int)d.hidden;
@@ -530,8 +531,10 @@ static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
                       c->hash, tokens, c->hash_vocab};
   Span span(c, URB_STAGE_ROUTER, s);
   if (c->router_lane8) {
+    // gate_logit: the Qwen3.6 shared-expert gate row in the same launch
     urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status, s,
-                             n == 1 ? xp : nullptr);
+                             n == 1 ? xp : nullptr, gate_logit ? c->shared_gate8 : nullptr,
+                             gate_logit);
   } else if (n == 1) {
     // one token: a GEMV over the row-major router beats the 32-token MFMA tile
     rp.slices = urb::router_gemv_slices(E);
@@ -601,11 +604,11 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
     // stream (one token: see shared_stream), each shared projection in the launch of the
     // routed work beside it: the routing beside the shared gate+up, the routed gate+up beside
     // the shared down.
-    const urb::RouteParams rp = launch_router_chunk(c, xc, tokens, 1, ws.logits, s, ws.xp);
+    // QWEN36 (an 8-lane router): the gate logit's row runs in the router's launch
+    const urb::RouteParams rp = launch_router_chunk(c, xc, tokens, 1, ws.logits, s, ws.xp,
+                                                    qwen ? ws.gate_logit : nullptr);
     {
       Span span(c, URB_STAGE_SHARED_GATE_UP, s);
-      if (qwen)
-        urb::launch_router_lane8(c->shared_gate8, 1, H, xc, 1, ws.gate_logit, 1, ws.status, s);
       const urb::RouteJob job{ws.logits, K, rp, idc, wc, qwen ? ws.asc : nullptr};
       urb::launch_shared_gate_up_route(d.shared_format, c->shared_table, H, Is, ws.xp, nullptr,
                                        ws.shared_xp, epi, ws.status, s, E, job);

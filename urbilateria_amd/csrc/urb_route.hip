@@ -49,19 +49,28 @@ constexpr int kLane8Ring = 8;
 // WAVES waves per workgroup, wave w running the chains of expert group WAVES blockIdx.x + w:
 // the staged token row is shared by 8 WAVES experts.  RING chain batches are in flight per
 // lane.
+// `w8b` (optional): a second matrix of one row (Qwen3.6's shared-expert gate), run by one more
+// workgroup (the last along x) into logits_b, so that row needs no launch of its own.
 template <int kLane8Tokens, int WAVES = 1, int RING = kLane8Ring>
 __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
     const uint16_t* __restrict__ w8, int E, int H, const float* __restrict__ x, int T,
-    float* __restrict__ logits, int round_bf16, int* status, uint16_t* __restrict__ xp) {
+    float* __restrict__ logits, int round_bf16, int* status, uint16_t* __restrict__ xp,
+    const uint16_t* __restrict__ w8b = nullptr, float* __restrict__ logits_b = nullptr) {
   // [tok][8][H8 + 4] transposed chains: the pad of 4 floats puts the 8 chains of a column in
   // different LDS banks and keeps 16-byte alignment.  H is a multiple of 128.
   extern __shared__ float xs[];
+  const bool second = w8b && blockIdx.x == gridDim.x - 1;
+  if (second) {
+    w8 = w8b;
+    E = 1;
+    logits = logits_b;
+  }
   const int H8 = H / 8, H8p = H8 + 4;
   const int t0 = blockIdx.y * kLane8Tokens;
   const int nt = min(kLane8Tokens, T - t0);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int el = lane >> 3, j = lane & 7;
-  const int g = blockIdx.x * WAVES + wave;
+  const int g = (second ? 0 : blockIdx.x) * WAVES + wave;
   const bool live = g < (E + 7) / 8;
   const int e = g * 8 + el;
   const uint16_t* chains = w8 + (size_t)(live ? g : 0) * 8 * H + 8 * lane;
@@ -1067,14 +1076,20 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 }
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
-                         int round_bf16, int* status, hipStream_t s, uint16_t* xp) {
+                         int round_bf16, int* status, hipStream_t s, uint16_t* xp,
+                         const uint16_t* w8b, float* logits_b) {
   const size_t per_tok = (size_t)8 * (H / 8 + 4) * sizeof(float);
   if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
-    router_lane8_kernel<1><<<dim3((E + 7) / 8, T), 64, per_tok, s>>>(w8, E, H, x, T, logits,
-                                                                     round_bf16, status, xp);
+    const int gx = (E + 7) / 8 + (w8b ? 1 : 0);
+    router_lane8_kernel<1><<<dim3(gx, T), 64, per_tok, s>>>(w8, E, H, x, T, logits, round_bf16,
+                                                            status, xp, w8b, logits_b);
     return;
+  }
+  if (w8b) {
+    // batches: the one-row matrix as a launch of its own
+    launch_router_lane8(w8b, 1, H, x, T, logits_b, round_bf16, status, s);
   }
   // ... from 64 tokens four waves share one staged token row (32 experts' chains per
   // workgroup; measured on MI355X at 128 tokens x 128 experts x 2048, 13.8 us with 64-thread
