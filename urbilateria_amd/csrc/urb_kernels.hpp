@@ -157,9 +157,11 @@ struct RouteJob {
 // With `xp` (T = 1 only), the kernel also writes the token's BF16 piece vector there.
 // w8b / logits_b (optional): a one-row matrix in the same layout (Qwen3.6's shared-expert gate)
 // computed in the same launch below 64 tokens.
+// xq: the token's piece vector (xp, one token) as the hi/lo split of x (0) or as
+// simulate_e4m3_activation in blocks of xq = 32 or 128 values (the MX-activation compositions).
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int round_bf16, int* status, hipStream_t s, uint16_t* xp = nullptr,
-                         const uint16_t* w8b = nullptr, float* logits_b = nullptr);
+                         const uint16_t* w8b = nullptr, float* logits_b = nullptr, int xq = 0);
 
 // GLM router logits: MFMA BF16 with f64 accumulation of 32-k partials, split over K into
 // f64 partial slices.  The router weight is packed in the panel layout with router_rows(E)
@@ -173,7 +175,8 @@ void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, 
 // (router_gemv_slices(E) slices, exact products summed in f64).
 int router_gemv_slices(int E);
 void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, double* part,
-                            int slices, int* status, hipStream_t s, uint16_t* xp = nullptr);
+                            int slices, int* status, hipStream_t s, uint16_t* xp = nullptr,
+                            int xq = 0);
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s);
 // Top-k routing, one wavefront per token (logits is an output when p.part is set).
 void launch_route(float* logits, int T, int E, int K, const RouteParams& p, int32_t* ids,

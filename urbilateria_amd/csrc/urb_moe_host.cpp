@@ -522,7 +522,7 @@ void urb_moe_destroy(urb_moe_ctx* ctx) {
 static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
                                             const uint32_t* tokens, int n, float* logits,
                                             hipStream_t s, uint16_t* xp = nullptr,
-                                            float* gate_logit = nullptr) {
+                                            float* gate_logit = nullptr, int xq = 0) {
   const urb_moe_desc& d = c->desc;
   const bool qwen = d.composition == URB_COMPOSE_QWEN36;
   const int E = (int)d.n_experts, H = (int)d.hidden;
@@ -534,13 +534,13 @@ static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
     // gate_logit: the Qwen3.6 shared-expert gate row in the same launch
     urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status, s,
                              n == 1 ? xp : nullptr, gate_logit ? c->shared_gate8 : nullptr,
-                             gate_logit);
+                             gate_logit, xq);
   } else if (n == 1) {
     // one token: a GEMV over the row-major router beats the 32-token MFMA tile
     rp.slices = urb::router_gemv_slices(E);
     rp.part = c->ws.router_part;
     urb::launch_router_gemv_f64(c->router, E, H, x, c->ws.router_part, rp.slices, c->ws.status,
-                                s, xp);
+                                s, xp, xq);
   } else {
     rp.slices = urb::router_slices(E, H, n);
     rp.part = c->ws.router_part;
@@ -554,9 +554,9 @@ static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
 // vector.
 static urb_status route_chunk(urb_moe_ctx* c, const float* x, const uint32_t* tokens, int n,
                               float* logits, int32_t* ids, float* weights, hipStream_t s,
-                              uint16_t* xp = nullptr) {
+                              uint16_t* xp = nullptr, int xq = 0) {
   const urb_moe_desc& d = c->desc;
-  const urb::RouteParams rp = launch_router_chunk(c, x, tokens, n, logits, s, xp);
+  const urb::RouteParams rp = launch_router_chunk(c, x, tokens, n, logits, s, xp, nullptr, xq);
   Span span(c, URB_STAGE_ROUTE, s);
   const bool ascending = d.composition != URB_COMPOSE_GLM;
   urb::launch_route(logits, n, (int)d.n_experts, (int)d.top_k, rp, ids, weights,
@@ -681,8 +681,15 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
   const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
   const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
-  urb::launch_quantize(xc, 1, (size_t)H, nullptr, nullptr, nullptr, ws.status, s, 0, nullptr,
-                       nullptr, block, ws.xp);
+  // The token's quantized pieces: a side job of the f64 GEMV router's launch (DeepSeek-V4 T=1
+  // 41.7 -> 40.0 us, Hy4 on C4 68.7 -> 67.7 us).  Beside the 8-lane router (DeepSeek-V4.1) they
+  // keep a launch of their own: that router's 48 workgroups at E 384 took 2.5 us longer with
+  // the 7168 values to quantize than the quantize launch costs.
+  const int xq = c->router_lane8 ? 0 : block;
+  uint16_t* rxp = xq ? ws.xp : nullptr;
+  if (!xq)
+    urb::launch_quantize(xc, 1, (size_t)H, nullptr, nullptr, nullptr, ws.status, s, 0, nullptr,
+                         nullptr, block, ws.xp);
   Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, idc, K};
   // Hy4 re-quantizes the SwiGLU output (expert.rs:677); DeepSeek first scales each row by its
   // route weight and rounds to BF16 (runtime.rs:2254-2258); one token: slot = row
@@ -694,7 +701,8 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
     // In line on the caller's stream (one token: see shared_stream), each shared projection in
     // the launch of the routed work beside it: the routing beside the shared gate+up, the
     // routed gate+up beside the shared down.
-    const urb::RouteParams rp = launch_router_chunk(c, xc, tokens, 1, ws.logits, s);
+    const urb::RouteParams rp =
+        launch_router_chunk(c, xc, tokens, 1, ws.logits, s, rxp, nullptr, xq);
     {
       Span span(c, URB_STAGE_SHARED_GATE_UP, s);
       const urb::RouteJob job{ws.logits, K, rp, idc, wc, ws.asc};
@@ -711,7 +719,7 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
                                                   ws.status, s);
     quantize_act();
   } else {
-    route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s);
+    route_chunk(c, xc, tokens, 1, ws.logits, idc, wc, s, rxp, xq);
     Span span(c, URB_STAGE_GATE_UP, s);
     urb::launch_gemv_mfma_gate_up(d.expert_format, c->table, perm, std::min(E, K), H, I, ws.xp,
                                   ws.act, nullptr, routed, ws.status, s);

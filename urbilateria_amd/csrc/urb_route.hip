@@ -3,10 +3,33 @@
 #include "urb_device.hpp"
 #include "urb_kernels.hpp"
 #include "urb_panel.hpp"
+#include "urb_quant.hpp"
 
 #include <algorithm>
 
 namespace urb {
+
+// A token's piece vector, written as a side job of a one-token router launch by lanes gtid,
+// gtid + stride, ... of its grid: the hi/lo BF16 split of x (xq = 0), or for the MX-activation
+// compositions simulate_e4m3_activation of x in blocks of xq = 32 or 128 values (pieces with
+// a zero low half), which then needs no launch of its own.  stride is a multiple of 64 and
+// gtid % 64 the lane, so a block's 32 lanes are one half wavefront, as the quantizer needs.
+__device__ __forceinline__ void token_pieces(const float* __restrict__ x, int H, uint16_t* xp,
+                                             int xq, int* status, size_t gtid, size_t stride) {
+  if (xq == 0) {
+    split_vector(x, H / 8, xp, gtid, stride);
+    return;
+  }
+  const size_t nblocks = (size_t)H / xq;
+  for (size_t g = gtid; g < nblocks * 32; g += stride) {
+    if (xq == 128)
+      quantize_lanes<4>(x, nblocks, H, nullptr, nullptr, nullptr, status, 0, nullptr, nullptr,
+                        xp, g);
+    else
+      quantize_lanes<1>(x, nblocks, H, nullptr, nullptr, nullptr, status, 0, nullptr, nullptr,
+                        xp, g);
+  }
+}
 
 // ------------------------------------------------------------------------------------------
 // Qwen router: `linear(router)` = Bf16Matrix::matvec_fp32 + BF16 (src/models/qwen3_8/math.rs:
@@ -55,7 +78,8 @@ template <int kLane8Tokens, int WAVES = 1, int RING = kLane8Ring>
 __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
     const uint16_t* __restrict__ w8, int E, int H, const float* __restrict__ x, int T,
     float* __restrict__ logits, int round_bf16, int* status, uint16_t* __restrict__ xp,
-    const uint16_t* __restrict__ w8b = nullptr, float* __restrict__ logits_b = nullptr) {
+    const uint16_t* __restrict__ w8b = nullptr, float* __restrict__ logits_b = nullptr,
+    int xq = 0) {
   // [tok][8][H8 + 4] transposed chains: the pad of 4 floats puts the 8 chains of a column in
   // different LDS banks and keeps 16-byte alignment.  H is a multiple of 128.
   extern __shared__ float xs[];
@@ -99,9 +123,10 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
     }
   }
   if (bad) flag(status, kStatusNonFinite);
-  // one token: the workgroups also write its BF16 piece vector (the decode GEMVs' input)
+  // one token: the workgroups also write its piece vector (the decode GEMVs' input)
   if (xp && T == 1)
-    split_vector(x, H / 8, xp, blockIdx.x * blockDim.x + threadIdx.x, gridDim.x * blockDim.x);
+    token_pieces(x, H, xp, xq, status, blockIdx.x * blockDim.x + threadIdx.x,
+                 gridDim.x * blockDim.x);
   __syncthreads();
   if (!live) return;
   float acc[kLane8Tokens];
@@ -1018,7 +1043,8 @@ __global__ __launch_bounds__(64) void router_gemv_f64_kernel(const uint16_t* __r
                                                              int units_per_slice,
                                                              double* __restrict__ part,
                                                              int* status,
-                                                             uint16_t* __restrict__ xp) {
+                                                             uint16_t* __restrict__ xp,
+                                                             int xq) {
   const int e = blockIdx.x, z = blockIdx.y, lane = threadIdx.x;
   const int units = H / 8;
   const int u0 = z * units_per_slice, u1 = min(units, u0 + units_per_slice);
@@ -1042,9 +1068,9 @@ __global__ __launch_bounds__(64) void router_gemv_f64_kernel(const uint16_t* __r
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
   if (lane == 0) part[(size_t)z * router_rows(E) + e] = acc;
-  // the token's BF16 piece vector (the decode GEMVs' input), spread over the workgroups
+  // the token's piece vector (the decode GEMVs' input), spread over the workgroups
   if (xp)
-    split_vector(x, units, xp, (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane,
+    token_pieces(x, H, xp, xq, status, (blockIdx.y * gridDim.x + blockIdx.x) * 64 + lane,
                  gridDim.x * gridDim.y * 64);
 }
 
@@ -1054,10 +1080,10 @@ int router_gemv_slices(int E) {
 }
 
 void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, double* part,
-                            int slices, int* status, hipStream_t s, uint16_t* xp) {
+                            int slices, int* status, hipStream_t s, uint16_t* xp, int xq) {
   const int units = H / 8;
   const int per = (units + slices - 1) / slices;
-  router_gemv_f64_kernel<<<dim3(E, slices), 64, 0, s>>>(w, E, H, x, per, part, status, xp);
+  router_gemv_f64_kernel<<<dim3(E, slices), 64, 0, s>>>(w, E, H, x, per, part, status, xp, xq);
 }
 
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
@@ -1077,14 +1103,14 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int round_bf16, int* status, hipStream_t s, uint16_t* xp,
-                         const uint16_t* w8b, float* logits_b) {
+                         const uint16_t* w8b, float* logits_b, int xq) {
   const size_t per_tok = (size_t)8 * (H / 8 + 4) * sizeof(float);
   if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
     const int gx = (E + 7) / 8 + (w8b ? 1 : 0);
     router_lane8_kernel<1><<<dim3(gx, T), 64, per_tok, s>>>(w8, E, H, x, T, logits, round_bf16,
-                                                            status, xp, w8b, logits_b);
+                                                            status, xp, w8b, logits_b, xq);
     return;
   }
   if (w8b) {
