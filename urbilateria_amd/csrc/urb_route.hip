@@ -669,8 +669,11 @@ __global__ __launch_bounds__(256) void route_kernel(float* __restrict__ logits, 
 // workgroup waits for another; the routing's latency hides under the GEMV.  The routing
 // handles up to 64 * EPL experts.
 // ------------------------------------------------------------------------------------------
+// One-token BF16 gate+up GEMVs (the shared expert's, and the routed one that routes in every
+// workgroup) run as half panel pairs: twice the workgroups, for matrices whose whole pairs
+// would leave CUs idle or unevenly loaded.
 template <int FMT>
-constexpr bool kSharedHalfPairs = FMT == kFmtBF16;
+constexpr bool kHalfPairs = FMT == kFmtBF16;
 
 template <int FMT, int EPL, int MODE>
 __global__ __launch_bounds__(64 * 8) void gemv_gate_up_route_kernel(
@@ -692,7 +695,7 @@ __global__ __launch_bounds__(64 * 8) void gemv_gate_up_route_kernel(
   // whole pairs: their steps are 1-2 KiB per panel, and halving them made DeepSeek-V4 Flash's
   // MXFP4 shared gate+up 12.3 -> 13.7 us.
   gemv_mfma_body<FMT, true, 1, decode_depth<FMT, true>(), decode_max_waves<FMT, true>(),
-                 kSharedHalfPairs<FMT>>(mats, perm, rows, cols, ksplit, xp, out, out_xp, epi,
+                 kHalfPairs<FMT>>(mats, perm, rows, cols, ksplit, xp, out, out_xp, epi,
                                         status, pieces_lds, blockIdx.x, blockIdx.y);
 }
 
@@ -702,7 +705,7 @@ static void launch_gate_up_route_as(const ExpertMats* mats, int H, int I, const 
                                     hipStream_t s, int E, const RouteJob& job) {
   const Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, 1, nullptr, nullptr, 0};
   // half panel pairs: 2 I / 16 groups
-  GemvShape g = gemv_mfma_shape<FMT, true>(kSharedHalfPairs<FMT> ? 2 * I : I, H, 1);
+  GemvShape g = gemv_mfma_shape<FMT, true>(kHalfPairs<FMT> ? 2 * I : I, H, 1);
   g.grid.x += 1;
   g.lds = std::max(g.lds, (size_t)(kMaxExperts + 64) * sizeof(float));
   gemv_gate_up_route_kernel<FMT, EPL, MODE><<<g.grid, 64 * g.waves, g.lds, s>>>(
@@ -777,17 +780,16 @@ __global__ __launch_bounds__(64 * 8) void gemv_route_gate_up_kernel(
   }
   __syncthreads();
   const Perm perm{nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr, ids_l, job.K};
-  gemv_mfma_body<FMT, true, decode_panels<FMT, true>(), decode_depth<FMT, true>(),
-                 decode_max_waves<FMT, true>()>(mats, perm, rows, cols, ksplit, xp, nullptr,
-                                                out_xp, epi, status, pieces_lds, blockIdx.x,
-                                                blockIdx.y);
+  gemv_mfma_body<FMT, true, 1, decode_depth<FMT, true>(), decode_max_waves<FMT, true>(),
+                 kHalfPairs<FMT>>(mats, perm, rows, cols, ksplit, xp, nullptr, out_xp, epi,
+                                        status, pieces_lds, blockIdx.x, blockIdx.y);
 }
 
 template <int FMT, int EPL, int MODE>
 static void launch_route_gate_up_as(const ExpertMats* mats, int H, int I, const uint16_t* xp,
                                     uint16_t* act_xp, Epi epi, int* status, hipStream_t s, int E,
                                     const RouteJob& job) {
-  const GemvShape g = gemv_mfma_shape<FMT, true>(I, H, job.K);
+  const GemvShape g = gemv_mfma_shape<FMT, true>(kHalfPairs<FMT> ? 2 * I : I, H, job.K);
   gemv_route_gate_up_kernel<FMT, EPL, MODE><<<g.grid, 64 * g.waves, g.lds, s>>>(
       mats, I, H, g.ksplit, xp, act_xp, epi, status, job, E);
 }
