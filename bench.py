@@ -30,7 +30,8 @@ MFMA_PEAK = {"bf16": 2.5e15, "fp8": 5.0e15, "fp4": 10.1e15}  # dense FLOP/s
 HEADLINE = ("c5_mxfp4_zipf_prefill", 1024)
 RUNS = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
         ("c3_mxfp4_decode", 32), ("c4_mxfp8", 1), ("c4_mxfp8", 512),
-        ("c5_mxfp4_zipf_prefill", 1024), ("c5_mxfp4_zipf_hot", 1024)]
+        ("c5_mxfp4_zipf_prefill", 1024), ("c5_mxfp4_zipf_flat", 1024),
+        ("c5_mxfp4_zipf_hot", 1024)]
 # the projection stages a roofline block may name (routing kernels are latency-bound)
 # The routed projections run on the caller's stream, on the critical path of the call; the
 # shared expert's run beside them on a side stream (batches), where their spans include the
@@ -282,7 +283,7 @@ def run_one(name, T, args, want_cpu, cpu_budget):
 
     w = C.workload(name)
     spec = w.spec
-    beta, bias = C.workload_bias(w)
+    zipf, bias = C.workload_bias(w)
     table = tok = None
     if w.hash_vocab:
         from urbilateria_amd import synth
@@ -364,8 +365,8 @@ def run_one(name, T, args, want_cpu, cpu_budget):
         "distinct_experts": distinct, "max_tokens_per_expert": int(counts.max()),
         "layer_copies_rotated": copies, "stages": stage_rows, "dominant_stage": dom,
     }
-    if w.zipf_s:
-        rec["zipf_bias_beta"] = float(beta)
+    if zipf:
+        rec["zipf_bias"] = zipf
     rec["roofline"] = roofline_block(rec, spec, C, name, T)
     cpu_job = None
     if want_cpu:

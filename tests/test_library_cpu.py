@@ -145,6 +145,65 @@ def test_zipf_bias_is_monotone_in_rank():
     assert len(np.unique(b)) == 384
 
 
+def _inclusion_by_enumeration(p, k):
+    """Inclusion probabilities of successive sampling by summing every ordered k-draw."""
+    import itertools
+    p = np.asarray(p, np.float64) / np.sum(p)
+    pi = np.zeros(len(p))
+    for seq in itertools.permutations(range(len(p)), k):
+        pr, rest = 1.0, 1.0
+        for e in seq:
+            pr *= p[e] / rest
+            rest -= p[e]
+        pi[list(seq)] += pr
+    return pi
+
+
+@pytest.mark.parametrize("E,k", [(5, 1), (5, 2), (6, 3), (7, 4), (4, 4)])
+def test_zipf_inclusion_equals_enumeration(E, k):
+    # brute force over all ordered draws; k = 1 is p itself, k = E is all ones
+    p = np.linspace(1.0, 0.05, E) ** 3
+    got = C.zipf_inclusion(p, k)
+    ref = _inclusion_by_enumeration(p, k)
+    assert np.allclose(got, ref, atol=1e-6), (got, ref)
+    assert abs(got.sum() - k) < 1e-5
+    if k == 1:
+        assert np.allclose(got, p / p.sum(), atol=1e-6)
+
+
+def test_selection_bias_fit_meets_its_targets():
+    # i.i.d. U(0, 1) scores over 12 experts, top-3: the fitted bias must reproduce any
+    # feasible marginals, here a geometric popularity profile
+    u = synth.unit_f64(synth.splitmix64(synth.stream_seed("test.fit"), 0, 4000 * 12))
+    scores = u.reshape(4000, 12)
+    pi = C.zipf_inclusion(0.7 ** np.arange(12), 3)
+    bias, counts = C.fit_selection_bias(scores, 3, 4000 * pi)
+    assert counts.sum() == 4000 * 3
+    assert np.abs(counts - 4000 * pi).max() <= 3, (counts, 4000 * pi)
+    # the counts are the top-3 of the biased scores
+    top = np.argsort(-(scores + bias[None, :]), axis=1, kind="stable")[:, :3]
+    assert np.array_equal(np.bincount(top.ravel(), minlength=12), counts)
+    assert np.all(np.diff(bias[np.argsort(-pi)]) <= 1e-9)  # more popular, larger bias
+
+
+def test_c5_bias_gives_zipf_top8_marginals():
+    # the headline's per-expert bias: the hottest expert at its inclusion probability under
+    # Zipf(1.1) top-8 without replacement (0.854), on the calibration draw and on the
+    # benchmark's own 1024 tokens through the seeded router
+    w = C.workload("c5_mxfp4_zipf_prefill")
+    info, bias = C.workload_bias(w)
+    assert info["fit"] == "marginals" and abs(info["target_top_share"] - 0.8544) < 1e-3
+    assert info["max_abs_count_error"] <= 8
+    spec = w.spec
+    router = synth.bf16_to_f32(synth.bf16_matrix("router", spec.n_experts, spec.hidden, 0.02))
+    x = synth.activations("x", 1024, spec.hidden)
+    g = C.router_scores(spec.router, (x.astype(np.float64) @ router.T.astype(np.float64)))
+    top = np.argpartition(-(g + bias[None, :]), spec.top_k - 1, axis=1)[:, :spec.top_k]
+    counts = np.bincount(top.ravel(), minlength=spec.n_experts)
+    assert 800 <= counts.max() <= 900 and (counts > 0).sum() >= 360, (counts.max(),
+                                                                      (counts > 0).sum())
+
+
 @pytest.mark.parametrize("fmt", [C.FMT_BF16, C.FMT_MXFP4, C.FMT_MXFP8])
 def test_expert_views_slice_consolidated_tensors(fmt):
     # urb_expert_views only computes addresses, so host tensors stand in for device ones.  The

@@ -33,17 +33,33 @@ def _hipcc() -> str:
     return "hipcc"
 
 
-def _compile(sources, out, verbose=False):
-    srcs = [os.path.join(CSRC, s) for s in sources if os.path.exists(os.path.join(CSRC, s))]
-    tmp = out + ".tmp"
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-o", tmp, *srcs]
+def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed ({' '.join(cmd)}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+    return err
+
+
+def _compile(sources, out, verbose=False):
+    """Each source to an object in parallel (one hipcc per file), then one link."""
+    from concurrent.futures import ThreadPoolExecutor
+    srcs = [os.path.join(CSRC, s) for s in sources if os.path.exists(os.path.join(CSRC, s))]
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    objs = [os.path.join(objdir, os.path.basename(s) + ".o") for s in srcs]
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", "0") or 0) or os.cpu_count() or 1))
+    with ThreadPoolExecutor(jobs) as pool:
+        errs = list(pool.map(lambda so: _run([_hipcc(), *flags, "-c", "-o", so[1], so[0]]),
+                             zip(srcs, objs)))
+    tmp = out + ".tmp"
+    errs.append(_run([_hipcc(), *HIPCC_FLAGS, "-o", tmp, *objs]))
+    if verbose:
+        for e in errs:
+            if e.strip():
+                print(e, file=sys.stderr)
     os.replace(tmp, out)
 
 

@@ -98,8 +98,15 @@ class Workload:
     zipf_s: Optional[float] = None
     description: str = ""
     hash_vocab: int = 0   # > 0: routed by a synthetic tid2eid table of this many token ids
-    # > 0: the Zipf bias's beta is set so the hottest expert takes this share of the tokens,
-    # instead of by the log-log slope fit
+    # How the Zipf(zipf_s) correction bias is fitted (``workload_bias``):
+    #   "marginals"  one bias per expert, fitted so that each expert's selection frequency is its
+    #                inclusion probability in a top-k draw without replacement from the Zipf
+    #                popularity (the popularity model of a Zipf-skewed router);
+    #   "slope"      b_e = beta ln p_e, beta set so the log-log slope of selection frequency
+    #                against rank is -zipf_s;
+    #   "top_share"  b_e = beta ln p_e, beta set so the hottest expert takes zipf_top_share of
+    #                the tokens.
+    zipf_fit: str = "marginals"
     zipf_top_share: float = 0.0
 
 
@@ -138,22 +145,32 @@ WORKLOADS: Dict[str, Workload] = {
                   router=ROUTER_SIGMOID_NOAUX_TC, composition=COMPOSE_GLM, n_group=1,
                   topk_group=1, normalize=True, routed_scaling_factor=1.0),
         (1024,), zipf_s=1.1,
-        description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias I2048 + BF16 shared, "
+        description="MXFP4 H7168 E384 sigmoid top-8 with a per-expert bias giving Zipf(1.1) "
+                    "expert popularity (top-8 without replacement) I2048 + BF16 shared, "
                     "prefill 1024"),
-    # c5_mxfp4_zipf_prefill with the load imbalance the Zipf(1.1) popularity model predicts for
-    # top-8 selection
-    # without replacement: the hottest expert routed by ~850 of 1024 tokens.  (Fitting the
-    # log-log slope of the whole frequency curve, as c5_mxfp4_zipf_prefill does, lets the
-    # Gaussian tail of the logits dominate and gives a much flatter head.)
+    # The same layer with a one-parameter bias b_e = beta ln p_e.  "flat": beta fitted to the
+    # log-log slope of the whole frequency curve, where the Gaussian tail of the logits
+    # dominates and the head stays flat (hottest expert ~160 of 1024 tokens).  "hot": beta set
+    # so the hottest expert takes ~850 of 1024 tokens, which also concentrates the rest on ~55
+    # experts.
+    "c5_mxfp4_zipf_flat": Workload(
+        "c5_mxfp4_zipf_flat",
+        LayerSpec(hidden=7168, n_experts=384, top_k=8, intermediate=2048,
+                  shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_BF16,
+                  router=ROUTER_SIGMOID_NOAUX_TC, composition=COMPOSE_GLM, n_group=1,
+                  topk_group=1, normalize=True, routed_scaling_factor=1.0),
+        (1024,), zipf_s=1.1, zipf_fit="slope",
+        description="MXFP4 H7168 E384 sigmoid top-8 + single-beta Zipf(1.1) bias fitted to "
+                    "the frequency slope I2048 + BF16 shared, prefill 1024"),
     "c5_mxfp4_zipf_hot": Workload(
         "c5_mxfp4_zipf_hot",
         LayerSpec(hidden=7168, n_experts=384, top_k=8, intermediate=2048,
                   shared_intermediate=2048, expert_format=FMT_MXFP4, shared_format=FMT_BF16,
                   router=ROUTER_SIGMOID_NOAUX_TC, composition=COMPOSE_GLM, n_group=1,
                   topk_group=1, normalize=True, routed_scaling_factor=1.0),
-        (1024,), zipf_s=1.1, zipf_top_share=850.0 / 1024.0,
-        description="MXFP4 H7168 E384 sigmoid top-8 + Zipf(1.1) bias, hottest expert ~850 of "
-                    "1024 tokens, I2048 + BF16 shared, prefill 1024"),
+        (1024,), zipf_s=1.1, zipf_fit="top_share", zipf_top_share=850.0 / 1024.0,
+        description="MXFP4 H7168 E384 sigmoid top-8 + single-beta Zipf(1.1) bias, hottest "
+                    "expert ~850 of 1024 tokens, I2048 + BF16 shared, prefill 1024"),
 }
 
 # The MX-activation mode on the shapes of c4_mxfp8 and c5_mxfp4_zipf_prefill: Hy4's
@@ -359,23 +376,144 @@ def calibrate_zipf_beta(n_experts: int, top_k: int, s: float, logit_std: np.ndar
     return 0.5 * (lo + hi)
 
 
-_BIAS_CACHE: Dict[str, Tuple[float, np.ndarray]] = {}
+def zipf_popularity(n_experts: int, s: float,
+                    base_seed: int = synth.BASE_SEED) -> Tuple[np.ndarray, np.ndarray]:
+    """(rank [E], popularity p [E]): ranks 1..E from a seeded permutation of the expert ids,
+    p_e proportional to rank_e^-s, normalised."""
+    keys = synth.splitmix64(synth.stream_seed("zipf.rank", base_seed), 0, n_experts)
+    rank = np.empty(n_experts, np.int64)
+    rank[np.argsort(keys, kind="stable")] = np.arange(1, n_experts + 1)
+    p = rank.astype(np.float64) ** (-s)
+    return rank, p / p.sum()
 
 
-def workload_bias(w: Workload) -> Tuple[Optional[float], Optional[np.ndarray]]:
-    """(beta, correction bias [E]) of a Zipf workload, calibrated as the benchmark runs it
-    (None, None without a Zipf bias).  The logit std of a BF16 N(0, 0.02) router row on N(0, 1)
-    inputs is 0.02 sqrt(H)."""
+def zipf_inclusion(p: np.ndarray, top_k: int, points: int = 2000) -> np.ndarray:
+    """Inclusion probability of each item in a draw of top_k items without replacement, each
+    draw picking a remaining item with probability proportional to p (successive sampling).
+
+    Exact up to quadrature: with independent clocks X_f ~ Exp(p_f), the draw order is the
+    clock order, so pi_e = integral over t of P(fewer than top_k other clocks fired by t)
+    d(1 - exp(-p_e t)).  The count of other fired clocks is Poisson-binomial; its
+    distribution truncated at top_k comes from prefix and suffix products over the items,
+    leaving item e out.  The t grid is geometric, 'points' cells (2000: within 1e-6 of the
+    exact value at 384 items, top-8)."""
+    p = np.asarray(p, np.float64)
+    p = p / p.sum()
+    E, K = len(p), top_k
+    if K >= E:
+        return np.ones(E)
+    edges = np.concatenate([[0.0], np.geomspace(1e-6 / p.max(), 60.0 / p.min(), points)])
+    mids = np.concatenate([[edges[1] / 2], np.sqrt(edges[2:] * edges[1:-1]), [edges[-1] * 2]])
+    q = -np.expm1(-np.outer(p, mids))            # clock f fired by the cell's midpoint
+
+    def step(d, qf):
+        n = d * (1.0 - qf)[:, None]
+        n[:, 1:] += d[:, :-1] * qf[:, None]
+        n[:, K] += d[:, K] * qf                   # index K: K or more fired
+        return n
+
+    M = len(mids)
+    pre = np.zeros((E + 1, M, K + 1))
+    pre[0, :, 0] = 1.0
+    for f in range(E):
+        pre[f + 1] = step(pre[f], q[f])
+    suf = np.zeros((E + 1, M, K + 1))
+    suf[E, :, 0] = 1.0
+    for f in range(E - 1, -1, -1):
+        suf[f] = step(suf[f + 1], q[f])
+    cum = np.cumsum(suf[1:, :, :K], axis=2)
+    below = np.zeros((E, M))
+    for i in range(K):
+        below += pre[:E, :, i] * cum[:, :, K - 1 - i]
+    cdf = -np.expm1(-np.outer(p, np.concatenate([edges, [np.inf]])))
+    return (below * np.diff(cdf, axis=1)).sum(axis=1)
+
+
+def router_scores(router: int, logits: np.ndarray) -> np.ndarray:
+    """The selection score a biased router ranks by (before the bias): sigmoid for noaux_tc
+    (src/math/routing.rs:62-67), sqrt(softplus) for sqrt-softplus
+    (src/models/deepseek_v4/math.rs:480-487)."""
+    if router == ROUTER_SQRT_SOFTPLUS:
+        return np.sqrt(np.logaddexp(0.0, logits))
+    return 1.0 / (1.0 + np.exp(-logits))
+
+
+def calibration_scores(spec: LayerSpec, tokens: int,
+                       base_seed: int = synth.BASE_SEED) -> np.ndarray:
+    """Selection scores [tokens, E] of calibration tokens: logits drawn independently as
+    N(0, ||w_e||^2), the distribution the layer's seeded BF16 router row w_e gives on N(0, 1)
+    activations (the rows are near-orthogonal: |cos| ~ 1/sqrt(H))."""
+    w = synth.bf16_to_f32(synth.bf16_matrix("router", spec.n_experts, spec.hidden, 0.02,
+                                            base_seed)).astype(np.float64)
+    std = np.sqrt((w * w).sum(axis=1))
+    z = synth.normals(synth.stream_seed("zipf.calibration", base_seed),
+                      tokens * spec.n_experts).astype(np.float64)
+    return router_scores(spec.router, z.reshape(tokens, spec.n_experts) * std[None, :])
+
+
+def fit_selection_bias(scores: np.ndarray, top_k: int, target: np.ndarray,
+                       iters: int = 40, damping: float = 0.5) -> Tuple[np.ndarray, np.ndarray]:
+    """A per-expert bias b [E] under which top-k selection by scores + b picks expert e in
+    about target[e] of the rows (sum(target) = rows * top_k).  Damped Jacobi iteration: given
+    the others' biases, expert e is picked in row n exactly when s_ne + b_e exceeds the k-th
+    largest biased score among the other experts (the row's (k+1)-th largest when e is picked,
+    its k-th otherwise), so each step sets every b_e to the value that meets its target with
+    the other biases held, and moves halfway there.  Returns (bias, counts under it)."""
+    N, E = scores.shape
+    K = top_k
+    b = np.zeros(E)
+    cols = np.arange(E)
+    t = np.clip(np.asarray(target, np.float64), 0.5, N - 0.5)
+    lo = np.floor(t).astype(np.int64)
+    counts = None
+    for _ in range(iters + 1):
+        sel = scores + b[None, :]
+        part = np.partition(sel, (E - K - 1, E - K), axis=1)
+        kth, k1th = part[:, E - K], part[:, E - K - 1]
+        picked = sel >= kth[:, None]
+        counts = picked.sum(axis=0)
+        d = scores - np.where(picked, k1th[:, None], kth[:, None])  # picked iff d + b_e > 0
+        ds = -np.sort(-d, axis=0)
+        c = 0.5 * (ds[np.clip(lo - 1, 0, N - 1), cols] + ds[np.clip(lo, 0, N - 1), cols])
+        b = b + damping * (-c - b)
+    return b, counts
+
+
+_BIAS_CACHE: Dict[str, Tuple[dict, np.ndarray]] = {}
+ZIPF_CALIBRATION_TOKENS = 8192
+
+
+def workload_bias(w: Workload) -> Tuple[Optional[dict], Optional[np.ndarray]]:
+    """(fit record, correction bias [E] f32) of a Zipf workload, as the benchmark runs it
+    (None, None without a Zipf bias).  The record names the fit and, for "marginals", the
+    targets and the calibration's own head counts; for the single-beta fits, beta."""
     if not w.zipf_s:
         return None, None
     if w.name not in _BIAS_CACHE:
         spec = w.spec
-        std = np.full(spec.n_experts, 0.02 * np.sqrt(spec.hidden))
-        beta = calibrate_zipf_beta(spec.n_experts, spec.top_k, w.zipf_s, std,
-                                   router=spec.router, top_target=w.zipf_top_share)
-        _BIAS_CACHE[w.name] = (beta, zipf_bias(spec.n_experts, w.zipf_s, beta))
-    beta, bias = _BIAS_CACHE[w.name]
-    return beta, bias.copy()
+        if w.zipf_fit == "marginals":
+            rank, p = zipf_popularity(spec.n_experts, w.zipf_s)
+            pi = zipf_inclusion(p, spec.top_k)
+            N = ZIPF_CALIBRATION_TOKENS
+            scores = calibration_scores(spec, N)
+            bias, counts = fit_selection_bias(scores, spec.top_k, N * pi)
+            ok = counts > 0
+            info = {"fit": "marginals", "zipf_s": w.zipf_s, "calibration_tokens": N,
+                    "target_top_share": float(pi.max()),
+                    "calibration_top_share": float(counts.max() / N),
+                    "max_abs_count_error": float(np.abs(counts - N * pi).max()),
+                    "calibration_slope": float(np.polyfit(np.log(rank[ok]),
+                                                          np.log(counts[ok]), 1)[0])}
+            _BIAS_CACHE[w.name] = (info, bias.astype(np.float32))
+        else:
+            std = np.full(spec.n_experts, 0.02 * np.sqrt(spec.hidden))
+            top = w.zipf_top_share if w.zipf_fit == "top_share" else 0.0
+            beta = calibrate_zipf_beta(spec.n_experts, spec.top_k, w.zipf_s, std,
+                                       router=spec.router, top_target=top)
+            _BIAS_CACHE[w.name] = ({"fit": w.zipf_fit, "zipf_s": w.zipf_s, "beta": beta},
+                                   zipf_bias(spec.n_experts, w.zipf_s, beta))
+    info, bias = _BIAS_CACHE[w.name]
+    return dict(info), bias.copy()
 
 
 def with_tokens(w: Workload, tokens: int) -> Tuple[LayerSpec, int]:

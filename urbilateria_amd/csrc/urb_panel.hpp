@@ -226,55 +226,6 @@ __device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + m * kALd + k));
 }
 
-// ---- MX-activation operands of v_mfma_scale_f32_16x16x128_f8f6f4 (one 128-k step) ----
-// Lane l = ln + 16 c of a wavefront feeds row ln of a 16-row block.  Measured operand layout:
-//   E4M3: bytes 0..15 = k 16 c + [0, 16), bytes 16..31 = k 64 + 16 c + [0, 16);
-//   E2M1: nibbles 0..31 (low nibble first) = k 32 c + [0, 32), bytes 16..31 unused;
-// and the E8M0 scale a lane supplies covers k 32 c + [0, 32) of its row, i.e. MX block
-// 4 step + c: one byte per lane, as the panel scale slabs hold them.
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
-// An MXFP4 panel slab's unit (block 4 step + c of row ln) is the E2M1 operand as it stands.
-__device__ __forceinline__ i32x8 mx_operand(const BRaw<kFmtMXFP4>& r) {
-  return i32x8{(int)r.q.x, (int)r.q.y, (int)r.q.z, (int)r.q.w, 0, 0, 0, 0};
-}
-
-// MXFP8 slabs 2 step and 2 step + 1 give lane group c the halves P_c, Q_c of block
-// 4 step + c; the E4M3 operand wants (P_{c/2} | P_{2+c/2}) for even c and (Q_{c/2} | Q_{2+c/2})
-// for odd c.  permlane16_swap(P, Q) = ([P0 Q0 P2 Q2], [P1 Q1 P3 Q3]) (rows of 16 lanes), then
-// permlane32_swap of those = ([P0 Q0 P1 Q1], [P2 Q2 P3 Q3]).
-__device__ __forceinline__ i32x8 mx_operand(const BRaw<kFmtMXFP8>& r) {
-  const uint32_t p[4] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w};
-  const uint32_t q[4] = {r.q[1].x, r.q[1].y, r.q[1].z, r.q[1].w};
-  i32x8 o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const auto a = __builtin_amdgcn_permlane16_swap(p[i], q[i], false, false);
-    const auto b = __builtin_amdgcn_permlane32_swap(a[0], a[1], false, false);
-    o[i] = (int)b[0];
-    o[4 + i] = (int)b[1];
-  }
-  return o;
-}
-
-// Quantized activations staged in LDS: one 128-byte step of a row at pitch kQLd (the 16-byte
-// pad makes the 16 rows of a lane group hit distinct banks).
-constexpr int kQLd = kKS + 16;
-__device__ __forceinline__ i32x8 lds_qfrag(const uint8_t* base, int m, int c) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(base + m * kQLd + 16 * c);
-  const uint4 hi = *reinterpret_cast<const uint4*>(base + m * kQLd + 64 + 16 * c);
-  return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-               (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-}
-
-template <int FMT>
-__device__ __forceinline__ f32x4 mfma_mx(const i32x8& a, int sa, const i32x8& b, int sb,
-                                         f32x4 c) {
-  // A: E4M3 (format 0); B: E2M1 (format 4) or E4M3.
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, FMT == kFmtMXFP4 ? 4 : 0,
-                                                          0, sa, 0, sb);
-}
-
 template <int N>
 using Int = std::integral_constant<int, N>;
 
