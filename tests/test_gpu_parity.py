@@ -1067,6 +1067,39 @@ def test_nonfinite_input_is_reported():
         layer.close()
 
 
+# GLM batches with MX experts run the down projection on f16 MFMAs when every down matrix's
+# E8M0 codes keep its weights exact in f16 (MXFP4 104..140, MXFP8 112..134), and on the BF16
+# hi + lo pair otherwise.  Both must meet the bar: scales at the edges of the f16 range, and
+# scales outside it (one block of one expert) that switch the layer to the BF16 path.
+@pytest.mark.parametrize("name,codes", [("c3_mxfp4_decode", (104, 140)),
+                                        ("c3_mxfp4_decode", (103, 125)),
+                                        ("c3_mxfp4_decode", (119, 160)),
+                                        ("c4_mxfp8", (112, 134)),
+                                        ("c4_mxfp8", (111, 125))])
+def test_down_projection_scale_range_matches_oracle(name, codes):
+    host = _small_layer(name)
+    spec = host.spec
+    rng = np.random.default_rng(codes[0] * 1000 + codes[1])
+    for e in range(spec.n_experts):
+        data, scales = host.experts[e][2]
+        s = scales.copy()
+        s[:] = rng.integers(119, 126, s.shape, dtype=np.uint8)
+        # the range's two ends, in blocks of every expert's down matrix
+        s[0, 0], s[-1, -1] = codes
+        host.experts[e][2] = (data, s)
+    for T in (5, 40):
+        x = synth.activations(f"x.f16range.{T}", T, spec.hidden)
+        layer = moe_mod().MoeLayer(host, max_tokens=T)
+        y, ids, _ = layer.forward(torch.from_numpy(x).cuda())
+        layer.sync()
+        ref = _oracle(host, x)
+        assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+        err = rel_l2(y.cpu().numpy(), ref.output)
+        print(f"{name} codes {codes} T={T}: rel L2 {err:.3e}")
+        assert err < REL_L2_BAR, err
+        layer.close()
+
+
 def test_invalid_payloads_rejected_at_create():
     host = _small_layer("c3_mxfp4_decode")
     host.experts[3][1][1][2, 1] = 0xFF

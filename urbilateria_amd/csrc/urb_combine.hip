@@ -154,7 +154,8 @@ void launch_combine_glm(const float* y_perm, const int32_t* pos_of_slot, const f
 //   MX    any E8M0 scale 0xFF (src/math/mxfp.rs:890-898, 1431-1435)             -> bit 2
 // ------------------------------------------------------------------------------------------
 __global__ void validate_kernel(int fmt, const uint8_t* __restrict__ data, size_t nbytes,
-                                const uint8_t* __restrict__ scales, size_t sbytes, int* flags) {
+                                const uint8_t* __restrict__ scales, size_t sbytes, int* flags,
+                                int f16_lo, int f16_hi) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   const size_t tid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
   int f = 0;
@@ -178,16 +179,21 @@ __global__ void validate_kernel(int fmt, const uint8_t* __restrict__ data, size_
       }
     }
   }
-  for (size_t i = tid; i < sbytes; i += stride)
-    if (scales[i] == 0xffu) f |= 2;
+  for (size_t i = tid; i < sbytes; i += stride) {
+    const int v = scales[i];
+    if (v == 0xff) f |= 2;
+    if (f16_lo <= f16_hi && (v < f16_lo || v > f16_hi)) f |= 4;
+  }
   if (f) atomicOr(flags, f);
 }
 
 void launch_validate(int fmt, const uint8_t* data, size_t data_bytes, const uint8_t* scales,
-                     size_t scale_bytes, int* flags, hipStream_t s) {
+                     size_t scale_bytes, int* flags, hipStream_t s, bool f16_range) {
   size_t work = std::max(data_bytes / 4, scale_bytes);
   int blocks = (int)std::min<size_t>(std::max<size_t>((work + 255) / 256, 1), 4096);
-  validate_kernel<<<blocks, 256, 0, s>>>(fmt, data, data_bytes, scales, scale_bytes, flags);
+  const int lo = f16_range ? kF16ScaleLo[fmt] : 1, hi = f16_range ? kF16ScaleHi[fmt] : 0;
+  validate_kernel<<<blocks, 256, 0, s>>>(fmt, data, data_bytes, scales, scale_bytes, flags, lo,
+                                         hi);
 }
 
 // Dequantised rows, value = decode(code) * scale in f32 (bit-exact parity hook).

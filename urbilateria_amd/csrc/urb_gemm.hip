@@ -25,29 +25,32 @@
 namespace urb {
 
 
-// NP panels per wave (the workgroup covers 4 NP panels = 64 NP weight rows): every staged
-// activation fragment feeds NP (x2 for gate+up) MFMAs.  MT tokens per tile (32 or 64; 64 for
-// large dense batches, so each weight byte feeds twice the MFMAs before it is re-read).
-// Placement: gemm_place (urb_kernels.hpp); xsplit > 1 only for a dense batch (one expert).
-template <int FMT, bool PAIR, int DEPTH, int NP, int MT, int AD = 1>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
-                                                      Perm perm, int max_tiles, int xsplit,
-                                                      int rows, int K,
-                                                      const float* __restrict__ in,
-                                                      float* __restrict__ out, Epi epi,
-                                                      int* status, int block0) {
+// Activation staging of one workgroup in LDS: hi and lo BF16 halves of MT token rows, double
+// buffered, plus the per-wave lo-half flags of each buffer.
+template <int MT>
+struct GemmLds {
+  u16 a_hi[2][MT * kALd];
+  u16 a_lo[2][MT * kALd];
+  int lo_flag[2][4];
+  int rexp[MT];  // row exponents: the f16 down's scales, the gate/up's row maxima
+};
+
+// One workgroup's tile: `w` (a row tile of the permutation, or dense tile w) times panel group
+// `group` of the weight rows.  NP panels per wave (the workgroup covers 4 NP panels = 64 NP
+// weight rows): every staged activation fragment feeds NP (x2 for gate+up) MFMAs.  MT tokens per
+// tile (32 or 64; 64 for large dense batches, so each weight byte feeds twice the MFMAs before
+// it is re-read).  F16 (the down projection of a batch with epi.rowexp): the rows are staged in
+// f16 with their power-of-two scales and the MFMAs take f16 operands (see Epi).
+template <int FMT, bool PAIR, int DEPTH, int NP, int MT, int AD, bool F16 = false>
+__device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, const Perm& perm,
+                                          int w, int group, int rows, int K,
+                                          const float* __restrict__ in, float* __restrict__ out,
+                                          const Epi& epi, int* status, GemmLds<MT>& lds) {
   constexpr int RG = MT / 32;       // staging rows per thread
   constexpr int MBMAX = MT / 16;    // 16-token MFMA blocks per tile
-  __shared__ __attribute__((aligned(16))) u16 a_hi[2][MT * kALd];
-  __shared__ __attribute__((aligned(16))) u16 a_lo[2][MT * kALd];
-  __shared__ __attribute__((aligned(16))) int lo_flag[2][4];  // per staging buffer, per wave
-
-  // ---- which tile and panel group
-  const int groups = rows / (kNT * NP);
-  const int ntiles = min(perm.dense_tokens > 0 ? (perm.dense_tokens + MT - 1) / MT : perm.meta[1],
-                         max_tiles);
-  int w, group;
-  if (!gemm_place(block0 + blockIdx.x, ntiles, groups, xsplit, &w, &group)) return;
+  auto& a_hi = lds.a_hi;
+  auto& a_lo = lds.a_lo;
+  auto& lo_flag = lds.lo_flag;
   int expert, base, count, m0;
   if (perm.dense_tokens > 0) {
     expert = 0;
@@ -91,6 +94,20 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
     a_src[g] = in + (size_t)src_row * K;
   }
+  // F16: each staged row's exponent shift, 141 - (largest exponent field of the row over the
+  // gate/up panel groups), which takes the row's largest |value| into [2^14, 2^15)
+  int a_shift[RG];
+  if constexpr (F16) {
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const int r = am + 32 * g < mrows ? am + 32 * g : 0;
+      const int* ex = epi.rowexp + (size_t)(base + m0 + r) * epi.groups;
+      int e = 0;
+      for (int gg = 0; gg < epi.groups; ++gg) e = max(e, ex[gg]);
+      a_shift[g] = 141 - e;
+      if ((threadIdx.x & 7) == 0) lds.rexp[am + 32 * g] = a_shift[g];
+    }
+  }
 
   f32x4 acc0[NP][MBMAX], acc1[NP][MBMAX];
 #pragma unroll
@@ -120,13 +137,34 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
     auto stage = [&](AStage (&as)[RG], int buf) {
       bool any = false;
 #pragma unroll
-      for (int g = 0; g < RG; ++g) any |= store_a(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
+      for (int g = 0; g < RG; ++g) {
+        if constexpr (F16) store_a16(as[g], a_hi[buf], a_shift[g], am + 32 * g);
+        else any |= store_a(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
+      }
       return any;
     };
     // One K step from ring slot `slot`; the lo-half MFMAs only when some lo half is non-zero.
     // (A uniform runtime branch: compiling both variants straight-line spills the MXFP4
     // four-panel kernel.)
     auto mma = [&](int slot, const u16* hi, const u16* lo, bool with_lo) {
+      if constexpr (F16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int kf = frag_k<FMT>(j, lq);
+          f16x8 ah[NMB];
+#pragma unroll
+          for (int mb = 0; mb < NMB; ++mb)
+            ah[mb] = __builtin_bit_cast(f16x8, lds_frag(hi, mb * 16 + ln, kf));
+#pragma unroll
+          for (int q = 0; q < NP; ++q) {
+            const f16x8 f0 = decode_b16<FMT>(r0[slot][q], j);
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb)
+              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mb], f0, acc0[q][mb], 0, 0, 0);
+          }
+        }
+        return;
+      }
       const bool LO = with_lo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -217,6 +255,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
 
   // ---- epilogue: lane holds column `row` of panel q, rows 4*lq + i of each 16-row block
   bool bad = false;
+  // gate/up with rowexp: the largest exponent field of each token row's activations here
+  const bool rowmax = PAIR && epi.rowexp != nullptr;
+  int ex[MBMAX][4];
+#pragma unroll
+  for (int mb = 0; mb < MBMAX; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ex[mb][i] = 0;
 #pragma unroll
   for (int q = 0; q < NP; ++q) {
     const int row = (panel0 + q) * kPanelRows + ln;
@@ -227,14 +272,57 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restri
         const int mm = mb * 16 + 4 * lq + i;
         if (mm >= mrows) continue;
         const size_t p = (size_t)(base + m0 + mm);
-        if constexpr (PAIR)
-          out[p * rows + row] = epi_gate_up(epi, acc0[q][mb][i], acc1[q][mb][i], bad);
-        else
+        if constexpr (PAIR) {
+          const float a = epi_gate_up(epi, acc0[q][mb][i], acc1[q][mb][i], bad);
+          out[p * rows + row] = a;
+          ex[mb][i] = max(ex[mb][i], (int)((__float_as_uint(a) >> 23) & 0xffu));
+        } else if constexpr (F16) {
+          out[p * rows + row] = epi_down<FMT>(epi, ldexpf(acc0[q][mb][i], -lds.rexp[mm]), bad);
+        } else {
           out[p * rows + row] = epi_down<FMT>(epi, acc0[q][mb][i], bad);
+        }
       }
     }
   }
   if (bad) flag(status, kStatusNonFinite);
+  if (rowmax) {
+    // over the 16 lanes of each k-quad (the rows ln), then the four waves through LDS
+#pragma unroll
+    for (int mb = 0; mb < MBMAX; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int x = 1; x < 16; x <<= 1) ex[mb][i] = max(ex[mb][i], __shfl_xor(ex[mb][i], x));
+    if (threadIdx.x < MT) lds.rexp[threadIdx.x] = 0;
+    __syncthreads();
+    if (ln == 0) {
+#pragma unroll
+      for (int mb = 0; mb < MBMAX; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) atomicMax(&lds.rexp[mb * 16 + 4 * lq + i], ex[mb][i]);
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < mrows)
+      epi.rowexp[(size_t)(base + m0 + threadIdx.x) * epi.groups + group] = lds.rexp[threadIdx.x];
+  }
+}
+
+// Placement: gemm_place (urb_kernels.hpp); xsplit > 1 only for a dense batch (one expert).
+template <int FMT, bool PAIR, int DEPTH, int NP, int MT, int AD = 1, bool F16 = false>
+__global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
+                                                      Perm perm, int max_tiles, int xsplit,
+                                                      int rows, int K,
+                                                      const float* __restrict__ in,
+                                                      float* __restrict__ out, Epi epi,
+                                                      int* status, int block0) {
+  __shared__ __attribute__((aligned(16))) GemmLds<MT> lds;
+  const int groups = rows / (kNT * NP);
+  const int ntiles = min(perm.dense_tokens > 0 ? (perm.dense_tokens + MT - 1) / MT : perm.meta[1],
+                         max_tiles);
+  int w, group;
+  if (!gemm_place(block0 + blockIdx.x, ntiles, groups, xsplit, &w, &group)) return;
+  gemm_tile<FMT, PAIR, DEPTH, NP, MT, AD, F16>(mats, perm, w, group, rows, K, in, out, epi,
+                                               status, lds);
 }
 
 int gemm_xsplit(int dense_tokens, int ntiles, int groups, double wbytes, double abytes) {
@@ -260,7 +348,7 @@ static int xcd_split(const Perm& perm, int max_tiles, int rows, int K) {
 // Workgroups per XCD (32 CUs) of one launch of a dense batch: one per CU.
 constexpr int kDenseBlocksPerXcd = 32;
 
-template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT, int AD = 1>
+template <int FMT, bool PAIR, int DEPTH, int NP, int MT = kMT, int AD = 1, bool F16 = false>
 static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles, int rows, int K,
                          const float* in, float* out, Epi epi, int* status, hipStream_t s,
                          bool beside) {
@@ -272,9 +360,9 @@ static void launch_shape(const ExpertMats* mats, const Perm& perm, int max_tiles
   // slot keeps its XCD).
   const int step = beside && perm.dense_tokens > 0 ? kDenseBlocksPerXcd : per_xcd;
   for (int b0 = 0; b0 < per_xcd; b0 += step)
-    gemm_kernel<FMT, PAIR, DEPTH, NP, MT, AD><<<dim3(8 * std::min(step, per_xcd - b0)), 256, 0,
-                                                s>>>(mats, perm, max_tiles, xsplit, rows, K, in,
-                                                     out, epi, status, 8 * b0);
+    gemm_kernel<FMT, PAIR, DEPTH, NP, MT, AD, F16><<<dim3(8 * std::min(step, per_xcd - b0)), 256,
+                                                     0, s>>>(mats, perm, max_tiles, xsplit, rows,
+                                                             K, in, out, epi, status, 8 * b0);
 }
 
 // Weight steps in flight per wave (DEPTH) and panels per wave (NP), per format.  BF16 steps are
@@ -308,8 +396,12 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
     // slower)
     if constexpr (!PAIR) {
       if (gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens) == 4) {
-        launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
-                                      beside);
+        if (epi.rowexp)
+          launch_shape<FMT, PAIR, 1, 4, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                      status, s, beside);
+        else
+          launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                        beside);
         return;
       }
     }
@@ -317,7 +409,12 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
     // faster in isolation on f32 token rows (512 tokens over 160 experts of 6144 x 2048: 782-787
     // -> 776-777 us) but 1.5 % slower on BF16-valued rows, which skip the lo-half MFMAs
     // (774-776 -> 786-787 us in the layer call)
-    launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
+    if (!PAIR && epi.rowexp)
+      launch_shape<FMT, PAIR, 1, 2, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                   status, s, beside);
+    else
+      launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                    beside);
   }
   else {
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
@@ -325,16 +422,26 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
       // the down projection: eight panels per wave where the rows allow (1024 tokens, top-8 over
       // 384 experts of 7168 x 2048, in isolation: 797-808 -> 755-770 us against four)
       if (np == 8) {
-        launch_shape<FMT, PAIR, 1, 8>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
-                                      beside);
+        if (epi.rowexp)
+          launch_shape<FMT, PAIR, 1, 8, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                      status, s, beside);
+        else
+          launch_shape<FMT, PAIR, 1, 8>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                        beside);
         return;
       }
     }
-    if (np == 4)
+    if (np == 4 && !PAIR && epi.rowexp)
+      launch_shape<FMT, PAIR, 1, 4, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                   status, s, beside);
+    else if (np == 4)
       // the gate/up pair gathers its activation rows two steps ahead (the same 1024-token
       // batch's gate/up in isolation: 1417 -> 1253 us)
       launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out,
                                                         epi, status, s, beside);
+    else if (!PAIR && epi.rowexp)
+      launch_shape<FMT, PAIR, 2, 2, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                   status, s, beside);
     else
       launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
                                     beside);

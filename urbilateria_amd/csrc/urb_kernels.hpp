@@ -60,10 +60,21 @@ struct Perm {
 //   kEpiHy4Shared Hy4 shared DenseMlp (src/models/hy4/runtime.rs:1311-1321):
 //                 bf16(silu(bf16(g)) * bf16(u)); BF16 outputs.
 enum { kEpiGated = 0, kEpiQwen = 1, kEpiHy4 = 2, kEpiHy4Shared = 3 };
+// rowexp (GatedMlp batches, MX weights): the gate/up projection also writes, per permuted row and
+// panel group, the largest f32 exponent field of the row's activations (rowexp[row * groups +
+// group]); the down projection then stages each row in f16 scaled by a power of two so that
+// its largest value falls in [2^14, 2^15), runs one f16 MFMA per product and rescales the sums
+// exactly (11 significant bits of each activation instead of the 16 of the BF16 hi + lo pair).
 struct Epi {
   int kind;
   float limit;
+  int* rowexp = nullptr;
+  int groups = 0;
 };
+// E8M0 codes whose scale keeps every element of an MX matrix exact in f16 (MXFP4: 6 2^13 is
+// the largest value and 0.5 2^-23 = 2^-24 the f16 grid; MXFP8: 448 2^7, 2^-9 2^-15).
+constexpr int kF16ScaleLo[3] = {0, 104, 112};
+constexpr int kF16ScaleHi[3] = {-1, 140, 134};
 
 // Grouped GEMM (MFMA) tiling: tokens per tile, weight rows per workgroup (four panels), K per
 // step.
@@ -259,9 +270,10 @@ void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const f
 // kStatusNonFinite in `status` (may be null).
 void launch_rms_norm(const float* h, const float* weight, int T, int H, float eps, float* out,
                      int* status, hipStream_t s);
-// Payload validation: bit 1 = non-finite BF16 / E4M3 NaN code, bit 2 = E8M0 0xFF.
+// Payload validation: bit 1 = non-finite BF16 / E4M3 NaN code, bit 2 = E8M0 0xFF, bit 4 (with
+// f16_range) = an E8M0 code outside [kF16ScaleLo, kF16ScaleHi] of the format.
 void launch_validate(int fmt, const uint8_t* data, size_t data_bytes, const uint8_t* scales,
-                     size_t scale_bytes, int* flags, hipStream_t s);
+                     size_t scale_bytes, int* flags, hipStream_t s, bool f16_range = false);
 void launch_dequant(int fmt, const uint8_t* data, const uint8_t* scales, int rows, int cols,
                     int row0, int count, float* out, hipStream_t s);
 void launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t s);

@@ -48,6 +48,7 @@ struct Workspace {
   float* xq = nullptr;  // HY4, DSV41, DSV4: the simulated E4M3 token activations [chunk, H]
   float* xn = nullptr;  // QWEN36 block calls: the normalized BF16 token activations [chunk, H]
   float* gate_logit = nullptr;  // QWEN36 shared expert: bf16(shared_expert_gate . x) [chunk]
+  int32_t* rowexp = nullptr;    // GLM, MX experts: [chunk * k, gate/up panel groups]
   // one-token calls: BF16 piece vectors (urb_panel.hpp) of the token, the k SwiGLU rows and
   // the shared expert's SwiGLU row, the decode GEMVs' A operands
   uint16_t* xp = nullptr;
@@ -88,6 +89,10 @@ struct urb_moe_ctx {
   uint32_t hash_vocab = 0;
   ExpertMats* table = nullptr;         // device [E]
   ExpertMats* shared_table = nullptr;  // device [1]
+  // GLM batches with MX experts: the down projection runs on f16 MFMAs from row-scaled f16
+  // activations (urb::Epi::rowexp) -- every down matrix's E8M0 codes keep its weights exact in
+  // f16 (checked at create and by urb_moe_set_expert, which clears it otherwise)
+  bool down_f16 = false;
   Workspace ws;
   hipStream_t side = nullptr;          // shared expert runs here, concurrently with routing
   hipEvent_t fork = nullptr, join = nullptr;
@@ -230,6 +235,12 @@ static void destroy_ctx(urb_moe_ctx* c) {
 
 // The per-call buffers for chunks of up to `chunk` tokens, carved from one region into `w`
 // (a Bump with a null base only sizes the region: every pointer it hands out is null).
+// Panel groups of the routed gate/up launch (one rowexp column each).
+static size_t rowexp_groups(const urb_moe_desc& d) {
+  const int np = urb::gemm_panels_per_wave((int)d.expert_format, (int)d.intermediate, true, 0);
+  return d.intermediate / (urb::kGemmNTile * (size_t)np);
+}
+
 static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspace& w) {
   const urb_moe_desc& d = c->desc;
   const size_t C = chunk, E = d.n_experts, K = d.top_k, H = d.hidden, I = d.intermediate;
@@ -261,6 +272,8 @@ static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspa
   if (mx_activation(d.composition)) w.xq = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36) w.xn = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36 && d.shared_intermediate) w.gate_logit = b.take<float>(C);
+  if (d.composition == URB_COMPOSE_GLM && d.expert_format != URB_FMT_BF16)
+    w.rowexp = b.take<int32_t>(C * K * rowexp_groups(d));
   w.xp = b.take<uint16_t>(H / 8 * urb::kPieceUnit);
   w.act_xp = b.take<uint16_t>(K * (I / 8) * urb::kPieceUnit);
   w.shared_xp = b.take<uint16_t>(std::max<size_t>(d.shared_intermediate, 8) / 8 *
@@ -447,11 +460,12 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   int* flags = c->ws.status + 1;
   urb::launch_validate(URB_FMT_BF16, reinterpret_cast<const uint8_t*>(router), E * H * 2, nullptr,
                        0, flags, nullptr);
+  const bool f16_check = d->composition == URB_COMPOSE_GLM && d->expert_format != URB_FMT_BF16;
   for (size_t e = 0; e < E; ++e)
     for (int m = 0; m < 3; ++m) {
       size_t sb, db = matrix_bytes(d->expert_format, dims[m][0], dims[m][1], &sb);
       urb::launch_validate(d->expert_format, table[e].data[m], db, table[e].scales[m], sb, flags,
-                           nullptr);
+                           nullptr, f16_check && m == 2);
     }
   if (has_shared)
     for (int m = 0; m < 3; ++m) {
@@ -473,6 +487,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
     return d->router == URB_ROUTER_SQRT_SOFTPLUS ? URB_ERR_NONFINITE : URB_ERR_INVALID_GEOMETRY;
   if (host_flags[1] & 1) return URB_ERR_NONFINITE;
   if (host_flags[1] & 2) return URB_ERR_INVALID_SCALE;
+  c->down_f16 = f16_check && !(host_flags[1] & 4);
   urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
 
   if (qwen_gate) urb::launch_relayout_lane8(gate_rows, 1, (int)H, c->shared_gate8, nullptr);
@@ -921,16 +936,21 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
     else
       route_and_permute(s);
     const int max_tiles = urb::gemm_max_tiles(n, K, E);
+    urb::Epi repi = epi;
+    if (c->down_f16) {
+      repi.rowexp = ws.rowexp;
+      repi.groups = (int)rowexp_groups(d);
+    }
     // grouped MFMA GEMMs over the row tiles
     {
       Span span(c, URB_STAGE_GATE_UP, s);
-      urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act, epi,
-                               ws.status, s);
+      urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act,
+                               repi, ws.status, s);
     }
     {
       Span span(c, URB_STAGE_DOWN, s);
       urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act, ws.y_perm,
-                            epi, ws.status, s);
+                            repi, ws.status, s);
     }
     if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {
@@ -1170,7 +1190,8 @@ urb_status urb_moe_set_expert(urb_moe_ctx* c, uint32_t expert, const urb_matrix*
     size_t sb, db = matrix_bytes(d.expert_format, dims[m][0], dims[m][1], &sb);
     e.data[m] = static_cast<const uint8_t*>(mats[m].data);
     e.scales[m] = sb ? mats[m].scales : nullptr;
-    urb::launch_validate(d.expert_format, e.data[m], db, e.scales[m], sb, flags, s);
+    urb::launch_validate(d.expert_format, e.data[m], db, e.scales[m], sb, flags, s,
+                         c->down_f16 && m == 2);
   }
   URB_HIP(hipGetLastError());
   int host_flags = 0;
@@ -1178,6 +1199,7 @@ urb_status urb_moe_set_expert(urb_moe_ctx* c, uint32_t expert, const urb_matrix*
   URB_HIP(hipStreamSynchronize(s));
   if (host_flags & 1) return URB_ERR_NONFINITE;
   if (host_flags & 2) return URB_ERR_INVALID_SCALE;
+  if (host_flags & 4) c->down_f16 = false;  // this expert's down scales leave the f16 range
   // the table entry changes in stream order: calls queued before keep the previous matrices
   URB_HIP(hipMemcpyAsync(c->table + expert, &e, sizeof(ExpertMats), hipMemcpyHostToDevice, s));
   URB_HIP(hipStreamSynchronize(s));

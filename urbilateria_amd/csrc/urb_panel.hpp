@@ -108,6 +108,31 @@ __device__ __forceinline__ bf16x8 decode_b(const BRaw<FMT>& r, int j) {
   }
 }
 
+// MFMA j's B operand as f16 for the MX formats (exact for E8M0 codes within
+// [kF16ScaleLo, kF16ScaleHi] of the format; urb_moe_create checks the down projections).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+template <int FMT>
+__device__ __forceinline__ f16x8 decode_b16(const BRaw<FMT>& r, int j) {
+  static_assert(FMT != kFmtBF16, "BF16 weights have no exact f16 form");
+  const float sc = e8m0_to_f32(r.s);
+  uint32_t p[4];
+  if constexpr (FMT == kFmtMXFP4) {
+    const uint32_t w = j == 0 ? r.q.x : j == 1 ? r.q.y : j == 2 ? r.q.z : r.q.w;
+    p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 0));
+    p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 1));
+    p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 2));
+    p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 3));
+  } else {
+    const uint4 q = r.q[j >> 1];
+    const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
+    p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, sc, false));
+    p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, sc, true));
+    p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, sc, false));
+    p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, sc, true));
+  }
+  return __builtin_bit_cast(f16x8, make_uint4(p[0], p[1], p[2], p[3]));
+}
+
 // ---- projection epilogues (kinds in urb_kernels.hpp) ----
 // Gate/up pair -> activation; `bad` is set on a failure the reference reports.
 __device__ __forceinline__ float epi_gate_up(const Epi& e, float g0, float u0, bool& bad) {
@@ -207,6 +232,23 @@ __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
   dl[0] = make_uint4(l[0], l[1], l[2], l[3]);
   dl[1] = make_uint4(l[4], l[5], l[6], l[7]);
   return (lor & 0x7fff7fffu) != 0;
+}
+
+// Writes the staged values times 2^e2 (exact) as f16 (round to nearest even) into LDS row m.
+__device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,
+                                          int m = (int)(threadIdx.x >> 3)) {
+  typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+  const int kc = (threadIdx.x & 7) * 16;
+  const float* v = reinterpret_cast<const float*>(a.v);
+  uint32_t h[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    h[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                            f32x2v{ldexpf(v[2 * i], e2), ldexpf(v[2 * i + 1], e2)},
+                                            f16x2v));
+  uint4* d = reinterpret_cast<uint4*>(dst + m * kALd + kc);
+  d[0] = make_uint4(h[0], h[1], h[2], h[3]);
+  d[1] = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
 // A workgroup barrier that also ORs a per-thread flag over the four waves of a 256-thread
