@@ -32,11 +32,14 @@ RUNS = [("c1_bf16_decode", 1), ("c2_bf16_prefill", 128), ("c3_mxfp4_decode", 1),
         ("c3_mxfp4_decode", 32), ("c4_mxfp8", 1), ("c4_mxfp8", 512),
         ("c5_mxfp4_zipf_prefill", 1024), ("c5_mxfp4_zipf_flat", 1024),
         ("c5_mxfp4_zipf_hot", 1024)]
-# the projection stages a roofline block may name (routing kernels are latency-bound)
-# The routed projections run on the caller's stream, on the critical path of the call; the
-# shared expert's run beside them on a side stream (batches), where their spans include the
-# time they wait for CUs, so the dominant kernel is the slower routed projection.
+# The projection stages a roofline block may name (routing kernels are latency-bound).  The
+# routed projections always run on the caller's stream, on the critical path.  The shared
+# expert's run there too for one token and for batches of SHARED_INLINE_TOKENS or more in the
+# f32-activation compositions; other batches run them on a side stream beside the routing, where
+# their spans include the time they wait for CUs, so they are not candidates then.
 PROJECTIONS = ("gate_up", "down")
+SHARED_PROJECTIONS = ("shared_gate_up", "shared_down")
+SHARED_INLINE_TOKENS = 256
 MALL_BYTES = 256 << 20   # Infinity Cache: rotate enough layer copies to stream past it
 
 
@@ -257,22 +260,54 @@ def cpu_baseline(name, spec, C, dev, x, budget_s, tok=None):
             "host": host_disclosure(threads)}
 
 
+def shared_in_line(spec, C, tokens):
+    """Whether the layer call runs the shared expert on the caller's stream (urb_moe_host.cpp,
+    shared_stream): one token, or f32-activation batches of SHARED_INLINE_TOKENS or more."""
+    mx = spec.composition in (C.COMPOSE_HY4, C.COMPOSE_DSV41, C.COMPOSE_DSV4)
+    return bool(spec.shared_intermediate) and (tokens == 1 or
+                                               (not mx and tokens >= SHARED_INLINE_TOKENS))
+
+
+def committed_trace(workload, tokens, stage):
+    """The committed rocprofv3 kernel-trace statistics of a stage's kernel
+    (profiles/kernel_traces.json: kernel name, calls, average/min/max duration and the command),
+    or None."""
+    path = os.path.join(ROOT, "profiles", "kernel_traces.json")
+    try:
+        with open(path) as f:
+            m = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for e in m.get("traces", []):
+        if (e.get("workload"), e.get("tokens"), e.get("stage")) == (workload, tokens, stage):
+            return e
+    return None
+
+
 def roofline_block(rec, spec, C, workload, tokens):
     """The dominant projection kernel of a run: algorithmic bytes per launch over its average
     launch duration (HIP events on its stream), against 8 TB/s; its MFMA rate against the
-    dense BF16 peak; and the counter-measured HBM bytes per launch when profiles/ holds them."""
+    dense BF16 peak; the counter-measured HBM bytes per launch when profiles/ holds them; and
+    the same kernel's average duration and fraction in the committed rocprofv3 kernel trace."""
     stages = rec["stages"]
-    cands = [k for k in PROJECTIONS if k in stages]
+    names = PROJECTIONS + (SHARED_PROJECTIONS if shared_in_line(spec, C, tokens) else ())
+    cands = [k for k in names if k in stages]
     if not cands:
         return None
     dom = max(cands, key=lambda k: stages[k]["avg_us"])
     st = stages[dom]
     achieved = st["bytes"] / (st["avg_us"] * 1e-6) / 1e9
-    return {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK / 1e9,
-            "unit": "GB/s", "frac": achieved / (HBM_PEAK / 1e9),
-            "traffic": measured_traffic(workload, tokens, dom),
-            "bytes_per_launch": st["bytes"], "avg_launch_us": st["avg_us"],
-            "mfma_frac_bf16": st.get("flops", 0) / (st["avg_us"] * 1e-6) / MFMA_PEAK["bf16"]}
+    block = {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK / 1e9,
+             "unit": "GB/s", "frac": achieved / (HBM_PEAK / 1e9),
+             "traffic": measured_traffic(workload, tokens, dom),
+             "bytes_per_launch": st["bytes"], "avg_launch_us": st["avg_us"],
+             "mfma_frac_bf16": st.get("flops", 0) / (st["avg_us"] * 1e-6) / MFMA_PEAK["bf16"]}
+    tr = committed_trace(workload, tokens, dom)
+    if tr:
+        block["trace"] = {"kernel_name": tr["kernel"], "avg_us": tr["avg_us"],
+                          "frac": st["bytes"] / (tr["avg_us"] * 1e-6) / HBM_PEAK,
+                          "file": "profiles/kernel_traces.json"}
+    return block
 
 
 def run_one(name, T, args, want_cpu, cpu_budget):

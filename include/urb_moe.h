@@ -339,7 +339,12 @@ typedef struct {
  * plain BF16 [rows, cols] without a sidecar -> URB_FMT_BF16; F8_E4M3 [rows, cols] with a U8
  * [rows, ceil(cols/32)] sidecar (ModelOpt 1x32) -> URB_FMT_MXFP8; I8 (F8_E8M0 sidecar) or U8
  * ".weight_packed" (U8 sidecar) [rows, ceil(cols/2)] with a [rows, ceil(cols/32)] sidecar ->
- * URB_FMT_MXFP4.  *resident_bytes = payload + sidecar bytes.  Errors: rows or cols 0, or a
+ * URB_FMT_MXFP4.  *resident_bytes = payload + sidecar bytes.  A plain BF16 matrix stays
+ * compact BF16 in this layer (its resident bytes are the payload, rows * cols * 2, as the
+ * reference's inspect_compact_bf16_matrix reports, weight.rs:337-380, fixture :1237-1243);
+ * this differs on purpose from inspect_weight_matrix, which widens plain matrices to F32
+ * (rows * cols * 4, weight.rs:155-170, fixture :1267-1273): the GPU layer never widens.
+ * Errors: rows or cols 0, or a
  * shape or sidecar that does not match the format the dtypes select -> URB_ERR_SHAPE
  * (InvalidShape); layouts the reference reads but this layer does not take -> URB_ERR_ARGUMENT
  * (F16/F32 plain matrices, E4M3 with 32x32 or 128x128 E8M0 block scales or without a sidecar,

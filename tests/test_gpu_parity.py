@@ -739,6 +739,11 @@ def test_consolidated_checkpoint_layer_equals_per_expert_layer():
             y1, i1, w1 = a.forward(x[:T].contiguous())
             y2, i2, w2 = b.forward(x[:T].contiguous())
             assert torch.equal(y1, y2) and torch.equal(i1, i2) and torch.equal(w1, w2)
+            # and the consolidated layer against the oracle on the same host weights
+            ref = _oracle(host, x[:T].cpu().numpy())
+            assert ids_match(i2.cpu().numpy(), ref.ids,
+                             _scores(host.spec, ref, host.correction_bias))
+            assert rel_l2(y2.cpu().numpy(), ref.output) < REL_L2_BAR
         a.close()
         b.close()
 
@@ -861,6 +866,11 @@ def test_streamed_residency_layer_equals_resident_layer(name):
         assert torch.equal(y, torch.cat([p[0] for p in parts]))
         assert torch.equal(ids, torch.cat([p[1] for p in parts]))
         assert torch.equal(w, torch.cat([p[2] for p in parts]))
+        # the streamed layer against the oracle on the host weights it streams from
+        ref = _oracle(host, x.cpu().numpy())
+        assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, host.correction_bias))
+        assert rel_l2(y.cpu().numpy(), ref.output) < REL_L2_BAR
+        assert np.allclose(w.cpu().numpy(), ref.weights, rtol=1e-5, atol=1e-7)
         for t in range(T):
             for key in sorted(ids[t].tolist()):
                 replay.access(rt, 0, key, lambda key=key: (key, 1, 1))

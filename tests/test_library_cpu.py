@@ -307,6 +307,9 @@ def test_inspect_matrix_selects_formats_from_metadata_like_the_reference():
     assert F(_meta("F8_E4M3", (2, 33)), _meta("U8", (2, 2)), 2, 33) == (C.FMT_MXFP8, 70)
     assert F(_meta("I8", (2048, 3584)), _meta("F8_E8M0", (2048, 224)), 2048, 7168) == \
         (C.FMT_MXFP4, 2048 * 3584 + 2048 * 224)
+    # plain BF16 [2, 2]: compact BF16, 8 resident bytes -- inspect_compact_bf16_matrix's answer
+    # for the reference's fixture (weight.rs:1237-1243); inspect_weight_matrix would widen the
+    # same tensor to F32, 16 bytes (weight.rs:1267-1273), which this layer never does
     assert F(_meta("BF16", (2, 2), 2), None, 2, 2) == (C.FMT_BF16, 8)
 
 
