@@ -756,12 +756,14 @@ def _qwen_shared_layer(hidden=256, n_experts=16, intermediate=128):
     return C.make_host_layer(spec)
 
 
-@pytest.mark.parametrize("comp,T", [(C.COMPOSE_GLM, 256), (C.COMPOSE_GLM, 300),
-                                    (C.COMPOSE_GLM, 520), (C.COMPOSE_QWEN36, 300)])
-def test_dense_shared_batch_matches_oracle(comp, T):
-    # f32-activation batches of 256+ tokens run the BF16 shared expert in line, as dense
-    # 32-token tiles of two (gate+up) or four (down) panels per wave; 300 and 520 end in a
-    # partial tile
+@pytest.mark.parametrize("comp,T,bf16_x", [(C.COMPOSE_GLM, 256, True), (C.COMPOSE_GLM, 300, True),
+                                           (C.COMPOSE_GLM, 520, True), (C.COMPOSE_GLM, 520, False),
+                                           (C.COMPOSE_QWEN36, 300, True)])
+def test_dense_shared_batch_matches_oracle(comp, T, bf16_x):
+    # f32-activation batches of 256+ tokens run the BF16 shared expert in line: the gate/up on
+    # the split-K dense kernel (256-token tiles; 300 and 520 end in a partial tile; f32 token
+    # rows take the lo-half MFMAs, BF16-valued ones skip them), the down on dense 32-token tiles
+    # of four panels per wave
     if comp == C.COMPOSE_GLM:
         spec = C.LayerSpec(hidden=512, n_experts=16, top_k=4, intermediate=256,
                            shared_intermediate=256, expert_format=C.FMT_MXFP4,
@@ -773,6 +775,9 @@ def test_dense_shared_batch_matches_oracle(comp, T):
         host = _qwen_shared_layer()
         spec = host.spec
     x = synth.activations(f"x.dense.{comp}.{T}", T, spec.hidden)
+    if not bf16_x:
+        x = synth.normals(synth.stream_seed(f"x.dense.f32.{T}"), T * spec.hidden).reshape(
+            T, spec.hidden)
     layer = moe_mod().MoeLayer(host, max_tokens=T)
     y, ids, w = layer.forward(torch.from_numpy(x).cuda())
     ref = _oracle(host, x)

@@ -20,7 +20,7 @@ HIPCC_FLAGS = [
 ]
 
 MOE_SOURCES = ["urb_route.hip", "urb_panel.hip", "urb_combine.hip", "urb_gemm.hip", "urb_hy4.hip",
-               "urb_decode.hip", "urb_scratch.hip",
+               "urb_decode.hip", "urb_scratch.hip", "urb_dense.hip",
                "urb_block.hip",
                "urb_moe_host.cpp", "urb_residency.cpp"]
 SYNTH_SOURCES = ["urb_synth.hip"]

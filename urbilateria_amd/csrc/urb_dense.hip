@@ -1,0 +1,297 @@
+// urb_dense.hip -- the shared expert of a large batch: dense BF16 GEMMs on CDNA4 MFMA.
+//
+// C[T, N] = A[T, K] . W[N, K]^T with W a BF16 matrix in the panel layout (urb_kernels.hpp) and
+// A f32 activations.  A workgroup of eight waves (two per SIMD, one workgroup per CU) owns a
+// 256-token x 256-row tile and one of S equal K ranges (split K, so that the 1024 x 4096 shared
+// gate/up of a 1024-token batch still gives 256 workgroups); each wave computes 128 tokens x 64
+// rows with v_mfma_f32_16x16x32_bf16 (8 x 4 accumulator blocks, 128 accumulator registers).  Per 32-column K step both operands are
+// staged in LDS in MFMA fragment order (1 KiB per 16 rows, lane l = row l % 16, columns
+// 8 (l / 16) + [0, 8)), double buffered, from a register stage loaded two steps ahead:
+//  * W: the panel layout's slabs are that fragment order already -- copied verbatim;
+//  * A: each thread converts one token row's 32 values into BF16 hi + lo halves (16
+//    significant bits, as the grouped GEMMs), and the lo MFMAs are skipped for a step whose lo
+//    halves are all zero (BF16-valued activations).
+// Against the grouped GEMM's 32-token dense tiles, every weight byte is read by 4 instead of 32
+// tiles and every activation by 16 instead of 32.  The S partial sums [S, T, N] go to a
+// workspace; the reduce kernels add them in order of K range (deterministic) and apply the
+// gate/up epilogue (SwiGLU, the composition's boundaries) or the down epilogue.
+#include "urb_device.hpp"
+#include "urb_kernels.hpp"
+#include "urb_panel.hpp"
+
+#include <algorithm>
+
+namespace urb {
+
+namespace {
+
+constexpr int kDM = 256;       // tokens per tile
+constexpr int kDN = 256;       // weight rows per tile
+constexpr int kDK = 32;        // K per step (one MFMA)
+constexpr int kDFrag = 512;    // u16 per 16-row fragment (1 KiB)
+
+struct DenseLds {
+  u16 a_hi[2][kDM / 16][kDFrag];
+  u16 a_lo[2][kDM / 16][kDFrag];
+  u16 b[2][kDN / 16][kDFrag];
+  int lo_flag[2][8];
+};
+
+// Rows n0 .. n0 + 255 of the stacked matrix [W0; W1] (rows < n_split from W0): panel p's base.
+__device__ __forceinline__ const uint8_t* dense_panel(const uint8_t* w0, const uint8_t* w1,
+                                                      int n_split, size_t pbytes, int row) {
+  return row < n_split ? w0 + (size_t)(row / kPanelRows) * pbytes
+                       : w1 + (size_t)((row - n_split) / kPanelRows) * pbytes;
+}
+
+// LDS position of A fragment unit u (lane u of the MFMA operand): units 32..63 swap their
+// halves of 8, so the two threads that stage one row (units u and u + 32 of a group of 16
+// lanes) write different banks; the reading lanes 32..47 still cover one contiguous 256 B.
+__device__ __forceinline__ int a_swz(int u) { return u ^ ((u >> 5) << 3); }
+
+// Tile placement: work item w = m + Mt (n + Nt z) (m fastest, so the m tiles that read the
+// same weight rows and K range are consecutive); XCD c (block % 8) takes the contiguous run c of
+// the items, so those tiles share its L2.
+__device__ __forceinline__ bool dense_place(int block, int Mt, int Nt, int S, int* m, int* n,
+                                            int* z) {
+  const int total = Mt * Nt * S;
+  const int xcd = block & 7, local = block >> 3;
+  const int w = xcd * total / 8 + local;
+  if (w >= (xcd + 1) * total / 8) return false;
+  *m = w % Mt;
+  *n = (w / Mt) % Nt;
+  *z = w / (Mt * Nt);
+  return true;
+}
+
+// A workgroup barrier that also ORs a per-thread flag over the eight waves of a 512-thread
+// workgroup (one s_barrier; `slots`, 8 ints, double buffered with the data they describe).
+__device__ __forceinline__ bool barrier_or8(bool pred, int* slots) {
+  const bool any = __ballot(pred) != 0;
+  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = any;
+  __syncthreads();
+  const int4 v0 = *reinterpret_cast<const int4*>(slots);
+  const int4 v1 = *reinterpret_cast<const int4*>(slots + 4);
+  return (v0.x | v0.y | v0.z | v0.w | v1.x | v1.y | v1.z | v1.w) != 0;
+}
+
+__global__ __launch_bounds__(512, 1) void dense_gemm_kernel(
+    const float* __restrict__ a, int T, int K, const uint8_t* __restrict__ w0,
+    const uint8_t* __restrict__ w1, int n_split, int N, int S, float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) DenseLds lds;
+  const int Mt = (T + kDM - 1) / kDM, Nt = N / kDN;
+  int mt, nt, z;
+  if (!dense_place(blockIdx.x, Mt, Nt, S, &mt, &nt, &z)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;  // tokens 128 wm + [0, 128), rows 64 wn + [0, 64)
+  const int ksteps = K / kDK;
+  const int s_begin = ksteps * z / S, n_steps = ksteps * (z + 1) / S - s_begin;
+  const size_t pbytes = (size_t)kPanelRows * K * 2;
+
+  // ---- this thread's staging: half tid % 2 of token row m0 + tid / 2 (a row past T re-reads
+  // row m0: its products land in accumulator rows that are never stored; two threads read one
+  // 128-byte row segment), and two 16-byte units of the weight slabs: panel tid / 32, units
+  // tid % 32 and tid % 32 + 32, so each group of 16 lanes writes 256 contiguous bytes of LDS.
+  const int m0 = mt * kDM;
+  const int tok = tid >> 1, half = tid & 1;
+  const int arow = m0 + tok < T ? m0 + tok : m0;
+  const float* a_src = a + (size_t)arow * K + 16 * half;
+  const int bp = tid >> 5, bu = tid & 31;
+  const uint8_t* b_src =
+      dense_panel(w0, w1, n_split, pbytes, nt * kDN + bp * kPanelRows) + bu * 16;
+  // LDS fragment slots of this thread's A values: block tok / 16, lanes (tok % 16) + 16 lq for
+  // lq = 2 half, 2 half + 1
+  const int a_blk = tok >> 4, a_ln = tok & 15;
+
+  struct Stage {
+    float4 a[4];
+    uint4 b[2];
+  };
+  auto load = [&](Stage& st, int s) {
+    const int k0 = (s_begin + s) * kDK;
+    const float4* pa = reinterpret_cast<const float4*>(a_src + k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.a[i] = pa[i];
+    const uint8_t* pb = b_src + (size_t)(s_begin + s) * 1024;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) st.b[i] = ldg16(pb + 512 * i);
+  };
+  // returns whether any lo half is non-zero
+  auto store = [&](const Stage& st, int buf) {
+    const float* v = reinterpret_cast<const float*>(st.a);
+    uint32_t lor = 0;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        split_bf16(v[8 * q + 2 * i], v[8 * q + 2 * i + 1], h[i], l[i]);
+        lor |= l[i];
+      }
+      const int u = a_swz(a_ln + 16 * (2 * half + q));
+      *reinterpret_cast<uint4*>(&lds.a_hi[buf][a_blk][8 * u]) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4*>(&lds.a_lo[buf][a_blk][8 * u]) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<uint4*>(&lds.b[buf][bp][8 * (bu + 32 * i)]) = st.b[i];
+    return (lor & 0x7fff7fffu) != 0;
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto mma = [&](int buf, bool with_lo) {
+    bf16x8 bf[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+      bf[nb] = __builtin_bit_cast(bf16x8,
+                                  *reinterpret_cast<const uint4*>(&lds.b[buf][wn * 4 + nb][8 * lane]));
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const bf16x8 ah = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const uint4*>(&lds.a_hi[buf][wm * 8 + mb][8 * a_swz(lane)]));
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bf[nb], acc[mb][nb], 0, 0, 0);
+    }
+    if (with_lo) {
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        const bf16x8 al = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const uint4*>(&lds.a_lo[buf][wm * 8 + mb][8 * a_swz(lane)]));
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bf[nb], acc[mb][nb], 0, 0, 0);
+      }
+    }
+  };
+
+  // register stages two steps ahead, LDS double buffered; the steady state issues every load
+  // unguarded (one issue order on every path, so the compiler's wait counts stay exact)
+  Stage st[2];
+  load(st[0], 0);
+  if (n_steps > 1) load(st[1], 1);
+  bool lo = barrier_or8(store(st[0], 0), lds.lo_flag[0]);
+  int s = 0;
+  for (; s + 4 <= n_steps; s += 2) {
+    // step s from buffer 0, step s + 1 from buffer 1
+    load(st[0], s + 2);
+    mma(0, lo);
+    lo = barrier_or8(store(st[1], 1), lds.lo_flag[1]);
+    load(st[1], s + 3);
+    mma(1, lo);
+    lo = barrier_or8(store(st[0], 0), lds.lo_flag[0]);
+  }
+  // the last one to three steps (s is even: buffer 0 holds step s, st[1] step s + 1), with
+  // compile-time stage indices (a runtime index would put the register stages in scratch)
+  if (s < n_steps) {
+    mma(0, lo);
+    if (s + 1 < n_steps) {
+      if (s + 2 < n_steps) load(st[0], s + 2);
+      lo = barrier_or8(store(st[1], 1), lds.lo_flag[1]);
+      mma(1, lo);
+      if (s + 2 < n_steps) {
+        lo = barrier_or8(store(st[0], 0), lds.lo_flag[0]);
+        mma(0, lo);
+      }
+    }
+  }
+
+  // ---- the partial sums: lane holds rows (tokens) 4 lq + i, column (weight row) ln of each block
+  const int ln = lane & 15, lq = lane >> 4;
+  float* pz = part + (size_t)z * T * N;
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = m0 + wm * 128 + mb * 16 + 4 * lq + i;
+      if (t >= T) continue;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        pz[(size_t)t * N + nt * kDN + wn * 64 + nb * 16 + ln] = acc[mb][nb][i];
+    }
+}
+
+// act[t, j] = epi_gate_up(sum_z gate partial, sum_z up partial): the gate rows are columns
+// 0..I-1 of the partial sums, the up rows columns I..2I-1.
+__global__ void dense_reduce_gate_up_kernel(const float* __restrict__ part, int T, int I, int S,
+                                            Epi epi, float* __restrict__ act, int* status) {
+  const size_t n = (size_t)T * I, stride = (size_t)T * 2 * I;
+  bool bad = false;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = i / I, j = i - t * I;
+    const float* p = part + t * 2 * I + j;
+    float g = 0.0f, u = 0.0f;
+    for (int z = 0; z < S; ++z) {
+      g += p[z * stride];
+      u += p[z * stride + I];
+    }
+    act[i] = epi_gate_up(epi, g, u, bad);
+  }
+  if (bad) flag(status, kStatusNonFinite);
+}
+
+__global__ void dense_reduce_down_kernel(const float* __restrict__ part, int T, int H, int S,
+                                         Epi epi, float* __restrict__ out, int* status) {
+  const size_t n = (size_t)T * H;
+  bool bad = false;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float v = 0.0f;
+    for (int z = 0; z < S; ++z) v += part[z * n + i];
+    out[i] = epi_down<kFmtBF16>(epi, v, bad);
+  }
+  if (bad) flag(status, kStatusNonFinite);
+}
+
+int reduce_blocks(size_t n) {
+  return (int)std::min<size_t>(std::max<size_t>((n + 255) / 256, 1), 8192);
+}
+
+}  // namespace
+
+// K splits of one dense launch: enough workgroups to cover the CUs (256), within the partial
+// sums' room, each K range a multiple of the 32-column step.
+// (one workgroup per CU: the doubling stops past ~1.25 rounds of the 256 CUs)
+int dense_splits(int T, int N, int K, size_t part_floats) {
+  const int tiles = ((T + kDM - 1) / kDM) * (N / kDN);
+  int S = 1;
+  while (S < 4 && tiles * 2 * S <= 320 && (size_t)(2 * S) * T * N <= part_floats &&
+         (K / kDK) / (2 * S) >= 8)
+    S *= 2;
+  return S;
+}
+
+bool dense_fits(int T, int I, int H, size_t part_floats) {
+  return T >= kDM && (2 * I) % kDN == 0 && H % kDN == 0 && I % kDK == 0 && H % kDK == 0 &&
+         (size_t)T * 2 * I <= part_floats && (size_t)T * H <= part_floats;
+}
+
+void launch_dense_gate_up(const ExpertMats& m, int T, int H, int I, const float* x, float* act,
+                          Epi epi, int* status, float* part, size_t part_floats, hipStream_t s) {
+  const int S = dense_splits(T, 2 * I, H, part_floats);
+  const int blocks = ((T + kDM - 1) / kDM) * (2 * I / kDN) * S;
+  dense_gemm_kernel<<<(blocks + 7) / 8 * 8, 512, 0, s>>>(x, T, H, m.data[0], m.data[1], I,
+                                                        2 * I, S, part);
+  dense_reduce_gate_up_kernel<<<reduce_blocks((size_t)T * I), 256, 0, s>>>(part, T, I, S, epi,
+                                                                          act, status);
+}
+
+void launch_dense_down(const ExpertMats& m, int T, int H, int I, const float* act, float* out,
+                       Epi epi, int* status, float* part, size_t part_floats, hipStream_t s) {
+  const int S = dense_splits(T, H, I, part_floats);
+  const int blocks = ((T + kDM - 1) / kDM) * (H / kDN) * S;
+  dense_gemm_kernel<<<(blocks + 7) / 8 * 8, 512, 0, s>>>(act, T, I, m.data[2], m.data[2], H, H,
+                                                        S, part);
+  dense_reduce_down_kernel<<<reduce_blocks((size_t)T * H), 256, 0, s>>>(part, T, H, S, epi, out,
+                                                                      status);
+}
+
+}  // namespace urb

@@ -89,6 +89,7 @@ struct urb_moe_ctx {
   uint32_t hash_vocab = 0;
   ExpertMats* table = nullptr;         // device [E]
   ExpertMats* shared_table = nullptr;  // device [1]
+  ExpertMats shared_host{};            // the same pointers on the host
   // GLM batches with MX experts: the down projection runs on f16 MFMAs from row-scaled f16
   // activations (urb::Epi::rowexp) -- every down matrix's E8M0 codes keep its weights exact in
   // f16 (checked at create and by urb_moe_set_expert, which clears it otherwise)
@@ -445,6 +446,7 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
     }
   URB_HIP(hipMemcpy(c->table, table.data(), sizeof(ExpertMats) * E, hipMemcpyHostToDevice));
   URB_HIP(hipMemcpy(c->shared_table, &shared, sizeof(ExpertMats), hipMemcpyHostToDevice));
+  c->shared_host = shared;
 
   // ---- workspace
   Workspace unsized;
@@ -921,8 +923,15 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
         if (qwen)
           urb::launch_router_lane8(c->shared_gate8, 1, H, xc, n, ws.gate_logit, 1, ws.status,
                                    ss);
-        urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is, xc,
-                                 ws.shared_act, sepi, ws.status, ss, ss != s);
+        // in line (256+ tokens): the dense split-K kernel (urb_dense.hip), its partial sums in
+        // the routed outputs' buffer, which nothing reads until the routed down projection
+        const size_t part_floats = (size_t)c->chunk * K * H;
+        if (ss == s && d.shared_format == URB_FMT_BF16 && urb::dense_fits(n, Is, H, part_floats))
+          urb::launch_dense_gate_up(c->shared_host, n, H, Is, xc, ws.shared_act, sepi, ws.status,
+                                    ws.y_perm, part_floats, s);
+        else
+          urb::launch_gemm_gate_up(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                                   xc, ws.shared_act, sepi, ws.status, ss, ss != s);
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, ss);
