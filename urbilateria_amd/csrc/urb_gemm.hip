@@ -134,10 +134,17 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
           load_b<FMT, STREAM>(r1[slot][q], pd1 + q * pbytes, doff, ps1 + q * pscales, soff, s);
       }
     };
+    // Staging rows this tile's MFMA blocks read: NMB 16 of them.  The rest (a tile of <= 16
+    // tokens leaves rows 16..31, waves 2 and 3, idle) neither load nor stage.
+    auto staged = [&](int g) { return am + 32 * g < NMB * 16; };
+    auto fill = [&](AStage& a, int g, int k0) {
+      if (staged(g)) load_a(a, a_src[g], true, k0);
+    };
     auto stage = [&](AStage (&as)[RG], int buf) {
       bool any = false;
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
+        if (!staged(g)) continue;
         if constexpr (F16) store_a16(as[g], a_hi[buf], a_shift[g], am + 32 * g);
         else any |= store_a(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
       }
@@ -204,14 +211,14 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
     constexpr int U = (R % AD == 0) ? R : R * AD;
     AStage as[AD][RG];
 #pragma unroll
-    for (int g = 0; g < RG; ++g) load_a(as[0][g], a_src[g], true, 0);
+    for (int g = 0; g < RG; ++g) fill(as[0][g], g, 0);
     bool lo_any = barrier_or4(stage(as[0], 0), lo_flag[0]);
     if constexpr (AD > 1) {
 #pragma unroll
       for (int e = 1; e <= AD; ++e)
         if (e < steps)
 #pragma unroll
-          for (int g = 0; g < RG; ++g) load_a(as[e % AD][g], a_src[g], true, e * kKS);
+          for (int g = 0; g < RG; ++g) fill(as[e % AD][g], g, e * kKS);
     }
     for (int s0 = 0; s0 < steps; s0 += U) {
 #pragma unroll
@@ -223,7 +230,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
         if constexpr (AD == 1) {
           if (more) {
 #pragma unroll
-            for (int g = 0; g < RG; ++g) load_a(as[0][g], a_src[g], true, (s + 1) * kKS);
+            for (int g = 0; g < RG; ++g) fill(as[0][g], g, (s + 1) * kKS);
           }
         }
         // refill the slot step s - 1 used, DEPTH steps ahead
@@ -234,7 +241,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
           if (s + 1 + AD < steps)
 #pragma unroll
             for (int g = 0; g < RG; ++g)
-              load_a(as[(d + 1) % AD][g], a_src[g], true, (s + 1 + AD) * kKS);
+              fill(as[(d + 1) % AD][g], g, (s + 1 + AD) * kKS);
         }
       }
     }
