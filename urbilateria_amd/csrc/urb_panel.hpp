@@ -180,20 +180,33 @@ __device__ __forceinline__ float epi_down(const Epi& e, float y, bool& bad) {
 constexpr int kMT = kGemmMTile;   // 32 tokens: two 16-row MFMA blocks
 constexpr int kNT = kGemmNTile;   // 64 weight rows: one 16-row panel per wave
 constexpr int kKS = kGemmKStep;   // 128 k per step
-constexpr int kALd = kKS + 8;     // LDS row pitch in bf16 (16 B pad against bank conflicts)
+constexpr int kALd = kKS;         // LDS row pitch in bf16: 16 chunks of 8 values
 
+// A staged row is 16 chunks of 8 bf16 (16 B); chunk c of row m sits at chunk c ^ a_swizzle(m) of
+// the row.  Measured on MI355X (SQ_LDS_BANK_CONFLICT): 16-byte stores are conflict-free when each
+// 8 consecutive lanes write one row's chunks 0..7 (or 8..15), and the MFMA fragment reads of 16
+// rows at one chunk each (ds_read_b128) cost the same 4 cycles as any non-contiguous 16-byte read
+// pattern.  Without the swizzle those reads hit one bank group (the unpadded pitch: 28 cycles).
+__device__ __forceinline__ int a_swizzle(int m) {
+  const int r = (m >> 1) & 7;
+  return (r & 3) | ((r & 1) << 2) | ((r >> 2) << 3);
+}
 
+// bf16 offset of chunk c of staged row m
+__device__ __forceinline__ int a_chunk(int m, int c) {
+  return m * kALd + 8 * (c ^ a_swizzle(m));
+}
 
-
-// A staging: thread t covers row t/8 and 16 consecutive k at 16*(t%8) of the K step.
+// A staging: thread t covers row t/8 and the k chunks t%8 and 8 + t%8 of the K step (8 values
+// each: the eight threads of a row read its first 256 B, then its second).
 struct AStage { float4 v[4]; };
 
 __device__ __forceinline__ void load_a(AStage& a, const float* __restrict__ src, bool valid,
                                        int k0) {
-  const int kc = (threadIdx.x & 7) * 16;
+  const int c = threadIdx.x & 7;
   if (valid) {
-    const float4* p = reinterpret_cast<const float4*>(src + k0 + kc);
-    a.v[0] = p[0]; a.v[1] = p[1]; a.v[2] = p[2]; a.v[3] = p[3];
+    const float4* p = reinterpret_cast<const float4*>(src + k0);
+    a.v[0] = p[2 * c]; a.v[1] = p[2 * c + 1]; a.v[2] = p[16 + 2 * c]; a.v[3] = p[17 + 2 * c];
   } else {
     a.v[0] = a.v[1] = a.v[2] = a.v[3] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
@@ -217,7 +230,7 @@ __device__ __forceinline__ void split_bf16(float v0, float v1, uint32_t& hi, uin
 // row); returns whether any lo half is non-zero.
 __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
                                         int m = (int)(threadIdx.x >> 3)) {
-  const int kc = (threadIdx.x & 7) * 16;
+  const int c = threadIdx.x & 7;
   const float* v = reinterpret_cast<const float*>(a.v);
   uint32_t h[8], l[8], lor = 0;
 #pragma unroll
@@ -225,12 +238,11 @@ __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
     split_bf16(v[2 * i], v[2 * i + 1], h[i], l[i]);
     lor |= l[i];
   }
-  uint4* dh = reinterpret_cast<uint4*>(hi + m * kALd + kc);
-  uint4* dl = reinterpret_cast<uint4*>(lo + m * kALd + kc);
-  dh[0] = make_uint4(h[0], h[1], h[2], h[3]);
-  dh[1] = make_uint4(h[4], h[5], h[6], h[7]);
-  dl[0] = make_uint4(l[0], l[1], l[2], l[3]);
-  dl[1] = make_uint4(l[4], l[5], l[6], l[7]);
+  const int o0 = a_chunk(m, c), o1 = a_chunk(m, 8 + c);
+  *reinterpret_cast<uint4*>(hi + o0) = make_uint4(h[0], h[1], h[2], h[3]);
+  *reinterpret_cast<uint4*>(hi + o1) = make_uint4(h[4], h[5], h[6], h[7]);
+  *reinterpret_cast<uint4*>(lo + o0) = make_uint4(l[0], l[1], l[2], l[3]);
+  *reinterpret_cast<uint4*>(lo + o1) = make_uint4(l[4], l[5], l[6], l[7]);
   return (lor & 0x7fff7fffu) != 0;
 }
 
@@ -238,7 +250,7 @@ __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
 __device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,
                                           int m = (int)(threadIdx.x >> 3)) {
   typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
-  const int kc = (threadIdx.x & 7) * 16;
+  const int c = threadIdx.x & 7;
   const float* v = reinterpret_cast<const float*>(a.v);
   uint32_t h[8];
 #pragma unroll
@@ -246,9 +258,8 @@ __device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,
     h[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
                                             f32x2v{ldexpf(v[2 * i], e2), ldexpf(v[2 * i + 1], e2)},
                                             f16x2v));
-  uint4* d = reinterpret_cast<uint4*>(dst + m * kALd + kc);
-  d[0] = make_uint4(h[0], h[1], h[2], h[3]);
-  d[1] = make_uint4(h[4], h[5], h[6], h[7]);
+  *reinterpret_cast<uint4*>(dst + a_chunk(m, c)) = make_uint4(h[0], h[1], h[2], h[3]);
+  *reinterpret_cast<uint4*>(dst + a_chunk(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
 // A workgroup barrier that also ORs a per-thread flag over the four waves of a 256-thread
@@ -264,8 +275,9 @@ __device__ __forceinline__ bool barrier_or4(bool pred, int* slots) {
   return (v.x | v.y | v.z | v.w) != 0;
 }
 
+// The 8 staged values of row m at k (a multiple of 8).
 __device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + m * kALd + k));
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + a_chunk(m, k >> 3)));
 }
 
 template <int N>
