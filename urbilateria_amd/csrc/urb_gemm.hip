@@ -145,8 +145,8 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
         if (!staged(g)) continue;
-        if constexpr (F16) store_a16(as[g], a_hi[buf], a_shift[g], am + 32 * g);
-        else any |= store_a(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
+        if constexpr (F16) store_a16<MT>(as[g], a_hi[buf], a_shift[g], am + 32 * g);
+        else any |= store_a<MT>(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
       }
       return any;
     };
@@ -161,7 +161,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
           f16x8 ah[NMB];
 #pragma unroll
           for (int mb = 0; mb < NMB; ++mb)
-            ah[mb] = __builtin_bit_cast(f16x8, lds_frag(hi, mb * 16 + ln, kf));
+            ah[mb] = __builtin_bit_cast(f16x8, lds_frag<MT>(hi, mb * 16 + ln, kf));
 #pragma unroll
           for (int q = 0; q < NP; ++q) {
             const f16x8 f0 = decode_b16<FMT>(r0[slot][q], j);
@@ -179,8 +179,8 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
         bf16x8 ah[NMB], al[NMB];
 #pragma unroll
         for (int mb = 0; mb < NMB; ++mb) {
-          ah[mb] = lds_frag(hi, mb * 16 + ln, kf);
-          if (LO) al[mb] = lds_frag(lo, mb * 16 + ln, kf);
+          ah[mb] = lds_frag<MT>(hi, mb * 16 + ln, kf);
+          if (LO) al[mb] = lds_frag<MT>(lo, mb * 16 + ln, kf);
         }
         // one panel's operands decoded at a time: few registers live beside the ring
 #pragma unroll

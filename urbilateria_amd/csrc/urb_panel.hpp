@@ -180,21 +180,21 @@ __device__ __forceinline__ float epi_down(const Epi& e, float y, bool& bad) {
 constexpr int kMT = kGemmMTile;   // 32 tokens: two 16-row MFMA blocks
 constexpr int kNT = kGemmNTile;   // 64 weight rows: one 16-row panel per wave
 constexpr int kKS = kGemmKStep;   // 128 k per step
-constexpr int kALd = kKS;         // LDS row pitch in bf16: 16 chunks of 8 values
+constexpr int kALd = kKS;         // bf16 values per staged row: 16 chunks of 8
 
-// A staged row is 16 chunks of 8 bf16 (16 B); chunk c of row m sits at chunk c ^ a_swizzle(m) of
-// the row.  Measured on MI355X (SQ_LDS_BANK_CONFLICT): 16-byte stores are conflict-free when each
-// 8 consecutive lanes write one row's chunks 0..7 (or 8..15), and the MFMA fragment reads of 16
-// rows at one chunk each (ds_read_b128) cost the same 4 cycles as any non-contiguous 16-byte read
-// pattern.  Without the swizzle those reads hit one bank group (the unpadded pitch: 28 cycles).
-__device__ __forceinline__ int a_swizzle(int m) {
-  const int r = (m >> 1) & 7;
-  return (r & 3) | ((r & 1) << 2) | ((r >> 2) << 3);
-}
-
-// bf16 offset of chunk c of staged row m
+// LDS layout of MT staged rows: chunk c (8 bf16 at k = 8c, 16 B) of row m sits in the 128 B block
+// c * MT/8 + m/8, at position (m ^ h(c)) & 7 of the block, where h swaps bits 1 and 2 of c.
+// Measured on MI355X (SQ_LDS_BANK_CONFLICT over 35 lane patterns): 64 banks of 4 B; a 16-byte
+// read is served in four passes of 16 lanes, a pass being the lanes with equal lane bit 5 and
+// equal parity of lane bits 2-4, and is conflict-free when each pass hits 16 distinct 16 B bank
+// slots; a 16-byte store is conflict-free when each 8 consecutive lanes hit 8 distinct positions
+// mod 8.  MFMA fragment reads (row m = 16 mb + lane % 16 at chunk 4 (lane / 16) + j, or
+// 4 j + lane / 16 for BF16 weights) and staging stores (one row's chunks 0..7 or 8..15 per 8
+// lanes) then cost no extra cycles; row-major rows at any padding cost 4 per read.
+template <int MT>
 __device__ __forceinline__ int a_chunk(int m, int c) {
-  return m * kALd + 8 * (c ^ a_swizzle(m));
+  const int h = (c & 1) | ((c >> 1) & 2) | ((c << 1) & 4);
+  return 8 * ((c * (MT / 8) + (m >> 3)) * 8 + ((m ^ h) & 7));
 }
 
 // A staging: thread t covers row t/8 and the k chunks t%8 and 8 + t%8 of the K step (8 values
@@ -226,8 +226,9 @@ __device__ __forceinline__ void split_bf16(float v0, float v1, uint32_t& hi, uin
   lo = pk_bf16(v0 - u2f(hi << 16), v1 - u2f(hi & 0xffff0000u));
 }
 
-// Writes hi/lo BF16 halves of the staged values into LDS row m (default: this thread's staging
-// row); returns whether any lo half is non-zero.
+// Writes hi/lo BF16 halves of the staged values into LDS row m of MT (default: this thread's
+// staging row); returns whether any lo half is non-zero.
+template <int MT = kMT>
 __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
                                         int m = (int)(threadIdx.x >> 3)) {
   const int c = threadIdx.x & 7;
@@ -238,7 +239,7 @@ __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
     split_bf16(v[2 * i], v[2 * i + 1], h[i], l[i]);
     lor |= l[i];
   }
-  const int o0 = a_chunk(m, c), o1 = a_chunk(m, 8 + c);
+  const int o0 = a_chunk<MT>(m, c), o1 = a_chunk<MT>(m, 8 + c);
   *reinterpret_cast<uint4*>(hi + o0) = make_uint4(h[0], h[1], h[2], h[3]);
   *reinterpret_cast<uint4*>(hi + o1) = make_uint4(h[4], h[5], h[6], h[7]);
   *reinterpret_cast<uint4*>(lo + o0) = make_uint4(l[0], l[1], l[2], l[3]);
@@ -247,6 +248,7 @@ __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
 }
 
 // Writes the staged values times 2^e2 (exact) as f16 (round to nearest even) into LDS row m.
+template <int MT>
 __device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,
                                           int m = (int)(threadIdx.x >> 3)) {
   typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
@@ -258,8 +260,8 @@ __device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,
     h[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
                                             f32x2v{ldexpf(v[2 * i], e2), ldexpf(v[2 * i + 1], e2)},
                                             f16x2v));
-  *reinterpret_cast<uint4*>(dst + a_chunk(m, c)) = make_uint4(h[0], h[1], h[2], h[3]);
-  *reinterpret_cast<uint4*>(dst + a_chunk(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
+  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, c)) = make_uint4(h[0], h[1], h[2], h[3]);
+  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
 // A workgroup barrier that also ORs a per-thread flag over the four waves of a 256-thread
@@ -275,9 +277,10 @@ __device__ __forceinline__ bool barrier_or4(bool pred, int* slots) {
   return (v.x | v.y | v.z | v.w) != 0;
 }
 
-// The 8 staged values of row m at k (a multiple of 8).
+// The 8 staged values of row m (of MT) at k (a multiple of 8).
+template <int MT = kMT>
 __device__ __forceinline__ bf16x8 lds_frag(const u16* base, int m, int k) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + a_chunk(m, k >> 3)));
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + a_chunk<MT>(m, k >> 3)));
 }
 
 template <int N>
