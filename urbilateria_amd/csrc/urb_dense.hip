@@ -45,9 +45,10 @@ __device__ __forceinline__ const uint8_t* dense_panel(const uint8_t* w0, const u
 }
 
 // LDS position of A fragment unit u (lane u of the MFMA operand): units 32..63 swap their
-// halves of 8, so the two threads that stage one row (units u and u + 32 of a group of 16
-// lanes) write different banks; the reading lanes 32..47 still cover one contiguous 256 B.
-__device__ __forceinline__ int a_swz(int u) { return u ^ ((u >> 5) << 3); }
+// quarters of 4, so the 8 consecutive threads that stage four rows (units r and r + 32 for four
+// consecutive r) hit 8 distinct 16 B positions mod 8 (a conflict-free 16-byte store on MI355X),
+// while each 16-lane read pass still covers 16 distinct bank slots.
+__device__ __forceinline__ int a_swz(int u) { return u ^ ((u >> 5) << 2); }
 
 // Tile placement: work item w = m + Mt (n + Nt z) (m fastest, so the m tiles that read the
 // same weight rows and K range are consecutive); XCD c (block % 8) takes the contiguous run c of
