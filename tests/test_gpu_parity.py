@@ -640,8 +640,11 @@ def test_forward_is_deterministic_and_chunked_calls_equal_tokenwise():
     single = moe_mod().MoeLayer(host, max_tokens=1)
     for t in (0, 1023, 1024, 1099):
         ys, _, _ = single.forward(x[t:t + 1].contiguous())
-        # the single token takes the GEMV path, the batch the MFMA GEMM: f32 order differs
-        assert rel_l2(ys.cpu().numpy(), y1[t:t + 1].cpu().numpy()) < 1e-5
+        # the single token takes the GEMV path (f32 products of BF16 pieces, ~1e-6 of the
+        # oracle); the batch the MFMA GEMMs, whose MX down projection multiplies the SwiGLU rows
+        # rounded to f16 after a per-row power-of-two scale (2^-11 relative per element): the
+        # two agree within the layer's 1e-3 bar, not to f32 rounding
+        assert rel_l2(ys.cpu().numpy(), y1[t:t + 1].cpu().numpy()) < 1e-3
     layer.close()
     single.close()
 
