@@ -38,8 +38,10 @@ struct GemmLds {
 // One workgroup's tile: `w` (a row tile of the permutation, or dense tile w) times panel group
 // `group` of the weight rows.  NP panels per wave (the workgroup covers 4 NP panels = 64 NP
 // weight rows): every staged activation fragment feeds NP (x2 for gate+up) MFMAs.  MT tokens per
-// tile (32 or 64; 64 for large dense batches, so each weight byte feeds twice the MFMAs before
-// it is re-read).  F16 (the down projection of a batch with epi.rowexp): the rows are staged in
+// tile: 32 in every launch.  (The template also builds 64-token tiles, each weight byte feeding
+// twice the MFMAs before it is re-read; with the panels per wave halved to fit the registers they
+// measured slower, on dense batches and on the hot experts of a Zipf-routed 1024-token batch
+// alike.)  F16 (the down projection of a batch with epi.rowexp): the rows are staged in
 // f16 with their power-of-two scales and the MFMAs take f16 operands (see Epi).
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT, int AD, bool F16 = false>
 __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, const Perm& perm,
