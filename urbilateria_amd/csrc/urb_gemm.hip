@@ -124,9 +124,12 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
   // B registers: a ring of R = DEPTH + 1 step slots, the step loop unrolled R times so that
   // step s computes from slot s % R while slot (s + DEPTH) % R fills (no register copies).
   constexpr int R = DEPTH + 1;
-  auto body = [&](auto nmb, auto streamed) {
+  auto body = [&](auto nmb, auto streamed, auto dynamic_lo) {
     constexpr int NMB = decltype(nmb)::value;  // 16-token MFMA blocks this tile needs
     constexpr bool STREAM = decltype(streamed)::value;
+    // DYNLO: the lo halves may be non-zero, checked per K step; otherwise the rows are
+    // BF16-valued and only their hi halves are staged and multiplied
+    constexpr bool DYNLO = decltype(dynamic_lo)::value;
     BRaw<FMT> r0[R][NP], r1[R][NP];
     auto fetch = [&](int slot, int s) {
 #pragma unroll
@@ -148,13 +151,21 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
       for (int g = 0; g < RG; ++g) {
         if (!staged(g)) continue;
         if constexpr (F16) store_a16<MT>(as[g], a_hi[buf], a_shift[g], am + 32 * g);
-        else any |= store_a<MT>(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
+        else if constexpr (DYNLO) any |= store_a<MT>(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
+        else store_a_hi<MT>(as[g], a_hi[buf], am + 32 * g);
       }
       return any;
     };
+    // staging then the workgroup barrier; returns whether any lo half of the step is non-zero
+    auto publish = [&](AStage (&as)[RG], int buf) {
+      if constexpr (DYNLO) return barrier_or4(stage(as, buf), lo_flag[buf]);
+      stage(as, buf);
+      __syncthreads();
+      return false;
+    };
     // One K step from ring slot `slot`; the lo-half MFMAs only when some lo half is non-zero.
-    // (A uniform runtime branch: compiling both variants straight-line spills the MXFP4
-    // four-panel kernel.)
+    // (With DYNLO a uniform runtime branch around each MFMA pair: compiling both variants
+    // straight-line spills the MXFP4 four-panel kernel.  Without it the step is one basic block.)
     auto mma = [&](int slot, const u16* hi, const u16* lo, bool with_lo) {
       if constexpr (F16) {
 #pragma unroll
@@ -174,7 +185,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
         }
         return;
       }
-      const bool LO = with_lo;
+      const bool LO = DYNLO && with_lo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int kf = frag_k<FMT>(j, lq);
@@ -214,7 +225,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
     AStage as[AD][RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g) fill(as[0][g], g, 0);
-    bool lo_any = barrier_or4(stage(as[0], 0), lo_flag[0]);
+    bool lo_any = publish(as[0], 0);
     if constexpr (AD > 1) {
 #pragma unroll
       for (int e = 1; e <= AD; ++e)
@@ -238,7 +249,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
         // refill the slot step s - 1 used, DEPTH steps ahead
         if (s + DEPTH < steps) fetch((d + DEPTH) % R, s + DEPTH);
         mma(d % R, a_hi[buf], a_lo[buf], lo_any);
-        if (more) lo_any = barrier_or4(stage(as[(d + 1) % AD], buf ^ 1), lo_flag[buf ^ 1]);
+        if (more) lo_any = publish(as[(d + 1) % AD], buf ^ 1);
         if constexpr (AD > 1) {
           if (s + 1 + AD < steps)
 #pragma unroll
@@ -250,17 +261,23 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
   };
   using Stream = std::true_type;
   using Cached = std::false_type;
-  if constexpr (MT == 64) {
-    if (mrows > 32) body(Int<4>{}, Cached{});
-    else if (mrows > 16) body(Int<2>{}, Cached{});
-    else body(Int<1>{}, Cached{});
-  } else if (stream) {
-    if (mrows > 16) body(Int<2>{}, Stream{});
-    else body(Int<1>{}, Stream{});
-  } else {
-    if (mrows > 16) body(Int<2>{}, Cached{});
-    else body(Int<1>{}, Cached{});
-  }
+  auto run = [&](auto dyn) {
+    if constexpr (MT == 64) {
+      if (mrows > 32) body(Int<4>{}, Cached{}, dyn);
+      else if (mrows > 16) body(Int<2>{}, Cached{}, dyn);
+      else body(Int<1>{}, Cached{}, dyn);
+    } else if (stream) {
+      if (mrows > 16) body(Int<2>{}, Stream{}, dyn);
+      else body(Int<1>{}, Stream{}, dyn);
+    } else {
+      if (mrows > 16) body(Int<2>{}, Cached{}, dyn);
+      else body(Int<1>{}, Cached{}, dyn);
+    }
+  };
+  // BF16-valued rows (Epi::no_lo, or no lo half seen by this call's router, Epi::lo_word)
+  if constexpr (F16) run(std::false_type{});
+  else if (epi.no_lo || (epi.lo_word && *epi.lo_word != epi.lo_gen)) run(std::false_type{});
+  else run(std::true_type{});
 
   // ---- epilogue: lane holds column `row` of panel q, rows 4*lq + i of each 16-row block
   bool bad = false;

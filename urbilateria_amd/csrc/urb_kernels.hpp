@@ -65,11 +65,19 @@ enum { kEpiGated = 0, kEpiQwen = 1, kEpiHy4 = 2, kEpiHy4Shared = 3 };
 // group]); the down projection then stages each row in f16 scaled by a power of two so that
 // its largest value falls in [2^14, 2^15), runs one f16 MFMA per product and rescales the sums
 // exactly (11 significant bits of each activation instead of the 16 of the BF16 hi + lo pair).
+// no_lo: the projection's input rows are BF16-valued by construction (a Qwen38Expert's BF16
+// SwiGLU output, a simulated E4M3 activation, the normalized input of a block call), so the
+// grouped GEMM stages and multiplies their hi halves only.  lo_word / lo_gen: the same when the
+// batched router found every lo half of this call's input zero -- it stores lo_gen into
+// *lo_word when it sees a non-zero one (urb_route.hip, router_mfma_kernel).
 struct Epi {
   int kind;
   float limit;
   int* rowexp = nullptr;
   int groups = 0;
+  bool no_lo = false;
+  const unsigned* lo_word = nullptr;
+  unsigned lo_gen = 0;
 };
 // E8M0 codes whose scale keeps every element of an MX matrix exact in f16 (MXFP4: 6 2^13 is
 // the largest value and 0.5 2^-23 = 2^-24 the f16 grid; MXFP8: 448 2^7, 2^-9 2^-15).
@@ -180,8 +188,11 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
 __host__ __device__ inline int router_rows(int E) { return (E + kGemmNTile - 1) / kGemmNTile * kGemmNTile; }
 constexpr int kRouterMaxSlices = 16;
 int router_slices(int E, int H, int T);
+// lo_word (optional): set to lo_gen when some lo half of x's hi/lo BF16 split is non-zero (the
+// grouped GEMMs' Epi::lo_word test).
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
-                        int slices, int* status, hipStream_t s);
+                        int slices, int* status, hipStream_t s, unsigned* lo_word = nullptr,
+                        unsigned lo_gen = 0);
 // One token: the f64 partial slices part[z][0][e] of the row-major router [E, H] from a GEMV
 // (router_gemv_slices(E) slices, exact products summed in f64).
 int router_gemv_slices(int E);

@@ -55,6 +55,9 @@ struct Workspace {
   uint16_t* act_xp = nullptr;
   uint16_t* shared_xp = nullptr;
   int* status = nullptr;  // [0] latched numerical failures, [1] validation flags
+  // status + 4: the batched router's lo-half word (urb::Epi::lo_word), in the status block's
+  // allocation so that it stays the context's own in no-alloc calls
+  unsigned* lo_word = nullptr;
 };
 
 // Sequential bump allocator over one device allocation.
@@ -94,6 +97,7 @@ struct urb_moe_ctx {
   // activations (urb::Epi::rowexp) -- every down matrix's E8M0 codes keep its weights exact in
   // f16 (checked at create and by urb_moe_set_expert, which clears it otherwise)
   bool down_f16 = false;
+  unsigned lo_gen = 0;  // generation of the batched router's lo-half word, one per chunk
   Workspace ws;
   hipStream_t side = nullptr;          // shared expert runs here, concurrently with routing
   hipEvent_t fork = nullptr, join = nullptr;
@@ -245,7 +249,8 @@ static size_t rowexp_groups(const urb_moe_desc& d) {
 static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspace& w) {
   const urb_moe_desc& d = c->desc;
   const size_t C = chunk, E = d.n_experts, K = d.top_k, H = d.hidden, I = d.intermediate;
-  w.status = b.take<int>(4);
+  w.status = b.take<int>(8);
+  w.lo_word = reinterpret_cast<unsigned*>(w.status + 4);
   w.logits = b.take<float>(C * E);
   if (d.composition != URB_COMPOSE_QWEN36) {
     size_t most = 0;  // largest slices x tokens any call can need
@@ -562,7 +567,7 @@ static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
     rp.slices = urb::router_slices(E, H, n);
     rp.part = c->ws.router_part;
     urb::launch_router_mfma(c->router_panel, E, H, x, n, c->ws.router_part, rp.slices,
-                            c->ws.status, s);
+                            c->ws.status, s, c->ws.lo_word, c->lo_gen);
   }
   return rp;
 }
@@ -778,10 +783,13 @@ static urb_status forward_mx(urb_moe_ctx* c, const float* xc, const uint32_t* to
   const bool dsv = d.composition == URB_COMPOSE_DSV41 || d.composition == URB_COMPOSE_DSV4;
   hipStream_t ss = shared_stream(c, n, s, true);
   const int block = d.composition == URB_COMPOSE_DSV4 ? 128 : 32;  // activation block width
-  const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
+  // every projection's input is simulated E4M3 (4 significant bits, scales >= 2^-22): BF16-valued
+  urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
+  routed.no_lo = true;
   // Hy4's shared DenseMlp is a plain BF16 SwiGLU; DeepSeek's shared expert is a routed expert
   // without a weight
-  const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
+  urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
+  dense_mlp.no_lo = true;
   // mx_activation(input) once per token (runtime.rs:1397); the shared expert quantizes the same
   // input the same way (runtime.rs:1312), so both read it.
   urb::launch_quantize(xc, (size_t)n, (size_t)H, ws.xq, nullptr, nullptr, ws.status, s, 0,
@@ -892,6 +900,8 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
     // The routing and the permutation; with a shared expert in line (batches of 256+ tokens),
     // they run beside it on the side stream instead, and the routed GEMMs wait for both.
     const bool route_beside = has_shared && ss == s;
+    // this chunk's generation of the batched router's lo-half word
+    const unsigned lo_gen = ++c->lo_gen;
     Perm perm{ws.meta, ws.active, ws.offsets, ws.counts, ws.perm_token, 0, ws.tiles, nullptr, K};
     auto route_and_permute = [&](hipStream_t rs) {
       route_chunk(c, xc, tc, n, ws.logits, idc, wc, rs);
@@ -915,7 +925,12 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
         URB_HIP(hipEventRecord(c->fork, s));
         URB_HIP(hipStreamWaitEvent(ss, c->fork, 0));
       }
-      const urb::Epi sepi = qwen ? epi : gated;
+      // the shared gate/up reads the (normalized BF16) block input; a Qwen38Expert's down
+      // reads its BF16 SwiGLU rows
+      urb::Epi sepi = qwen ? epi : gated;
+      urb::Epi sdepi = sepi;
+      sepi.no_lo = blk != nullptr;
+      sdepi.no_lo = qwen;
       Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
       const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
       {
@@ -936,7 +951,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       {
         Span span(c, URB_STAGE_SHARED_DOWN, ss);
         urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                              ws.shared_act, ws.shared_out, sepi, ws.status, ss, ss != s);
+                              ws.shared_act, ws.shared_out, sdepi, ws.status, ss, ss != s);
       }
       if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
     }
@@ -950,16 +965,26 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       repi.rowexp = ws.rowexp;
       repi.groups = (int)rowexp_groups(d);
     }
+    // Which activation rows are BF16-valued: a block call's normalized input, a Qwen38Expert's
+    // SwiGLU rows; otherwise the token input when the batched router saw no non-zero lo half.
+    urb::Epi gepi = repi, depi = repi;
+    if (blk) {
+      gepi.no_lo = true;
+    } else if (!c->router_lane8) {
+      gepi.lo_word = ws.lo_word;
+      gepi.lo_gen = lo_gen;
+    }
+    depi.no_lo = qwen;
     // grouped MFMA GEMMs over the row tiles
     {
       Span span(c, URB_STAGE_GATE_UP, s);
       urb::launch_gemm_gate_up(d.expert_format, c->table, perm, max_tiles, H, I, xc, ws.act,
-                               repi, ws.status, s);
+                               gepi, ws.status, s);
     }
     {
       Span span(c, URB_STAGE_DOWN, s);
       urb::launch_gemm_down(d.expert_format, c->table, perm, max_tiles, H, I, ws.act, ws.y_perm,
-                            repi, ws.status, s);
+                            depi, ws.status, s);
     }
     if (has_shared && ss != s) URB_HIP(hipStreamWaitEvent(s, c->join, 0));
     {
@@ -1001,6 +1026,7 @@ urb_status urb_moe_forward_noalloc(urb_moe_ctx* c, const float* x, uint32_t toke
   Bump b{static_cast<char*>(region)};
   carve_workspace(c, b, tokens, ws);
   ws.status = c->ws.status;  // failures still latch in the context's status word
+  ws.lo_word = c->ws.lo_word;
   const Workspace own = c->ws;
   const uint32_t chunk = c->chunk;
   c->ws = ws;

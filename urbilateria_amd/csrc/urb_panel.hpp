@@ -247,6 +247,20 @@ __device__ __forceinline__ bool store_a(const AStage& a, u16* hi, u16* lo,
   return (lor & 0x7fff7fffu) != 0;
 }
 
+// Writes the BF16 (round to nearest even) of the staged values into LDS row m: the hi halves
+// alone, for rows whose values are BF16 already.
+template <int MT = kMT>
+__device__ __forceinline__ void store_a_hi(const AStage& a, u16* hi,
+                                           int m = (int)(threadIdx.x >> 3)) {
+  const int c = threadIdx.x & 7;
+  const float* v = reinterpret_cast<const float*>(a.v);
+  uint32_t h[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = pk_bf16(v[2 * i], v[2 * i + 1]);
+  *reinterpret_cast<uint4*>(hi + a_chunk<MT>(m, c)) = make_uint4(h[0], h[1], h[2], h[3]);
+  *reinterpret_cast<uint4*>(hi + a_chunk<MT>(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
+}
+
 // Writes the staged values times 2^e2 (exact) as f16 (round to nearest even) into LDS row m.
 template <int MT>
 __device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,

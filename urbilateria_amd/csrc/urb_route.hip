@@ -942,7 +942,8 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
                                                              const float* __restrict__ x,
                                                              int T, int slice,
                                                              double* __restrict__ part,
-                                                             int* status) {
+                                                             int* status, unsigned* lo_word,
+                                                             unsigned lo_gen) {
   __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
   __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
   __shared__ __attribute__((aligned(16))) int lo_flag[2][4];  // per staging buffer, per wave
@@ -980,6 +981,7 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
     load_a(as, a_src, a_valid, s_begin * kKS);
     check(as);
     bool lo_any = barrier_or4(store_a(as, a_hi[0], a_lo[0]), lo_flag[0]);
+    bool saw_lo = lo_any;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = s_begin; s0 < s_end; s0 += DEPTH) {
 #pragma unroll
@@ -1009,9 +1011,12 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
         if (more) {
           check(as);
           lo_any = barrier_or4(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]), lo_flag[buf ^ 1]);
+          saw_lo |= lo_any;
         }
       }
     }
+    // the workgroup's rows had a non-zero lo half: the grouped GEMMs of this call keep theirs
+    if (saw_lo && lo_word && threadIdx.x == 0) *lo_word = lo_gen;
   };
   if (mrows > 16) body(Int<2>{});
   else body(Int<1>{});
@@ -1089,11 +1094,13 @@ void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, dou
 }
 
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
-                        int slices, int* status, hipStream_t s) {
+                        int slices, int* status, hipStream_t s, unsigned* lo_word,
+                        unsigned lo_gen) {
   const int steps = H / kKS;
   const int per = (steps + slices - 1) / slices;
   dim3 grid(router_rows(E) / kNT, (T + kMT - 1) / kMT, slices);
-  router_mfma_kernel<4><<<grid, 256, 0, s>>>(wp, router_rows(E), H, x, T, per, part, status);
+  router_mfma_kernel<4><<<grid, 256, 0, s>>>(wp, router_rows(E), H, x, T, per, part, status,
+                                             lo_word, lo_gen);
 }
 
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s) {
