@@ -178,9 +178,11 @@ struct RouteJob {
 // computed in the same launch below 64 tokens.
 // xq: the token's piece vector (xp, one token) as the hi/lo split of x (0) or as
 // simulate_e4m3_activation in blocks of xq = 32 or 128 values (the MX-activation compositions).
+// lo_word (optional): set to lo_gen when some value of x is not BF16 (as launch_router_mfma).
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int round_bf16, int* status, hipStream_t s, uint16_t* xp = nullptr,
-                         const uint16_t* w8b = nullptr, float* logits_b = nullptr, int xq = 0);
+                         const uint16_t* w8b = nullptr, float* logits_b = nullptr, int xq = 0,
+                         unsigned* lo_word = nullptr, unsigned lo_gen = 0);
 
 // GLM router logits: MFMA BF16 with f64 accumulation of 32-k partials, split over K into
 // f64 partial slices.  The router weight is packed in the panel layout with router_rows(E)

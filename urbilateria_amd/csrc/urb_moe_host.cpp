@@ -556,7 +556,7 @@ static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
     // gate_logit: the Qwen3.6 shared-expert gate row in the same launch
     urb::launch_router_lane8(c->router_lane8, E, H, x, n, logits, qwen ? 1 : 0, c->ws.status, s,
                              n == 1 ? xp : nullptr, gate_logit ? c->shared_gate8 : nullptr,
-                             gate_logit, xq);
+                             gate_logit, xq, c->ws.lo_word, c->lo_gen);
   } else if (n == 1) {
     // one token: a GEMV over the row-major router beats the 32-token MFMA tile
     rp.slices = urb::router_gemv_slices(E);
@@ -966,11 +966,11 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       repi.groups = (int)rowexp_groups(d);
     }
     // Which activation rows are BF16-valued: a block call's normalized input, a Qwen38Expert's
-    // SwiGLU rows; otherwise the token input when the batched router saw no non-zero lo half.
+    // SwiGLU rows; otherwise the token input when the router saw no value off the BF16 grid.
     urb::Epi gepi = repi, depi = repi;
     if (blk) {
       gepi.no_lo = true;
-    } else if (!c->router_lane8) {
+    } else {
       gepi.lo_word = ws.lo_word;
       gepi.lo_gen = lo_gen;
     }

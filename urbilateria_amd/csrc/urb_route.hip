@@ -79,7 +79,7 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
     const uint16_t* __restrict__ w8, int E, int H, const float* __restrict__ x, int T,
     float* __restrict__ logits, int round_bf16, int* status, uint16_t* __restrict__ xp,
     const uint16_t* __restrict__ w8b = nullptr, float* __restrict__ logits_b = nullptr,
-    int xq = 0) {
+    int xq = 0, unsigned* lo_word = nullptr, unsigned lo_gen = 0) {
   // [tok][8][H8 + 4] transposed chains: the pad of 4 floats puts the 8 chains of a column in
   // different LDS banks and keeps 16-byte alignment.  H is a multiple of 128.
   extern __shared__ float xs[];
@@ -107,8 +107,9 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
       ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d) * 512);
       ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d + 1) * 512);
     }
-  // Stage x with coalesced float4 loads, transposed into per-lane chains.
-  bool bad = false;
+  // Stage x with coalesced float4 loads, transposed into per-lane chains.  `lo`: some value is
+  // not BF16 (its hi/lo BF16 split, the grouped GEMMs' staging, has a non-zero lo half).
+  bool bad = false, lo = false;
   const int n4 = nt * H / 4;
   for (int i = threadIdx.x; i < n4; i += 64 * WAVES) {
     const float4 v4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H)[i];
@@ -119,10 +120,12 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
       // MI355X, the division in this loop was 0.5-0.7 of the one-token router's 6.8 us)
       const int flat = 4 * i + u, tt = kLane8Tokens == 1 ? 0 : flat / H, c = flat - tt * H;
       bad |= !finite(vv[u]);
+      lo |= (__float_as_uint(vv[u]) & 0xffffu) != 0;
       xs[(tt * 8 + (c & 7)) * H8p + (c >> 3)] = vv[u];
     }
   }
   if (bad) flag(status, kStatusNonFinite);
+  if (lo_word && __ballot(lo) != 0 && lane == 0) *lo_word = lo_gen;
   // one token: the workgroups also write its piece vector (the decode GEMVs' input)
   if (xp && T == 1)
     token_pieces(x, H, xp, xq, status, blockIdx.x * blockDim.x + threadIdx.x,
@@ -188,7 +191,8 @@ constexpr int kLane8ChunkBatches = 4;  // 16-element chain batches per staged x 
 template <int TB>
 __global__ __launch_bounds__(256) void router_lane8_tiled_kernel(
     const uint16_t* __restrict__ w8, int E, int H, const float* __restrict__ x, int T,
-    float* __restrict__ logits, int round_bf16, int* status) {
+    float* __restrict__ logits, int round_bf16, int* status, unsigned* lo_word,
+    unsigned lo_gen) {
   constexpr int CP = 16 * kLane8ChunkBatches + 4;  // chunk chain pitch (4-float pad)
   __shared__ __attribute__((aligned(16))) float xs[TB * 8 * CP];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(256) void router_lane8_tiled_kernel(
   float acc[TB];
 #pragma unroll
   for (int tt = 0; tt < TB; ++tt) acc[tt] = 0.0f;
-  bool bad = false;
+  bool bad = false, lo = false;  // lo: some value is not BF16 (router_lane8_kernel)
   for (int b0 = 0; b0 < nb; b0 += 8) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -230,6 +234,7 @@ __global__ __launch_bounds__(256) void router_lane8_tiled_kernel(
         for (int u = 0; u < 4; ++u) {
           const int c = c0 + u;
           bad |= !finite(vv[u]);
+          lo |= (__float_as_uint(vv[u]) & 0xffffu) != 0;
           xs[(tt * 8 + (c & 7)) * CP + (c >> 3)] = vv[u];
         }
       }
@@ -264,6 +269,7 @@ __global__ __launch_bounds__(256) void router_lane8_tiled_kernel(
     }
   }
   if (bad) flag(status, kStatusNonFinite);
+  if (lo_word && __ballot(lo) != 0 && lane == 0) *lo_word = lo_gen;
   if (!live) return;
   const int base = el * 8;
 #pragma unroll
@@ -1112,14 +1118,16 @@ void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStr
 
 void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T, float* logits,
                          int round_bf16, int* status, hipStream_t s, uint16_t* xp,
-                         const uint16_t* w8b, float* logits_b, int xq) {
+                         const uint16_t* w8b, float* logits_b, int xq, unsigned* lo_word,
+                         unsigned lo_gen) {
   const size_t per_tok = (size_t)8 * (H / 8 + 4) * sizeof(float);
   if (T < 64) {
     // One token per 64-thread workgroup: the most independent waves.  Each workgroup streams
     // its 8 experts' chains from L2, so the traffic grows with T x E x H ...
     const int gx = (E + 7) / 8 + (w8b ? 1 : 0);
     router_lane8_kernel<1><<<dim3(gx, T), 64, per_tok, s>>>(w8, E, H, x, T, logits, round_bf16,
-                                                            status, xp, w8b, logits_b, xq);
+                                                            status, xp, w8b, logits_b, xq,
+                                                            lo_word, lo_gen);
     return;
   }
   if (w8b) {
@@ -1135,13 +1143,17 @@ void launch_router_lane8(const uint16_t* w8, int E, int H, const float* x, int T
   const int eg = (E + 31) / 32;
   if (T <= 512)
     router_lane8_kernel<1, 4><<<dim3(eg, T), 256, per_tok, s>>>(w8, E, H, x, T, logits,
-                                                                round_bf16, status, nullptr);
+                                                                round_bf16, status, nullptr,
+                                                                nullptr, nullptr, 0, lo_word,
+                                                                lo_gen);
   else if ((long)eg * ((T + 15) / 16) >= 256)
     router_lane8_tiled_kernel<16><<<dim3(eg, (T + 15) / 16), 256, 0, s>>>(w8, E, H, x, T, logits,
-                                                                        round_bf16, status);
+                                                                        round_bf16, status,
+                                                                        lo_word, lo_gen);
   else
     router_lane8_tiled_kernel<8><<<dim3(eg, (T + 7) / 8), 256, 0, s>>>(w8, E, H, x, T, logits,
-                                                                     round_bf16, status);
+                                                                     round_bf16, status,
+                                                                     lo_word, lo_gen);
 }
 
 template <int EPL>
