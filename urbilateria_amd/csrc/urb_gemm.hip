@@ -171,17 +171,17 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int kf = frag_k<FMT>(j, lq);
-          f16x8 ah[NMB];
+          f16x8 ah[NMB], bh[NP];
 #pragma unroll
           for (int mb = 0; mb < NMB; ++mb)
             ah[mb] = __builtin_bit_cast(f16x8, lds_frag<MT>(hi, mb * 16 + ln, kf));
 #pragma unroll
-          for (int q = 0; q < NP; ++q) {
-            const f16x8 f0 = decode_b16<FMT>(r0[slot][q], j);
+          for (int q = 0; q < NP; ++q) bh[q] = decode_b16<FMT>(r0[slot][q], j);
+#pragma unroll
+          for (int q = 0; q < NP; ++q)
 #pragma unroll
             for (int mb = 0; mb < NMB; ++mb)
-              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mb], f0, acc0[q][mb], 0, 0, 0);
-          }
+              acc0[q][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[mb], bh[q], acc0[q][mb], 0, 0, 0);
         }
         return;
       }
