@@ -13,6 +13,8 @@ namespace urb {
 //   c = bf16(w * y), acc = bf16(acc + c), acc from +0.0.
 // GLM (src/models/glm/runtime/moe.rs:162-171): acc = f64(shared) (or 0), then in ranking
 //   order acc += f64(w) * f64(y); out = f32(acc).
+// Every input row is read once and the output is not read back by this call, so both go
+// through non-temporal loads and stores (C5's GLM combine 54 -> 50 us).
 // ------------------------------------------------------------------------------------------
 template <int KMAX>
 __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restrict__ y,
@@ -39,7 +41,7 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
     if (j < K) {
       wt[j] = w[(size_t)t * K + rk[j]];
       const int p = pos ? pos[(size_t)t * K + rk[j]] : rk[j];
-      v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
+      v[j] = u2f4(ldg16_stream(y + (size_t)p * H + 4 * h4));
     }
   }
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -61,7 +63,7 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
     // the gated shared expert, added last (src/models/qwen3_6/runtime.rs:1449-1461):
     // c = bf16(scale * s), acc = bf16(acc + c)
     const float sc = qwen_shared_scale(gate[t], bad);
-    const float4 s4 = reinterpret_cast<const float4*>(shared + (size_t)t * H)[h4];
+    const float4 s4 = u2f4(ldg16_stream(shared + (size_t)t * H + 4 * h4));
     const float ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -73,7 +75,7 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
   }
   if (res) {
     // add_residual with BF16 activations (src/models/qwen3_6/runtime.rs:1470-1494)
-    const float4 r4 = reinterpret_cast<const float4*>(res + (size_t)t * H)[h4];
+    const float4 r4 = u2f4(ldg16_stream(res + (size_t)t * H + 4 * h4));
     const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restri
     }
   }
   if (bad) flag(status, kStatusNonFinite);
-  reinterpret_cast<float4*>(out + (size_t)t * H)[h4] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  stg16_stream(out + (size_t)t * H + 4 * h4, make_float4(acc[0], acc[1], acc[2], acc[3]));
 }
 
 template <int KMAX>
@@ -102,12 +104,12 @@ __global__ __launch_bounds__(256) void combine_glm_kernel(const float* __restric
     if (j < K) {
       wt[j] = w[(size_t)t * K + j];
       const int p = pos ? pos[(size_t)t * K + j] : j;
-      v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
+      v[j] = u2f4(ldg16_stream(y + (size_t)p * H + 4 * h4));
     }
   }
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
   if (shared) {
-    const float4 s = reinterpret_cast<const float4*>(shared + (size_t)t * H)[h4];
+    const float4 s = u2f4(ldg16_stream(shared + (size_t)t * H + 4 * h4));
     acc[0] = s.x; acc[1] = s.y; acc[2] = s.z; acc[3] = s.w;
   }
 #pragma unroll
@@ -120,8 +122,8 @@ __global__ __launch_bounds__(256) void combine_glm_kernel(const float* __restric
       acc[3] += wd * (double)v[j].w;
     }
   }
-  reinterpret_cast<float4*>(out + (size_t)t * H)[h4] =
-      make_float4((float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]);
+  stg16_stream(out + (size_t)t * H + 4 * h4,
+               make_float4((float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]));
 }
 
 void launch_combine_qwen(const float* y_perm, const int32_t* pos_of_slot, const float* weights,

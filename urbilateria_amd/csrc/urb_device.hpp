@@ -31,6 +31,16 @@ __device__ __forceinline__ uint4 ldg16_stream(const void* p) {
       __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)p);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ float4 u2f4(uint4 u) {
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                     __uint_as_float(u.w));
+}
+// Non-temporal store of 16 bytes (outputs no kernel of the same call reads back soon).
+__device__ __forceinline__ void stg16_stream(void* p, float4 v) {
+  const u32x4_t u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                     __float_as_uint(v.w)};
+  __builtin_nontemporal_store(u, (__attribute__((address_space(1))) u32x4_t*)p);
+}
 __device__ __forceinline__ uint32_t ldg_u8(const void* p) {
   return *(const __attribute__((address_space(1))) uint8_t*)p;
 }
