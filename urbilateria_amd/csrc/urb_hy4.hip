@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void combine_hy4_kernel(const float* __restric
     if (j < K) {
       wt[j] = w ? w[(size_t)t * K + rk[j]] : 1.0f;
       const int p = pos ? pos[(size_t)t * K + rk[j]] : rk[j];
-      v[j] = reinterpret_cast<const float4*>(y + (size_t)p * H)[h4];
+      v[j] = u2f4(ldg16_stream(y + (size_t)p * H + 4 * h4));
     }
   }
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void combine_hy4_kernel(const float* __restric
     }
   }
   if (shared) {
-    const float4 sh = reinterpret_cast<const float4*>(shared + (size_t)t * H)[h4];
+    const float4 sh = u2f4(ldg16_stream(shared + (size_t)t * H + 4 * h4));
     acc[0] = acc[0] + sh.x;
     acc[1] = acc[1] + sh.y;
     acc[2] = acc[2] + sh.z;
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void combine_hy4_kernel(const float* __restric
       r[u] = acc[u];
     }
   if (bad) flag(status, kStatusNonFinite);
-  reinterpret_cast<float4*>(out + (size_t)t * H)[h4] = make_float4(r[0], r[1], r[2], r[3]);
+  stg16_stream(out + (size_t)t * H + 4 * h4, make_float4(r[0], r[1], r[2], r[3]));
 }
 
 void launch_combine_hy4(const float* y_perm, const int32_t* pos_of_slot, const float* weights,
