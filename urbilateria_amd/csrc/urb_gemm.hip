@@ -302,10 +302,11 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
           const float a = epi_gate_up(epi, acc0[q][mb][i], acc1[q][mb][i], bad);
           out[p * rows + row] = a;
           ex[mb][i] = max(ex[mb][i], (int)((__float_as_uint(a) >> 23) & 0xffu));
-        } else if constexpr (F16) {
-          out[p * rows + row] = epi_down<FMT>(epi, ldexpf(acc0[q][mb][i], -lds.rexp[mm]), bad);
         } else {
-          out[p * rows + row] = epi_down<FMT>(epi, acc0[q][mb][i], bad);
+          const float v = F16 ? epi_down<FMT>(epi, ldexpf(acc0[q][mb][i], -lds.rexp[mm]), bad)
+                              : epi_down<FMT>(epi, acc0[q][mb][i], bad);
+          if (epi.stream_out) __builtin_nontemporal_store(v, &out[p * rows + row]);
+          else out[p * rows + row] = v;
         }
       }
     }

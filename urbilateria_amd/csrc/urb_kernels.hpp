@@ -70,6 +70,9 @@ enum { kEpiGated = 0, kEpiQwen = 1, kEpiHy4 = 2, kEpiHy4Shared = 3 };
 // grouped GEMM stages and multiplies their hi halves only.  lo_word / lo_gen: the same when the
 // batched router found every lo half of this call's input zero -- it stores lo_gen into
 // *lo_word when it sees a non-zero one (urb_route.hip, router_mfma_kernel).
+// stream_out (down projections): the outputs are read once, by the combine at the end of the
+// call, so they are stored non-temporally and do not hold L2 lines during the GEMMs between
+// (the shared expert's down rows of a batch).
 struct Epi {
   int kind;
   float limit;
@@ -78,6 +81,7 @@ struct Epi {
   bool no_lo = false;
   const unsigned* lo_word = nullptr;
   unsigned lo_gen = 0;
+  bool stream_out = false;
 };
 // E8M0 codes whose scale keeps every element of an MX matrix exact in f16 (MXFP4: 6 2^13 is
 // the largest value and 0.5 2^-23 = 2^-24 the f16 grid; MXFP8: 448 2^7, 2^-9 2^-15).

@@ -931,6 +931,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       urb::Epi sdepi = sepi;
       sepi.no_lo = blk != nullptr;
       sdepi.no_lo = qwen;
+      sdepi.stream_out = true;  // read only by the combine, after the routed GEMMs
       Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
       const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
       {
