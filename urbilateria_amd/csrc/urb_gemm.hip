@@ -89,25 +89,30 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
   // epilogue never stores, and the loads need no mask.
   const int am = threadIdx.x >> 3;
   const float* a_src[RG];
+  const u16* a16[RG];  // F16: the rows as f16 (the gate/up epilogue's output)
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const int r = am + 32 * g < mrows ? am + 32 * g : 0;
     const int p = base + m0 + r;
     const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
     a_src[g] = in + (size_t)src_row * K;
+    a16[g] = reinterpret_cast<const u16*>(in) + (size_t)src_row * K;
   }
-  // F16: each staged row's exponent shift, 141 - (largest exponent field of the row over the
-  // gate/up panel groups), which takes the row's largest |value| into [2^14, 2^15)
-  int a_shift[RG];
+  // F16: each staged row's largest exponent field over the gate/up panel groups (rowexp); the
+  // row is staged times 2^(141 - that), which takes its largest |value| into [2^14, 2^15).  Its
+  // f16 values are stored at the scale of their own group (e of the group instead).
+  int a_emax[RG];
+  const int* a_gex[RG];
+  const int gw = F16 ? K / epi.groups : 1;  // columns per panel group
   if constexpr (F16) {
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
       const int r = am + 32 * g < mrows ? am + 32 * g : 0;
-      const int* ex = epi.rowexp + (size_t)(base + m0 + r) * epi.groups;
+      a_gex[g] = epi.rowexp + (size_t)(base + m0 + r) * epi.groups;
       int e = 0;
-      for (int gg = 0; gg < epi.groups; ++gg) e = max(e, ex[gg]);
-      a_shift[g] = 141 - e;
-      if ((threadIdx.x & 7) == 0) lds.rexp[am + 32 * g] = a_shift[g];
+      for (int gg = 0; gg < epi.groups; ++gg) e = max(e, a_gex[g][gg]);
+      a_emax[g] = e;
+      if ((threadIdx.x & 7) == 0) lds.rexp[am + 32 * g] = 141 - e;
     }
   }
 
@@ -142,22 +147,26 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
     // Staging rows this tile's MFMA blocks read: NMB 16 of them.  The rest (a tile of <= 16
     // tokens leaves rows 16..31, waves 2 and 3, idle) neither load nor stage.
     auto staged = [&](int g) { return am + 32 * g < NMB * 16; };
-    auto fill = [&](AStage& a, int g, int k0) {
-      if (staged(g)) load_a(a, a_src[g], true, k0);
+    using Stage = std::conditional_t<F16, AStage16, AStage>;
+    auto fill = [&](Stage& a, int g, int k0) {
+      if (staged(g)) {
+        if constexpr (F16) load_a16(a, a16[g], a_gex[g], gw, k0);
+        else load_a(a, a_src[g], true, k0);
+      }
     };
-    auto stage = [&](AStage (&as)[RG], int buf) {
+    auto stage = [&](Stage (&as)[RG], int buf) {
       bool any = false;
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
         if (!staged(g)) continue;
-        if constexpr (F16) store_a16<MT>(as[g], a_hi[buf], a_shift[g], am + 32 * g);
+        if constexpr (F16) store_a16g<MT>(as[g], a_hi[buf], a_emax[g], am + 32 * g);
         else if constexpr (DYNLO) any |= store_a<MT>(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
         else store_a_hi<MT>(as[g], a_hi[buf], am + 32 * g);
       }
       return any;
     };
     // staging then the workgroup barrier; returns whether any lo half of the step is non-zero
-    auto publish = [&](AStage (&as)[RG], int buf) {
+    auto publish = [&](Stage (&as)[RG], int buf) {
       if constexpr (DYNLO) return barrier_or4(stage(as, buf), lo_flag[buf]);
       stage(as, buf);
       __syncthreads();
@@ -222,7 +231,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
     // staged in LDS (at the end of step t - 1); the step loop is unrolled lcm(R, AD) times so
     // both rings are indexed by compile-time slots
     constexpr int U = (R % AD == 0) ? R : R * AD;
-    AStage as[AD][RG];
+    Stage as[AD][RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g) fill(as[0][g], g, 0);
     bool lo_any = publish(as[0], 0);
@@ -281,7 +290,10 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
 
   // ---- epilogue: lane holds column `row` of panel q, rows 4*lq + i of each 16-row block
   bool bad = false;
-  // gate/up with rowexp: the largest exponent field of each token row's activations here
+  // gate/up with rowexp (the input of an f16 down projection): the largest exponent field e of
+  // each token row's activations in this panel group first, then the activations as f16 times
+  // 2^(141 - e) (the group's largest |value| in [2^14, 2^15)); the down projection rescales
+  // each group to its row's largest e as it stages the row
   const bool rowmax = PAIR && epi.rowexp != nullptr;
   int ex[MBMAX][4];
 #pragma unroll
@@ -300,8 +312,12 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
         const size_t p = (size_t)(base + m0 + mm);
         if constexpr (PAIR) {
           const float a = epi_gate_up(epi, acc0[q][mb][i], acc1[q][mb][i], bad);
-          out[p * rows + row] = a;
-          ex[mb][i] = max(ex[mb][i], (int)((__float_as_uint(a) >> 23) & 0xffu));
+          if (rowmax) {
+            acc0[q][mb][i] = a;
+            ex[mb][i] = max(ex[mb][i], (int)((__float_as_uint(a) >> 23) & 0xffu));
+          } else {
+            out[p * rows + row] = a;
+          }
         } else {
           const float v = F16 ? epi_down<FMT>(epi, ldexpf(acc0[q][mb][i], -lds.rexp[mm]), bad)
                               : epi_down<FMT>(epi, acc0[q][mb][i], bad);
@@ -329,6 +345,20 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
         for (int i = 0; i < 4; ++i) atomicMax(&lds.rexp[mb * 16 + 4 * lq + i], ex[mb][i]);
     }
     __syncthreads();
+    u16* out16 = reinterpret_cast<u16*>(out);
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int row = (panel0 + q) * kPanelRows + ln;
+#pragma unroll
+      for (int mb = 0; mb < MBMAX; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int mm = mb * 16 + 4 * lq + i;
+          if (mm >= mrows) continue;
+          const _Float16 h = (_Float16)ldexpf(acc0[q][mb][i], 141 - lds.rexp[mm]);
+          out16[(size_t)(base + m0 + mm) * rows + row] = __builtin_bit_cast(u16, h);
+        }
+    }
     if ((int)threadIdx.x < mrows)
       epi.rowexp[(size_t)(base + m0 + threadIdx.x) * epi.groups + group] = lds.rexp[threadIdx.x];
   }

@@ -278,6 +278,38 @@ __device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,
   *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
+// f16 activation rows (the f16 down projection's input, written by the gate/up epilogue at the
+// scale of each row's panel group): thread c of row m loads chunks c and 8 + c of the K step at
+// k0, and the exponent field `e` of the group they belong to (`gex` = the row's groups, `gw` =
+// columns per group).
+struct AStage16 { uint4 v[2]; int e; };
+__device__ __forceinline__ void load_a16(AStage16& a, const u16* __restrict__ src,
+                                         const int* __restrict__ gex, int gw, int k0) {
+  const int c = threadIdx.x & 7;
+  a.v[0] = ldg16(src + k0 + 8 * c);
+  a.v[1] = ldg16(src + k0 + 64 + 8 * c);
+  a.e = gex[k0 / gw];
+}
+// Stages them at the row's scale: times 2^(e - emax) (<= 1; exact unless the result is
+// subnormal in f16, i.e. below 2^-29 of the row's largest value).
+template <int MT = kMT>
+__device__ __forceinline__ void store_a16g(const AStage16& a, u16* dst, int emax,
+                                           int m = (int)(threadIdx.x >> 3)) {
+  typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+  const int c = threadIdx.x & 7, d = a.e - emax;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(a.v);
+  uint32_t h[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f16x2v v = __builtin_bit_cast(f16x2v, w[i]);
+    v[0] = __builtin_amdgcn_ldexph(v[0], d);
+    v[1] = __builtin_amdgcn_ldexph(v[1], d);
+    h[i] = __builtin_bit_cast(uint32_t, v);
+  }
+  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, c)) = make_uint4(h[0], h[1], h[2], h[3]);
+  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
+}
+
 // A workgroup barrier that also ORs a per-thread flag over the four waves of a 256-thread
 // workgroup, with one s_barrier: each wave's lane 0 writes the wave's OR into its slot before
 // the barrier and every wave reads the four slots after it.  (HIP's __syncthreads_or reduces
