@@ -14,7 +14,7 @@ namespace urb {
 // GLM (src/models/glm/runtime/moe.rs:162-171): acc = f64(shared) (or 0), then in ranking
 //   order acc += f64(w) * f64(y); out = f32(acc).
 // Every input row is read once and the output is not read back by this call, so both go
-// through non-temporal loads and stores (C5's GLM combine 54 -> 50 us).
+// through non-temporal loads and stores (GLM, 1024 tokens x 8 routes x 7168: 54 -> 50 us).
 // ------------------------------------------------------------------------------------------
 template <int KMAX>
 __global__ __launch_bounds__(256) void combine_qwen_kernel(const float* __restrict__ y,

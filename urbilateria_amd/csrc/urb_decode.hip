@@ -323,7 +323,7 @@ bool launch_gemv_mfma_down_combine(int fmt, const ExpertMats* mats, const int32_
   // one task per wave: split K while the workgroup stays within 16 waves, 2+ steps a part
   int ksplit = 1;
   while (K * ksplit * 2 <= kDecodeMaxWaves && steps / (2 * ksplit) >= 2) ksplit *= 2;
-  // half panels where whole ones leave CUs idle (C1 and Qwen3.6's H 2048: 128 -> 256)
+  // half panels where whole ones leave CUs idle (hidden 2048: 128 -> 256 workgroups)
   const bool half = H / kPanelRows < 256;
   const dim3 grid(half ? H / 8 : H / kPanelRows), block(64 * K * ksplit);
   const size_t lds = (size_t)K * I * 4;

@@ -642,9 +642,10 @@ static urb_status forward_one(urb_moe_ctx* c, const float* xc, const uint32_t* t
                                                   ws.shared_xp, ws.shared_out, epi, ws.status, s);
   } else {
     // With f32 logits from the router (the 8-lane routers), the routing runs inside the routed
-    // gate+up launch (every workgroup routes the token): C1 T=1 32.9 -> 31.9 us.  A sliced f64
-    // router keeps its routing kernel: reading the slices in every workgroup made C4 T=1's
-    // gate+up 36 -> 45 us.
+    // gate+up launch (every workgroup routes the token): one token through 128 BF16 experts of
+    // 2048 x 768, 32.9 -> 31.9 us.  A sliced f64 router keeps its routing kernel: reading the
+    // slices in every workgroup made one token's MXFP8 gate+up (160 experts, 6144 x 2048)
+    // 36 -> 45 us.
     const urb::RouteParams rp = launch_router_chunk(c, xc, tokens, 1, ws.logits, s, ws.xp);
     const bool ascending = d.composition != URB_COMPOSE_GLM;
     const urb::RouteJob job{ws.logits, K, rp, idc, wc, ascending ? ws.asc : nullptr};
@@ -704,9 +705,9 @@ static urb_status forward_mx_one(urb_moe_ctx* c, const float* xc, const uint32_t
   const urb::Epi routed{urb::kEpiHy4, d.swiglu_limit};
   const urb::Epi dense_mlp = dsv ? routed : urb::Epi{urb::kEpiHy4Shared, 0.0f};
   // The token's quantized pieces: a side job of the f64 GEMV router's launch (DeepSeek-V4 T=1
-  // 41.7 -> 40.0 us, Hy4 on C4 68.7 -> 67.7 us).  Beside the 8-lane router (DeepSeek-V4.1) they
-  // keep a launch of their own: that router's 48 workgroups at E 384 took 2.5 us longer with
-  // the 7168 values to quantize than the quantize launch costs.
+  // 41.7 -> 40.0 us, Hy4 with 160 MXFP8 experts 68.7 -> 67.7 us).  Beside the 8-lane router
+  // (DeepSeek-V4.1) they keep a launch of their own: that router's 48 workgroups at E 384 took
+  // 2.5 us longer with the 7168 values to quantize than the quantize launch costs.
   const int xq = c->router_lane8 ? 0 : block;
   uint16_t* rxp = xq ? ws.xp : nullptr;
   if (!xq)

@@ -261,23 +261,6 @@ __device__ __forceinline__ void store_a_hi(const AStage& a, u16* hi,
   *reinterpret_cast<uint4*>(hi + a_chunk<MT>(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
-// Writes the staged values times 2^e2 (exact) as f16 (round to nearest even) into LDS row m.
-template <int MT>
-__device__ __forceinline__ void store_a16(const AStage& a, u16* dst, int e2,
-                                          int m = (int)(threadIdx.x >> 3)) {
-  typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
-  const int c = threadIdx.x & 7;
-  const float* v = reinterpret_cast<const float*>(a.v);
-  uint32_t h[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    h[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
-                                            f32x2v{ldexpf(v[2 * i], e2), ldexpf(v[2 * i + 1], e2)},
-                                            f16x2v));
-  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, c)) = make_uint4(h[0], h[1], h[2], h[3]);
-  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
-}
-
 // f16 activation rows (the f16 down projection's input, written by the gate/up epilogue at the
 // scale of each row's panel group): thread c of row m loads chunks c and 8 + c of the K step at
 // k0, and the exponent field `e` of the group they belong to (`gex` = the row's groups, `gw` =

@@ -697,7 +697,7 @@ __global__ __launch_bounds__(64 * 8) void gemv_gate_up_route_kernel(
     return;
   }
   // BF16: half panel pairs, so a dense 2048-row gate+up offers 256 workgroups, one per CU
-  // (C3's 2 x 2048 x 7168 shared gate+up 16.3-17.6 -> 15.3-15.8 us).  The MX formats keep
+  // (a 2 x 2048 x 7168 shared gate+up 16.3-17.6 -> 15.3-15.8 us).  The MX formats keep
   // whole pairs: their steps are 1-2 KiB per panel, and halving them made DeepSeek-V4 Flash's
   // MXFP4 shared gate+up 12.3 -> 13.7 us.
   gemv_mfma_body<FMT, true, 1, decode_depth<FMT, true>(), decode_max_waves<FMT, true>(),
@@ -1039,9 +1039,9 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
 }
 
 // K slices of the batched router: as many as keep the launch within one round of two
-// workgroups per CU (512), so no slice waits for a second round (C5, 1024 tokens over 384
-// experts: 3 slices, 576 workgroups -> 2 slices, 384: router 62 -> 48 us beside the shared
-// expert, the layer 2.25 -> 2.24 ms).
+// workgroups per CU (512), so no slice waits for a second round (1024 tokens over 384
+// experts, hidden 7168: 3 slices, 576 workgroups -> 2 slices, 384: router 62 -> 48 us beside
+// the shared expert, the layer 2.25 -> 2.24 ms).
 int router_slices(int E, int H, int T) {
   const int steps = H / kKS;
   const int base = (router_rows(E) / kNT) * ((T + kMT - 1) / kMT);
