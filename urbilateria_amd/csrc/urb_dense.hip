@@ -220,34 +220,27 @@ __global__ __launch_bounds__(512, 1) void dense_gemm_kernel(
 }
 
 // act[t, j] = epi_gate_up(sum_z gate partial, sum_z up partial): the gate rows are columns
-// 0..I-1 of the partial sums, the up rows columns I..2I-1.
+// 0..I-1 of the partial sums, the up rows columns I..2I-1.  Four consecutive j per thread
+// (I % 4 == 0), the K parts added in order.
 __global__ void dense_reduce_gate_up_kernel(const float* __restrict__ part, int T, int I, int S,
                                             Epi epi, float* __restrict__ act, int* status) {
-  const size_t n = (size_t)T * I, stride = (size_t)T * 2 * I;
+  const size_t n4 = (size_t)T * I / 4, stride = (size_t)T * 2 * I;
   bool bad = false;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4;
        i += (size_t)gridDim.x * blockDim.x) {
-    const size_t t = i / I, j = i - t * I;
+    const size_t e = 4 * i, t = e / I, j = e - t * I;
     const float* p = part + t * 2 * I + j;
-    float g = 0.0f, u = 0.0f;
+    float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int z = 0; z < S; ++z) {
-      g += p[z * stride];
-      u += p[z * stride + I];
+      const float4 a = *reinterpret_cast<const float4*>(p + z * stride);
+      const float4 b = *reinterpret_cast<const float4*>(p + z * stride + I);
+      g[0] += a.x; g[1] += a.y; g[2] += a.z; g[3] += a.w;
+      u[0] += b.x; u[1] += b.y; u[2] += b.z; u[3] += b.w;
     }
-    act[i] = epi_gate_up(epi, g, u, bad);
-  }
-  if (bad) flag(status, kStatusNonFinite);
-}
-
-__global__ void dense_reduce_down_kernel(const float* __restrict__ part, int T, int H, int S,
-                                         Epi epi, float* __restrict__ out, int* status) {
-  const size_t n = (size_t)T * H;
-  bool bad = false;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * blockDim.x) {
-    float v = 0.0f;
-    for (int z = 0; z < S; ++z) v += part[z * n + i];
-    out[i] = epi_down<kFmtBF16>(epi, v, bad);
+    float o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = epi_gate_up(epi, g[k], u[k], bad);
+    *reinterpret_cast<float4*>(act + e) = make_float4(o[0], o[1], o[2], o[3]);
   }
   if (bad) flag(status, kStatusNonFinite);
 }
@@ -281,18 +274,8 @@ void launch_dense_gate_up(const ExpertMats& m, int T, int H, int I, const float*
   const int blocks = ((T + kDM - 1) / kDM) * (2 * I / kDN) * S;
   dense_gemm_kernel<<<(blocks + 7) / 8 * 8, 512, 0, s>>>(x, T, H, m.data[0], m.data[1], I,
                                                         2 * I, S, part);
-  dense_reduce_gate_up_kernel<<<reduce_blocks((size_t)T * I), 256, 0, s>>>(part, T, I, S, epi,
-                                                                          act, status);
-}
-
-void launch_dense_down(const ExpertMats& m, int T, int H, int I, const float* act, float* out,
-                       Epi epi, int* status, float* part, size_t part_floats, hipStream_t s) {
-  const int S = dense_splits(T, H, I, part_floats);
-  const int blocks = ((T + kDM - 1) / kDM) * (H / kDN) * S;
-  dense_gemm_kernel<<<(blocks + 7) / 8 * 8, 512, 0, s>>>(act, T, I, m.data[2], m.data[2], H, H,
-                                                        S, part);
-  dense_reduce_down_kernel<<<reduce_blocks((size_t)T * H), 256, 0, s>>>(part, T, H, S, epi, out,
-                                                                      status);
+  dense_reduce_gate_up_kernel<<<reduce_blocks((size_t)T * I / 4), 256, 0, s>>>(part, T, I, S, epi,
+                                                                              act, status);
 }
 
 }  // namespace urb

@@ -297,13 +297,12 @@ void launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t s);
 
 // The shared expert of a large batch (urb_dense.hip): dense BF16 GEMMs over 256 x 256 tiles
 // with split K, partial sums in `part` (part_floats floats, >= T * max(2 I, H)), then the
-// gate/up epilogue into act [T, I] or the down epilogue into out [T, H].  dense_fits: the shapes
-// and batch it takes (T >= 256; 2 I and H multiples of 256).
+// gate/up epilogue into act [T, I].  dense_fits: the shapes and batch it takes (T >= 256; 2 I
+// and H multiples of 256).  (The down projection measured faster on the grouped GEMM's dense
+// tiles and runs there.)
 bool dense_fits(int T, int I, int H, size_t part_floats);
 void launch_dense_gate_up(const ExpertMats& m, int T, int H, int I, const float* x, float* act,
                           Epi epi, int* status, float* part, size_t part_floats, hipStream_t s);
-void launch_dense_down(const ExpertMats& m, int T, int H, int I, const float* act, float* out,
-                       Epi epi, int* status, float* part, size_t part_floats, hipStream_t s);
 
 // The allocation-free layer call's scratch (urb_scratch.hip): kScratchBytes of device memory per
 // GPU, held until the process ends; the current device's address.
