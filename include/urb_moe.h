@@ -306,7 +306,8 @@ urb_status urb_moe_profile(urb_moe_ctx *ctx, int enable);
  * (arrays of URB_STAGE_COUNT). */
 urb_status urb_moe_profile_read(const urb_moe_ctx *ctx, double *ms, uint64_t *launches);
 
-/* HBM bytes the context holds for weights (own arena; 0 when borrowed) and workspace. */
+/* HBM bytes the context holds for weights (own arena, plus the f16 copy of a GLM layer's BF16
+ * shared down matrix that its batches of 256+ tokens multiply; 0 when borrowed) and workspace. */
 urb_status urb_moe_memory(const urb_moe_ctx *ctx, size_t *weight_bytes, size_t *workspace_bytes);
 
 const char *urb_status_string(urb_status status);

@@ -790,6 +790,36 @@ def test_dense_shared_batch_matches_oracle(comp, T, bf16_x):
     layer.close()
 
 
+def test_dense_shared_down_f16_range_matches_oracle():
+    # GLM batches of 256+ tokens with a BF16 shared expert run its down projection on f16 MFMAs
+    # over an f16 copy of the matrix when every non-zero value is exactly an f16 after one power
+    # of two (exponents within 32 binades); one weight 2^-67 among values near 2^-4 leaves that
+    # range, so the context keeps no copy (its weight bytes show it) and the BF16 hi/lo path runs
+    spec = C.LayerSpec(hidden=512, n_experts=16, top_k=4, intermediate=256,
+                       shared_intermediate=256, expert_format=C.FMT_MXFP4,
+                       shared_format=C.FMT_BF16, router=C.ROUTER_SIGMOID_NOAUX_TC,
+                       composition=C.COMPOSE_GLM, n_group=4, topk_group=2, normalize=True,
+                       routed_scaling_factor=2.5)
+    host = C.make_host_layer(spec, bias=C.zipf_bias(16, 1.1, 0.05))
+    down, scales = host.shared[2]
+    wide = down.copy()
+    wide.reshape(-1)[7] = (60 << 7) | 0x25  # BF16 exponent field 60: ~2^-67
+    wide_host = replace(host, shared=[host.shared[0], host.shared[1], (wide, scales)])
+    x = synth.activations("x.dense.f16range", 300, spec.hidden)
+    sizes = []
+    for h in (host, wide_host):
+        layer = moe_mod().MoeLayer(h, max_tokens=300)
+        y, ids, w = layer.forward(torch.from_numpy(x).cuda())
+        ref = _oracle(h, x)
+        assert ids_match(ids.cpu().numpy(), ref.ids, _scores(spec, ref, h.correction_bias))
+        err = rel_l2(y.cpu().numpy(), ref.output)
+        assert err < REL_L2_BAR, err
+        sizes.append(layer.memory()[0])
+        layer.close()
+    # the f16 copy: the down matrix's 512 x 256 values at 2 bytes, after a 256-byte header
+    assert sizes[0] - sizes[1] == 512 * 256 * 2 + 256
+
+
 def _lo_layer(comp):
     if comp == "glm":
         spec = C.LayerSpec(hidden=512, n_experts=16, top_k=4, intermediate=256,

@@ -245,6 +245,85 @@ __global__ void dense_reduce_gate_up_kernel(const float* __restrict__ part, int 
   if (bad) flag(status, kStatusNonFinite);
 }
 
+// The same sums and SwiGLU for one token row per workgroup, written as f16 times 2^(141 - e),
+// e = the largest exponent field of the row's values (its largest |value| then lies in
+// [2^14, 2^15)), and e in rowexp[t]: the input of an f16 down projection (Epi::rowexp with one
+// group).  The row's values wait in LDS (I floats) while the workgroup finds e.
+__global__ __launch_bounds__(256) void dense_reduce_gate_up_f16_kernel(
+    const float* __restrict__ part, int T, int I, int S, Epi epi, u16* __restrict__ act16,
+    int* __restrict__ rowexp, int* status) {
+  extern __shared__ float4 rowv[];  // I / 4
+  __shared__ int emax;
+  const int t = blockIdx.x;
+  const size_t stride = (size_t)T * 2 * I;
+  const float* p = part + (size_t)t * 2 * I;
+  if (threadIdx.x == 0) emax = 0;
+  __syncthreads();
+  bool bad = false;
+  int e = 0;
+  for (int j = 4 * threadIdx.x; j < I; j += 4 * blockDim.x) {
+    float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int z = 0; z < S; ++z) {
+      const float4 a = *reinterpret_cast<const float4*>(p + z * stride + j);
+      const float4 b = *reinterpret_cast<const float4*>(p + z * stride + I + j);
+      g[0] += a.x; g[1] += a.y; g[2] += a.z; g[3] += a.w;
+      u[0] += b.x; u[1] += b.y; u[2] += b.z; u[3] += b.w;
+    }
+    float o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[k] = epi_gate_up(epi, g[k], u[k], bad);
+      e = max(e, (int)((__float_as_uint(o[k]) >> 23) & 0xffu));
+    }
+    rowv[j / 4] = make_float4(o[0], o[1], o[2], o[3]);
+  }
+#pragma unroll
+  for (int x = 1; x < 64; x <<= 1) e = max(e, __shfl_xor(e, x));
+  if ((threadIdx.x & 63) == 0) atomicMax(&emax, e);
+  __syncthreads();
+  const int sh = 141 - emax;
+  u16* out = act16 + (size_t)t * I;
+  for (int j = 4 * threadIdx.x; j < I; j += 4 * blockDim.x) {
+    const float4 v = rowv[j / 4];
+    const _Float16 h[4] = {(_Float16)ldexpf(v.x, sh), (_Float16)ldexpf(v.y, sh),
+                           (_Float16)ldexpf(v.z, sh), (_Float16)ldexpf(v.w, sh)};
+    *reinterpret_cast<uint2*>(out + j) = __builtin_bit_cast(uint2, h);
+  }
+  if (threadIdx.x == 0) rowexp[t] = emax;
+  if (bad) flag(status, kStatusNonFinite);
+}
+
+// Exponent fields of a BF16 matrix's non-zero values (subnormals as 1): range[0] = min,
+// range[1] = max (pre-set to 255 and 0).
+__global__ void bf16_exp_range_kernel(const uint16_t* __restrict__ w, size_t n, int* range) {
+  int lo = 255, hi = 0;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t u = w[i];
+    if ((u & 0x7fffu) == 0) continue;
+    const int e = max((int)((u >> 7) & 0xffu), 1);
+    lo = min(lo, e);
+    hi = max(hi, e);
+  }
+#pragma unroll
+  for (int x = 1; x < 64; x <<= 1) {
+    lo = min(lo, __shfl_xor(lo, x));
+    hi = max(hi, __shfl_xor(hi, x));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMin(&range[0], lo);
+    atomicMax(&range[1], hi);
+  }
+}
+
+// BF16 values times 2^shift as f16 (exact for the shifts bf16_f16_shift returns).
+__global__ void bf16_to_f16_kernel(const uint16_t* __restrict__ w, size_t n, int shift,
+                                   u16* __restrict__ out) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = __builtin_bit_cast(u16, (_Float16)ldexpf(bf16_lo(w[i]), shift));
+}
+
 int reduce_blocks(size_t n) {
   return (int)std::min<size_t>(std::max<size_t>((n + 255) / 256, 1), 8192);
 }
@@ -276,6 +355,41 @@ void launch_dense_gate_up(const ExpertMats& m, int T, int H, int I, const float*
                                                         2 * I, S, part);
   dense_reduce_gate_up_kernel<<<reduce_blocks((size_t)T * I / 4), 256, 0, s>>>(part, T, I, S, epi,
                                                                               act, status);
+}
+
+void launch_dense_gate_up_f16(const ExpertMats& m, int T, int H, int I, const float* x,
+                              uint16_t* act16, int* rowexp, Epi epi, int* status, float* part,
+                              size_t part_floats, hipStream_t s) {
+  const int S = dense_splits(T, 2 * I, H, part_floats);
+  const int blocks = ((T + kDM - 1) / kDM) * (2 * I / kDN) * S;
+  dense_gemm_kernel<<<(blocks + 7) / 8 * 8, 512, 0, s>>>(x, T, H, m.data[0], m.data[1], I,
+                                                        2 * I, S, part);
+  dense_reduce_gate_up_f16_kernel<<<T, 256, (size_t)I * 4, s>>>(part, T, I, S, epi, act16,
+                                                                 rowexp, status);
+}
+
+int bf16_f16_shift(const uint16_t* w, size_t n) {
+  int* range = nullptr;
+  if (hipMalloc(&range, 2 * sizeof(int)) != hipSuccess) return kNoF16Shift;
+  const int init[2] = {255, 0};
+  int got[2] = {255, 0};
+  bool ok = hipMemcpy(range, init, sizeof(init), hipMemcpyHostToDevice) == hipSuccess;
+  if (ok) {
+    bf16_exp_range_kernel<<<reduce_blocks(n), 256>>>(w, n, range);
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpy(got, range, sizeof(got), hipMemcpyDeviceToHost) == hipSuccess;
+  }
+  (void)hipFree(range);
+  if (!ok) return kNoF16Shift;
+  if (got[1] == 0) return 0;  // all zero
+  // largest value below 2^16 (f16's largest finite value holds any 8-bit significand there);
+  // every value's last significand bit at or above 2^-24 (the f16 grid)
+  if (got[1] - got[0] > 32) return kNoF16Shift;
+  return 142 - got[1];
+}
+
+void launch_bf16_to_f16(const uint16_t* w, size_t n, int shift, uint16_t* out, hipStream_t s) {
+  bf16_to_f16_kernel<<<reduce_blocks(n), 256, 0, s>>>(w, n, shift, out);
 }
 
 }  // namespace urb

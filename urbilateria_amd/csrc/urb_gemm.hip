@@ -319,8 +319,9 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
             out[p * rows + row] = a;
           }
         } else {
-          const float v = F16 ? epi_down<FMT>(epi, ldexpf(acc0[q][mb][i], -lds.rexp[mm]), bad)
-                              : epi_down<FMT>(epi, acc0[q][mb][i], bad);
+          const float v =
+              F16 ? epi_down<FMT>(epi, ldexpf(acc0[q][mb][i], -lds.rexp[mm] - epi.wshift), bad)
+                  : epi_down<FMT>(epi, acc0[q][mb][i], bad);
           if (epi.stream_out) __builtin_nontemporal_store(v, &out[p * rows + row]);
           else out[p * rows + row] = v;
         }
@@ -436,14 +437,26 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
     // -> 117-121 us against 64-token tiles, down 120-125 -> 81-84 us against one panel)
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
     if constexpr (!PAIR) {
+      // epi.rowexp: f16 rows times f16 panels (a BF16 matrix converted by launch_to_f16)
+      if (np == 4 && epi.rowexp) {
+        launch_shape<FMT, PAIR, 1, 4, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                    status, s, beside);
+        return;
+      }
       if (np == 4) {
         launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
                                       beside);
         return;
       }
     }
-    if (np == 2)
+    if (!PAIR && np == 2 && epi.rowexp)
+      launch_shape<FMT, PAIR, 1, 2, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                   status, s, beside);
+    else if (np == 2)
       launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
+    else if (!PAIR && epi.rowexp)
+      launch_shape<FMT, PAIR, 1, 1, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                   status, s, beside);
     else
       launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   }

@@ -73,6 +73,8 @@ enum { kEpiGated = 0, kEpiQwen = 1, kEpiHy4 = 2, kEpiHy4Shared = 3 };
 // stream_out (down projections): the outputs are read once, by the combine at the end of the
 // call, so they are stored non-temporally and do not hold L2 lines during the GEMMs between
 // (the shared expert's down rows of a batch).
+// wshift (an f16 down projection over BF16-layout panels holding a BF16 matrix converted to f16
+// times 2^wshift, launch_to_f16): the sums are scaled back by 2^-wshift as well.
 struct Epi {
   int kind;
   float limit;
@@ -82,6 +84,7 @@ struct Epi {
   const unsigned* lo_word = nullptr;
   unsigned lo_gen = 0;
   bool stream_out = false;
+  int wshift = 0;
 };
 // E8M0 codes whose scale keeps every element of an MX matrix exact in f16 (MXFP4: 6 2^13 is
 // the largest value and 0.5 2^-23 = 2^-24 the f16 grid; MXFP8: 448 2^7, 2^-9 2^-15).
@@ -303,6 +306,18 @@ void launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t s);
 bool dense_fits(int T, int I, int H, size_t part_floats);
 void launch_dense_gate_up(const ExpertMats& m, int T, int H, int I, const float* x, float* act,
                           Epi epi, int* status, float* part, size_t part_floats, hipStream_t s);
+// The same, the SwiGLU rows as f16 at each row's scale with the row's largest exponent field in
+// rowexp[T] (the input of an f16 down projection: Epi::rowexp with one group).  I <= 16384.
+void launch_dense_gate_up_f16(const ExpertMats& m, int T, int H, int I, const float* x,
+                              uint16_t* act16, int* rowexp, Epi epi, int* status, float* part,
+                              size_t part_floats, hipStream_t s);
+// A BF16 matrix (n values, any layout) as f16: bf16_f16_shift returns the power of two that
+// makes every value exactly an f16 (the non-zero values' exponents span at most 32 binades:
+// the largest lands below 2^16, every significand bit at or above 2^-24), or kNoF16Shift;
+// launch_bf16_to_f16 writes the values times 2^shift, element for element.
+constexpr int kNoF16Shift = -1000;
+int bf16_f16_shift(const uint16_t* w, size_t n);
+void launch_bf16_to_f16(const uint16_t* w, size_t n, int shift, uint16_t* out, hipStream_t s);
 
 // The allocation-free layer call's scratch (urb_scratch.hip): kScratchBytes of device memory per
 // GPU, held until the process ends; the current device's address.

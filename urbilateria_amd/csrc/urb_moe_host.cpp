@@ -49,6 +49,7 @@ struct Workspace {
   float* xn = nullptr;  // QWEN36 block calls: the normalized BF16 token activations [chunk, H]
   float* gate_logit = nullptr;  // QWEN36 shared expert: bf16(shared_expert_gate . x) [chunk]
   int32_t* rowexp = nullptr;    // GLM, MX experts: [chunk * k, gate/up panel groups]
+  int32_t* shared_rowexp = nullptr;  // GLM, f16 shared down: [chunk] row exponents
   // one-token calls: BF16 piece vectors (urb_panel.hpp) of the token, the k SwiGLU rows and
   // the shared expert's SwiGLU row, the decode GEMVs' A operands
   uint16_t* xp = nullptr;
@@ -93,6 +94,13 @@ struct urb_moe_ctx {
   ExpertMats* table = nullptr;         // device [E]
   ExpertMats* shared_table = nullptr;  // device [1]
   ExpertMats shared_host{};            // the same pointers on the host
+  // GLM with a BF16 shared expert: its down matrix as f16 times 2^shared_wshift, in the BF16
+  // panel layout (urb::bf16_f16_shift; absent when its values span more than f16 holds
+  // exactly, or when the weights are borrowed), for batches whose shared gate+up runs on the
+  // dense kernel: the down projection then runs on f16 MFMAs from f16 SwiGLU rows
+  void* shared16 = nullptr;            // [ExpertMats] then the f16 matrix
+  ExpertMats* shared16_table = nullptr;
+  int shared_wshift = 0;
   // GLM batches with MX experts: the down projection runs on f16 MFMAs from row-scaled f16
   // activations (urb::Epi::rowexp) -- every down matrix's E8M0 codes keep its weights exact in
   // f16 (checked at create and by urb_moe_set_expert, which clears it otherwise)
@@ -235,6 +243,7 @@ static void destroy_ctx(urb_moe_ctx* c) {
   if (c->join) (void)hipEventDestroy(c->join);
   if (c->arena) (void)hipFree(c->arena);
   if (c->work) (void)hipFree(c->work);
+  if (c->shared16) (void)hipFree(c->shared16);
   delete c;
 }
 
@@ -280,6 +289,8 @@ static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspa
   if (d.composition == URB_COMPOSE_QWEN36 && d.shared_intermediate) w.gate_logit = b.take<float>(C);
   if (d.composition == URB_COMPOSE_GLM && d.expert_format != URB_FMT_BF16)
     w.rowexp = b.take<int32_t>(C * K * rowexp_groups(d));
+  if (d.composition == URB_COMPOSE_GLM && d.shared_intermediate && d.shared_format == URB_FMT_BF16)
+    w.shared_rowexp = b.take<int32_t>(C);
   w.xp = b.take<uint16_t>(H / 8 * urb::kPieceUnit);
   w.act_xp = b.take<uint16_t>(K * (I / 8) * urb::kPieceUnit);
   w.shared_xp = b.take<uint16_t>(std::max<size_t>(d.shared_intermediate, 8) / 8 *
@@ -496,6 +507,27 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
   if (host_flags[1] & 2) return URB_ERR_INVALID_SCALE;
   c->down_f16 = f16_check && !(host_flags[1] & 4);
   urb::launch_fill_i32(c->ws.status, 0, 4, nullptr);
+
+  // the BF16 shared down matrix as f16 (see urb_moe_ctx::shared16), own weights only
+  if (!borrow && has_shared && d->composition == URB_COMPOSE_GLM &&
+      d->shared_format == URB_FMT_BF16 && Is <= 16384) {
+    const size_t n = H * Is;
+    const uint16_t* down = reinterpret_cast<const uint16_t*>(shared.data[2]);
+    const int shift = urb::bf16_f16_shift(down, n);
+    if (shift != urb::kNoF16Shift) {
+      const size_t head = align_up(sizeof(ExpertMats));
+      URB_HIP(hipMalloc(&c->shared16, head + n * 2));
+      uint16_t* data16 = reinterpret_cast<uint16_t*>(static_cast<char*>(c->shared16) + head);
+      urb::launch_bf16_to_f16(down, n, shift, data16, nullptr);
+      URB_HIP(hipGetLastError());
+      ExpertMats m16{};
+      m16.data[2] = reinterpret_cast<const uint8_t*>(data16);
+      c->shared16_table = static_cast<ExpertMats*>(c->shared16);
+      URB_HIP(hipMemcpy(c->shared16_table, &m16, sizeof(m16), hipMemcpyHostToDevice));
+      c->shared_wshift = shift;
+      c->weight_bytes += head + n * 2;
+    }
+  }
 
   if (qwen_gate) urb::launch_relayout_lane8(gate_rows, 1, (int)H, c->shared_gate8, nullptr);
   if (lane8)
@@ -935,6 +967,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       sdepi.stream_out = true;  // read only by the combine, after the routed GEMMs
       Perm dense{nullptr, nullptr, nullptr, nullptr, nullptr, n, nullptr, nullptr, 0};
       const int dense_tiles = (n + urb::kGemmMTile - 1) / urb::kGemmMTile;
+      bool dense_gu = false, f16_down = false;
       {
         Span span(c, URB_STAGE_SHARED_GATE_UP, ss);
         if (qwen)
@@ -943,7 +976,16 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
         // in line (256+ tokens): the dense split-K kernel (urb_dense.hip), its partial sums in
         // the routed outputs' buffer, which nothing reads until the routed down projection
         const size_t part_floats = (size_t)c->chunk * K * H;
-        if (ss == s && d.shared_format == URB_FMT_BF16 && urb::dense_fits(n, Is, H, part_floats))
+        dense_gu = ss == s && d.shared_format == URB_FMT_BF16 &&
+                   urb::dense_fits(n, Is, H, part_floats);
+        // with the f16 shared down matrix: the SwiGLU rows as f16 for the f16 down projection
+        f16_down = dense_gu && c->shared16_table != nullptr;
+        if (f16_down)
+          urb::launch_dense_gate_up_f16(c->shared_host, n, H, Is, xc,
+                                        reinterpret_cast<uint16_t*>(ws.shared_act),
+                                        ws.shared_rowexp, sepi, ws.status, ws.y_perm,
+                                        part_floats, s);
+        else if (dense_gu)
           urb::launch_dense_gate_up(c->shared_host, n, H, Is, xc, ws.shared_act, sepi, ws.status,
                                     ws.y_perm, part_floats, s);
         else
@@ -952,8 +994,17 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       }
       {
         Span span(c, URB_STAGE_SHARED_DOWN, ss);
-        urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
-                              ws.shared_act, ws.shared_out, sdepi, ws.status, ss, ss != s);
+        if (f16_down) {
+          urb::Epi e16 = sdepi;
+          e16.rowexp = ws.shared_rowexp;
+          e16.groups = 1;
+          e16.wshift = c->shared_wshift;
+          urb::launch_gemm_down(URB_FMT_BF16, c->shared16_table, dense, dense_tiles, H, Is,
+                                ws.shared_act, ws.shared_out, e16, ws.status, ss, ss != s);
+        } else {
+          urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
+                                ws.shared_act, ws.shared_out, sdepi, ws.status, ss, ss != s);
+        }
       }
       if (ss != s) URB_HIP(hipEventRecord(c->join, ss));
     }

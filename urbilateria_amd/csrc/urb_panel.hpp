@@ -109,28 +109,33 @@ __device__ __forceinline__ bf16x8 decode_b(const BRaw<FMT>& r, int j) {
 }
 
 // MFMA j's B operand as f16 for the MX formats (exact for E8M0 codes within
-// [kF16ScaleLo, kF16ScaleHi] of the format; urb_moe_create checks the down projections).
+// [kF16ScaleLo, kF16ScaleHi] of the format; urb_moe_create checks the down projections).  In the
+// BF16 layout the panels hold f16 values already (a BF16 matrix converted exactly, times a power
+// of two, by launch_to_f16): the operand is the 16 bytes as loaded.
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 template <int FMT>
 __device__ __forceinline__ f16x8 decode_b16(const BRaw<FMT>& r, int j) {
-  static_assert(FMT != kFmtBF16, "BF16 weights have no exact f16 form");
-  const float sc = e8m0_to_f32(r.s);
-  uint32_t p[4];
-  if constexpr (FMT == kFmtMXFP4) {
-    const uint32_t w = j == 0 ? r.q.x : j == 1 ? r.q.y : j == 2 ? r.q.z : r.q.w;
-    p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 0));
-    p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 1));
-    p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 2));
-    p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 3));
+  if constexpr (FMT == kFmtBF16) {
+    return __builtin_bit_cast(f16x8, r.q[j]);
   } else {
-    const uint4 q = r.q[j >> 1];
-    const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
-    p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, sc, false));
-    p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, sc, true));
-    p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, sc, false));
-    p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, sc, true));
+    const float sc = e8m0_to_f32(r.s);
+    uint32_t p[4];
+    if constexpr (FMT == kFmtMXFP4) {
+      const uint32_t w = j == 0 ? r.q.x : j == 1 ? r.q.y : j == 2 ? r.q.z : r.q.w;
+      p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 0));
+      p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 1));
+      p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 2));
+      p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, sc, 3));
+    } else {
+      const uint4 q = r.q[j >> 1];
+      const uint32_t w0 = (j & 1) ? q.z : q.x, w1 = (j & 1) ? q.w : q.y;
+      p[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, sc, false));
+      p[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, sc, true));
+      p[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, sc, false));
+      p[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, sc, true));
+    }
+    return __builtin_bit_cast(f16x8, make_uint4(p[0], p[1], p[2], p[3]));
   }
-  return __builtin_bit_cast(f16x8, make_uint4(p[0], p[1], p[2], p[3]));
 }
 
 // ---- projection epilogues (kinds in urb_kernels.hpp) ----
