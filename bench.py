@@ -143,23 +143,31 @@ def stage_flops(spec, stage, tokens):
 
 
 def stage_bytes(spec, C, stage, tokens, distinct):
-    """Algorithmic HBM bytes of one launch of a stage (weights touched once, f32 activations)."""
+    """Algorithmic HBM bytes of one launch of a stage: weights touched once, f32 activations,
+    and the SwiGLU rows between gate/up and down at the width the path stores them (f16 where
+    the down projection runs on f16 MFMAs, f32 otherwise)."""
     H, I, E, k, Is = spec.hidden, spec.intermediate, spec.n_experts, spec.top_k, \
         spec.shared_intermediate
     eb = lambda fmt, r, c: sum(C.matrix_bytes(fmt, r, c))
     ef = spec.expert_format
+    glm = spec.composition == C.COMPOSE_GLM
+    # batches of a GLM layer with MX experts: f16 SwiGLU rows (urb_moe_host.cpp, down_f16)
+    act_w = 2 if glm and ef != C.FMT_BF16 and tokens > 1 else 4
+    # in-line batches of a GLM layer's BF16 shared expert: f16 SwiGLU rows (shared16)
+    sact_w = 2 if (glm and spec.shared_format == C.FMT_BF16 and tokens > 1
+                   and shared_in_line(spec, C, tokens)) else 4
     if stage == "gate_up":
-        routed = distinct * 2 * eb(ef, I, H) + tokens * H * 4 + tokens * k * I * 4
+        routed = distinct * 2 * eb(ef, I, H) + tokens * H * 4 + tokens * k * I * act_w
         if tokens == 1 and Is and spec.composition in (C.COMPOSE_GLM, C.COMPOSE_QWEN36):
             # one token: the shared expert's down projection runs in the routed gate+up launch
             routed += stage_bytes(spec, C, "shared_down", tokens, distinct)
         return routed
     if stage == "down":
-        return distinct * eb(ef, H, I) + tokens * k * I * 4 + tokens * k * H * 4
+        return distinct * eb(ef, H, I) + tokens * k * I * act_w + tokens * k * H * 4
     if stage == "shared_gate_up":
-        return 2 * eb(spec.shared_format, Is, H) + tokens * H * 4 + tokens * Is * 4
+        return 2 * eb(spec.shared_format, Is, H) + tokens * H * 4 + tokens * Is * sact_w
     if stage == "shared_down":
-        return eb(spec.shared_format, H, Is) + tokens * Is * 4 + tokens * H * 4
+        return eb(spec.shared_format, H, Is) + tokens * Is * sact_w + tokens * H * 4
     if stage == "router":
         return E * H * 2 + tokens * H * 4 + tokens * E * 4
     if stage == "combine":

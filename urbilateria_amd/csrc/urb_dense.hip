@@ -294,25 +294,50 @@ __global__ __launch_bounds__(256) void dense_reduce_gate_up_f16_kernel(
 }
 
 // Exponent fields of a BF16 matrix's non-zero values (subnormals as 1): range[0] = min,
-// range[1] = max (pre-set to 255 and 0).
-__global__ void bf16_exp_range_kernel(const uint16_t* __restrict__ w, size_t n, int* range) {
+// range[1] = max (pre-set to 255 and 0).  Eight values per thread and load; one pair of atomics
+// per workgroup.
+__global__ __launch_bounds__(256) void bf16_exp_range_kernel(const uint16_t* __restrict__ w,
+                                                             size_t n, int* range) {
+  __shared__ int lo_s, hi_s;
+  if (threadIdx.x == 0) {
+    lo_s = 255;
+    hi_s = 0;
+  }
+  __syncthreads();
   int lo = 255, hi = 0;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const uint32_t u = w[i];
-    if ((u & 0x7fffu) == 0) continue;
+  auto take = [&](uint32_t u) {
+    if ((u & 0x7fffu) == 0) return;
     const int e = max((int)((u >> 7) & 0xffu), 1);
     lo = min(lo, e);
     hi = max(hi, e);
+  };
+  const size_t n8 = n / 8;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n8;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const uint4 q = *reinterpret_cast<const uint4*>(w + 8 * i);
+    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      take(v[k] & 0xffffu);
+      take(v[k] >> 16);
+    }
   }
+  for (size_t i = 8 * n8 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    take(w[i]);
 #pragma unroll
   for (int x = 1; x < 64; x <<= 1) {
     lo = min(lo, __shfl_xor(lo, x));
     hi = max(hi, __shfl_xor(hi, x));
   }
   if ((threadIdx.x & 63) == 0) {
-    atomicMin(&range[0], lo);
-    atomicMax(&range[1], hi);
+    atomicMin(&lo_s, lo);
+    atomicMax(&hi_s, hi);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomicMin(&range[0], lo_s);
+    atomicMax(&range[1], hi_s);
   }
 }
 
@@ -375,7 +400,8 @@ int bf16_f16_shift(const uint16_t* w, size_t n) {
   int got[2] = {255, 0};
   bool ok = hipMemcpy(range, init, sizeof(init), hipMemcpyHostToDevice) == hipSuccess;
   if (ok) {
-    bf16_exp_range_kernel<<<reduce_blocks(n), 256>>>(w, n, range);
+    bf16_exp_range_kernel<<<(int)std::min<size_t>((n / 8 + 255) / 256 + 1, 1024), 256>>>(w, n,
+                                                                                        range);
     ok = hipGetLastError() == hipSuccess &&
          hipMemcpy(got, range, sizeof(got), hipMemcpyDeviceToHost) == hipSuccess;
   }
