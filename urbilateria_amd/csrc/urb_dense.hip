@@ -219,6 +219,142 @@ __global__ __launch_bounds__(512, 1) void dense_gemm_kernel(
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// The f16 down projection of the same batch: out[T, N] = A16[T, K] . W16[N, K]^T, A16 the
+// SwiGLU rows as f16 at each row's scale (rowexp, dense_reduce_gate_up_f16_kernel) and W16 the
+// f16 copy of the BF16 down matrix times 2^wshift (bf16_to_f16_kernel) in the panel layout.
+// One f16 piece per value, so half the gate/up tile's MFMAs per byte staged: the tile is 128
+// tokens x 256 rows (a 1024 x 7168 output gives 224 workgroups) and K is not split -- the
+// epilogue scales each sum back (2^-(141 - rowexp) 2^-wshift, exact) and applies the down
+// epilogue, with no partial sums and no reduce launch.  Eight waves of 64 tokens x 64 rows
+// (4 x 4 accumulator blocks of v_mfma_f32_16x16x32_f16); both operands staged per 32-column K
+// step in LDS in fragment order, double buffered, from registers loaded two steps ahead.
+// ------------------------------------------------------------------------------------------
+constexpr int kDM16 = 128;  // tokens per f16 down tile
+
+struct DenseDownLds {
+  u16 a[2][kDM16 / 16][kDFrag];
+  u16 b[2][kDN / 16][kDFrag];
+};
+
+__global__ __launch_bounds__(512, 1) void dense_down_f16_kernel(
+    const u16* __restrict__ a16, const int* __restrict__ rowexp, int T, int K,
+    const uint8_t* __restrict__ w16, int N, Epi epi, float* __restrict__ out, int* status) {
+  __shared__ __attribute__((aligned(16))) DenseDownLds lds;
+  const int Mt = (T + kDM16 - 1) / kDM16, Nt = N / kDN;
+  int mt, nt, z;
+  if (!dense_place(blockIdx.x, Mt, Nt, 1, &mt, &nt, &z)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;  // tokens 64 wm + [0, 64), rows 64 wn + [0, 64)
+  const int ksteps = K / kDK;
+  const size_t pbytes = (size_t)kPanelRows * K * 2;
+
+  // ---- staging: A unit (row, k-quad c) per thread, 8 consecutive threads on 8 consecutive
+  // rows of one k-quad (eight distinct 16-byte LDS positions mod 16: no store conflict; a
+  // row past T re-reads row m0, whose products land in rows never stored); B as the gate/up
+  // tile: panel tid / 32, units tid % 32 and tid % 32 + 32.
+  const int m0 = mt * kDM16;
+  const int c = (tid >> 3) & 3, tok = (tid & 7) + 8 * (tid >> 5);
+  const int arow = m0 + tok < T ? m0 + tok : m0;
+  const u16* a_src = a16 + (size_t)arow * K + 8 * c;
+  const int a_blk = tok >> 4, a_unit = (tok & 15) + 16 * c;
+  const int bp = tid >> 5, bu = tid & 31;
+  const uint8_t* b_src = w16 + (size_t)(nt * (kDN / kPanelRows) + bp) * pbytes + bu * 16;
+
+  struct Stage {
+    uint4 a;
+    uint4 b[2];
+  };
+  auto load = [&](Stage& st, int s) {
+    st.a = ldg16(a_src + s * kDK);
+    const uint8_t* pb = b_src + (size_t)s * 1024;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) st.b[i] = ldg16(pb + 512 * i);
+  };
+  auto store = [&](const Stage& st, int buf) {
+    *reinterpret_cast<uint4*>(&lds.a[buf][a_blk][8 * a_unit]) = st.a;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<uint4*>(&lds.b[buf][bp][8 * (bu + 32 * i)]) = st.b[i];
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](int buf) {
+    f16x8 bf[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+      bf[nb] = __builtin_bit_cast(f16x8,
+                                  *reinterpret_cast<const uint4*>(&lds.b[buf][wn * 4 + nb][8 * lane]));
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const f16x8 af = __builtin_bit_cast(
+          f16x8, *reinterpret_cast<const uint4*>(&lds.a[buf][wm * 4 + mb][8 * lane]));
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nb], acc[mb][nb], 0, 0, 0);
+    }
+  };
+
+  // the gate/up tile's pipeline: register stages two steps ahead, LDS double buffered, one
+  // barrier per step, the steady state's loads unguarded
+  Stage st[2];
+  load(st[0], 0);
+  if (ksteps > 1) load(st[1], 1);
+  store(st[0], 0);
+  __syncthreads();
+  int s = 0;
+  for (; s + 4 <= ksteps; s += 2) {
+    load(st[0], s + 2);
+    mma(0);
+    store(st[1], 1);
+    __syncthreads();
+    load(st[1], s + 3);
+    mma(1);
+    store(st[0], 0);
+    __syncthreads();
+  }
+  if (s < ksteps) {
+    mma(0);
+    if (s + 1 < ksteps) {
+      if (s + 2 < ksteps) load(st[0], s + 2);
+      store(st[1], 1);
+      __syncthreads();
+      mma(1);
+      if (s + 2 < ksteps) {
+        store(st[0], 0);
+        __syncthreads();
+        mma(0);
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds tokens 4 lq + i, row ln of each block
+  const int ln = lane & 15, lq = lane >> 4;
+  bool bad = false;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = m0 + wm * 64 + mb * 16 + 4 * lq + i;
+      if (t >= T) continue;
+      const int sh = rowexp[t] - 141 - epi.wshift;
+      float* o = out + (size_t)t * N + nt * kDN + wn * 64 + ln;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const float v = epi_down<kFmtBF16>(epi, ldexpf(acc[mb][nb][i], sh), bad);
+        if (epi.stream_out) __builtin_nontemporal_store(v, o + nb * 16);
+        else o[nb * 16] = v;
+      }
+    }
+  if (bad) flag(status, kStatusNonFinite);
+}
+
 // act[t, j] = epi_gate_up(sum_z gate partial, sum_z up partial): the gate rows are columns
 // 0..I-1 of the partial sums, the up rows columns I..2I-1.  Four consecutive j per thread
 // (I % 4 == 0), the K parts added in order.
@@ -391,6 +527,13 @@ void launch_dense_gate_up_f16(const ExpertMats& m, int T, int H, int I, const fl
                                                         2 * I, S, part);
   dense_reduce_gate_up_f16_kernel<<<T, 256, (size_t)I * 4, s>>>(part, T, I, S, epi, act16,
                                                                  rowexp, status);
+}
+
+void launch_dense_down_f16(const uint16_t* w16, int T, int H, int I, const uint16_t* act16,
+                           const int* rowexp, Epi epi, float* out, int* status, hipStream_t s) {
+  const int blocks = ((T + kDM16 - 1) / kDM16) * (H / kDN);
+  dense_down_f16_kernel<<<(blocks + 7) / 8 * 8, 512, 0, s>>>(
+      act16, rowexp, T, I, reinterpret_cast<const uint8_t*>(w16), H, epi, out, status);
 }
 
 int bf16_f16_shift(const uint16_t* w, size_t n) {

@@ -301,8 +301,8 @@ void launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t s);
 // The shared expert of a large batch (urb_dense.hip): dense BF16 GEMMs over 256 x 256 tiles
 // with split K, partial sums in `part` (part_floats floats, >= T * max(2 I, H)), then the
 // gate/up epilogue into act [T, I].  dense_fits: the shapes and batch it takes (T >= 256; 2 I
-// and H multiples of 256).  (The down projection measured faster on the grouped GEMM's dense
-// tiles and runs there.)
+// and H multiples of 256).  (A BF16 down projection from f32 rows measured faster on the
+// grouped GEMM's dense tiles and runs there; the f16 one runs launch_dense_down_f16.)
 bool dense_fits(int T, int I, int H, size_t part_floats);
 void launch_dense_gate_up(const ExpertMats& m, int T, int H, int I, const float* x, float* act,
                           Epi epi, int* status, float* part, size_t part_floats, hipStream_t s);
@@ -311,6 +311,11 @@ void launch_dense_gate_up(const ExpertMats& m, int T, int H, int I, const float*
 void launch_dense_gate_up_f16(const ExpertMats& m, int T, int H, int I, const float* x,
                               uint16_t* act16, int* rowexp, Epi epi, int* status, float* part,
                               size_t part_floats, hipStream_t s);
+// The f16 down projection out[T, H] of those f16 rows (rowexp) with w16, the f16 copy of the
+// BF16 down matrix times 2^epi.wshift in the panel layout: 128-token x 256-row tiles, no K
+// split, the down epilogue applied (the shapes dense_fits takes).
+void launch_dense_down_f16(const uint16_t* w16, int T, int H, int I, const uint16_t* act16,
+                           const int* rowexp, Epi epi, float* out, int* status, hipStream_t s);
 // A BF16 matrix (n values, any layout) as f16: bf16_f16_shift returns the power of two that
 // makes every value exactly an f16 (the non-zero values' exponents span at most 32 binades:
 // the largest lands below 2^16, every significand bit at or above 2^-24), or kNoF16Shift;

@@ -98,8 +98,8 @@ struct urb_moe_ctx {
   // panel layout (urb::bf16_f16_shift; absent when its values span more than f16 holds
   // exactly, or when the weights are borrowed), for batches whose shared gate+up runs on the
   // dense kernel: the down projection then runs on f16 MFMAs from f16 SwiGLU rows
-  void* shared16 = nullptr;            // [ExpertMats] then the f16 matrix
-  ExpertMats* shared16_table = nullptr;
+  // (urb::launch_dense_down_f16)
+  uint16_t* shared16 = nullptr;
   int shared_wshift = 0;
   // GLM batches with MX experts: the down projection runs on f16 MFMAs from row-scaled f16
   // activations (urb::Epi::rowexp) -- every down matrix's E8M0 codes keep its weights exact in
@@ -515,17 +515,11 @@ static urb_status create_impl(const urb_moe_desc* d, const urb_moe_weights* w,
     const uint16_t* down = reinterpret_cast<const uint16_t*>(shared.data[2]);
     const int shift = urb::bf16_f16_shift(down, n);
     if (shift != urb::kNoF16Shift) {
-      const size_t head = align_up(sizeof(ExpertMats));
-      URB_HIP(hipMalloc(&c->shared16, head + n * 2));
-      uint16_t* data16 = reinterpret_cast<uint16_t*>(static_cast<char*>(c->shared16) + head);
-      urb::launch_bf16_to_f16(down, n, shift, data16, nullptr);
+      URB_HIP(hipMalloc(&c->shared16, n * 2));
+      urb::launch_bf16_to_f16(down, n, shift, c->shared16, nullptr);
       URB_HIP(hipGetLastError());
-      ExpertMats m16{};
-      m16.data[2] = reinterpret_cast<const uint8_t*>(data16);
-      c->shared16_table = static_cast<ExpertMats*>(c->shared16);
-      URB_HIP(hipMemcpy(c->shared16_table, &m16, sizeof(m16), hipMemcpyHostToDevice));
       c->shared_wshift = shift;
-      c->weight_bytes += head + n * 2;
+      c->weight_bytes += n * 2;
     }
   }
 
@@ -979,7 +973,7 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
         dense_gu = ss == s && d.shared_format == URB_FMT_BF16 &&
                    urb::dense_fits(n, Is, H, part_floats);
         // with the f16 shared down matrix: the SwiGLU rows as f16 for the f16 down projection
-        f16_down = dense_gu && c->shared16_table != nullptr;
+        f16_down = dense_gu && c->shared16 != nullptr;
         if (f16_down)
           urb::launch_dense_gate_up_f16(c->shared_host, n, H, Is, xc,
                                         reinterpret_cast<uint16_t*>(ws.shared_act),
@@ -996,11 +990,10 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
         Span span(c, URB_STAGE_SHARED_DOWN, ss);
         if (f16_down) {
           urb::Epi e16 = sdepi;
-          e16.rowexp = ws.shared_rowexp;
-          e16.groups = 1;
           e16.wshift = c->shared_wshift;
-          urb::launch_gemm_down(URB_FMT_BF16, c->shared16_table, dense, dense_tiles, H, Is,
-                                ws.shared_act, ws.shared_out, e16, ws.status, ss, ss != s);
+          urb::launch_dense_down_f16(c->shared16, n, H, Is,
+                                     reinterpret_cast<const uint16_t*>(ws.shared_act),
+                                     ws.shared_rowexp, e16, ws.shared_out, ws.status, s);
         } else {
           urb::launch_gemm_down(d.shared_format, c->shared_table, dense, dense_tiles, H, Is,
                                 ws.shared_act, ws.shared_out, sdepi, ws.status, ss, ss != s);

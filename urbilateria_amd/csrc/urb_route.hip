@@ -99,38 +99,72 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
   const int e = g * 8 + el;
   const uint16_t* chains = w8 + (size_t)(live ? g : 0) * 8 * H + 8 * lane;
   const int nb = H8 / 16;
-  // The first RING batches are requested before the activations are staged.
-  uint4 ring[RING][2];
-#pragma unroll
-  for (int d = 0; d < RING; ++d)
-    if (d < nb) {
-      ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d) * 512);
-      ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * d + 1) * 512);
-    }
-  // Stage x with coalesced float4 loads, transposed into per-lane chains.  `lo`: some value is
-  // not BF16 (its hi/lo BF16 split, the grouped GEMMs' staging, has a non-zero lo half).
+  // Stage x with coalesced float4 loads, transposed into per-lane chains, kXR loads per thread
+  // in flight at a time.  The first kXR go out before the first RING weight batches (loads
+  // complete in order: the stores then wait for x alone, one round trip, instead of for the
+  // weights and then one round trip per float4); later ones, for long rows, after them.  A
+  // load past the end re-reads (and restages) the last float4.  `lo`: some value is not BF16
+  // (its hi/lo BF16 split, the grouped GEMMs' staging, has a non-zero lo half).
+  constexpr int kXR = 8 / WAVES;
+  const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H);
+  const int n4 = nt * H / 4, nth = 64 * WAVES;
   bool bad = false, lo = false;
-  const int n4 = nt * H / 4;
-  for (int i = threadIdx.x; i < n4; i += 64 * WAVES) {
-    const float4 v4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H)[i];
-    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+  float4 xv[kXR];
+  auto xload = [&](int i0) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      // token and column of the value (one token per workgroup: no division; measured on
-      // MI355X, the division in this loop was 0.5-0.7 of the one-token router's 6.8 us)
-      const int flat = 4 * i + u, tt = kLane8Tokens == 1 ? 0 : flat / H, c = flat - tt * H;
-      bad |= !finite(vv[u]);
-      lo |= (__float_as_uint(vv[u]) & 0xffffu) != 0;
-      xs[(tt * 8 + (c & 7)) * H8p + (c >> 3)] = vv[u];
+    for (int u = 0; u < kXR; ++u) xv[u] = x4[min(i0 + u * nth, n4 - 1)];
+  };
+  auto xstore = [&](int i0) {
+#pragma unroll
+    for (int u = 0; u < kXR; ++u) {
+      const int i = min(i0 + u * nth, n4 - 1);
+      const float vv[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // token and column of the value (one token per workgroup: no division; measured on
+        // MI355X, the division in this loop was 0.5-0.7 of the one-token router's 6.8 us)
+        const int flat = 4 * i + q, tt = kLane8Tokens == 1 ? 0 : flat / H, c = flat - tt * H;
+        bad |= !finite(vv[q]);
+        lo |= (__float_as_uint(vv[q]) & 0xffffu) != 0;
+        xs[(tt * 8 + (c & 7)) * H8p + (c >> 3)] = vv[q];
+      }
     }
+  };
+  // weight batch b into ring slot d; every fetch is issued, batches past the last clamped to
+  // it (a re-read), so that no load sits on one path only: the compiler's wait counts then
+  // stay exact instead of waiting for every load in flight
+  uint4 ring[RING][2];
+  auto fetch = [&](int d, int b) {
+    b = min(b, nb - 1);
+    ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * b) * 512);
+    ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * b + 1) * 512);
+  };
+  xload(threadIdx.x);
+  __builtin_amdgcn_sched_barrier(0);  // the x loads stay ahead of the weights'
+#pragma unroll
+  for (int d = 0; d < RING; ++d) fetch(d, d);
+  __builtin_amdgcn_sched_barrier(0);
+  xstore(threadIdx.x);
+  for (int i0 = threadIdx.x + kXR * nth; i0 < n4; i0 += kXR * nth) {
+    xload(i0);
+    xstore(i0);
   }
   if (bad) flag(status, kStatusNonFinite);
   if (lo_word && __ballot(lo) != 0 && lane == 0) *lo_word = lo_gen;
-  // one token: the workgroups also write its piece vector (the decode GEMVs' input)
-  if (xp && T == 1)
+  // one token, MX-activation input: the workgroups also write its quantized piece vector
+  if (xp && T == 1 && xq != 0)
     token_pieces(x, H, xp, xq, status, blockIdx.x * blockDim.x + threadIdx.x,
                  gridDim.x * blockDim.x);
   __syncthreads();
+  // one token: its piece vector (the decode GEMVs' input) from the staged row
+  if (xp && T == 1 && xq == 0) {
+    for (int u = blockIdx.x * blockDim.x + threadIdx.x; u < H8; u += gridDim.x * blockDim.x) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = xs[k * H8p + u];
+      store_piece_unit(v, xp + (size_t)u * kPieceUnit);
+    }
+  }
   if (!live) return;
   float acc[kLane8Tokens];
 #pragma unroll
@@ -142,10 +176,7 @@ __global__ __launch_bounds__(64 * WAVES) void router_lane8_kernel(
       const int b = b0 + d;
       if (b >= nb) break;
       const uint4 qa = ring[d][0], qb = ring[d][1];
-      if (b + RING < nb) {
-        ring[d][0] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + RING)) * 512);
-        ring[d][1] = *reinterpret_cast<const uint4*>(chains + (size_t)(2 * (b + RING) + 1) * 512);
-      }
+      fetch(d, b + RING);
       const float wv[16] = {bf16_lo(qa.x), bf16_hi(qa.x), bf16_lo(qa.y), bf16_hi(qa.y),
                             bf16_lo(qa.z), bf16_hi(qa.z), bf16_lo(qa.w), bf16_hi(qa.w),
                             bf16_lo(qb.x), bf16_hi(qb.x), bf16_lo(qb.y), bf16_hi(qb.y),
