@@ -231,10 +231,12 @@ __global__ __launch_bounds__(512, 1) void dense_gemm_kernel(
 // step in LDS in fragment order, double buffered, from registers loaded two steps ahead.
 // ------------------------------------------------------------------------------------------
 constexpr int kDM16 = 128;  // tokens per f16 down tile
+constexpr int kDStages = 2;  // register stages of the f16 down tile (4 measured no faster)
 
 struct DenseDownLds {
   u16 a[2][kDM16 / 16][kDFrag];
   u16 b[2][kDN / 16][kDFrag];
+  int sh[kDM16];  // the tile's rows' epilogue shifts
 };
 
 __global__ __launch_bounds__(512, 1) void dense_down_f16_kernel(
@@ -301,36 +303,38 @@ __global__ __launch_bounds__(512, 1) void dense_down_f16_kernel(
     }
   };
 
-  // the gate/up tile's pipeline: register stages two steps ahead, LDS double buffered, one
-  // barrier per step, the steady state's loads unguarded
-  Stage st[2];
-  load(st[0], 0);
-  if (ksteps > 1) load(st[1], 1);
+  // kDStages register stages (step s + kDStages loads while step s computes; its data has
+  // kDStages - 1 steps to arrive before it is stored), LDS double buffered, one barrier per
+  // step.  The steady state's loop has no exit between its steps and issues every load
+  // unguarded, so that the compiler's wait counts follow one issue order on every path; the
+  // last steps run in an unrolled tail.
+  // each row's epilogue shift (2^-(141 - rowexp) 2^-wshift), read from LDS by the epilogue
+  if (tid < kDM16) lds.sh[tid] = rowexp[min(m0 + tid, T - 1)] - 141 - epi.wshift;
+  Stage st[kDStages];
+#pragma unroll
+  for (int i = 0; i < kDStages; ++i)
+    if (i < ksteps) load(st[i], i);
   store(st[0], 0);
   __syncthreads();
   int s = 0;
-  for (; s + 4 <= ksteps; s += 2) {
-    load(st[0], s + 2);
-    mma(0);
-    store(st[1], 1);
-    __syncthreads();
-    load(st[1], s + 3);
-    mma(1);
-    store(st[0], 0);
-    __syncthreads();
-  }
-  if (s < ksteps) {
-    mma(0);
-    if (s + 1 < ksteps) {
-      if (s + 2 < ksteps) load(st[0], s + 2);
-      store(st[1], 1);
+  for (; s + 2 * kDStages <= ksteps; s += kDStages) {
+#pragma unroll
+    for (int d = 0; d < kDStages; ++d) {
+      load(st[d], s + d + kDStages);               // st[d] held step s + d, stored last step
+      mma(d & 1);                                  // step s + d
+      store(st[(d + 1) % kDStages], (d + 1) & 1);  // step s + d + 1 into the other buffer
       __syncthreads();
-      mma(1);
-      if (s + 2 < ksteps) {
-        store(st[0], 0);
-        __syncthreads();
-        mma(0);
-      }
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 2 * kDStages; ++d) {
+    const int step = s + d;
+    if (step >= ksteps) break;
+    if (step + kDStages < ksteps) load(st[d % kDStages], step + kDStages);
+    mma(d & 1);
+    if (step + 1 < ksteps) {
+      store(st[(d + 1) % kDStages], (d + 1) & 1);
+      __syncthreads();
     }
   }
 
@@ -343,7 +347,7 @@ __global__ __launch_bounds__(512, 1) void dense_down_f16_kernel(
     for (int i = 0; i < 4; ++i) {
       const int t = m0 + wm * 64 + mb * 16 + 4 * lq + i;
       if (t >= T) continue;
-      const int sh = rowexp[t] - 141 - epi.wshift;
+      const int sh = lds.sh[t - m0];
       float* o = out + (size_t)t * N + nt * kDN + wn * 64 + ln;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
