@@ -96,7 +96,9 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
     const int p = base + m0 + r;
     const int src_row = PAIR ? (perm.dense_tokens > 0 ? p : perm.perm_token[p]) : p;
     a_src[g] = in + (size_t)src_row * K;
-    a16[g] = reinterpret_cast<const u16*>(in) + (size_t)src_row * K;
+    // F16: the f16 rows; gate/up: the router's BF16 copy of the token rows (Epi::xb)
+    const u16* abase = F16 ? reinterpret_cast<const u16*>(in) : epi.xb;
+    a16[g] = abase ? abase + (size_t)src_row * K : nullptr;
   }
   // F16: each staged row's largest exponent field over the gate/up panel groups (rowexp); the
   // row is staged times 2^(141 - that), which takes its largest |value| into [2^14, 2^15).  Its
@@ -133,8 +135,10 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
     constexpr int NMB = decltype(nmb)::value;  // 16-token MFMA blocks this tile needs
     constexpr bool STREAM = decltype(streamed)::value;
     // DYNLO: the lo halves may be non-zero, checked per K step; otherwise the rows are
-    // BF16-valued and only their hi halves are staged and multiplied
-    constexpr bool DYNLO = decltype(dynamic_lo)::value;
+    // BF16-valued and only their hi halves are staged and multiplied -- XB: taken from the
+    // router's BF16 copy of the rows (Epi::xb) instead of converted from the f32 rows
+    constexpr int AMODE = decltype(dynamic_lo)::value;  // 0 hi of f32, 1 hi + lo, 2 BF16 copy
+    constexpr bool DYNLO = AMODE == 1, XB = AMODE == 2;
     BRaw<FMT> r0[R][NP], r1[R][NP];
     auto fetch = [&](int slot, int s) {
 #pragma unroll
@@ -147,10 +151,11 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
     // Staging rows this tile's MFMA blocks read: NMB 16 of them.  The rest (a tile of <= 16
     // tokens leaves rows 16..31, waves 2 and 3, idle) neither load nor stage.
     auto staged = [&](int g) { return am + 32 * g < NMB * 16; };
-    using Stage = std::conditional_t<F16, AStage16, AStage>;
+    using Stage = std::conditional_t<F16 || XB, AStage16, AStage>;
     auto fill = [&](Stage& a, int g, int k0) {
       if (staged(g)) {
         if constexpr (F16) load_a16(a, a16[g], a_gex[g], gw, k0);
+        else if constexpr (XB) load_ab(a, a16[g], k0);
         else load_a(a, a_src[g], true, k0);
       }
     };
@@ -160,6 +165,7 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
       for (int g = 0; g < RG; ++g) {
         if (!staged(g)) continue;
         if constexpr (F16) store_a16g<MT>(as[g], a_hi[buf], a_emax[g], am + 32 * g);
+        else if constexpr (XB) store_ab<MT>(as[g], a_hi[buf], am + 32 * g);
         else if constexpr (DYNLO) any |= store_a<MT>(as[g], a_hi[buf], a_lo[buf], am + 32 * g);
         else store_a_hi<MT>(as[g], a_hi[buf], am + 32 * g);
       }
@@ -283,10 +289,20 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
       else body(Int<1>{}, Cached{}, dyn);
     }
   };
-  // BF16-valued rows (Epi::no_lo, or no lo half seen by this call's router, Epi::lo_word)
-  if constexpr (F16) run(std::false_type{});
-  else if (epi.no_lo || (epi.lo_word && *epi.lo_word != epi.lo_gen)) run(std::false_type{});
-  else run(std::true_type{});
+  // BF16-valued rows (Epi::no_lo, or no lo half seen by this call's router, Epi::lo_word),
+  // from the router's BF16 copy where there is one
+  if constexpr (F16) {
+    run(std::false_type{});
+  } else if (epi.no_lo || (epi.lo_word && *epi.lo_word != epi.lo_gen)) {
+    if constexpr (PAIR) {
+      if (epi.xb) run(Int<2>{});
+      else run(std::false_type{});
+    } else {
+      run(std::false_type{});
+    }
+  } else {
+    run(std::true_type{});
+  }
 
   // ---- epilogue: lane holds column `row` of panel q, rows 4*lq + i of each 16-row block
   bool bad = false;

@@ -85,6 +85,10 @@ struct Epi {
   unsigned lo_gen = 0;
   bool stream_out = false;
   int wshift = 0;
+  // gate/up: the token rows as BF16 [T, K] (written by the batched MFMA router beside its own
+  // staging), staged in place of the f32 rows when they are BF16-valued (no lo half: no_lo or
+  // lo_word): half the activation bytes and no conversion per K step
+  const uint16_t* xb = nullptr;
 };
 // E8M0 codes whose scale keeps every element of an MX matrix exact in f16 (MXFP4: 6 2^13 is
 // the largest value and 0.5 2^-23 = 2^-24 the f16 grid; MXFP8: 448 2^7, 2^-9 2^-15).
@@ -198,10 +202,11 @@ __host__ __device__ inline int router_rows(int E) { return (E + kGemmNTile - 1) 
 constexpr int kRouterMaxSlices = 16;
 int router_slices(int E, int H, int T);
 // lo_word (optional): set to lo_gen when some lo half of x's hi/lo BF16 split is non-zero (the
-// grouped GEMMs' Epi::lo_word test).
+// grouped GEMMs' Epi::lo_word test).  xb (optional): x's hi halves (x as BF16 where it is
+// BF16-valued), [T, H] row-major, for Epi::xb.
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
                         int slices, int* status, hipStream_t s, unsigned* lo_word = nullptr,
-                        unsigned lo_gen = 0);
+                        unsigned lo_gen = 0, uint16_t* xb = nullptr);
 // One token: the f64 partial slices part[z][0][e] of the row-major router [E, H] from a GEMV
 // (router_gemv_slices(E) slices, exact products summed in f64).
 int router_gemv_slices(int E);

@@ -59,6 +59,9 @@ struct Workspace {
   // status + 4: the batched router's lo-half word (urb::Epi::lo_word), in the status block's
   // allocation so that it stays the context's own in no-alloc calls
   unsigned* lo_word = nullptr;
+  // the batched MFMA router's BF16 copy of a chunk's token rows [chunk, H] (urb::Epi::xb;
+  // contexts whose batches route with router_mfma_kernel, outside the allocation-free call)
+  uint16_t* xb = nullptr;
 };
 
 // Sequential bump allocator over one device allocation.
@@ -255,7 +258,8 @@ static size_t rowexp_groups(const urb_moe_desc& d) {
   return d.intermediate / (urb::kGemmNTile * (size_t)np);
 }
 
-static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspace& w) {
+static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspace& w,
+                            bool with_xb = true) {
   const urb_moe_desc& d = c->desc;
   const size_t C = chunk, E = d.n_experts, K = d.top_k, H = d.hidden, I = d.intermediate;
   w.status = b.take<int>(8);
@@ -285,6 +289,10 @@ static void carve_workspace(const urb_moe_ctx* c, Bump& b, size_t chunk, Workspa
   w.shared_act = b.take<float>(C * std::max<size_t>(d.shared_intermediate, 1));
   w.shared_out = b.take<float>(C * H);
   if (mx_activation(d.composition)) w.xq = b.take<float>(C * H);
+  // the routed gate+up reads the rows the router read only outside the MX-activation
+  // compositions (those read their quantized rows); the 8-lane routers write no copy
+  const bool lane8 = d.composition == URB_COMPOSE_QWEN36 || d.composition == URB_COMPOSE_DSV41;
+  if (with_xb && !lane8 && !mx_activation(d.composition)) w.xb = b.take<uint16_t>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36) w.xn = b.take<float>(C * H);
   if (d.composition == URB_COMPOSE_QWEN36 && d.shared_intermediate) w.gate_logit = b.take<float>(C);
   if (d.composition == URB_COMPOSE_GLM && d.expert_format != URB_FMT_BF16)
@@ -593,7 +601,7 @@ static urb::RouteParams launch_router_chunk(urb_moe_ctx* c, const float* x,
     rp.slices = urb::router_slices(E, H, n);
     rp.part = c->ws.router_part;
     urb::launch_router_mfma(c->router_panel, E, H, x, n, c->ws.router_part, rp.slices,
-                            c->ws.status, s, c->ws.lo_word, c->lo_gen);
+                            c->ws.status, s, c->ws.lo_word, c->lo_gen, c->ws.xb);
   }
   return rp;
 }
@@ -1020,6 +1028,8 @@ static urb_status forward_impl(urb_moe_ctx* c, const float* x, const uint32_t* t
       gepi.lo_word = ws.lo_word;
       gepi.lo_gen = lo_gen;
     }
+    // the router's BF16 copy of the same rows (batched MFMA router; null otherwise)
+    gepi.xb = ws.xb;
     depi.no_lo = qwen;
     // grouped MFMA GEMMs over the row tiles
     {
@@ -1065,12 +1075,12 @@ urb_status urb_moe_forward_noalloc(urb_moe_ctx* c, const float* x, uint32_t toke
   // this call's buffers, carved from the GPU's static scratch instead of the context workspace
   Workspace ws;
   Bump sizing{nullptr};
-  carve_workspace(c, sizing, tokens, ws);
+  carve_workspace(c, sizing, tokens, ws, false);
   if (sizing.off > urb::kScratchBytes) return URB_ERR_SHAPE;
   void* region = nullptr;
   URB_HIP(urb::scratch_region(&region));
   Bump b{static_cast<char*>(region)};
-  carve_workspace(c, b, tokens, ws);
+  carve_workspace(c, b, tokens, ws, false);
   ws.status = c->ws.status;  // failures still latch in the context's status word
   ws.lo_word = c->ws.lo_word;
   const Workspace own = c->ws;

@@ -298,6 +298,21 @@ __device__ __forceinline__ void store_a16g(const AStage16& a, u16* dst, int emax
   *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, 8 + c)) = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
+// BF16 activation rows (Epi::xb): thread c of row m loads chunks c and 8 + c of the K step at
+// k0 and stages them as they are -- the BF16-valued rows' hi halves, with no conversion.
+__device__ __forceinline__ void load_ab(AStage16& a, const u16* __restrict__ src, int k0) {
+  const int c = threadIdx.x & 7;
+  a.v[0] = ldg16(src + k0 + 8 * c);
+  a.v[1] = ldg16(src + k0 + 64 + 8 * c);
+}
+template <int MT = kMT>
+__device__ __forceinline__ void store_ab(const AStage16& a, u16* dst,
+                                         int m = (int)(threadIdx.x >> 3)) {
+  const int c = threadIdx.x & 7;
+  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, c)) = a.v[0];
+  *reinterpret_cast<uint4*>(dst + a_chunk<MT>(m, 8 + c)) = a.v[1];
+}
+
 // A workgroup barrier that also ORs a per-thread flag over the four waves of a 256-thread
 // workgroup, with one s_barrier: each wave's lane 0 writes the wave's OR into its slot before
 // the barrier and every wave reads the four slots after it.  (HIP's __syncthreads_or reduces

@@ -980,7 +980,8 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
                                                              int T, int slice,
                                                              double* __restrict__ part,
                                                              int* status, unsigned* lo_word,
-                                                             unsigned lo_gen) {
+                                                             unsigned lo_gen,
+                                                             u16* __restrict__ xb) {
   __shared__ __attribute__((aligned(16))) u16 a_hi[2][kMT * kALd];
   __shared__ __attribute__((aligned(16))) u16 a_lo[2][kMT * kALd];
   __shared__ __attribute__((aligned(16))) int lo_flag[2][4];  // per staging buffer, per wave
@@ -1008,6 +1009,20 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
 #pragma unroll
     for (int i = 0; i < 16; ++i) bad |= !finite(v[i]);
   };
+  // the workgroups also write x's hi halves (chunks c and 8 + c of the K step at k0, as
+  // load_a read them) for the grouped GEMMs (Epi::xb): K step s of a token tile by expert
+  // group s % gridDim.x, so each row and K step of x once, spread over the expert groups
+  u16* xrow = xb && a_valid ? xb + (size_t)(m0 + am) * H : nullptr;
+  auto put_xb = [&](const AStage& as, int k0) {
+    if (!xrow || (k0 / kKS) % (int)gridDim.x != (int)blockIdx.x) return;
+    const float* v = reinterpret_cast<const float*>(as.v);
+    const int c = threadIdx.x & 7;
+    uint32_t h[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = pk_bf16(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<uint4*>(xrow + k0 + 8 * c) = make_uint4(h[0], h[1], h[2], h[3]);
+    *reinterpret_cast<uint4*>(xrow + k0 + 64 + 8 * c) = make_uint4(h[4], h[5], h[6], h[7]);
+  };
   auto body = [&](auto nmb) {
     constexpr int NMB = decltype(nmb)::value;
     BRaw<kFmtBF16> r[DEPTH];
@@ -1017,6 +1032,7 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
     AStage as;
     load_a(as, a_src, a_valid, s_begin * kKS);
     check(as);
+    put_xb(as, s_begin * kKS);
     bool lo_any = barrier_or4(store_a(as, a_hi[0], a_lo[0]), lo_flag[0]);
     bool saw_lo = lo_any;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -1047,6 +1063,7 @@ __global__ __launch_bounds__(256, 2) void router_mfma_kernel(const uint8_t* __re
         }
         if (more) {
           check(as);
+          put_xb(as, (s + 1) * kKS);
           lo_any = barrier_or4(store_a(as, a_hi[buf ^ 1], a_lo[buf ^ 1]), lo_flag[buf ^ 1]);
           saw_lo |= lo_any;
         }
@@ -1136,12 +1153,12 @@ void launch_router_gemv_f64(const uint16_t* w, int E, int H, const float* x, dou
 
 void launch_router_mfma(const uint8_t* wp, int E, int H, const float* x, int T, double* part,
                         int slices, int* status, hipStream_t s, unsigned* lo_word,
-                        unsigned lo_gen) {
+                        unsigned lo_gen, uint16_t* xb) {
   const int steps = H / kKS;
   const int per = (steps + slices - 1) / slices;
   dim3 grid(router_rows(E) / kNT, (T + kMT - 1) / kMT, slices);
   router_mfma_kernel<4><<<grid, 256, 0, s>>>(wp, router_rows(E), H, x, T, per, part, status,
-                                             lo_word, lo_gen);
+                                             lo_word, lo_gen, xb);
 }
 
 void launch_relayout_lane8(const uint16_t* w, int E, int H, uint16_t* w8, hipStream_t s) {
