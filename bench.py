@@ -143,9 +143,11 @@ def stage_flops(spec, stage, tokens):
 
 
 def stage_bytes(spec, C, stage, tokens, distinct):
-    """Algorithmic HBM bytes of one launch of a stage: weights touched once, f32 activations,
-    and the SwiGLU rows between gate/up and down at the width the path stores them (f16 where
-    the down projection runs on f16 MFMAs, f32 otherwise)."""
+    """Algorithmic HBM bytes of one launch of a stage: weights touched once, the token rows at
+    the width the gate/up reads them (a GLM batch's BF16 copy from the MFMA router, as the
+    synthetic rows are BF16-valued; f32 otherwise), and the
+    SwiGLU rows between gate/up and down at the width the path stores them (f16 where the down
+    projection runs on f16 MFMAs, f32 otherwise)."""
     H, I, E, k, Is = spec.hidden, spec.intermediate, spec.n_experts, spec.top_k, \
         spec.shared_intermediate
     eb = lambda fmt, r, c: sum(C.matrix_bytes(fmt, r, c))
@@ -156,8 +158,12 @@ def stage_bytes(spec, C, stage, tokens, distinct):
     # in-line batches of a GLM layer's BF16 shared expert: f16 SwiGLU rows (shared16)
     sact_w = 2 if (glm and spec.shared_format == C.FMT_BF16 and tokens > 1
                    and shared_in_line(spec, C, tokens)) else 4
+    # the routed gate+up of a GLM batch reads the MFMA router's BF16 copy of the token rows
+    # (urb_moe_host.cpp, Workspace::xb; the other compositions route with the 8-lane tree or
+    # read quantized rows)
+    x_w = 2 if glm and tokens > 1 else 4
     if stage == "gate_up":
-        routed = distinct * 2 * eb(ef, I, H) + tokens * H * 4 + tokens * k * I * act_w
+        routed = distinct * 2 * eb(ef, I, H) + tokens * H * x_w + tokens * k * I * act_w
         if tokens == 1 and Is and spec.composition in (C.COMPOSE_GLM, C.COMPOSE_QWEN36):
             # one token: the shared expert's down projection runs in the routed gate+up launch
             routed += stage_bytes(spec, C, "shared_down", tokens, distinct)
