@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="all",
-                    help="comma list of name:tokens (default: all seven runs; the "
+                    help="comma list of name:tokens (default: all nine runs; the "
                          "MX-activation variants c4_mxfp8_mx_activation and "
                          "c5_mxfp4_mx_activation run when named)")
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
