@@ -451,28 +451,18 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
     // panels per wave, each staged activation fragment feeding as many weight panels (a
     // 1024-token batch through a 2048 x 7168 BF16 shared expert, in isolation: gate+up 136-140
     // -> 117-121 us against 64-token tiles, down 120-125 -> 81-84 us against one panel)
+    // (BF16 weights take f32 or BF16 rows here; the f16 down projection of a BF16 matrix runs
+    // on urb_dense.hip's dense_down_f16_kernel)
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
     if constexpr (!PAIR) {
-      // epi.rowexp: f16 rows times f16 panels (a BF16 matrix converted by launch_to_f16)
-      if (np == 4 && epi.rowexp) {
-        launch_shape<FMT, PAIR, 1, 4, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                    status, s, beside);
-        return;
-      }
       if (np == 4) {
         launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
                                       beside);
         return;
       }
     }
-    if (!PAIR && np == 2 && epi.rowexp)
-      launch_shape<FMT, PAIR, 1, 2, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                   status, s, beside);
-    else if (np == 2)
+    if (np == 2)
       launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
-    else if (!PAIR && epi.rowexp)
-      launch_shape<FMT, PAIR, 1, 1, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                   status, s, beside);
     else
       launch_shape<FMT, PAIR, 1, 1>(mats, perm, max_tiles, rows, K, in, out, epi, status, s, beside);
   }

@@ -73,8 +73,8 @@ enum { kEpiGated = 0, kEpiQwen = 1, kEpiHy4 = 2, kEpiHy4Shared = 3 };
 // stream_out (down projections): the outputs are read once, by the combine at the end of the
 // call, so they are stored non-temporally and do not hold L2 lines during the GEMMs between
 // (the shared expert's down rows of a batch).
-// wshift (an f16 down projection over BF16-layout panels holding a BF16 matrix converted to f16
-// times 2^wshift, launch_to_f16): the sums are scaled back by 2^-wshift as well.
+// wshift (the dense f16 down projection over a BF16 matrix converted to f16 times 2^wshift,
+// launch_bf16_to_f16): the sums are scaled back by 2^-wshift as well.
 struct Epi {
   int kind;
   float limit;

@@ -109,15 +109,12 @@ __device__ __forceinline__ bf16x8 decode_b(const BRaw<FMT>& r, int j) {
 }
 
 // MFMA j's B operand as f16 for the MX formats (exact for E8M0 codes within
-// [kF16ScaleLo, kF16ScaleHi] of the format; urb_moe_create checks the down projections).  In the
-// BF16 layout the panels hold f16 values already (a BF16 matrix converted exactly, times a power
-// of two, by launch_to_f16): the operand is the 16 bytes as loaded.
+// [kF16ScaleLo, kF16ScaleHi] of the format; urb_moe_create checks the down projections).
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 template <int FMT>
 __device__ __forceinline__ f16x8 decode_b16(const BRaw<FMT>& r, int j) {
-  if constexpr (FMT == kFmtBF16) {
-    return __builtin_bit_cast(f16x8, r.q[j]);
-  } else {
+  static_assert(FMT != kFmtBF16, "BF16 matrices take f16 MFMAs only on the dense kernel");
+  {
     const float sc = e8m0_to_f32(r.s);
     uint32_t p[4];
     if constexpr (FMT == kFmtMXFP4) {
