@@ -381,14 +381,19 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
   }
 }
 
+// Workgroups per CU a shape is compiled for: two (up to 256 VGPRs), three for the MXFP4 gate/up
+// pair (168 VGPRs: two panels per wave, two weight steps in flight, rows gathered two ahead).
+template <int FMT, bool PAIR, int DEPTH, int NP, int AD>
+constexpr int gemm_blocks_per_cu() {
+  return FMT == kFmtMXFP4 && PAIR && DEPTH == 2 && NP == 2 && AD == 2 ? 3 : 2;
+}
+
 // Placement: gemm_place (urb_kernels.hpp); xsplit > 1 only for a dense batch (one expert).
 template <int FMT, bool PAIR, int DEPTH, int NP, int MT, int AD = 1, bool F16 = false>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(const ExpertMats* __restrict__ mats,
-                                                      Perm perm, int max_tiles, int xsplit,
-                                                      int rows, int K,
-                                                      const float* __restrict__ in,
-                                                      float* __restrict__ out, Epi epi,
-                                                      int* status, int block0) {
+__global__ __launch_bounds__(256, (gemm_blocks_per_cu<FMT, PAIR, DEPTH, NP, AD>())) void
+gemm_kernel(const ExpertMats* __restrict__ mats, Perm perm, int max_tiles, int xsplit, int rows,
+            int K, const float* __restrict__ in, float* __restrict__ out, Epi epi, int* status,
+            int block0) {
   __shared__ __attribute__((aligned(16))) GemmLds<MT> lds;
   const int groups = rows / (kNT * NP);
   const int ntiles = min(perm.dense_tokens > 0 ? (perm.dense_tokens + MT - 1) / MT : perm.meta[1],
@@ -492,32 +497,32 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
       launch_shape<FMT, PAIR, 1, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
                                     beside);
   }
-  else {
+  else if constexpr (PAIR) {
+    // the gate/up pair: two panels per wave with two weight steps in flight and the activation
+    // rows gathered two steps ahead, at three workgroups per CU (1024 tokens, top-8 over 384
+    // experts of 7168 x 2048, Zipf-routed: 1,207-1,210 against 1,224 us for four panels one
+    // step deep at two per CU; gathering two steps ahead took that shape 1417 -> 1253 us)
+    launch_shape<FMT, PAIR, 2, 2, kMT, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status,
+                                          s, beside);
+  } else {
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
-    if constexpr (!PAIR) {
-      // the down projection: eight panels per wave where the rows allow (1024 tokens, top-8 over
-      // 384 experts of 7168 x 2048, in isolation: 797-808 -> 755-770 us against four)
-      if (np == 8) {
-        if (epi.rowexp)
-          launch_shape<FMT, PAIR, 1, 8, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                      status, s, beside);
-        else
-          launch_shape<FMT, PAIR, 1, 8>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
-                                        beside);
-        return;
-      }
-    }
-    if (np == 4 && !PAIR && epi.rowexp)
-      launch_shape<FMT, PAIR, 1, 4, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                   status, s, beside);
+    // the down projection: eight panels per wave where the rows allow (1024 tokens, top-8 over
+    // 384 experts of 7168 x 2048, in isolation: 797-808 -> 755-770 us against four)
+    if (np == 8 && epi.rowexp)
+      launch_shape<FMT, PAIR, 1, 8, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                  status, s, beside);
+    else if (np == 8)
+      launch_shape<FMT, PAIR, 1, 8>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                    beside);
+    else if (np == 4 && epi.rowexp)
+      launch_shape<FMT, PAIR, 1, 4, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                  status, s, beside);
     else if (np == 4)
-      // the gate/up pair gathers its activation rows two steps ahead (the same 1024-token
-      // batch's gate/up in isolation: 1417 -> 1253 us)
-      launch_shape<FMT, PAIR, 1, 4, kMT, PAIR ? 2 : 1>(mats, perm, max_tiles, rows, K, in, out,
-                                                        epi, status, s, beside);
-    else if (!PAIR && epi.rowexp)
-      launch_shape<FMT, PAIR, 2, 2, kMT, 1, !PAIR>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                   status, s, beside);
+      launch_shape<FMT, PAIR, 1, 4>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
+                                    beside);
+    else if (epi.rowexp)
+      launch_shape<FMT, PAIR, 2, 2, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
+                                                  status, s, beside);
     else
       launch_shape<FMT, PAIR, 2, 2>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
                                     beside);
@@ -530,7 +535,8 @@ int gemm_panels_per_wave(int fmt, int rows, bool pair, int dense_tokens) {
     return !pair && rows % (kNT * 4) == 0 ? 4 : 2;
   }
   if (fmt == kFmtMXFP8) return !pair && rows % (kNT * 4) == 0 ? 4 : 2;
-  if (!pair && rows % (kNT * 8) == 0) return 8;
+  if (pair) return 2;
+  if (rows % (kNT * 8) == 0) return 8;
   return rows % (kNT * 4) == 0 ? 4 : 2;
 }
 
