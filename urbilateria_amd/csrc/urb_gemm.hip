@@ -381,11 +381,14 @@ __device__ __forceinline__ void gemm_tile(const ExpertMats* __restrict__ mats, c
   }
 }
 
-// Workgroups per CU a shape is compiled for: two (up to 256 VGPRs), three for the MXFP4 gate/up
-// pair (168 VGPRs: two panels per wave, two weight steps in flight, rows gathered two ahead).
+// Workgroups per CU a shape is compiled for: two (up to 256 VGPRs), three (168 VGPRs) for the
+// MX gate/up pairs: MXFP4 with two panels per wave, two weight steps in flight and the rows
+// gathered two ahead; MXFP8 with two panels, one step, rows one ahead.
 template <int FMT, bool PAIR, int DEPTH, int NP, int AD>
 constexpr int gemm_blocks_per_cu() {
-  return FMT == kFmtMXFP4 && PAIR && DEPTH == 2 && NP == 2 && AD == 2 ? 3 : 2;
+  if (FMT == kFmtMXFP4 && PAIR && DEPTH == 2 && NP == 2 && AD == 2) return 3;
+  if (FMT == kFmtMXFP8 && PAIR && DEPTH == 1 && NP == 2 && AD == 1) return 3;
+  return 2;
 }
 
 // Placement: gemm_place (urb_kernels.hpp); xsplit > 1 only for a dense batch (one expert).
@@ -486,6 +489,8 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
         return;
       }
     }
+    // the gate/up pair runs at three workgroups per CU (512 tokens over 160 experts of 6144 x
+    // 2048: 735-736 -> 689 us against two per CU, in one process).
     // activation rows gathered one step ahead: two steps ahead (as the MXFP4 gate+up) was 1 %
     // faster in isolation on f32 token rows (512 tokens over 160 experts of 6144 x 2048: 782-787
     // -> 776-777 us) but 1.5 % slower on BF16-valued rows, which skip the lo-half MFMAs
