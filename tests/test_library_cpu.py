@@ -263,7 +263,7 @@ def _groups(fmt, rows, pair, dense):
     elif fmt == C.FMT_MXFP8:
         np_ = 4 if not pair and rows % 256 == 0 else 2
     else:
-        np_ = 2 if pair else 8 if rows % 512 == 0 else 4 if rows % 256 == 0 else 2
+        np_ = 2 if pair else 4 if rows % 256 == 0 else 2
     return rows // (64 * np_)
 
 

@@ -511,15 +511,10 @@ static void launch(const ExpertMats* mats, const Perm& perm, int max_tiles, int 
                                           s, beside);
   } else {
     const int np = gemm_panels_per_wave(FMT, rows, PAIR, perm.dense_tokens);
-    // the down projection: eight panels per wave where the rows allow (1024 tokens, top-8 over
-    // 384 experts of 7168 x 2048, in isolation: 797-808 -> 755-770 us against four)
-    if (np == 8 && epi.rowexp)
-      launch_shape<FMT, PAIR, 1, 8, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
-                                                  status, s, beside);
-    else if (np == 8)
-      launch_shape<FMT, PAIR, 1, 8>(mats, perm, max_tiles, rows, K, in, out, epi, status, s,
-                                    beside);
-    else if (np == 4 && epi.rowexp)
+    // the down projection: four panels per wave where the rows allow, four workgroups per CU
+    // on the f16 rows (127 VGPRs; 1024 tokens, top-8 over 384 experts of 7168 x 2048: 690
+    // against 713-716 us for eight panels at two per CU, in one process)
+    if (np == 4 && epi.rowexp)
       launch_shape<FMT, PAIR, 1, 4, kMT, 1, true>(mats, perm, max_tiles, rows, K, in, out, epi,
                                                   status, s, beside);
     else if (np == 4)
@@ -541,7 +536,6 @@ int gemm_panels_per_wave(int fmt, int rows, bool pair, int dense_tokens) {
   }
   if (fmt == kFmtMXFP8) return !pair && rows % (kNT * 4) == 0 ? 4 : 2;
   if (pair) return 2;
-  if (rows % (kNT * 8) == 0) return 8;
   return rows % (kNT * 4) == 0 ? 4 : 2;
 }
 
